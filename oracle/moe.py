@@ -1,0 +1,348 @@
+"""The MoE expert path of bux off a Blackwell GPU, restated in numpy. TEST
+INFRASTRUCTURE ONLY (see `oracle`).
+
+Follows (all paths under ``src/bux/architecture/``):
+
+- `sort_by_expert`: ``experts/moe.py:776-797``;
+- `token_rows`, `picked_weights`, `sum_by_token`: ``experts/moe.py:991-1066``,
+  ``experts/grouped_blockscaled.py:141-148``;
+- `tiles_of`: ``experts/grouped_mxfp8.py:157-182``;
+- `rows_mx`, `contract_mx`: ``experts/grouped_blockscaled.py:220-250`` (XLA's
+  dequantize, then ``ragged_dot`` / ``ragged_dot_general`` in float32);
+- `ragged_dot_bf16`, `weight_grad_bf16`: ``experts/grouped.py:42-76,105-161`` off a
+  GPU (``jax.lax.ragged_dot`` of bfloat16, float32 sums);
+- `activate`, `weighted_units`, `weighted_units_backward`: ``layers/mlp.py:20-35``,
+  ``common/functional.py:12-40``, ``experts/moe.py:898-926``;
+- `layer_forward`, `layer_backward`: ``experts/moe.py:733-873`` with
+  ``grouped_blockscaled.py:167-211`` (``routed`` -> ``experts`` -> two
+  ``grouped_product``s, picked rows in, summed rows out).
+
+Pins, run by ``tests/test_oracle.py``:
+
+- `sort_by_expert`: against a brute-force stable sort (Python's ``sorted`` with the
+  position as tie-break) and ``np.bincount``; on the reference's size patterns
+  ``[70, 0, 100, 3, 77]`` (tests/test_grouped.py:24) and ``[0, 130, 1, 3, 256, 0,
+  300, 100]`` (tests/test_grouped_mxfp8.py:23); out-of-range picks sort last;
+- `tiles_of`: the reference's own invariant (tests/test_grouped_mxfp8.py:31-41):
+  every group row covered once, inside one tile, count ``ceil(m/t) + g - 1``;
+- `sum_by_token`: the transpose identity ``<token_rows(z), y> == <z, sum_by_token(y)>``
+  in float64, and brute-force loops;
+- `rows_mx`, `contract_mx`: brute-force float64 triple loops on small shapes; empty
+  groups and rows past the groups are 0; garbage past ``filled`` changes no dW
+  (tests/test_grouped.py:89-95);
+- `weighted_units_backward`: against torch.autograd of the same forward in float64.
+
+Bit-level parity of float sums is unpinned: XLA:CPU's summation order inside
+``ragged_dot`` and its bfloat16 excess-precision choices are not observable without
+jax. The oracle sums in float32 (numpy's BLAS) and rounds once to bfloat16; GPU
+results are compared to it within tolerances stated in each test.
+"""
+
+from typing import NamedTuple
+
+import numpy as np
+
+from oracle import bf16, mxfp8
+from oracle.mxfp8 import Blocks
+
+
+class Sorted(NamedTuple):
+    """`sort_by_expert`'s result (moe.py:776-791), plus the group offsets that the
+    kernels take (``cumsum(sizes) - sizes``, grouped_mxfp8.py:142)."""
+
+    order: np.ndarray  # int32 [M]
+    inverse: np.ndarray  # int32 [M]
+    sizes: np.ndarray  # int32 [E]
+    offsets: np.ndarray  # int32 [E]
+
+
+def sort_by_expert(idx: np.ndarray, num_experts: int) -> Sorted:
+    """Return the flat picks sorted by expert, stably; picks outside [0, E) sort
+    last and count for none (moe.py:776-797)."""
+    flat = np.asarray(idx).reshape(-1).astype(np.int64)
+    flat = np.where((flat >= 0) & (flat < num_experts), flat, num_experts)
+    order = np.argsort(flat, kind="stable").astype(np.int32)
+    sizes = np.bincount(flat, minlength=num_experts + 1)[:num_experts].astype(np.int32)
+    inverse = np.empty_like(order)
+    inverse[order] = np.arange(order.size, dtype=np.int32)
+    offsets = (np.cumsum(sizes) - sizes).astype(np.int32)
+    return Sorted(order, inverse, sizes, offsets)
+
+
+def token_rows(z: np.ndarray, order: np.ndarray, k: int) -> np.ndarray:
+    """Return ``z[order // k]`` (moe.py:991-1016)."""
+    return z[np.asarray(order) // k]
+
+
+def picked_weights(weights: np.ndarray, order: np.ndarray) -> np.ndarray:
+    """Return each sorted pick's weight, ``weights.reshape(-1)[order]``
+    (moe.py:1027-1032)."""
+    return np.asarray(weights).reshape(-1)[np.asarray(order)]
+
+
+def sum_by_token(y: np.ndarray, inverse: np.ndarray, out_bf16: bool = True) -> np.ndarray:
+    """Return each token's sum of its k rows of y at ``inverse`` (t, k), added in
+    float32 in pick order; an index outside y's rows adds 0
+    (grouped_blockscaled.py:141-148). y is bfloat16 bits or float32; the result is
+    bfloat16 bits if `out_bf16`, else float32."""
+    values = bf16.to_f32(y) if y.dtype == np.uint16 else np.asarray(y, np.float32)
+    inverse = np.asarray(inverse)
+    m = values.shape[0]
+    inside = (inverse >= 0) & (inverse < m)
+    total = np.zeros((inverse.shape[0], values.shape[1]), np.float32)
+    for j in range(inverse.shape[1]):
+        rows = values[np.where(inside[:, j], inverse[:, j], 0)]
+        total += np.where(inside[:, j, None], rows, np.float32(0))
+    return bf16.to_bf16(total) if out_bf16 else total
+
+
+def tiles_of(sizes: np.ndarray, m: int, tile: int, starts: np.ndarray | None = None) -> np.ndarray:
+    """Return, for each tile of `tile` rows of m that a group has rows in, the group
+    and where its rows there start and end, then (0, 0, 0) rows up to
+    ``ceil(m / tile) + g - 1`` (grouped_mxfp8.py:157-182)."""
+    sizes = np.asarray(sizes, np.int64)
+    g = sizes.shape[0]
+    starts = np.cumsum(sizes) - sizes if starts is None else np.asarray(starts, np.int64)
+    ends = starts + sizes
+    first = starts // tile
+    count = np.where(sizes > 0, -(-ends // tile) - first, 0)
+    before = np.cumsum(count) - count
+    at = np.arange(-(-m // tile) + g - 1)
+    group = np.searchsorted(before + count, at, side="right")
+    group = np.minimum(group, g - 1)
+    index = first[group] + at - before[group]
+    lo = np.maximum(starts[group], index * tile)
+    hi = np.minimum(ends[group], (index + 1) * tile)
+    real = at < count.sum()
+    return np.stack([group, np.where(real, lo, 0), np.where(real, hi, 0)], -1).astype(np.int32)
+
+
+def _cast(y: np.ndarray, out: str) -> np.ndarray:
+    return bf16.to_bf16(y) if out == "bf16" else y.astype(np.float32)
+
+
+def rows_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16", height: int | None = None) -> np.ndarray:
+    """Return each group's rows of a times its matrix b[g]^T: a (m, k) and b
+    (g, n, k) in MXFP8 along k, dequantized and multiplied in float32; rows past the
+    groups are 0 (grouped_blockscaled.py:220-233, grouped_mxfp8.py:116-154)."""
+    x = mxfp8.dequantized(a)
+    w = mxfp8.dequantized(b)
+    m = x.shape[0] if height is None else height
+    y = np.zeros((m, w.shape[1]), np.float32)
+    start = 0
+    for g, size in enumerate(np.asarray(sizes).tolist()):
+        if size:
+            y[start:start + size] = x[start:start + size] @ w[g].T
+        start += size
+    return _cast(y, out)
+
+
+def contract_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
+    """Return dW[g] = a[:, rows of g] b[:, rows of g]^T: a (d, m) and b (f, m) in
+    MXFP8 along m, dequantized and multiplied in float32 (grouped_blockscaled.py:
+    236-250)."""
+    x = mxfp8.dequantized(a)
+    y = mxfp8.dequantized(b)
+    sizes = np.asarray(sizes).tolist()
+    dw = np.zeros((len(sizes), x.shape[0], y.shape[0]), np.float32)
+    start = 0
+    for g, size in enumerate(sizes):
+        if size:
+            dw[g] = x[:, start:start + size] @ y[:, start:start + size].T
+        start += size
+    return _cast(dw, out)
+
+
+def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
+    """Return ``jax.lax.ragged_dot`` of bfloat16 x (m, k) and w (g, k, n): float32
+    sums rounded to bfloat16, rows past the groups 0 (grouped.py:42-60,105-117)."""
+    xf, wf = bf16.to_f32(x), bf16.to_f32(w)
+    y = np.zeros((xf.shape[0], wf.shape[2]), np.float32)
+    start = 0
+    for g, size in enumerate(np.asarray(sizes).tolist()):
+        if size:
+            y[start:start + size] = xf[start:start + size] @ wf[g]
+        start += size
+    return _cast(y, out)
+
+
+def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
+    """Return x^T dy per group (grouped.py:120-161), float32 sums."""
+    xf, gf = bf16.to_f32(x), bf16.to_f32(dy)
+    sizes = np.asarray(sizes).tolist()
+    dw = np.zeros((len(sizes), xf.shape[1], gf.shape[1]), np.float32)
+    start = 0
+    for g, size in enumerate(sizes):
+        if size:
+            dw[g] = xf[start:start + size].T @ gf[start:start + size]
+        start += size
+    return _cast(dw, out)
+
+
+# --- The expert FFN's activation ---------------------------------------------------
+
+
+class Ffn(NamedTuple):
+    """An expert FFN's activation settings (config.py:204-221): the gate's
+    activation, the clamp and the up branch's offset."""
+
+    activation: str = "swish"  # or "quick_gelu" (gpt-oss's x * sigmoid(1.702 x))
+    limit: float | None = None
+    up_offset: float = 0.0
+
+
+def _sigmoid(x: np.ndarray) -> np.ndarray:
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def _act(name: str, g: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Return act(g) and act'(g) (functional.py:12-40)."""
+    alpha = {"swish": 1.0, "quick_gelu": 1.702}[name]
+    s = _sigmoid(alpha * g)
+    return g * s, s + alpha * g * s * (1.0 - s)
+
+
+def weighted_units(ffn: Ffn, projected: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    """Return ``act(gate) * (up + offset) * w`` for projected (m, f, 2) [up, gate] and
+    row weights (m,), as bfloat16 bits, computed in float64 and rounded once
+    (mlp.py:20-35, moe.py:898-926)."""
+    p = bf16.to_f32(projected).astype(np.float64)
+    w = bf16.to_f32(weights).astype(np.float64)
+    up, gate = p[..., 0], p[..., 1]
+    if ffn.limit is not None:
+        up = np.clip(up, -ffn.limit, ffn.limit)
+        gate = np.minimum(gate, ffn.limit)
+    a, _ = _act(ffn.activation, gate)
+    return bf16.to_bf16((a * (up + ffn.up_offset) * w[:, None]).astype(np.float32))
+
+
+def weighted_units_backward(
+    ffn: Ffn, projected: np.ndarray, weights: np.ndarray, dh: np.ndarray
+) -> tuple[np.ndarray, np.ndarray]:
+    """Return the gradients of `weighted_units` to projected (m, f, 2) and to the row
+    weights (m,), as bfloat16 bits (the VJP jax takes of it, moe.py:898-910, with
+    jax's gradients of clip and minimum: 1 strictly inside, 0.5 at the limit, 0
+    outside)."""
+    p = bf16.to_f32(projected).astype(np.float64)
+    w = bf16.to_f32(weights).astype(np.float64)[:, None]
+    g_ = bf16.to_f32(dh).astype(np.float64)
+    up, gate = p[..., 0], p[..., 1]
+    up_pass = np.ones_like(up)
+    gate_pass = np.ones_like(gate)
+    if ffn.limit is not None:
+        # jnp.clip is maximum then minimum, whose gradients split 0.5 / 0.5 at a tie
+        up_pass = np.where(np.abs(up) < ffn.limit, 1.0, np.where(np.abs(up) == ffn.limit, 0.5, 0.0))
+        gate_pass = np.where(gate < ffn.limit, 1.0, np.where(gate == ffn.limit, 0.5, 0.0))
+        up = np.clip(up, -ffn.limit, ffn.limit)
+        gate = np.minimum(gate, ffn.limit)
+    a, da = _act(ffn.activation, gate)
+    u = up + ffn.up_offset
+    d_up = g_ * w * a * up_pass
+    d_gate = g_ * w * u * da * gate_pass
+    d_w = (g_ * a * u).sum(-1)
+    dp = np.stack([d_up, d_gate], -1).astype(np.float32)
+    return bf16.to_bf16(dp), bf16.to_bf16(d_w.astype(np.float32))
+
+
+# --- The layer: routed -> experts, forward and backward ----------------------------
+
+
+class Saved(NamedTuple):
+    """What the layer's backward takes of its forward (grouped_blockscaled.py:84)."""
+
+    sorted: Sorted
+    row_weights: np.ndarray
+    projected: np.ndarray  # bf16 bits (m, 2f)
+    h: np.ndarray  # bf16 bits (m, f)
+    x_m: Blocks | None
+    up_n: Blocks | None
+    h_m: Blocks | None
+    down_n: Blocks | None
+
+
+def layer_forward(
+    z: np.ndarray,
+    idx: np.ndarray,
+    weights: np.ndarray,
+    up: np.ndarray,
+    down: np.ndarray,
+    ffn: Ffn = Ffn(),
+    fmt: str = "mxfp8",
+) -> tuple[np.ndarray, Saved]:
+    """Return the MoE's routed experts' output (t, d) as bfloat16 bits, and what the
+    backward takes: ``routed`` (moe.py:733-773) on one device with picked rows in and
+    summed rows out, each grouped GEMM in MXFP8 (`fmt` "mxfp8") or bfloat16
+    ("compute").
+
+    Args:
+        z: tokens, bfloat16 bits (t, d).
+        idx: each token's k experts, int (t, k).
+        weights: their weights, bfloat16 bits (t, k).
+        up: the experts' up and gate kernels, bfloat16 bits (E, d, f, 2).
+        down: the experts' down kernels, bfloat16 bits (E, f, d).
+        ffn: the activation.
+        fmt: "mxfp8" or "compute".
+    """
+    t, k = idx.shape
+    e, d, f, p = up.shape
+    s = sort_by_expert(idx, e)
+    m = t * k
+    filled = int(s.sizes.sum())
+    tokens = s.order // k
+    inside = (idx.reshape(-1) >= 0) & (idx.reshape(-1) < e)
+    kept = np.where(inside, np.asarray(weights).reshape(-1), np.uint16(0)).astype(np.uint16)
+    row_weights = kept[s.order]
+    up2 = np.asarray(up).reshape(e, d, f * p)
+    x_m = up_n = h_m = down_n = None
+    if fmt == "mxfp8":
+        x_k, x_m = mxfp8.quantized_twice(z, filled, True, index=tokens)
+        up_n, up_k = mxfp8.quantized_twice(up2, d)
+        projected = rows_mx(x_k, up_k, s.sizes)
+    else:
+        projected = ragged_dot_bf16(z[tokens], up2, s.sizes)
+    h = weighted_units(ffn, projected.reshape(m, f, p), row_weights)
+    if fmt == "mxfp8":
+        h_k, h_m = mxfp8.quantized_twice(h, filled, True)
+        down_n, down_k = mxfp8.quantized_twice(down, f)
+        y = rows_mx(h_k, down_k, s.sizes)
+    else:
+        y = ragged_dot_bf16(h, down, s.sizes)
+    out = sum_by_token(y, s.inverse.reshape(t, k))
+    return out, Saved(s, row_weights, projected, h, x_m, up_n, h_m, down_n)
+
+
+def layer_backward(
+    saved: Saved, dy: np.ndarray, z: np.ndarray, up: np.ndarray, down: np.ndarray,
+    k: int, ffn: Ffn = Ffn(), fmt: str = "mxfp8",
+) -> dict[str, np.ndarray]:
+    """Return the gradients of `layer_forward`'s output, dy (t, d) bfloat16 bits, to
+    z, the weights, up and down (bfloat16 bits): grouped_blockscaled._backward
+    (:191-211) for each GEMM, weighted_units' VJP between them, and the gathers'
+    VJPs (moe.py:1018-1021,1060-1063)."""
+    s = saved.sorted
+    t = dy.shape[0]
+    e, d, f, p = up.shape
+    m = t * k
+    filled = int(s.sizes.sum())
+    tokens = s.order // k
+    up2 = np.asarray(up).reshape(e, d, f * p)
+    if fmt == "mxfp8":
+        dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens)
+        dh = rows_mx(dy_n, saved.down_n, s.sizes)
+        d_down = contract_mx(saved.h_m, dy_m, s.sizes)
+    else:
+        dy_rows = dy[tokens]
+        dh = ragged_dot_bf16(dy_rows, np.ascontiguousarray(np.swapaxes(down, 1, 2)), s.sizes)
+        d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes)
+    dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), saved.row_weights, dh)
+    dp = dp.reshape(m, f * p)
+    if fmt == "mxfp8":
+        dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True)
+        dx = rows_mx(dp_n, saved.up_n, s.sizes)
+        d_up = contract_mx(saved.x_m, dp_m, s.sizes)
+    else:
+        dx = ragged_dot_bf16(dp, np.ascontiguousarray(np.swapaxes(up2, 1, 2)), s.sizes)
+        d_up = weight_grad_bf16(z[tokens], dp, s.sizes)
+    dz = sum_by_token(dx, s.inverse.reshape(t, k))
+    d_weights = d_rows_w[s.inverse].reshape(t, k)
+    return {"z": dz, "weights": d_weights, "up": d_up.reshape(e, d, f, p), "down": d_down}

@@ -1,0 +1,193 @@
+"""MXFP8 1x32 block-scaled quantization and dequantization, restated from bux.
+TEST INFRASTRUCTURE ONLY (see `oracle`).
+
+The spec (``src/bux/architecture/precision/blockscaled.py:323-356``), per block b of 32
+values along the axis a GEMM contracts, x widened to float32 first (``:314``):
+
+- ``amax = max|b|``;
+- ``e = ceil_log2(amax / 448)``: the float32 quotient's bits, ``(bits >> 23) +
+  (mantissa != 0) - 127``, clipped to [-126, 126] (``:346-351``);
+- the scale byte is ``e + 127`` (E8M0's bits), 1..253; a block of zeros gets 1;
+- each value is ``clip(v * 2^-e, -448, 448)`` rounded to nearest even E4M3 (OCP
+  ``float8_e4m3fn``), a negative value that rounds to 0 giving 0x80 (``:340-342``).
+
+Which copies the path makes (``grouped_blockscaled.py:181-184,206-208,296-317``): an
+operand along its rows and its transpose along its rows (the original's columns), rows
+from ``filled`` on as 0 first; a stack of matrices (each expert's W) one matrix at a
+time.
+
+Pins, run by ``tests/test_oracle.py``:
+
+- `to_e4m3fn`: exhaustive over every finite bfloat16 value in [-448, 448] against
+  torch's own ``float8_e4m3fn`` cast (an independent RNE implementation), and against
+  a brute-force nearest-even search over the 254 finite codes;
+- `ceil_log2`: exhaustive over every positive finite bfloat16 divided by 448, against
+  ``math.ceil(math.log2(q))`` computed in exact rational arithmetic
+  (``fractions.Fraction``), clipped;
+- `in_e4m3`: the reference's invariants: a block of zeros gives byte 1; every scaled
+  value lands within [-448, 448]; the scale is the least power of two doing so
+  (brute force over exponents on random blocks); dequantization is within half an E4M3
+  ulp of each value;
+- `dequantized`: closed form ``value * 2^(byte - 127)`` checked against torch's
+  ``float8_e4m3fn`` -> float32 cast for all 256 codes.
+"""
+
+from typing import NamedTuple
+
+import numpy as np
+
+from oracle import bf16
+
+E4M3_MAX = 448.0  # blockscaled.py:40
+MX_BLOCK = 32  # blockscaled.py:277
+
+
+class Blocks(NamedTuple):
+    """An (r, c) matrix in MXFP8 along its rows (blockscaled.py:43-52): E4M3 codes
+    (uint8, r x c) and E8M0 scale bytes (uint8, r x c/32). The canonical layout every
+    bit-exact comparison uses."""
+
+    values: np.ndarray
+    scales: np.ndarray
+
+
+def ceil_log2(x: np.ndarray) -> np.ndarray:
+    """Return the least e with 2^e >= x (x >= 0, float32) from x's bits, clipped to
+    [-126, 126] (blockscaled.py:346-351)."""
+    bits = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    exponent = (bits >> 23).astype(np.int32) + ((bits & 0x7FFFFF) != 0)
+    return np.clip(exponent - 127, -126, 126).astype(np.int32)
+
+
+def power_of_two(e: np.ndarray) -> np.ndarray:
+    """Return 2^e exactly for integers e in [-126, 127] (blockscaled.py:354-356)."""
+    return ((np.asarray(e, np.int32) + 127).astype(np.uint32) << 23).view(np.float32)
+
+
+def to_e4m3fn(x: np.ndarray) -> np.ndarray:
+    """Return float32 values rounded to nearest even OCP E4M3 (float8_e4m3fn), as
+    codes: 3 mantissa bits, bias 7, subnormals 2^-9 apart, no inf; overflow past the
+    rounding range and NaN give 0x7F with the sign (ml_dtypes' non-saturating cast,
+    which the path never reaches after its clip to +-448)."""
+    x = np.asarray(x, np.float32)
+    sign = np.signbit(x).astype(np.uint8) << 7
+    a = np.abs(x).astype(np.float64)
+    _, p = np.frexp(a)
+    e = np.maximum(p - 1, -6)  # below 2^-6 the spacing is the subnormals' 2^-9
+    quantum = np.ldexp(1.0, e - 3)
+    q = np.rint(a / quantum) * quantum  # exact in float64; rint ties to even
+    _, p2 = np.frexp(q)
+    e2 = p2 - 1
+    normal = q >= 2.0**-6
+    with np.errstate(invalid="ignore", over="ignore"):
+        mant = np.where(normal, q / np.ldexp(1.0, e2) * 8 - 8, 0)
+        code = np.where(normal, ((e2 + 7) << 3) + mant, q / 2.0**-9)
+    code = np.where(np.isnan(x) | (q > E4M3_MAX), 0x7F, code)
+    return code.astype(np.uint8) | sign
+
+
+_E4M3 = None
+
+
+def e4m3_values() -> np.ndarray:
+    """Return the float32 value of each of the 256 E4M3 codes (NaN at 0x7F, 0xFF)."""
+    global _E4M3
+    if _E4M3 is None:
+        codes = np.arange(256)
+        s, e, m = codes >> 7, (codes >> 3) & 15, codes & 7
+        v = np.where(e == 0, np.ldexp(m.astype(np.float64), -9),
+                     np.ldexp((8 + m).astype(np.float64), e - 10))
+        v = np.where((e == 15) & (m == 7), np.nan, v)
+        _E4M3 = np.where(s == 1, -v, v).astype(np.float32)
+    return _E4M3
+
+
+def in_e4m3(x: np.ndarray, blocks: str = "rows") -> tuple[np.ndarray, np.ndarray]:
+    """Return x's (float32, r x c) E4M3 codes and its scales' biased exponents, in
+    blocks of 32 along its ``rows``, down its ``columns`` or in 32 x 32 ``tiles``
+    (blockscaled.py:323-343)."""
+    x = np.asarray(x, np.float32)
+    (r, c), b = x.shape, MX_BLOCK
+    shape, axes = {
+        "rows": ((r, c // b, b), (2,)),
+        "columns": ((r // b, b, c), (1,)),
+        "tiles": ((r // b, b, c // b, b), (1, 3)),
+    }[blocks]
+    blocked = x.reshape(shape)
+    largest = np.abs(blocked).max(axis=axes).astype(np.float32)
+    exponent = ceil_log2(largest / np.float32(E4M3_MAX))
+    down = power_of_two(-exponent)
+    scaled = blocked * np.expand_dims(down, axes)
+    values = to_e4m3fn(np.clip(scaled, -E4M3_MAX, E4M3_MAX))
+    return values.reshape(r, c), (exponent + 127).astype(np.uint8)
+
+
+def mx_quantize(x: np.ndarray) -> Blocks:
+    """Return x (float32, or bfloat16 bits as uint16) in MXFP8 along its rows
+    (blockscaled.py:312-314)."""
+    if x.dtype == np.uint16:
+        x = bf16.to_f32(x)
+    return Blocks(*in_e4m3(x, "rows"))
+
+
+def mx_twice(x: np.ndarray) -> tuple[Blocks, Blocks]:
+    """Return x and x^T in MXFP8, each along its rows (blockscaled.py:282-291, the
+    XLA branch)."""
+    return mx_quantize(x), mx_quantize(np.ascontiguousarray(x.T))
+
+
+def dequantized(blocks: Blocks) -> np.ndarray:
+    """Return the float32 values MXFP8 blocks hold: each code's value times its
+    block's 2^(byte - 127) (blockscaled.py:223-229)."""
+    values, scales = blocks
+    block = values.shape[-1] // scales.shape[-1]
+    scale = power_of_two(scales.astype(np.int32) - 127)
+    return e4m3_values()[values] * np.repeat(scale, block, axis=-1)
+
+
+def quantized_twice(
+    x: np.ndarray,
+    filled: int,
+    columns: bool = True,
+    index: np.ndarray | None = None,
+    height: int | None = None,
+) -> tuple[Blocks, Blocks | None]:
+    """Return the MXFP8 copies a grouped GEMM's operand takes
+    (grouped_blockscaled.py:296-317 off a Blackwell GPU; grouped_triton.py:44-101 for
+    ``index``): x along its rows and, if `columns`, x^T along its rows; rows from
+    `filled` on as 0.
+
+    Args:
+        x: bfloat16 bits (uint16) or float32, (r, c) or a stack (g, r, c).
+        filled: the rows that hold values; those from it on quantize as 0.
+        columns: whether to return x^T too.
+        index: rows to read, ``x[index]``, a row at -1 reading 0 (the Triton
+            kernel's meaning, grouped_triton.py:208-214); None for x itself.
+        height: rows of the copies, padded by 0 past x's (``ragged_dot``'s padding to
+            whole tiles of 128, grouped_blockscaled.py:122-128); None for x's own.
+
+    Returns:
+        The copies; a stack gives stacks (values (g, r, c) and (g, c, r)).
+    """
+    if x.dtype == np.uint16:
+        x = bf16.to_f32(x)
+    x = np.asarray(x, np.float32)
+    if index is not None:
+        index = np.asarray(index)
+        rows = x[np.maximum(index, 0)]
+        x = np.where((index >= 0)[:, None], rows, np.float32(0))
+    stack = x if x.ndim == 3 else x[None]
+    g, r, c = stack.shape
+    h = r if height is None else height
+    padded = np.zeros((g, h, c), np.float32)
+    padded[:, :r] = stack
+    kept = np.where((np.arange(h) < filled)[None, :, None], padded, np.float32(0))
+    rows_out = [mx_quantize(m) for m in kept]
+    cols_out = [mx_quantize(np.ascontiguousarray(m.T)) for m in kept] if columns else None
+
+    def stacked(parts: list[Blocks]) -> Blocks:
+        if x.ndim == 2:
+            return parts[0]
+        return Blocks(np.stack([p.values for p in parts]), np.stack([p.scales for p in parts]))
+
+    return stacked(rows_out), (stacked(cols_out) if columns else None)

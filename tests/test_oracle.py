@@ -1,0 +1,323 @@
+"""Pins of the CPU oracle (``oracle/``), independent of this repository's kernels:
+torch's own float8/bfloat16 casts, exact rational arithmetic, brute force on tiny
+inputs, and the invariants bux's own tests hold for this path
+(tests/test_grouped.py, tests/test_grouped_mxfp8.py, tests/test_precision.py in the
+reference). Each check is chosen so that a plausible slip in the oracle (a dropped
+term, a wrong sign, an off-by-one exponent, a transposed operand) fails it."""
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16, moe, mxfp8
+
+ALL_BF16 = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+FINITE = ALL_BF16[np.isfinite(bf16.to_f32(ALL_BF16))]
+
+
+# --- bfloat16 ---------------------------------------------------------------------
+
+
+def test_bf16_widening_is_torchs_for_every_pattern():
+    want = torch.from_numpy(ALL_BF16.view(np.int16)).view(torch.bfloat16).float().numpy()
+    got = bf16.to_f32(ALL_BF16)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_bf16_rounding_is_torchs():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        (rng.standard_normal(200000) * 10.0 ** rng.integers(-40, 38, 200000)).astype(np.float32),
+        # ties: exactly halfway between two bfloat16 values, both parities
+        ((np.arange(1, 4000, dtype=np.uint32) << 16) | 0x8000).view(np.float32),
+        np.array([3.4e38, -3.4e38, 1e-45, -1e-45, 0.0, -0.0], np.float32),
+    ])
+    x = x[np.isfinite(x)].astype(np.float32)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(bf16.to_bf16(x), want)
+
+
+# --- E4M3 and the quantizer -----------------------------------------------------------
+
+
+def _in_range_bf16() -> np.ndarray:
+    v = bf16.to_f32(FINITE)
+    return v[np.abs(v) <= 448]
+
+
+def test_e4m3_rounding_is_torchs_for_every_bf16_in_range():
+    """torch's float32 -> float8_e4m3fn cast is an independent RNE implementation;
+    the quantizer only ever casts values already clipped to [-448, 448]."""
+    v = _in_range_bf16()
+    want = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(mxfp8.to_e4m3fn(v), want)
+    # negatives that round to zero keep their sign: 0x80
+    assert mxfp8.to_e4m3fn(np.array([-1e-4, -0.0], np.float32)).tolist() == [0x80, 0x80]
+
+
+def test_e4m3_rounding_is_the_nearest_even_code():
+    """Brute force: the nearest of the 254 finite codes' values, ties to an even code."""
+    codes = np.arange(256)
+    values = mxfp8.e4m3_values()
+    finite = codes[~np.isnan(values) & (codes < 128)]
+    rng = np.random.default_rng(1)
+    v = _in_range_bf16()
+    v = v[rng.choice(v.size, 3000, replace=False)]
+    for x in v:
+        d = np.abs(values[finite].astype(np.float64) - abs(float(x)))
+        best = finite[d == d.min()]
+        code = int(best[best % 2 == 0][0]) if best.size > 1 else int(best[0])
+        code |= 0x80 if math.copysign(1, x) < 0 else 0
+        assert mxfp8.to_e4m3fn(np.array([x], np.float32))[0] == code, x
+
+
+def test_e4m3_values_are_torchs():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    want = codes.view(torch.float8_e4m3fn).float().numpy()
+    got = mxfp8.e4m3_values()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(got[ok], want[ok])
+
+
+def test_ceil_log2_is_exact_for_every_bf16_block_maximum():
+    """e = the least integer with 2^e >= fl32(amax / 448), clipped to [-126, 126],
+    computed from the quotient's exact rational value (not from its bits)."""
+    amax = bf16.to_f32(FINITE)
+    amax = amax[~np.signbit(amax)]  # |b|'s max is never -0
+    q = amax / np.float32(448.0)
+    got = mxfp8.ceil_log2(q)
+    for qi, gi in zip(q.tolist(), got.tolist()):
+        if qi == 0:
+            want = -126
+        else:
+            r = Fraction(qi)
+            e = math.floor(math.log2(qi)) - 2
+            while Fraction(2) ** e < r:
+                e += 1
+            want = min(max(e, -126), 126)
+        assert gi == want, (qi, gi, want)
+
+
+def test_a_block_takes_the_least_power_of_two_that_fits_it():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal((64, 256)) * 10.0 ** rng.integers(-30, 30, (64, 1))).astype(np.float32)
+    x = bf16.round_f32(x)
+    values, scales = mxfp8.in_e4m3(x, "rows")
+    blocks = x.reshape(64, 8, 32)
+    amax = np.abs(blocks).max(-1).astype(np.float64)
+    e = scales.astype(np.int64) - 127
+    assert (amax <= 448 * 2.0 ** e).all()
+    assert ((amax > 448 * 2.0 ** (e - 1)) | (e == -126)).all()
+    # dequantized is within half an E4M3 step (3 mantissa bits) of each value
+    deq = mxfp8.dequantized(mxfp8.Blocks(values, scales)).astype(np.float64)
+    step = np.maximum(2.0 ** (np.floor(np.log2(np.maximum(np.abs(x), 1e-300))) - 3),
+                      2.0 ** -9 * np.repeat(2.0 ** e, 32, axis=-1))
+    assert (np.abs(deq - x) <= step / 2 + 1e-300).all()
+
+
+def test_a_block_of_zeros_gets_byte_1():
+    """E8M0 has no 0: a zero block's scale is 2^-126 (test_grouped_mxfp8.py:62-68)."""
+    values, scales = mxfp8.in_e4m3(np.zeros((2, 64), np.float32))
+    assert (scales == 1).all() and (values == 0).all()
+
+
+def test_the_column_copy_is_the_transposes_row_copy():
+    rng = np.random.default_rng(3)
+    x = bf16.round_f32(rng.standard_normal((64, 96)).astype(np.float32))
+    v_cols, e_cols = mxfp8.in_e4m3(x, "columns")
+    v_t, e_t = mxfp8.in_e4m3(np.ascontiguousarray(x.T), "rows")
+    np.testing.assert_array_equal(v_cols.T, v_t)
+    np.testing.assert_array_equal(e_cols.T, e_t)
+
+
+def test_rows_past_filled_quantize_as_zero_and_picked_rows_as_their_copy():
+    rng = np.random.default_rng(4)
+    tokens = bf16.to_bf16(rng.standard_normal((40, 64)).astype(np.float32))
+    index = rng.integers(0, 40, 256)
+    got = mxfp8.quantized_twice(tokens, 200, True, index=index)
+    want = mxfp8.quantized_twice(tokens[index], 200, True)
+    for a, b in zip(got, want):
+        np.testing.assert_array_equal(a.values, b.values)
+        np.testing.assert_array_equal(a.scales, b.scales)
+    rows, cols = got
+    assert (rows.values[200:] == 0).all() and (rows.scales[200:] == 1).all()
+    assert (cols.values[:, 200:] == 0).all()
+
+
+# --- The token path ------------------------------------------------------------------
+
+
+def _brute_sort(idx, e):
+    flat = [int(v) if 0 <= v < e else e for v in np.asarray(idx).reshape(-1)]
+    order = sorted(range(len(flat)), key=lambda i: (flat[i], i))
+    sizes = [sum(1 for v in flat if v == g) for g in range(e)]
+    return order, sizes
+
+
+@pytest.mark.parametrize("sizes", [[70, 0, 100, 3, 77], [0, 130, 1, 3, 256, 0, 300, 100]])
+def test_sort_by_expert_on_the_references_size_patterns(sizes):
+    rng = np.random.default_rng(5)
+    flat = np.repeat(np.arange(len(sizes)), sizes)
+    rng.shuffle(flat)
+    idx = flat.reshape(-1, 1)
+    s = moe.sort_by_expert(idx, len(sizes))
+    order, want_sizes = _brute_sort(idx, len(sizes))
+    assert s.order.tolist() == order
+    assert s.sizes.tolist() == want_sizes == sizes
+    assert (s.order[s.inverse] == np.arange(flat.size)).all()
+    assert s.offsets.tolist() == (np.cumsum(sizes) - sizes).tolist()
+
+
+def test_sort_by_expert_puts_out_of_range_picks_last():
+    idx = np.array([[3, -1], [0, 7], [2, 3], [5, 0]])
+    s = moe.sort_by_expert(idx, 4)
+    order, sizes = _brute_sort(idx, 4)
+    assert s.order.tolist() == order and s.sizes.tolist() == sizes
+    assert set(s.order[-3:].tolist()) == {1, 3, 6}
+
+
+def test_the_tiles_of_rows_cover_each_groups_rows_once():
+    """tests/test_grouped_mxfp8.py:31-41, on the oracle's tile list."""
+    sizes = np.array([0, 130, 1, 3, 256, 0, 300, 100])
+    m = 1024
+    tiles = moe.tiles_of(sizes, m, 128)
+    group_of = np.searchsorted(np.cumsum(sizes), np.arange(m), side="right")
+    covered = np.full(m, -1)
+    for group, lo, hi in tiles:
+        assert lo == hi or lo // 128 == (hi - 1) // 128
+        assert (covered[lo:hi] == -1).all() and (group_of[lo:hi] == group).all()
+        covered[lo:hi] = group
+    assert (covered >= 0).sum() == sizes.sum()
+    assert len(tiles) == -(-m // 128) + len(sizes) - 1
+
+
+def test_sum_by_token_is_the_transpose_of_token_rows():
+    rng = np.random.default_rng(6)
+    t, k, d, e = 50, 4, 16, 7
+    idx = rng.integers(0, e, (t, k))
+    s = moe.sort_by_expert(idx, e)
+    z = rng.standard_normal((t, d))
+    y = bf16.round_f32(rng.standard_normal((t * k, d)).astype(np.float32))
+    rows = moe.token_rows(z, s.order, k)
+    sums = moe.sum_by_token(y, s.inverse.reshape(t, k), out_bf16=False).astype(np.float64)
+    np.testing.assert_allclose((rows * y).sum(), (z * sums).sum(), rtol=1e-6)
+    # brute force
+    for tok in range(t):
+        want = sum(y[s.inverse[tok * k + j]].astype(np.float64) for j in range(k))
+        np.testing.assert_allclose(sums[tok], want, rtol=1e-6, atol=1e-6)
+
+
+def _blocks(rng, shape):
+    x = rng.standard_normal(shape).astype(np.float32)
+    if len(shape) == 3:
+        parts = [mxfp8.mx_quantize(m) for m in x]
+        return mxfp8.Blocks(np.stack([p.values for p in parts]), np.stack([p.scales for p in parts]))
+    return mxfp8.mx_quantize(x)
+
+
+def test_rows_multiply_each_groups_rows_by_its_matrix():
+    """Brute force in float64 over dequantized codes, with the reference's sizes
+    (empty groups, a group of one row, rows past the groups)."""
+    rng = np.random.default_rng(7)
+    sizes = np.array([0, 13, 1, 3, 25, 0, 30, 10])
+    m, k, n = 100, 64, 24
+    a, b = _blocks(rng, (m, k)), _blocks(rng, (8, n, k))
+    got = moe.rows_mx(a, b, sizes, out="f32")
+    ea = mxfp8.e4m3_values()[a.values].astype(np.float64) * np.repeat(2.0 ** (a.scales - 127.0), 32, -1)
+    eb = mxfp8.e4m3_values()[b.values].astype(np.float64) * np.repeat(2.0 ** (b.scales - 127.0), 32, -1)
+    ends = np.cumsum(sizes)
+    for i in range(m):
+        g = int(np.searchsorted(ends, i, side="right"))
+        for j in range(n):
+            want = 0.0 if g >= 8 else sum(ea[i, c] * eb[g, j, c] for c in range(k))
+            assert abs(got[i, j] - want) <= 1e-5 * max(1.0, abs(want)), (i, j)
+    assert (got[sizes.sum():] == 0).all()
+
+
+def test_contract_sums_each_groups_rows_and_ignores_rows_past_them():
+    rng = np.random.default_rng(8)
+    sizes = np.array([70, 0, 100, 3, 77])
+    m, d, f = 320, 32, 64
+    a, b = _blocks(rng, (d, m)), _blocks(rng, (f, m))
+    got = moe.contract_mx(a, b, sizes, out="f32")
+    ea, eb = mxfp8.dequantized(a).astype(np.float64), mxfp8.dequantized(b).astype(np.float64)
+    start = 0
+    for g, size in enumerate(sizes):
+        want = sum(np.outer(ea[:, i], eb[:, i]) for i in range(start, start + size)) if size else 0
+        np.testing.assert_allclose(got[g], want, rtol=1e-5, atol=1e-4)
+        start += size
+    assert (got[1] == 0).all()
+    # garbage past the groups changes nothing (tests/test_grouped.py:89-95)
+    junk = a.values.copy()
+    junk[:, sizes.sum():] = 0x7E
+    np.testing.assert_array_equal(moe.contract_mx(mxfp8.Blocks(junk, a.scales), b, sizes, "f32"), got)
+
+
+@pytest.mark.parametrize("ffn", [moe.Ffn(), moe.Ffn("quick_gelu", 7.0, 1.0)])
+def test_the_activations_gradient_is_autograds(ffn):
+    rng = np.random.default_rng(9)
+    m, f = 64, 48
+    p = bf16.to_bf16((rng.standard_normal((m, f, 2)) * 4).astype(np.float32))
+    w = bf16.to_bf16(rng.random(m).astype(np.float32))
+    dh = bf16.to_bf16(rng.standard_normal((m, f)).astype(np.float32))
+    dp, dw = moe.weighted_units_backward(ffn, p, w, dh)
+    pt = torch.tensor(bf16.to_f32(p), dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(bf16.to_f32(w), dtype=torch.float64, requires_grad=True)
+    up, gate = pt[..., 0], pt[..., 1]
+    if ffn.limit is not None:  # maximum/minimum: gradient 0.5 at a tie, as jax's
+        lim = torch.tensor(ffn.limit, dtype=torch.float64)
+        up = torch.minimum(torch.maximum(up, -lim), lim)
+        gate = torch.minimum(gate, lim)
+    alpha = 1.0 if ffn.activation == "swish" else 1.702
+    h = gate * torch.sigmoid(alpha * gate) * (up + ffn.up_offset) * wt[:, None]
+    np.testing.assert_allclose(bf16.to_f32(moe.weighted_units(ffn, p, w)), h.detach().numpy(), rtol=8e-3, atol=1e-6)
+    h.backward(torch.tensor(bf16.to_f32(dh), dtype=torch.float64))
+    np.testing.assert_allclose(bf16.to_f32(dp), pt.grad.numpy(), rtol=8e-3, atol=1e-5)
+    np.testing.assert_allclose(bf16.to_f32(dw), wt.grad.numpy(), rtol=8e-3, atol=1e-4)
+
+
+def test_the_sorted_layer_is_the_dense_one_with_gradients():
+    """``sorted`` equals ``dense`` with gradients (tests/test_moe.py:475-484): the
+    oracle's layer, in bfloat16 ("compute"), against every token through each of its
+    experts one by one, differentiated by torch.autograd in float64."""
+    rng = np.random.default_rng(10)
+    t, k, e, d, f = 48, 2, 5, 32, 24
+    ffn = moe.Ffn("quick_gelu", 7.0, 1.0)
+    z = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
+    idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)])
+    w = bf16.to_bf16(rng.random((t, k)).astype(np.float32))
+    up = bf16.to_bf16((rng.standard_normal((e, d, f, 2)) * 0.3).astype(np.float32))
+    down = bf16.to_bf16((rng.standard_normal((e, f, d)) * 0.3).astype(np.float32))
+    dy = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
+    y, saved = moe.layer_forward(z, idx, w, up, down, ffn, fmt="compute")
+    grads = moe.layer_backward(saved, dy, z, up, down, k, ffn, fmt="compute")
+
+    def tensor(a):
+        return torch.tensor(bf16.to_f32(a), dtype=torch.float64, requires_grad=True)
+
+    zt, wt, upt, downt = tensor(z), tensor(w), tensor(up), tensor(down)
+    out = torch.zeros(t, d, dtype=torch.float64)
+    for tok in range(t):
+        for j in range(k):
+            g = int(idx[tok, j])
+            p = zt[tok] @ upt[g].reshape(d, 2 * f)
+            u, gate = p.reshape(f, 2)[:, 0], p.reshape(f, 2)[:, 1]
+            u, gate = torch.clamp(u, -7.0, 7.0), torch.clamp(gate, max=7.0)
+            h = gate * torch.sigmoid(1.702 * gate) * (u + 1.0) * wt[tok, j]
+            out = out.index_add(0, torch.tensor([tok]), (h @ downt[g])[None])
+    out.backward(torch.tensor(bf16.to_f32(dy), dtype=torch.float64))
+
+    def close(got, want, rtol):
+        got, want = bf16.to_f32(got).astype(np.float64), want.detach().numpy()
+        err = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert err < rtol, err
+
+    close(y, out, 1e-2)
+    close(grads["z"], zt.grad, 2e-2)
+    close(grads["weights"], wt.grad, 2e-2)
+    close(grads["up"], upt.grad, 2e-2)
+    close(grads["down"], downt.grad, 2e-2)
