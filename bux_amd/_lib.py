@@ -1,0 +1,78 @@
+"""The HIP library, ``libbux_amd.so``, through ctypes: every entry point that
+``include/bux_amd.h`` declares, with its argument types.
+
+`load()` returns the library, building nothing: ``python -m bux_amd.build`` (or
+``__graft_entry__.build()``) makes it. A missing library raises at once; there is no
+fallback to another implementation. `check(rc)` turns a nonzero return code into a
+`BuxError` carrying the library's message.
+"""
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PATH = os.path.join(HERE, "libbux_amd.so")
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_size = ctypes.c_size_t
+
+# name -> (restype, argtypes), as include/bux_amd.h declares them.
+SIGNATURES = {
+    "bux_last_error": (ctypes.c_char_p, []),
+    "bux_version": (_int, []),
+    "bux_moe_permute_workspace_size": (_size, [_i64, _i32]),
+    "bux_moe_permute": (_int, [_p, _i64, _i32, _p, _p, _p, _p, _p, _size, _p]),
+    "bux_mx_quantize": (_int, [_p, _p, _i32, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p, _p, _p]),
+    "bux_mx_grouped_rows_workspace_size": (_size, [_i32, _i64, _i64]),
+    "bux_mx_grouped_rows": (
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
+    "bux_mx_grouped_contract_workspace_size": (_size, [_i32]),
+    "bux_mx_grouped_contract": (
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
+    "bux_bf16_grouped_rows": (_int, [_p, _p, _int, _p, _i32, _i64, _i64, _i64, _p, _p]),
+    "bux_bf16_grouped_contract": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p]),
+    "bux_token_rows": (_int, [_p, _p, _i64, _i32, _i64, _p, _p]),
+    "bux_token_sums": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
+    "bux_glu_forward": (_int, [_p, _p, _p, _i64, _i64, _int, _f32, _f32, _p, _p]),
+    "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _f32, _f32, _p, _p, _p]),
+}
+
+# Constants of include/bux_amd.h.
+MX_ROWS, MX_COLUMNS = 1, 2
+BF16, F32 = 0, 1
+SWISH, QUICK_GELU = 0, 1
+
+
+class BuxError(RuntimeError):
+    """A call into the library failed: its code and message."""
+
+
+_LIB = None
+
+
+def load(path: str = PATH) -> ctypes.CDLL:
+    """Return the library, loaded once, each entry point typed. Raises if it is not
+    built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise BuxError(f"{path} is not built: run `python -m bux_amd.build`")
+    lib = ctypes.CDLL(path)
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _LIB = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    """Raise `BuxError` with the library's message if `rc` is nonzero."""
+    if rc != 0:
+        msg = load().bux_last_error().decode(errors="replace")
+        raise BuxError(f"bux_amd error {rc}: {msg}")

@@ -1,0 +1,34 @@
+// The library's error channel and version: a thread-local message behind each failed
+// call's nonzero code.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "common.h"
+
+namespace bux {
+
+static thread_local char last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(last_error, sizeof(last_error), fmt, args);
+  va_end(args);
+  return code;
+}
+
+void clear_error() { last_error[0] = '\0'; }
+
+int launched(const char* kernel) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(BUX_E_LAUNCH, "%s: %s", kernel, hipGetErrorString(err));
+  return BUX_OK;
+}
+
+}  // namespace bux
+
+extern "C" const char* bux_last_error(void) { return bux::last_error; }
+
+extern "C" int bux_version(void) { return 100; }

@@ -1,0 +1,74 @@
+// Shared pieces of the HIP library: the error channel, host-side argument checks and
+// small device helpers (bfloat16 bits, E4M3 conversion, wave reductions).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/bux_amd.h"
+
+namespace bux {
+
+// Sets this thread's last error message and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears this thread's last error message.
+void clear_error();
+// Returns BUX_OK, or BUX_E_LAUNCH with the HIP error of the last launch.
+int launched(const char* kernel);
+
+#define BUX_CHECK(cond, ...)                                  \
+  do {                                                        \
+    if (!(cond)) return ::bux::fail(BUX_E_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// --- device helpers --------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// float32 -> bfloat16 bits, rounding to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Two float32 -> two E4M3 (OCP float8_e4m3fn) codes, nearest even, in the low 16 bits:
+// gfx950's v_cvt_pk_fp8_f32. The quantizer only passes values already within +-448.
+__device__ __forceinline__ uint32_t e4m3x2(float a, float b) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xffffu;
+}
+
+// Four float32 -> four E4M3 codes packed in a word, a in the lowest byte.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+}
+
+// The biased exponent of the least power of two 2^e with 2^e >= q, e clipped to
+// [-126, 126]: the reference's _ceil_log2 (precision/blockscaled.py:346-351) of the
+// float32 quotient q = amax / 448, from its bits.
+__device__ __forceinline__ int scale_exponent(float amax) {
+  float q = amax / 448.0f;  // an IEEE division: hipcc rounds float division correctly
+  uint32_t bits = __float_as_uint(q);
+  int e = static_cast<int>(bits >> 23) + ((bits & 0x7fffffu) != 0u) - 127;
+  return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+// 2^-e as a float32, exactly, for e in [-126, 126].
+__device__ __forceinline__ float power_of_two_down(int e) {
+  return __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+}
+
+__device__ __forceinline__ float clip448(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
+
+}  // namespace bux

@@ -1,0 +1,201 @@
+/* bux_amd: the MoE expert path of bux (pilot7747/bux) as hand-written HIP kernels for
+ * MI355X (gfx950), behind a plain C ABI.
+ *
+ * Every entry point enqueues its kernels on the caller's HIP stream (`stream`, a
+ * hipStream_t; NULL for the default stream) and returns at once: no host
+ * synchronisation, no allocation. Buffers are device pointers owned by the caller;
+ * inputs are read only; outputs may hold anything on entry, and every element of them
+ * is written (0 where the reference's result is 0). Scratch memory comes in as a
+ * `workspace` of at least the size the matching `*_workspace_size` call returns.
+ *
+ * Return value: 0 on success; otherwise a nonzero BUX_E_* code, with a message that
+ * `bux_last_error` returns on the same thread. Shapes are checked on the host before
+ * any kernel is launched.
+ *
+ * Layouts (row-major throughout):
+ *   bfloat16   uint16_t bit patterns;
+ *   MXFP8      an (r, c) matrix in blocks of 32 along its rows: E4M3 codes uint8 (r, c)
+ *              and E8M0 scale bytes uint8 (r, c / 32) -- the reference's `Blocks`
+ *              (src/bux/architecture/precision/blockscaled.py:43-56). The kernels take
+ *              operands in exactly this layout, so there is no separate tiled form.
+ *
+ * References are to files under /root/reference (pilot7747/bux).
+ */
+#ifndef BUX_AMD_H
+#define BUX_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  BUX_OK = 0,
+  BUX_E_ARGUMENT = 1, /* a shape, pointer or flag the entry point does not take */
+  BUX_E_WORKSPACE = 2, /* the workspace is smaller than *_workspace_size says */
+  BUX_E_LAUNCH = 3, /* the HIP runtime refused a launch */
+  BUX_E_DEVICE = 4 /* the current device is not a gfx950 */
+};
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* bux_last_error(void);
+
+/* The library's version, major * 10000 + minor * 100 + patch. */
+int bux_version(void);
+
+/* ---------------------------------------------------------------------------------
+ * a-1. Sort the picks by expert.
+ *
+ * Replaces moe.sort_by_expert (src/bux/architecture/experts/moe.py:776-791) with
+ * in_range (:794), and the group offsets the grouped GEMMs derive from the sizes
+ * (grouped_mxfp8.py:142, ``cumsum(sizes) - sizes``).
+ *
+ * idx       int32 [n_picks]: each pick's expert (a token's k picks in a row).
+ * order     int32 [n_picks]: the picks sorted by expert, stably; picks outside
+ *           [0, num_experts) sort last.
+ * inverse   int32 [n_picks]: inverse[order[i]] = i.
+ * sizes     int32 [num_experts]: picks of each expert.
+ * offsets   int32 [num_experts + 1]: cumsum(sizes) - sizes, then sum(sizes) (the
+ *           rows that hold values, `filled` of grouped_blockscaled.py:180).
+ */
+size_t bux_moe_permute_workspace_size(int64_t n_picks, int32_t num_experts);
+int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_experts, int32_t* order,
+                    int32_t* inverse, int32_t* sizes, int32_t* offsets, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * a-4. MXFP8 quantization of a matrix and of its transpose, in one pass.
+ *
+ * Replaces grouped_triton.quantized_twice (src/bux/architecture/experts/
+ * grouped_triton.py:44-101) and, off a Blackwell GPU, grouped_blockscaled._quantized
+ * (grouped_blockscaled.py:296-317) with blockscaled.mx_twice / mx_quantize
+ * (precision/blockscaled.py:282-356): per 32 values, the scale 2^e with
+ * e = ceil_log2(amax / 448) clipped to [-126, 126] (byte e + 127, 1 for a block of
+ * zeros), each value times 2^-e clipped to +-448 and rounded to nearest even E4M3.
+ *
+ * x         bfloat16 [groups, rows, cols] (a stack of `groups` matrices), or, with an
+ *           index, the matrix the rows are read from.
+ * index     NULL, or int32 [rows]: row i is x[index[i] / index_div] (groups must be 1),
+ *           a row whose index is negative reading 0 -- the reference's `Picked` rows,
+ *           tokens[order // k] (grouped_blockscaled.py:53-62, grouped_triton.py:208-214).
+ * rows      rows of the matrix (x's, or the index's entries).
+ * height    rows of the copies, a multiple of 32, >= rows; rows from `rows` on are 0
+ *           (the reference pads to whole tiles, grouped_blockscaled.py:122-128).
+ * filled    NULL (every row holds values) or a device int32: rows from *filled on
+ *           quantize as 0 (grouped_blockscaled.py:314).
+ * flags     BUX_MX_ROWS: write values [groups, height, cols] and scales
+ *           [groups, height, cols/32]; BUX_MX_COLUMNS: write t_values
+ *           [groups, cols, height] and t_scales [groups, cols, height/32] (x^T in
+ *           blocks along its rows). cols must be a multiple of 32.
+ */
+enum { BUX_MX_ROWS = 1, BUX_MX_COLUMNS = 2 };
+int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t groups,
+                    int64_t rows, int64_t cols, int64_t height, const int32_t* filled, int flags,
+                    uint8_t* values, uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
+                    void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * a-6. Grouped MXFP8 GEMM over rows: y[i] = a[i] b[g(i)]^T.
+ *
+ * Replaces grouped_mxfp8.rows (src/bux/architecture/experts/grouped_mxfp8.py:116-154)
+ * with its tile list tiles_of (:157-182), and off Blackwell grouped_blockscaled._times
+ * (grouped_blockscaled.py:220-233): float32 sums, rows past sum(sizes) are 0.
+ *
+ * a_values/a_scales  MXFP8 [m, k]: the rows, group 0's first.
+ * b_values/b_scales  MXFP8 [groups, n, k]: each group's matrix.
+ * sizes     device int32 [groups].
+ * y         [height, n], bfloat16 (out_dtype BUX_BF16) or float32 (BUX_F32); rows
+ *           from sum(sizes) to height are 0, and a's rows past m read 0. Any height:
+ *           a's quantized copy may be padded past the height of y (e.g. to whole
+ *           tiles) and rows of the groups past height are not stored.
+ * k must be a multiple of 32.
+ */
+enum { BUX_BF16 = 0, BUX_F32 = 1 };
+size_t bux_mx_grouped_rows_workspace_size(int32_t groups, int64_t m, int64_t height);
+int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
+                        const uint8_t* b_scales, const int32_t* sizes, int32_t groups, int64_t m,
+                        int64_t n, int64_t k, int64_t height, int out_dtype, void* y,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * a-7. Grouped MXFP8 GEMM contracting each group's rows: dw[g] = a[:, g] b[:, g]^T.
+ *
+ * Replaces grouped_mxfp8.contract (grouped_mxfp8.py:185-210) with its edge tiles
+ * _edges (:240-256), and off Blackwell grouped_blockscaled._contract
+ * (grouped_blockscaled.py:236-250): the rows of a block of 32 that another group owns
+ * count as 0; float32 sums.
+ *
+ * a_values/a_scales  MXFP8 [d, m]: x^T in blocks along the rows m.
+ * b_values/b_scales  MXFP8 [f, m]: dy^T likewise.
+ * sizes     device int32 [groups]; sum(sizes) <= m; m a multiple of 32.
+ * dw        [groups, d, f], bfloat16 or float32 (out_dtype); 0 for an empty group.
+ */
+size_t bux_mx_grouped_contract_workspace_size(int32_t groups);
+int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a_scales,
+                            const uint8_t* b_values, const uint8_t* b_scales,
+                            const int32_t* sizes, int32_t groups, int64_t d, int64_t f,
+                            int64_t m, int out_dtype, void* dw, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * a-10. bfloat16 grouped GEMMs (the experts in "compute" precision).
+ *
+ * bux_bf16_grouped_rows replaces grouped.dot / jax.lax.ragged_dot
+ * (src/bux/architecture/experts/grouped.py:105-117): y[i] = x[i] w[g(i)], float32
+ * sums, bfloat16 out, rows past sum(sizes) 0. x bfloat16 [m, k]; w bfloat16
+ * [groups, k, n] (w_transposed 0) or [groups, n, k] (1: y[i] = x[i] w[g]^T, the dgrad).
+ * bux_bf16_grouped_contract replaces grouped.weight_grad (grouped.py:120-161):
+ * dw[g] = x[rows of g]^T dy[rows of g], x [m, k], dy [m, n] -> dw [groups, k, n].
+ */
+int bux_bf16_grouped_rows(const uint16_t* x, const uint16_t* w, int w_transposed,
+                          const int32_t* sizes, int32_t groups, int64_t m, int64_t n, int64_t k,
+                          uint16_t* y, void* stream);
+int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, const int32_t* sizes,
+                              int32_t groups, int64_t m, int64_t k, int64_t n, uint16_t* dw,
+                              void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * a-2 / a-3. The token path's gathers and sums.
+ *
+ * bux_token_rows replaces moe.token_rows (moe.py:991-1016) and picked_weights
+ * (:1027-1032): rows[i] = z[order[i] / k] for i < m (width columns, bfloat16).
+ * Any width; a multiple of 8 moves 16 bytes a lane.
+ * bux_token_sums replaces grouped_blockscaled.sum_by_token (grouped_blockscaled.py:
+ * 141-148) and moe.token_sums (moe.py:1035-1066): out[t] = sum_j y[inverse[t k + j]]
+ * added in float32 in pick order, rounded once to bfloat16; an inverse outside
+ * [0, y_rows) adds 0.
+ */
+int bux_token_rows(const uint16_t* z, const int32_t* order, int64_t m, int32_t k, int64_t width,
+                   uint16_t* rows, void* stream);
+int bux_token_sums(const uint16_t* y, int64_t y_rows, const int32_t* inverse, int64_t tokens,
+                   int32_t k, int64_t width, uint16_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * a-8. The experts' activation between the two GEMMs, times each row's weight.
+ *
+ * Replaces moe.weighted_units (moe.py:898-910) = weighted(hidden_units(...))
+ * (:913-926) with layers/mlp.py:20-35 and common/functional.py:12-40:
+ * h = act(gate) * (up + up_offset) * w, projected (m, f, 2) with [..., 0] up and
+ * [..., 1] gate (moe.py:845-846). activation BUX_SWISH: act(g) = g sigmoid(g);
+ * BUX_QUICK_GELU: g sigmoid(1.702 g). limit > 0 clamps up to [-limit, limit] and the
+ * gate to at most limit (gpt-oss, tests/test_moe.py:519-528); limit <= 0 clamps
+ * nothing. Rows from *filled on (if filled is not NULL) give 0.
+ * The backward gives d projected (m, f, 2) and d weights (m), the VJP that jax takes
+ * of the forward after its jax.checkpoint recompute (moe.py:906-910), with clip's
+ * and minimum's gradient 1 inside, 1/2 at the limit, 0 outside.
+ */
+enum { BUX_SWISH = 0, BUX_QUICK_GELU = 1 };
+int bux_glu_forward(const uint16_t* projected, const uint16_t* weights, const int32_t* filled,
+                    int64_t m, int64_t f, int activation, float limit, float up_offset,
+                    uint16_t* h, void* stream);
+int bux_glu_backward(const uint16_t* projected, const uint16_t* weights, const uint16_t* dh,
+                     const int32_t* filled, int64_t m, int64_t f, int activation, float limit,
+                     float up_offset, uint16_t* d_projected, uint16_t* d_weights, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BUX_AMD_H */

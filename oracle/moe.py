@@ -117,6 +117,12 @@ def tiles_of(sizes: np.ndarray, m: int, tile: int, starts: np.ndarray | None = N
     return np.stack([group, np.where(real, lo, 0), np.where(real, hi, 0)], -1).astype(np.int32)
 
 
+def whole(rows: int, tile: int = 128) -> int:
+    """Return `rows` rounded up to whole tiles, as ragged_dot pads its rows
+    (grouped_blockscaled.py:122-124, grouped_mxfp8.LANES)."""
+    return -(-rows // tile) * tile
+
+
 def _cast(y: np.ndarray, out: str) -> np.ndarray:
     return bf16.to_bf16(y) if out == "bf16" else y.astype(np.float32)
 
@@ -182,6 +188,9 @@ def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str 
 # --- The expert FFN's activation ---------------------------------------------------
 
 
+QUICK_GELU_ALPHA = float(bf16.round_f32(np.array([1.702], np.float32))[0])  # 1.703125
+
+
 class Ffn(NamedTuple):
     """An expert FFN's activation settings (config.py:204-221): the gate's
     activation, the clamp and the up branch's offset."""
@@ -197,7 +206,9 @@ def _sigmoid(x: np.ndarray) -> np.ndarray:
 
 def _act(name: str, g: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Return act(g) and act'(g) (functional.py:12-40)."""
-    alpha = {"swish": 1.0, "quick_gelu": 1.702}[name]
+    # functional.py:29 writes ``x * jax.nn.sigmoid(1.702 * x)``: jax casts the weakly
+    # typed 1.702 to x's dtype, bfloat16, whose nearest value is 1.703125.
+    alpha = {"swish": 1.0, "quick_gelu": QUICK_GELU_ALPHA}[name]
     s = _sigmoid(alpha * g)
     return g * s, s + alpha * g * s * (1.0 - s)
 
@@ -295,16 +306,17 @@ def layer_forward(
     up2 = np.asarray(up).reshape(e, d, f * p)
     x_m = up_n = h_m = down_n = None
     if fmt == "mxfp8":
-        x_k, x_m = mxfp8.quantized_twice(z, filled, True, index=tokens)
+        # rows padded by 0 to whole tiles of 128 (grouped_blockscaled.py:122-128)
+        x_k, x_m = mxfp8.quantized_twice(z, filled, True, index=tokens, height=whole(m))
         up_n, up_k = mxfp8.quantized_twice(up2, d)
-        projected = rows_mx(x_k, up_k, s.sizes)
+        projected = rows_mx(x_k, up_k, s.sizes, height=m)
     else:
         projected = ragged_dot_bf16(z[tokens], up2, s.sizes)
     h = weighted_units(ffn, projected.reshape(m, f, p), row_weights)
     if fmt == "mxfp8":
-        h_k, h_m = mxfp8.quantized_twice(h, filled, True)
+        h_k, h_m = mxfp8.quantized_twice(h, filled, True, height=whole(m))
         down_n, down_k = mxfp8.quantized_twice(down, f)
-        y = rows_mx(h_k, down_k, s.sizes)
+        y = rows_mx(h_k, down_k, s.sizes, height=m)
     else:
         y = ragged_dot_bf16(h, down, s.sizes)
     out = sum_by_token(y, s.inverse.reshape(t, k))
@@ -327,8 +339,8 @@ def layer_backward(
     tokens = s.order // k
     up2 = np.asarray(up).reshape(e, d, f * p)
     if fmt == "mxfp8":
-        dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens)
-        dh = rows_mx(dy_n, saved.down_n, s.sizes)
+        dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens, height=whole(m))
+        dh = rows_mx(dy_n, saved.down_n, s.sizes, height=m)
         d_down = contract_mx(saved.h_m, dy_m, s.sizes)
     else:
         dy_rows = dy[tokens]
@@ -337,8 +349,8 @@ def layer_backward(
     dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), saved.row_weights, dh)
     dp = dp.reshape(m, f * p)
     if fmt == "mxfp8":
-        dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True)
-        dx = rows_mx(dp_n, saved.up_n, s.sizes)
+        dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True, height=whole(m))
+        dx = rows_mx(dp_n, saved.up_n, s.sizes, height=m)
         d_up = contract_mx(saved.x_m, dp_m, s.sizes)
     else:
         dx = ragged_dot_bf16(dp, np.ascontiguousarray(np.swapaxes(up2, 1, 2)), s.sizes)

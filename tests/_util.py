@@ -1,0 +1,54 @@
+"""Helpers the tests share: moving bfloat16 bits between numpy and torch, seeded
+inputs, and printing which case a GPU step runs (so a failing run names it)."""
+
+import sys
+
+import numpy as np
+import torch
+
+from oracle import bf16
+
+
+def announce(*what) -> None:
+    """Print (and flush) the case a GPU step is about to run."""
+    print("[case]", *what, file=sys.stderr, flush=True)
+
+
+def to_gpu_bf16(bits: np.ndarray) -> torch.Tensor:
+    """Return bfloat16 bits (uint16) as a bfloat16 tensor on cuda:0."""
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def bf16_bits(t: torch.Tensor) -> np.ndarray:
+    """Return a bfloat16 tensor's bits as uint16 numpy."""
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def to_gpu(a: np.ndarray, dtype=None) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return (t if dtype is None else t.to(dtype)).cuda()
+
+
+def normal_bf16(rng: np.random.Generator, shape, scale: float = 1.0) -> np.ndarray:
+    """Return bfloat16 bits of N(0, scale^2) draws."""
+    return bf16.to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def with_outliers(rng: np.random.Generator, bits: np.ndarray, fraction: float = 1e-3,
+                  factor: float = 100.0) -> np.ndarray:
+    """Return bfloat16 bits with a seeded `fraction` of entries scaled by `factor`
+    (the benchmark configs' outliers, which exercise the scales)."""
+    v = bf16.to_f32(bits).copy()
+    flat = v.reshape(-1)
+    at = rng.choice(flat.size, max(1, int(flat.size * fraction)), replace=False)
+    flat[at] *= factor
+    return bf16.to_bf16(v)
+
+
+def rel_err(got: np.ndarray, want: np.ndarray) -> float:
+    """Return ||got - want|| / ||want|| in float64 (0 when both are 0)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    den = np.linalg.norm(want)
+    num = np.linalg.norm(got - want)
+    return float(num / den) if den > 0 else float(num)

@@ -1,0 +1,105 @@
+"""The C-ABI without a GPU: the built library loads, exports every entry point that
+include/bux_amd.h declares (and the ctypes table types each of them), and its host-side
+checks turn bad shapes, flags and workspaces into error codes and messages before any
+kernel launch."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from bux_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "bux_amd.h")
+
+
+def _declared() -> set[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(bux_\w+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.PATH):
+        pytest.fail(f"{_lib.PATH} is not built: run python -m bux_amd.build")
+    return _lib.load()
+
+
+def test_every_declared_entry_point_is_exported_and_typed(lib):
+    declared = _declared()
+    assert len(declared) >= 15
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version(lib):
+    assert lib.bux_version() >= 100
+
+
+def test_workspace_sizes(lib):
+    assert lib.bux_moe_permute_workspace_size(131072, 128) == 512 * 129 * 4
+    assert lib.bux_moe_permute_workspace_size(0, 8) == 0
+    assert lib.bux_mx_grouped_rows_workspace_size(128, 131072, 131072) >= (1024 + 128) * 12
+    assert lib.bux_mx_grouped_contract_workspace_size(128) == 129 * 4
+
+
+def _msg(lib) -> str:
+    return lib.bux_last_error().decode()
+
+
+def test_quantize_rejects_bad_shapes_and_flags(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: the checks fail first
+    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 48, 64, None, 3, p, p, p, p, None)
+    assert rc == 1 and "cols=48" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 40, None, 3, p, p, p, p, None)
+    assert rc == 1 and "height=40" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 0, p, p, p, p, None)
+    assert rc == 1 and "flags" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 2, p, p, None, None, None)
+    assert rc == 1 and "t_values" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, p, 1, 2, 64, 64, 64, None, 1, p, p, None, None, None)
+    assert rc == 1 and "index" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, p, 0, 1, 64, 64, 64, None, 1, p, p, None, None, None)
+    assert rc == 1 and "index_div" in _msg(lib)
+
+
+def test_gemms_reject_bad_shapes_and_small_workspaces(lib):
+    p = ctypes.c_void_p(16)
+    rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 4, 128, 128, 100, 128, 0, p, p, 1 << 20, None)
+    assert rc == 1 and "k=100" in _msg(lib)
+    rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 4, 128, 128, 128, 128, 0, p, p, 8, None)
+    assert rc == 2 and "workspace" in _msg(lib)
+    rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 0, 128, 128, 128, 128, 0, p, p, 1 << 20, None)
+    assert rc == 1 and "groups=0" in _msg(lib)
+    rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 4, 128, 128, 128, 128, 7, p, p, 1 << 20, None)
+    assert rc == 1 and "out_dtype" in _msg(lib)
+    rc = lib.bux_mx_grouped_contract(p, p, p, p, p, 4, 64, 64, 100, 0, p, p, 1 << 10, None)
+    assert rc == 1 and "m=100" in _msg(lib)
+    rc = lib.bux_mx_grouped_contract(p, p, p, p, p, 4, 64, 64, 128, 0, p, p, 4, None)
+    assert rc == 2 and "workspace" in _msg(lib)
+    rc = lib.bux_bf16_grouped_rows(p, p, 0, p, 4, 64, 100, 64, p, None)
+    assert rc == 1 and "multiples of 8" in _msg(lib)
+
+
+def test_permute_and_token_ops_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    rc = lib.bux_moe_permute(p, 100, 0, p, p, p, p, p, 1 << 20, None)
+    assert rc == 1 and "num_experts=0" in _msg(lib)
+    rc = lib.bux_moe_permute(p, 1000, 8, p, p, p, p, p, 4, None)
+    assert rc == 2 and "workspace" in _msg(lib)
+    rc = lib.bux_token_sums(p, 10, p, 5, 2, 12, p, None)
+    assert rc == 1 and "width=12" in _msg(lib)
+    rc = lib.bux_glu_forward(p, p, None, 10, 6, 0, 0.0, 0.0, p, None)
+    assert rc == 1 and "f=6" in _msg(lib)
+    rc = lib.bux_glu_forward(p, p, None, 10, 8, 9, 0.0, 0.0, p, None)
+    assert rc == 1 and "activation 9" in _msg(lib)
+
+
+def test_a_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(_lib.BuxError, match="not built"):
+        _lib.load(str(tmp_path / "libbux_amd.so"))

@@ -1,0 +1,242 @@
+"""The HIP grouped GEMMs against the oracle (the reference's XLA path off Blackwell:
+dequantize, then GEMMs per group), here summed in float64.
+
+Bars: float32 outputs within MAX_OF_MAX of the largest |value| and NORM in norm (set
+from the block-scaled MFMA's measured summation error, below; the reference's
+kernel-vs-XLA bar, scripts/gpu_smoke/grouped_mxfp8.py:45, is 1e-5 of the max between
+two float32 summations on Blackwell); bfloat16 outputs within ||y - y_ref|| / ||y_ref||
+<= 1e-3 (the north star's bar); empty groups and rows past the groups exactly 0; a
+wgrad ignores whatever lies past the groups (tests/test_grouped.py:89-95)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16, moe as omoe, mxfp8
+from tests._util import announce, bf16_bits, normal_bf16, rel_err, to_gpu, to_gpu_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _codes(rng, shape, scale=1.0):
+    """Random MXFP8 blocks of bfloat16 N(0, scale^2) draws, with outliers."""
+    x = bf16.to_f32(normal_bf16(rng, shape, scale))
+    x.reshape(-1)[rng.choice(x.size, max(1, x.size // 500), replace=False)] *= 100
+    if len(shape) == 3:
+        parts = [mxfp8.mx_quantize(a) for a in x]
+        return mxfp8.Blocks(np.stack([p.values for p in parts]), np.stack([p.scales for p in parts]))
+    return mxfp8.mx_quantize(x)
+
+
+def _gpu(blocks):
+    from bux_amd.grouped_mxfp8 import Blocks
+    return Blocks(to_gpu(blocks.values), to_gpu(blocks.scales))
+
+
+# The block-scaled MFMA does not sum a block's products in IEEE float32: measured on the
+# MI355X against float64 sums of the same products, its float32 outputs deviate by
+# 1.5e-5 in norm on Gaussian data, and by up to 8.5e-5 in norm (1.3e-4 of the largest
+# |value|) where x100 outliers share a block with ordinary values (the small products
+# lose bits beside the large one); an IEEE float32 sum would be near 1e-7. The bars are
+# set from those measurements with margin, against a float64 reference: a wrong block,
+# scale, row or group gives errors of order 1.
+MAX_OF_MAX = 5e-4  # |y - y_ref| <= this x max |y_ref|
+NORM = 2e-4  # ||y - y_ref|| / ||y_ref||
+
+
+def _close_f32(got, want, what=""):
+    got = got.astype(np.float64)
+    want = np.asarray(want, np.float64)
+    top = max(float(np.abs(want).max()), 1e-30)
+    err = np.abs(got - want)
+    print(f"[err] {what} max/max {err.max() / top:.3e} norm {rel_err(got, want):.3e}", flush=True)
+    assert err.max() <= MAX_OF_MAX * top, (err.max() / top, np.unravel_index(err.argmax(), err.shape))
+    assert rel_err(got, want) <= NORM
+
+
+def _rows64(a, b, sizes, height):
+    """The oracle's rows (dequantize, GEMM per group), summed in float64."""
+    x, w = mxfp8.dequantized(a).astype(np.float64), mxfp8.dequantized(b).astype(np.float64)
+    y = np.zeros((height, w.shape[1]))
+    start = 0
+    for g, size in enumerate(sizes.tolist()):
+        y[start:start + size] = x[start:start + size] @ w[g].T
+        start += size
+    return y
+
+
+def _contract64(a, b, sizes):
+    """The oracle's contract, summed in float64."""
+    x, y = mxfp8.dequantized(a).astype(np.float64), mxfp8.dequantized(b).astype(np.float64)
+    dw = np.zeros((len(sizes), x.shape[0], y.shape[0]))
+    start = 0
+    for g, size in enumerate(sizes.tolist()):
+        dw[g] = x[:, start:start + size] @ y[:, start:start + size].T
+        start += size
+    return dw
+
+
+ROW_CASES = [
+    # sizes, k, n, height (None: m)
+    ([0, 130, 1, 3, 256, 0, 300, 100], 256, 384, None),
+    ([70, 0, 100, 3, 77], 2880, 2880, 384),  # k and n not whole tiles of 128; padding rows
+    ([128, 128, 256], 128, 128, None),  # groups on tile edges
+    ([5], 64, 96, 64),
+    ([0, 0, 0], 128, 128, 128),  # no rows at all: every row 0
+]
+
+
+@pytest.mark.parametrize("sizes,k,n,height", ROW_CASES)
+def test_rows(lib, sizes, k, n, height):
+    from bux_amd import grouped_mxfp8
+    rng = np.random.default_rng(30)
+    sizes = np.array(sizes, np.int32)
+    m = max(int(sizes.sum()), 32)
+    m = -(-m // 32) * 32
+    a = _codes(rng, (m, k))
+    b = _codes(rng, (len(sizes), n, k), 0.02)
+    h = m if height is None else height
+    announce("rows", sizes.tolist(), m, k, n, h)
+    ga, gb, gs = _gpu(a), _gpu(b), to_gpu(sizes)
+    y32 = grouped_mxfp8.rows(ga, gb, gs, torch.float32, height=h)
+    y16 = grouped_mxfp8.rows(ga, gb, gs, torch.bfloat16, height=h)
+    torch.cuda.synchronize()
+    want = _rows64(a, b, sizes, max(h, m))[:h]
+    got = y32.cpu().numpy()
+    _close_f32(got, want, f"rows {sizes.tolist()} k={k}")
+    filled = int(sizes.sum())
+    assert (got[filled:] == 0).all()
+    # bfloat16 out against the reference's own bfloat16 rounding of its sums
+    got16 = bf16.to_f32(bf16_bits(y16)).astype(np.float64)
+    assert rel_err(got16, bf16.round_f32(want.astype(np.float32))) <= 1e-3 or np.abs(want).max() == 0
+    assert (got16[filled:] == 0).all()
+
+
+CONTRACT_CASES = [
+    ([70, 0, 100, 3, 77], 256, 192, 256),
+    ([0, 130, 1, 3, 256, 0, 300, 100], 2880, 160, 800),  # d not whole tiles, blocks across groups
+    ([128, 0, 384], 128, 256, 512),  # groups on tile edges
+    ([0, 0], 64, 64, 64),  # nothing: dW 0
+]
+
+
+@pytest.mark.parametrize("sizes,d,f,m", CONTRACT_CASES)
+def test_contract(lib, sizes, d, f, m):
+    from bux_amd import grouped_mxfp8
+    rng = np.random.default_rng(31)
+    sizes = np.array(sizes, np.int32)
+    a = _codes(rng, (d, m))
+    b = _codes(rng, (f, m), 0.01)
+    filled = int(sizes.sum())
+    # garbage past the groups (tests/test_grouped.py:89-95): it must add nothing
+    junk = a.values.copy()
+    junk[:, filled:] = 0x7E
+    a = mxfp8.Blocks(junk, a.scales)
+    announce("contract", sizes.tolist(), d, f, m)
+    ga, gb, gs = _gpu(a), _gpu(b), to_gpu(sizes)
+    dw32 = grouped_mxfp8.contract(ga, gb, gs, torch.float32)
+    dw16 = grouped_mxfp8.contract(ga, gb, gs, torch.bfloat16)
+    torch.cuda.synchronize()
+    want = _contract64(a, b, sizes)
+    got = dw32.cpu().numpy()
+    for g in range(len(sizes)):
+        if sizes[g] == 0:
+            assert (got[g] == 0).all()
+        else:
+            _close_f32(got[g], want[g], f"contract group {g} of {sizes.tolist()}")
+    got16 = bf16.to_f32(bf16_bits(dw16))
+    assert rel_err(got16, bf16.round_f32(want.astype(np.float32))) <= 1e-3 or np.abs(want).max() == 0
+
+
+def test_rows_at_config3_up_shape(lib):
+    """Config 3's gate/up fprop shape, 131072 rows of 2048 by 128 experts' (1536, 2048),
+    near-uniform loads: a seeded sample of 512 rows against the oracle; the whole
+    output against the same GEMM in float32 out (bfloat16 is its rounding)."""
+    from bux_amd import grouped_mxfp8
+    rng = np.random.default_rng(32)
+    e, m, k, n = 128, 131072, 2048, 1536
+    sizes = np.bincount(rng.integers(0, e, m), minlength=e).astype(np.int32)
+    announce("rows config3 up")
+    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+    w = (torch.randn(e, n, k, device="cuda") * 0.02).to(torch.bfloat16)
+    xa, _ = grouped_mxfp8.quantized_twice(x, columns=False)
+    wb, _ = grouped_mxfp8.quantized_twice(w, columns=False)
+    gs = to_gpu(sizes)
+    y16 = grouped_mxfp8.rows(xa, wb, gs)
+    y32 = grouped_mxfp8.rows(xa, wb, gs, torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y16, y32.to(torch.bfloat16))
+    sample = np.sort(rng.choice(m, 512, replace=False))
+    starts = np.cumsum(sizes) - sizes
+    a = mxfp8.Blocks(xa.values[torch.from_numpy(sample).cuda()].cpu().numpy(),
+                     xa.scales[torch.from_numpy(sample).cuda()].cpu().numpy())
+    deq_a = mxfp8.dequantized(a).astype(np.float64)
+    groups = np.searchsorted(starts + sizes, sample, side="right")
+    got = y32[torch.from_numpy(sample).cuda()].cpu().numpy()
+    for g in np.unique(groups):
+        rows = groups == g
+        wg = mxfp8.Blocks(wb.values[int(g)].cpu().numpy(), wb.scales[int(g)].cpu().numpy())
+        want = deq_a[rows] @ mxfp8.dequantized(wg).astype(np.float64).T
+        _close_f32(got[rows], want, f"config3 up rows of group {g}")
+
+
+def test_contract_at_config3_down_shape(lib):
+    """Config 3's down wgrad shape: h^T (768, 131072) and dy^T (2048, 131072), 128
+    experts; a seeded sample of 4 experts' dW against the oracle in float64."""
+    from bux_amd import grouped_mxfp8
+    rng = np.random.default_rng(33)
+    e, m, d, f = 128, 131072, 768, 2048
+    sizes = np.bincount(rng.integers(0, e, m), minlength=e).astype(np.int32)
+    announce("contract config3 down")
+    h = torch.randn(m, d, device="cuda", dtype=torch.bfloat16)
+    dy = (torch.randn(m, f, device="cuda") * 0.01).to(torch.bfloat16)
+    _, hm = grouped_mxfp8.quantized_twice(h, rows=False)
+    _, dym = grouped_mxfp8.quantized_twice(dy, rows=False)
+    gs = to_gpu(sizes)
+    dw = grouped_mxfp8.contract(hm, dym, gs, torch.float32)
+    torch.cuda.synchronize()
+    starts = np.cumsum(sizes) - sizes
+    for g in rng.choice(e, 4, replace=False):
+        lo, hi = int(starts[g]), int(starts[g] + sizes[g])
+        b0, b1 = lo // 32, -(-hi // 32)
+        a = mxfp8.Blocks(hm.values[:, 32 * b0:32 * b1].cpu().numpy(), hm.scales[:, b0:b1].cpu().numpy())
+        b = mxfp8.Blocks(dym.values[:, 32 * b0:32 * b1].cpu().numpy(), dym.scales[:, b0:b1].cpu().numpy())
+        da = mxfp8.dequantized(a).astype(np.float64)[:, lo - 32 * b0:hi - 32 * b0]
+        db = mxfp8.dequantized(b).astype(np.float64)[:, lo - 32 * b0:hi - 32 * b0]
+        want = da @ db.T
+        got = dw[int(g)].cpu().numpy()
+        _close_f32(got, want, f"config3 down dW group {g}")
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+def test_bf16_rows(lib, transposed):
+    from bux_amd import grouped
+    rng = np.random.default_rng(34)
+    sizes = np.array([1000, 0, 1500, 3, 1589], np.int32)
+    m, k, n = 4200, 256, 1024
+    x = normal_bf16(rng, (m, k))
+    w = normal_bf16(rng, (len(sizes), k, n), 0.02)
+    announce("bf16 rows", transposed)
+    wt = np.ascontiguousarray(np.swapaxes(w, 1, 2)) if transposed else w
+    y = grouped.dot(to_gpu_bf16(x), to_gpu_bf16(wt), to_gpu(sizes), transposed=transposed)
+    torch.cuda.synchronize()
+    want = omoe.ragged_dot_bf16(x, w, sizes, out="f32")
+    got = bf16.to_f32(bf16_bits(y))
+    assert rel_err(got, want) <= 4e-3
+    assert (got[sizes.sum():] == 0).all()
+
+
+def test_bf16_weight_grad(lib):
+    from bux_amd import grouped
+    rng = np.random.default_rng(35)
+    sizes = np.array([70, 0, 100, 3, 77], np.int32)
+    m, k, n = 256, 256, 512
+    x = normal_bf16(rng, (m, k))
+    dy = normal_bf16(rng, (m, n), 0.01)
+    announce("bf16 weight_grad")
+    dw = grouped.weight_grad(to_gpu_bf16(x), to_gpu_bf16(dy), to_gpu(sizes))
+    torch.cuda.synchronize()
+    want = omoe.weight_grad_bf16(x, dy, sizes, out="f32")
+    got = bf16.to_f32(bf16_bits(dw))
+    assert rel_err(got, want) <= 4e-3
+    assert (got[1] == 0).all()

@@ -272,7 +272,7 @@ def test_the_activations_gradient_is_autograds(ffn):
         lim = torch.tensor(ffn.limit, dtype=torch.float64)
         up = torch.minimum(torch.maximum(up, -lim), lim)
         gate = torch.minimum(gate, lim)
-    alpha = 1.0 if ffn.activation == "swish" else 1.702
+    alpha = 1.0 if ffn.activation == "swish" else moe.QUICK_GELU_ALPHA
     h = gate * torch.sigmoid(alpha * gate) * (up + ffn.up_offset) * wt[:, None]
     np.testing.assert_allclose(bf16.to_f32(moe.weighted_units(ffn, p, w)), h.detach().numpy(), rtol=8e-3, atol=1e-6)
     h.backward(torch.tensor(bf16.to_f32(dh), dtype=torch.float64))
@@ -307,7 +307,7 @@ def test_the_sorted_layer_is_the_dense_one_with_gradients():
             p = zt[tok] @ upt[g].reshape(d, 2 * f)
             u, gate = p.reshape(f, 2)[:, 0], p.reshape(f, 2)[:, 1]
             u, gate = torch.clamp(u, -7.0, 7.0), torch.clamp(gate, max=7.0)
-            h = gate * torch.sigmoid(1.702 * gate) * (u + 1.0) * wt[tok, j]
+            h = gate * torch.sigmoid(moe.QUICK_GELU_ALPHA * gate) * (u + 1.0) * wt[tok, j]
             out = out.index_add(0, torch.tensor([tok]), (h @ downt[g])[None])
     out.backward(torch.tensor(bf16.to_f32(dy), dtype=torch.float64))
 
