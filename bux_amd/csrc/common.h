@@ -42,6 +42,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Two float32 -> two bfloat16 (a in the low half), nearest even, by gfx950's
+// v_cvt_pk_bf16_f32: the same bits as f32_to_bf16 for every non-NaN value.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
+}
+
 // Two float32 -> two E4M3 (OCP float8_e4m3fn) codes, nearest even, in the low 16 bits:
 // gfx950's v_cvt_pk_fp8_f32. The quantizer only passes values already within +-448.
 __device__ __forceinline__ uint32_t e4m3x2(float a, float b) {

@@ -83,6 +83,7 @@ ROW_CASES = [
     ([128, 128, 256], 128, 128, None),  # groups on tile edges
     ([5], 64, 96, 64),
     ([0, 0, 0], 128, 128, 128),  # no rows at all: every row 0
+    ([700, 0, 1, 300, 513, 2000], 512, 640, 3712),  # tiles of 256 from each group's start
 ]
 
 
@@ -117,6 +118,7 @@ CONTRACT_CASES = [
     ([0, 130, 1, 3, 256, 0, 300, 100], 2880, 160, 800),  # d not whole tiles, blocks across groups
     ([128, 0, 384], 128, 256, 512),  # groups on tile edges
     ([0, 0], 64, 64, 64),  # nothing: dW 0
+    ([700, 0, 1, 300, 513, 2000], 640, 384, 3584),  # 256-wide tiles, a partial one
 ]
 
 
