@@ -11,14 +11,21 @@
 // v_i * 2^-e is exact in float32 as in bfloat16 (a power of two, no overflow), so the
 // float32 product gives the reference's bfloat16 product's code.
 //
+// The copies are written in the grouped GEMMs' tiled layout (include/bux_amd.h): codes
+// [K/64][rows][64] and scale bytes [K/128][rows][4], K padded to whole 128s by codes of
+// 0 and scale bytes of 1 (2^-126): the row copy's K is x's columns, the column copy's
+// K is the height.
+//
 // One workgroup of 256 threads (4 waves) takes a tile of 128 rows by 64 columns:
 //   - loads: thread t reads 16 bytes (8 values) of row t/8 + 32 i, columns 8 (t % 8):
 //     each row's 128 bytes in one coalesced burst of 8 lanes;
 //   - the row copy: a block of 32 columns is 4 neighbouring lanes, reduced by two
-//     xor-shuffles; each lane writes its 8 codes as one 8-byte store;
+//     xor-shuffles; each lane writes its 8 codes as one 8-byte store (8 lanes a row's
+//     64 bytes of a K chunk, consecutive rows consecutive);
 //   - the column copy: the tile goes through LDS; wave w takes rows 32w..32w+31, lane
 //     l column l, reading one LDS row per step (all lanes on one row: no bank
-//     conflicts), and writes its 32 codes of x^T's row l as two 16-byte stores.
+//     conflicts), and writes its 32 codes of x^T's row l as two 16-byte stores (half
+//     of the row's 64-byte K chunk; the other wave of the pair writes the other half).
 // HBM traffic per element: 2 bytes read, 2 x (1 + 1/32) bytes written.
 
 #include "common.h"
@@ -39,7 +46,9 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
 
   const int t = threadIdx.x;
   // Column tiles run fastest, so that neighbouring workgroups read one band of rows.
-  const int64_t col_tiles = (cols + TILE_COLS - 1) / TILE_COLS;
+  // They cover the K padding of the row copy too (columns read as 0 there).
+  const int64_t cols_pad = (cols + 127) / 128 * 128;
+  const int64_t col_tiles = cols_pad / TILE_COLS;
   const int64_t col0 = (static_cast<int64_t>(blockIdx.x) % col_tiles) * TILE_COLS;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) / col_tiles) * TILE_ROWS;
   const int64_t g = blockIdx.y;
@@ -68,8 +77,8 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
   }
 
   if (flags & BUX_MX_ROWS) {
-    uint8_t* vg = values + g * height * cols;
-    uint8_t* sg = scales + g * height * (cols / 32);
+    uint8_t* vg = values + g * height * cols_pad;
+    uint8_t* sg = scales + g * height * (cols_pad / 32);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t r = row0 + (t >> 3) + 32 * i;
@@ -92,9 +101,10 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
                        clip448(v[3] * down));
       codes.y = e4m3x4(clip448(v[4] * down), clip448(v[5] * down), clip448(v[6] * down),
                        clip448(v[7] * down));
-      if (r < height && col_in) {
-        *reinterpret_cast<uint2*>(vg + r * cols + col) = codes;
-        if ((chunk & 3) == 0) sg[r * (cols / 32) + col / 32] = static_cast<uint8_t>(e + 127);
+      if (r < height) {  // padding columns too: codes 0, scale byte 1
+        *reinterpret_cast<uint2*>(vg + ((col >> 6) * height + r) * 64 + (col & 63)) = codes;
+        const int64_t b = col >> 5;
+        if ((chunk & 3) == 0) sg[((b >> 2) * height + r) * 4 + (b & 3)] = static_cast<uint8_t>(e + 127);
       }
     }
   }
@@ -110,8 +120,9 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
   const int wave = t >> 6;
   const int lane = t & 63;
   const int64_t c = col0 + lane;
-  const int64_t rb = row0 + 32 * wave;  // the block's first row
-  if (c >= cols || rb >= height) return;
+  const int64_t rb = row0 + 32 * wave;  // the block's first row (below kt: tiles cover it)
+  const int64_t kt = (height + 127) / 128 * 128;  // the column copy's K, padded
+  if (c >= cols) return;
   float v[32];
   float amax = 0.0f;
 #pragma unroll
@@ -127,10 +138,12 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     w[j] = e4m3x4(clip448(v[4 * j] * down), clip448(v[4 * j + 1] * down),
                   clip448(v[4 * j + 2] * down), clip448(v[4 * j + 3] * down));
   }
-  uint8_t* out = t_values + g * cols * height + c * height + rb;
+  // x^T's row c, K (x's rows) from rb: 32 bytes of its 64-byte chunk rb / 64
+  uint8_t* out = t_values + g * cols * kt + ((rb >> 6) * cols + c) * 64 + (rb & 63);
   reinterpret_cast<uint4*>(out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
   reinterpret_cast<uint4*>(out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
-  t_scales[g * cols * (height / 32) + c * (height / 32) + rb / 32] = static_cast<uint8_t>(e + 127);
+  t_scales[g * cols * (kt / 32) + ((rb >> 7) * cols + c) * 4 + ((rb >> 5) & 3)] =
+      static_cast<uint8_t>(e + 127);
 }
 
 }  // namespace
@@ -160,7 +173,7 @@ extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t 
             (long long)groups);
   BUX_CHECK(groups <= 65535, "bux_mx_quantize: %lld matrices exceed one launch", (long long)groups);
   if (height == 0) return BUX_OK;
-  const int64_t tiles = ceil_div(height, TILE_ROWS) * ceil_div(cols, TILE_COLS);
+  const int64_t tiles = ceil_div(height, TILE_ROWS) * (ceil_div(cols, 128) * 128 / TILE_COLS);
   BUX_CHECK(tiles <= (1LL << 23), "bux_mx_quantize: %lld x %lld is too large for one launch",
             (long long)height, (long long)cols);
   dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));

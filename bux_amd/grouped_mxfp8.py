@@ -9,10 +9,13 @@ Mirrors, with the same argument meanings:
 - `rows`: ``grouped_mxfp8.rows`` (src/bux/architecture/experts/grouped_mxfp8.py:116-154);
 - `contract`: ``grouped_mxfp8.contract`` (grouped_mxfp8.py:185-210).
 
-Operands are `Blocks` in the canonical layout (E4M3 codes (..., r, c) and E8M0 scale
-bytes (..., r, c/32), row-major), which the kernels load as they are: the reference's
-``Tiled`` (grouped_mxfp8.py:93-103) is a Blackwell tensor-memory layout with no
-counterpart here.
+Operands are `Tiled`: a matrix's MXFP8 blocks along its rows (the reference's
+``Blocks``, src/bux/architecture/precision/blockscaled.py:43-56) in the layout the
+GEMMs load, as the reference's ``Tiled`` (grouped_mxfp8.py:93-103) is for its kernels:
+K (the row length) padded to whole 128s with codes 0 and scale bytes 1, E4M3 codes
+(..., K/64, r, 64) and E8M0 scale bytes (..., K/128, r, 4). `tiled` and `canonical`
+convert from and to the row-major ``Blocks`` layout (codes (..., r, c), scale bytes
+(..., r, c/32)).
 """
 
 from typing import NamedTuple
@@ -22,20 +25,62 @@ import torch
 from bux_amd import _lib
 from bux_amd.kernels import lib, ptr, require, stream, workspace
 
-LANES = 128  # rows a GEMM tile takes: copies are padded to whole tiles of them
+LANES = 128  # rows of the activations' copies: padded to whole tiles of them
+K_ALIGN = 128  # the tiled layout's K: whole 128s
 
 
-class Blocks(NamedTuple):
-    """A matrix (or a stack of them) in MXFP8 along its rows
-    (src/bux/architecture/precision/blockscaled.py:43-56)."""
+class Tiled(NamedTuple):
+    """A matrix (or a stack of them) in MXFP8 along its rows, tiled.
 
-    values: torch.Tensor  # uint8 (..., r, c): E4M3 codes
-    scales: torch.Tensor  # uint8 (..., r, c / 32): E8M0 biased exponents
+    Row i's code j is ``values[..., j // 64, i, j % 64]`` and its block b's scale byte
+    ``scales[..., b // 4, i, b % 4]``; codes past the matrix's columns are 0 and their
+    scale bytes 1."""
+
+    values: torch.Tensor  # uint8 (..., K/64, r, 64): E4M3 codes
+    scales: torch.Tensor  # uint8 (..., K/128, r, 4): E8M0 biased exponents
+
+    @property
+    def height(self) -> int:
+        """The matrix's rows."""
+        return self.values.shape[-2]
+
+    @property
+    def k(self) -> int:
+        """The padded row length, a multiple of 128."""
+        return self.values.shape[-3] * 64
 
 
 def whole(rows: int, tile: int = LANES) -> int:
     """Return `rows` rounded up to whole tiles (grouped_blockscaled.py:122-124)."""
     return -(-rows // tile) * tile
+
+
+def _swap_last_but_one(x: torch.Tensor, lead: int) -> torch.Tensor:
+    """Swap the two axes before the last, after `lead` leading axes."""
+    return x.permute(*range(lead), lead + 1, lead, lead + 2)
+
+
+def tiled(values: torch.Tensor, scales: torch.Tensor) -> Tiled:
+    """Return row-major blocks (codes (..., r, c), scale bytes (..., r, c/32)) tiled."""
+    *lead, r, c = values.shape
+    kp = whole(c, K_ALIGN)
+    v = torch.zeros(*lead, r, kp, dtype=torch.uint8, device=values.device)
+    v[..., :c] = values
+    sc = torch.ones(*lead, r, kp // 32, dtype=torch.uint8, device=values.device)
+    sc[..., :c // 32] = scales
+    n = len(lead)
+    v = _swap_last_but_one(v.reshape(*lead, r, kp // 64, 64), n).contiguous()
+    sc = _swap_last_but_one(sc.reshape(*lead, r, kp // 128, 4), n).contiguous()
+    return Tiled(v, sc)
+
+
+def canonical(t: Tiled, cols: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Return tiled blocks row-major: codes (..., r, cols), scale bytes (..., r, cols/32)."""
+    *lead, chunks, r, _ = t.values.shape
+    n = len(lead)
+    v = _swap_last_but_one(t.values, n).reshape(*lead, r, chunks * 64)
+    sc = _swap_last_but_one(t.scales, n).reshape(*lead, r, chunks * 2)
+    return v[..., :cols].contiguous(), sc[..., :cols // 32].contiguous()
 
 
 def quantized_twice(
@@ -46,13 +91,13 @@ def quantized_twice(
     index_div: int = 1,
     height: int | None = None,
     rows: bool = True,
-) -> tuple[Blocks | None, Blocks | None]:
+) -> tuple[Tiled | None, Tiled | None]:
     """Return x in MXFP8 along its rows and, if `columns`, x^T along its rows, in one
-    pass over x.
+    pass over x, both tiled.
 
     Args:
         x: bfloat16, a matrix (r, c) or a stack (g, r, c); with `index`, the matrix
-            the rows are read from.
+            the rows are read from. c is a multiple of 32.
         filled: a device int32 (one element): rows from it on quantize as 0; None
             for every row.
         columns: whether to return x^T too.
@@ -64,8 +109,8 @@ def quantized_twice(
         rows: whether to return the copy along the rows (False: None in its place).
 
     Returns:
-        (x along rows, x^T along rows): stacks (g, height, c) and (g, c, height) for a
-        stack.
+        (x along rows, x^T along rows): `height` rows of K = c padded to 128, and c
+        rows of K = height padded to 128 (a stack of g of each for a stack).
     """
     require(x, filled, index)
     if x.dtype != torch.bfloat16:
@@ -86,17 +131,19 @@ def quantized_twice(
     flags = 0
     if rows:
         flags |= _lib.MX_ROWS
-        vals = torch.empty(*lead, h, c, dtype=torch.uint8, device=dev)
-        scales = torch.empty(*lead, h, c // 32, dtype=torch.uint8, device=dev)
+        kc = whole(c, K_ALIGN)
+        vals = torch.empty(*lead, kc // 64, h, 64, dtype=torch.uint8, device=dev)
+        scales = torch.empty(*lead, kc // 128, h, 4, dtype=torch.uint8, device=dev)
     if columns:
         flags |= _lib.MX_COLUMNS
-        t_vals = torch.empty(*lead, c, h, dtype=torch.uint8, device=dev)
-        t_scales = torch.empty(*lead, c, h // 32, dtype=torch.uint8, device=dev)
+        kh = whole(h, K_ALIGN)
+        t_vals = torch.empty(*lead, kh // 64, c, 64, dtype=torch.uint8, device=dev)
+        t_scales = torch.empty(*lead, kh // 128, c, 4, dtype=torch.uint8, device=dev)
     _lib.check(lib().bux_mx_quantize(
         ptr(x), ptr(index), index_div, groups, r, c, h, ptr(filled), flags,
         ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))
-    along_rows = Blocks(vals, scales) if rows else None
-    along_columns = Blocks(t_vals, t_scales) if columns else None
+    along_rows = Tiled(vals, scales) if rows else None
+    along_columns = Tiled(t_vals, t_scales) if columns else None
     return along_rows, along_columns
 
 
@@ -104,23 +151,26 @@ _DTYPES = {torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
 
 
 def rows(
-    a: Blocks, b: Blocks, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16,
+    a: Tiled, b: Tiled, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16,
     height: int | None = None,
 ) -> torch.Tensor:
     """Return ``a @ b[g]^T`` for each group g's rows of a, (height, n), the rows past
     the groups 0.
 
     Args:
-        a: the rows (m, k), group 0's first, in MXFP8 along k.
-        b: the groups' matrices (g, n, k), in MXFP8 along k.
+        a: the rows (m of K), group 0's first.
+        b: the groups' matrices, a stack (g of n rows of K).
         sizes: int32 (g,) on the device: how many rows each group has.
         out: the output's dtype, bfloat16 or float32.
         height: rows of the output (a's rows past it are not stored); None for m.
     """
     require(a.values, a.scales, b.values, b.scales, sizes)
-    m, k = a.values.shape
-    groups, n, kb = b.values.shape
-    if kb != k or sizes.shape != (groups,) or sizes.dtype != torch.int32:
+    if a.values.dim() != 3 or b.values.dim() != 4:
+        raise ValueError(f"rows: a {tuple(a.values.shape)} is not one matrix or "
+                         f"b {tuple(b.values.shape)} not a stack")
+    m, k = a.height, a.k
+    groups, n = b.values.shape[0], b.height
+    if b.k != k or sizes.shape != (groups,) or sizes.dtype != torch.int32:
         raise ValueError(f"rows: a {tuple(a.values.shape)}, b {tuple(b.values.shape)}, "
                          f"sizes {tuple(sizes.shape)} {sizes.dtype}")
     h = m if height is None else height
@@ -133,21 +183,23 @@ def rows(
 
 
 def contract(
-    a: Blocks, b: Blocks, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16
+    a: Tiled, b: Tiled, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16
 ) -> torch.Tensor:
     """Return ``a[:, rows of g] b[:, rows of g]^T`` for each group g, (g, d, f).
 
     Args:
-        a: x^T (d, m) in MXFP8 along m.
-        b: dy^T (f, m) in MXFP8 along m.
+        a: x^T (d rows of m) in MXFP8 along m.
+        b: dy^T (f rows of m) in MXFP8 along m.
         sizes: int32 (g,) on the device, summing to at most m.
         out: the output's dtype.
     """
     require(a.values, a.scales, b.values, b.scales, sizes)
-    d, m = a.values.shape
-    f, mb = b.values.shape
+    if a.values.dim() != 3 or b.values.dim() != 3:
+        raise ValueError(f"contract: a {tuple(a.values.shape)}, b {tuple(b.values.shape)}")
+    d, m = a.height, a.k
+    f = b.height
     groups = sizes.shape[0]
-    if mb != m or sizes.dtype != torch.int32:
+    if b.k != m or sizes.dtype != torch.int32:
         raise ValueError(f"contract: a {tuple(a.values.shape)}, b {tuple(b.values.shape)}")
     dw = torch.empty(groups, d, f, dtype=out, device=a.values.device)
     ws = workspace(lib().bux_mx_grouped_contract_workspace_size(groups), dw.device)

@@ -25,7 +25,7 @@ from typing import NamedTuple
 import torch
 
 from bux_amd import _lib, grouped, grouped_mxfp8
-from bux_amd.grouped_mxfp8 import Blocks
+from bux_amd.grouped_mxfp8 import Tiled
 from bux_amd.kernels import lib, ptr, require, stream, workspace
 from bux_amd.spans import span
 
@@ -142,10 +142,10 @@ class Saved(NamedTuple):
     row_weights: torch.Tensor  # bfloat16 (m,)
     projected: torch.Tensor  # bfloat16 (m, 2f)
     h: torch.Tensor  # bfloat16 (m, f)
-    x_m: Blocks | None  # x^T along the rows (wgrad of up)
-    up_n: Blocks | None  # each W_up along n (dgrad of up)
-    h_m: Blocks | None  # h^T along the rows (wgrad of down)
-    down_n: Blocks | None  # each W_down along n (dgrad of down)
+    x_m: Tiled | None  # x^T along the rows (wgrad of up)
+    up_n: Tiled | None  # each W_up along n (dgrad of up)
+    h_m: Tiled | None  # h^T along the rows (wgrad of down)
+    down_n: Tiled | None  # each W_down along n (dgrad of down)
     rows: torch.Tensor | None  # the picks' rows, compute format only
 
 

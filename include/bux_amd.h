@@ -14,10 +14,15 @@
  *
  * Layouts (row-major throughout):
  *   bfloat16   uint16_t bit patterns;
- *   MXFP8      an (r, c) matrix in blocks of 32 along its rows: E4M3 codes uint8 (r, c)
- *              and E8M0 scale bytes uint8 (r, c / 32) -- the reference's `Blocks`
- *              (src/bux/architecture/precision/blockscaled.py:43-56). The kernels take
- *              operands in exactly this layout, so there is no separate tiled form.
+ *   MXFP8      an (r, c) matrix in blocks of 32 along its rows -- the reference's
+ *              `Blocks` (src/bux/architecture/precision/blockscaled.py:43-56): E4M3
+ *              codes and one E8M0 scale byte a block -- in the tiled layout the grouped
+ *              GEMMs load, which, as the reference's `Tiled` (experts/grouped_mxfp8.py:
+ *              93-103) does for its kernels, pads c to K = whole 128s (codes 0, scale
+ *              bytes 1) and lays K out in chunks:
+ *                codes   uint8 [K / 64][r][64]:  element (i, j) at ((j / 64) r + i) 64 + j % 64
+ *                scales  uint8 [K / 128][r][4]:  block b of row i at ((b / 4) r + i) 4 + b % 4
+ *              A stack of g matrices is g of these one after another.
  *
  * References are to files under /root/reference (pilot7747/bux).
  */
@@ -85,10 +90,12 @@ int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_experts, in
  *           (the reference pads to whole tiles, grouped_blockscaled.py:122-128).
  * filled    NULL (every row holds values) or a device int32: rows from *filled on
  *           quantize as 0 (grouped_blockscaled.py:314).
- * flags     BUX_MX_ROWS: write values [groups, height, cols] and scales
- *           [groups, height, cols/32]; BUX_MX_COLUMNS: write t_values
- *           [groups, cols, height] and t_scales [groups, cols, height/32] (x^T in
- *           blocks along its rows). cols must be a multiple of 32.
+ * flags     BUX_MX_ROWS: write values and scales, x (height, cols) in MXFP8 along its
+ *           rows, tiled with K = cols rounded up to 128: [groups, K/64, height, 64] and
+ *           [groups, K/128, height, 4]. BUX_MX_COLUMNS: write t_values and t_scales,
+ *           x^T (cols, height) likewise with K = height rounded up to 128:
+ *           [groups, K/64, cols, 64] and [groups, K/128, cols, 4].
+ *           cols must be a multiple of 32.
  */
 enum { BUX_MX_ROWS = 1, BUX_MX_COLUMNS = 2 };
 int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t groups,
@@ -103,14 +110,14 @@ int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, 
  * with its tile list tiles_of (:157-182), and off Blackwell grouped_blockscaled._times
  * (grouped_blockscaled.py:220-233): float32 sums, rows past sum(sizes) are 0.
  *
- * a_values/a_scales  MXFP8 [m, k]: the rows, group 0's first.
- * b_values/b_scales  MXFP8 [groups, n, k]: each group's matrix.
- * sizes     device int32 [groups].
+ * a_values/a_scales  MXFP8 tiled, m rows of k bytes: the rows, group 0's first.
+ * b_values/b_scales  MXFP8 tiled, a stack of groups matrices of n rows of k bytes.
+ * sizes     device int32 [groups], summing to at most m.
+ * k         the tiled K: the contracted length rounded up to a multiple of 128.
  * y         [height, n], bfloat16 (out_dtype BUX_BF16) or float32 (BUX_F32); rows
- *           from sum(sizes) to height are 0, and a's rows past m read 0. Any height:
- *           a's quantized copy may be padded past the height of y (e.g. to whole
- *           tiles) and rows of the groups past height are not stored.
- * k must be a multiple of 32.
+ *           from sum(sizes) to height are 0. Any height: a's quantized copy may be
+ *           padded past the height of y (e.g. to whole tiles) and rows of the groups
+ *           past height are not stored. n must be a multiple of 4.
  */
 enum { BUX_BF16 = 0, BUX_F32 = 1 };
 size_t bux_mx_grouped_rows_workspace_size(int32_t groups, int64_t m, int64_t height);
@@ -124,13 +131,15 @@ int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_scales, const 
  *
  * Replaces grouped_mxfp8.contract (grouped_mxfp8.py:185-210) with its edge tiles
  * _edges (:240-256), and off Blackwell grouped_blockscaled._contract
- * (grouped_blockscaled.py:236-250): the rows of a block of 32 that another group owns
- * count as 0; float32 sums.
+ * (grouped_blockscaled.py:236-250): in a block of 32 that two groups share, each
+ * group's sum takes a's codes of its own rows only (the others count as 0, under the
+ * block's one scale); float32 sums.
  *
- * a_values/a_scales  MXFP8 [d, m]: x^T in blocks along the rows m.
- * b_values/b_scales  MXFP8 [f, m]: dy^T likewise.
- * sizes     device int32 [groups]; sum(sizes) <= m; m a multiple of 32.
+ * a_values/a_scales  MXFP8 tiled, d rows of m bytes: x^T in blocks along the rows m.
+ * b_values/b_scales  MXFP8 tiled, f rows of m bytes: dy^T likewise.
+ * sizes     device int32 [groups]; sum(sizes) <= m; m a multiple of 128.
  * dw        [groups, d, f], bfloat16 or float32 (out_dtype); 0 for an empty group.
+ *           f must be a multiple of 4.
  */
 size_t bux_mx_grouped_contract_workspace_size(int32_t groups);
 int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a_scales,

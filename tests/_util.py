@@ -52,3 +52,23 @@ def rel_err(got: np.ndarray, want: np.ndarray) -> float:
     den = np.linalg.norm(want)
     num = np.linalg.norm(got - want)
     return float(num / den) if den > 0 else float(num)
+
+
+def untiled(t, cols: int) -> tuple[np.ndarray, np.ndarray]:
+    """Return a device `Tiled` (codes (..., K/64, r, 64), scale bytes (..., K/128, r, 4))
+    row-major on the host, codes (..., r, cols) and scale bytes (..., r, cols/32), after
+    checking that its K padding holds codes 0 and scale bytes 1."""
+    v = t.values.cpu().numpy()
+    s = t.scales.cpu().numpy()
+    n = v.ndim - 3
+    v = np.swapaxes(v, n, n + 1).reshape(*v.shape[:n], v.shape[-2], -1)
+    s = np.swapaxes(s, n, n + 1).reshape(*s.shape[:n], s.shape[-2], -1)
+    assert (v[..., cols:] == 0).all(), "codes past the columns are not 0"
+    assert (s[..., cols // 32:] == 1).all(), "scale bytes past the columns are not 1"
+    return v[..., :cols], s[..., :cols // 32]
+
+
+def to_gpu_tiled(blocks):
+    """Return row-major MXFP8 blocks (the oracle's) on cuda:0, tiled for the GEMMs."""
+    from bux_amd import grouped_mxfp8
+    return grouped_mxfp8.tiled(to_gpu(blocks.values), to_gpu(blocks.scales))

@@ -43,7 +43,8 @@ def test_version(lib):
 def test_workspace_sizes(lib):
     assert lib.bux_moe_permute_workspace_size(131072, 128) == 512 * 129 * 4
     assert lib.bux_moe_permute_workspace_size(0, 8) == 0
-    assert lib.bux_mx_grouped_rows_workspace_size(128, 131072, 131072) >= (1024 + 128) * 12
+    # group starts, then a tile list: tiles of 256 rows, one more a group at most
+    assert lib.bux_mx_grouped_rows_workspace_size(128, 131072, 131072) >= (512 + 128) * 12
     assert lib.bux_mx_grouped_contract_workspace_size(128) == 129 * 4
 
 
@@ -71,6 +72,9 @@ def test_gemms_reject_bad_shapes_and_small_workspaces(lib):
     p = ctypes.c_void_p(16)
     rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 4, 128, 128, 100, 128, 0, p, p, 1 << 20, None)
     assert rc == 1 and "k=100" in _msg(lib)
+    # the tiled layout's K is whole 128s
+    rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 4, 128, 128, 160, 128, 0, p, p, 1 << 20, None)
+    assert rc == 1 and "k=160" in _msg(lib)
     rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 4, 128, 128, 128, 128, 0, p, p, 8, None)
     assert rc == 2 and "workspace" in _msg(lib)
     rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 0, 128, 128, 128, 128, 0, p, p, 1 << 20, None)

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import bf16, moe as omoe, mxfp8
-from tests._util import announce, bf16_bits, normal_bf16, rel_err, to_gpu, to_gpu_bf16
+from tests._util import announce, bf16_bits, normal_bf16, rel_err, to_gpu, to_gpu_bf16, to_gpu_tiled
 
 pytestmark = pytest.mark.gpu
 
@@ -29,8 +29,7 @@ def _codes(rng, shape, scale=1.0):
 
 
 def _gpu(blocks):
-    from bux_amd.grouped_mxfp8 import Blocks
-    return Blocks(to_gpu(blocks.values), to_gpu(blocks.scales))
+    return to_gpu_tiled(blocks)
 
 
 # The block-scaled MFMA does not sum a block's products in IEEE float32: measured on the
@@ -170,14 +169,16 @@ def test_rows_at_config3_up_shape(lib):
     assert torch.equal(y16, y32.to(torch.bfloat16))
     sample = np.sort(rng.choice(m, 512, replace=False))
     starts = np.cumsum(sizes) - sizes
-    a = mxfp8.Blocks(xa.values[torch.from_numpy(sample).cuda()].cpu().numpy(),
-                     xa.scales[torch.from_numpy(sample).cuda()].cpu().numpy())
+    xa_v, xa_s = grouped_mxfp8.canonical(xa, k)
+    at = torch.from_numpy(sample).cuda()
+    a = mxfp8.Blocks(xa_v[at].cpu().numpy(), xa_s[at].cpu().numpy())
+    wb_v, wb_s = grouped_mxfp8.canonical(wb, k)
     deq_a = mxfp8.dequantized(a).astype(np.float64)
     groups = np.searchsorted(starts + sizes, sample, side="right")
     got = y32[torch.from_numpy(sample).cuda()].cpu().numpy()
     for g in np.unique(groups):
         rows = groups == g
-        wg = mxfp8.Blocks(wb.values[int(g)].cpu().numpy(), wb.scales[int(g)].cpu().numpy())
+        wg = mxfp8.Blocks(wb_v[int(g)].cpu().numpy(), wb_s[int(g)].cpu().numpy())
         want = deq_a[rows] @ mxfp8.dequantized(wg).astype(np.float64).T
         _close_f32(got[rows], want, f"config3 up rows of group {g}")
 
@@ -198,11 +199,13 @@ def test_contract_at_config3_down_shape(lib):
     dw = grouped_mxfp8.contract(hm, dym, gs, torch.float32)
     torch.cuda.synchronize()
     starts = np.cumsum(sizes) - sizes
+    hm_v, hm_s = grouped_mxfp8.canonical(hm, m)
+    dym_v, dym_s = grouped_mxfp8.canonical(dym, m)
     for g in rng.choice(e, 4, replace=False):
         lo, hi = int(starts[g]), int(starts[g] + sizes[g])
         b0, b1 = lo // 32, -(-hi // 32)
-        a = mxfp8.Blocks(hm.values[:, 32 * b0:32 * b1].cpu().numpy(), hm.scales[:, b0:b1].cpu().numpy())
-        b = mxfp8.Blocks(dym.values[:, 32 * b0:32 * b1].cpu().numpy(), dym.scales[:, b0:b1].cpu().numpy())
+        a = mxfp8.Blocks(hm_v[:, 32 * b0:32 * b1].cpu().numpy(), hm_s[:, b0:b1].cpu().numpy())
+        b = mxfp8.Blocks(dym_v[:, 32 * b0:32 * b1].cpu().numpy(), dym_s[:, b0:b1].cpu().numpy())
         da = mxfp8.dequantized(a).astype(np.float64)[:, lo - 32 * b0:hi - 32 * b0]
         db = mxfp8.dequantized(b).astype(np.float64)[:, lo - 32 * b0:hi - 32 * b0]
         want = da @ db.T

@@ -1,14 +1,15 @@
 """The HIP MXFP8 quantizer against the oracle, bit for bit: E4M3 codes and E8M0 scale
-bytes in the canonical layout, for both copies (along the rows, and x^T along its
-rows), every bfloat16 value at every scale exponent, gathered rows, rows past
-`filled`, padding, stacks, and the benchmark's full-size activations."""
+bytes (read back from the tiled layout row-major, its K padding checked), for both
+copies (along the rows, and x^T along its rows), every bfloat16 value at every scale
+exponent, gathered rows, rows past `filled`, padding, stacks, and the benchmark's
+full-size activations."""
 
 import numpy as np
 import pytest
 import torch
 
 from oracle import bf16, mxfp8
-from tests._util import announce, normal_bf16, to_gpu, to_gpu_bf16, with_outliers
+from tests._util import announce, normal_bf16, to_gpu, to_gpu_bf16, untiled, with_outliers
 
 pytestmark = pytest.mark.gpu
 
@@ -17,8 +18,7 @@ FINITE = ALL[np.isfinite(bf16.to_f32(ALL))]
 
 
 def _equal(got, want, what):
-    got_v = got.values.cpu().numpy()
-    got_s = got.scales.cpu().numpy()
+    got_v, got_s = untiled(got, want.values.shape[-1])
     assert got_v.shape == want.values.shape, (what, got_v.shape, want.values.shape)
     bad = np.flatnonzero(got_v.reshape(-1) != want.values.reshape(-1))
     assert bad.size == 0, f"{what}: {bad.size} codes differ, first at {bad[:5]}: " \
@@ -139,15 +139,16 @@ def test_config2_activations_full_size(lib):
     rows3, cols3 = _quantize(gathered)
     assert torch.equal(rows1.values, rows3.values) and torch.equal(cols1.scales, cols3.scales)
     assert torch.equal(cols1.values, cols3.values)
+    from bux_amd import grouped_mxfp8
     sample = rng.choice(m, 4096, replace=False)
     want = mxfp8.mx_quantize(z[order[sample] // k])
-    got = mxfp8.Blocks(rows1.values[torch.from_numpy(sample).cuda()].cpu().numpy(),
-                       rows1.scales[torch.from_numpy(sample).cuda()].cpu().numpy())
-    _equal(type(rows1)(torch.from_numpy(got.values), torch.from_numpy(got.scales)), want, "rows sample")
+    at = torch.from_numpy(sample).cuda()
+    rows_v, rows_s = grouped_mxfp8.canonical(rows1, d)
+    np.testing.assert_array_equal(rows_v[at].cpu().numpy(), want.values)
+    np.testing.assert_array_equal(rows_s[at].cpu().numpy(), want.scales)
+    cols_v, cols_s = grouped_mxfp8.canonical(cols1, m)
     for b in rng.choice(m // 32, 64, replace=False):
         block = z[order[32 * b:32 * b + 32] // k]  # 32 rows, all columns
         want = mxfp8.mx_quantize(np.ascontiguousarray(bf16.to_f32(block).T))
-        got_v = cols1.values[:, 32 * b:32 * b + 32].cpu().numpy()
-        got_s = cols1.scales[:, b].cpu().numpy()
-        np.testing.assert_array_equal(got_v, want.values)
-        np.testing.assert_array_equal(got_s, want.scales[:, 0])
+        np.testing.assert_array_equal(cols_v[:, 32 * b:32 * b + 32].cpu().numpy(), want.values)
+        np.testing.assert_array_equal(cols_s[:, b].cpu().numpy(), want.scales[:, 0])
