@@ -126,6 +126,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run only a plain device-to-device copy of MIB MiB, 10 times: the "
+                         "kernel of known traffic that scales rocprofv3's FETCH_SIZE and "
+                         "WRITE_SIZE counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (the MoE expert "
@@ -139,6 +143,15 @@ def main():
         raise SystemExit("bench.py needs a gfx950 GPU and the built library (python -m bux_amd.build)")
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "copies": 10}), flush=True)
+        return
     log(f"inputs: config 3, T={T} d={D} E={E} k={K} f={F}")
     z, idx, w, up, down, dy = inputs(T, D, E, K, F, device)
     torch.cuda.synchronize()
@@ -188,7 +201,7 @@ def main():
                    "gemm_tflop_per_step": total_flops / 1e12, "parallelism": "single GPU"},
         "roofline": {
             "bound": "mfma",
-            "kernel": f"{dominant} (rows_kernel/contract_kernel)",
+            "kernel": f"{dominant} ({'contract_kernel' if 'wgrad' in dominant else 'rows_kernel'})",
             "achieved": round(gemms[dominant]["tflops"], 2),
             "peak": PEAK_MXFP8_TFLOPS,
             "unit": "TFLOP/s",

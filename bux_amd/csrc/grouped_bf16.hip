@@ -3,8 +3,8 @@
 //
 //   rows      y[i] = x[i] w[g(i)]   (w [g, k, n]) or x[i] w[g(i)]^T (w [g, n, k])
 //             grouped.dot / jax.lax.ragged_dot, src/bux/architecture/experts/
-//             grouped.py:105-117: rows past sum(sizes) are 0.
-//   contract  dw[g] = x[rows of g]^T dy[rows of g]   grouped.py:120-161.
+//             grouped.py:90-102: rows past sum(sizes) are 0.
+//   contract  dw[g] = x[rows of g]^T dy[rows of g]   grouped.py:105-146.
 //
 // One mainloop computes C[r][c] = sum_k A(r, k) B(c, k) over a 128 x 128 tile, in steps
 // of 32 of k through LDS ([row][k], rows padded to 80 bytes so that ds_read_b128 of 32

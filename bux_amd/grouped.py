@@ -1,7 +1,7 @@
 """bfloat16 grouped GEMMs (the experts in "compute" precision) on MI355X.
 
 Mirrors ``grouped.dot`` and ``grouped.weight_grad``
-(src/bux/architecture/experts/grouped.py:105-161): float32 sums, bfloat16 out, the
+(src/bux/architecture/experts/grouped.py:90-146): float32 sums, bfloat16 out, the
 rows past the groups 0.
 """
 

@@ -14,7 +14,7 @@ Mirrors (src/bux/architecture/experts/):
 - `experts_forward`, `experts_backward`: ``moe.routed`` (moe.py:733-773) into
   ``moe.experts`` (moe.py:799-873) on one device, with ``grouped_blockscaled.
   ragged_dot``'s forward and backward (grouped_blockscaled.py:92-211) for each GEMM in
-  MXFP8, or ``grouped.ragged_dot`` (grouped.py:57-102) in "compute" (bfloat16).
+  MXFP8, or ``grouped.ragged_dot`` (grouped.py:42-102) in "compute" (bfloat16).
 
 Every op enqueues HIP kernels of ``libbux_amd.so`` on the current stream; torch only
 allocates the buffers.

@@ -152,10 +152,10 @@ int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a_scales,
  * a-10. bfloat16 grouped GEMMs (the experts in "compute" precision).
  *
  * bux_bf16_grouped_rows replaces grouped.dot / jax.lax.ragged_dot
- * (src/bux/architecture/experts/grouped.py:105-117): y[i] = x[i] w[g(i)], float32
+ * (src/bux/architecture/experts/grouped.py:90-102): y[i] = x[i] w[g(i)], float32
  * sums, bfloat16 out, rows past sum(sizes) 0. x bfloat16 [m, k]; w bfloat16
  * [groups, k, n] (w_transposed 0) or [groups, n, k] (1: y[i] = x[i] w[g]^T, the dgrad).
- * bux_bf16_grouped_contract replaces grouped.weight_grad (grouped.py:120-161):
+ * bux_bf16_grouped_contract replaces grouped.weight_grad (grouped.py:105-146):
  * dw[g] = x[rows of g]^T dy[rows of g], x [m, k], dy [m, n] -> dw [groups, k, n].
  */
 int bux_bf16_grouped_rows(const uint16_t* x, const uint16_t* w, int w_transposed,

@@ -9,7 +9,7 @@ Follows (all paths under ``src/bux/architecture/``):
 - `tiles_of`: ``experts/grouped_mxfp8.py:157-182``;
 - `rows_mx`, `contract_mx`: ``experts/grouped_blockscaled.py:220-250`` (XLA's
   dequantize, then ``ragged_dot`` / ``ragged_dot_general`` in float32);
-- `ragged_dot_bf16`, `weight_grad_bf16`: ``experts/grouped.py:42-76,105-161`` off a
+- `ragged_dot_bf16`, `weight_grad_bf16`: ``experts/grouped.py:42-146`` off a
   GPU (``jax.lax.ragged_dot`` of bfloat16, float32 sums);
 - `activate`, `weighted_units`, `weighted_units_backward`: ``layers/mlp.py:20-35``,
   ``common/functional.py:12-40``, ``experts/moe.py:898-926``;
@@ -161,7 +161,7 @@ def contract_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16") -> n
 
 def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
     """Return ``jax.lax.ragged_dot`` of bfloat16 x (m, k) and w (g, k, n): float32
-    sums rounded to bfloat16, rows past the groups 0 (grouped.py:42-60,105-117)."""
+    sums rounded to bfloat16, rows past the groups 0 (grouped.py:42-62,90-102)."""
     xf, wf = bf16.to_f32(x), bf16.to_f32(w)
     y = np.zeros((xf.shape[0], wf.shape[2]), np.float32)
     start = 0
@@ -173,7 +173,7 @@ def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = 
 
 
 def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
-    """Return x^T dy per group (grouped.py:120-161), float32 sums."""
+    """Return x^T dy per group (grouped.py:105-146), float32 sums."""
     xf, gf = bf16.to_f32(x), bf16.to_f32(dy)
     sizes = np.asarray(sizes).tolist()
     dw = np.zeros((len(sizes), xf.shape[1], gf.shape[1]), np.float32)
