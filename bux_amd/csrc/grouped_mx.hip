@@ -97,7 +97,8 @@ __device__ int32_t block_scan(int32_t* data, int n, int32_t* partial) {
 // starts[g] for g <= groups (starts[groups] = sum of sizes), then, if `tiles`, the
 // tile list of `slots` entries: each group's rows in tiles of BM from its first row
 // (the last one partial), then the rows from the sum of sizes to `height` as group
-// `groups`, then empty tiles (0, 0, 0).
+// `groups`, then empty tiles (0, 0, 0); and the number of tiles listed in
+// starts[groups + 1].
 __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __restrict__ sizes,
                                                            int32_t groups, int64_t height,
                                                            int64_t slots,
@@ -137,6 +138,7 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
     }
   }
   for (int64_t i = used + t; i < slots; i += THREADS) tiles[i] = Tile{0, 0, 0};
+  if (t == 0) starts_out[groups + 1] = used < slots ? used : static_cast<int32_t>(slots);
 }
 
 // --- the mainloop --------------------------------------------------------------------
@@ -204,10 +206,13 @@ __device__ __forceinline__ void load_lds4(i32x4 rsrc, uint32_t lds, int voffset,
 // over the operand, and each lane's byte offsets in them: 4 instructions of 16 rows x
 // 64 bytes (each 1 KiB in one run; a lane takes the 16-byte chunk that belongs in its
 // swizzled place) and one of the scale words of 64 rows. Rows past the operand read
-// whatever follows (0 past its end); their outputs are never stored.
+// whatever follows (0 past its end); their outputs are never stored. The 4 slices of a
+// wave are 1 KiB apart in both places (the swizzle of a row, (row / 4) % 4, is the
+// same for row r and r + 16), so one lane offset serves them, the scalar offset adding
+// 0, 1, 2 or 3 KiB.
 struct Loads {
   i32x4 values, scales;
-  int voff[4];
+  int voff;
   int soff;
   int chunk_stride;  // bytes from one 64-byte K chunk of the rows to the next
   int word_stride;   // bytes from one 128-byte K chunk's scale words to the next
@@ -218,11 +223,8 @@ __device__ __forceinline__ Loads loads_for(const Operand& op, int64_t row0) {
   Loads ld;
   ld.values = resource(op.values, op.k * op.rows);
   ld.scales = resource(op.scales, op.k / 32 * op.rows);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (w * 4 + i) * 16 + (l >> 2);
-    ld.voff[i] = static_cast<int>((row0 + r) * 64 + 16 * ((l & 3) ^ swizzle(r)));
-  }
+  const int r = w * 64 + (l >> 2);
+  ld.voff = static_cast<int>((row0 + r) * 64 + 16 * ((l & 3) ^ swizzle(r)));
   ld.soff = static_cast<int>((row0 + w * 64 + l) * 4);
   ld.chunk_stride = static_cast<int>(op.rows * 64);
   ld.word_stride = static_cast<int>(op.rows * 4);
@@ -232,17 +234,19 @@ __device__ __forceinline__ Loads loads_for(const Operand& op, int64_t row0) {
 // Direct load number q (0..9) of K step ks into stage `st`: q < 8 a 16-row slice of A's
 // (even q) or B's (odd q) tile, 8 and 9 the scale words of A's and B's 64 rows of this
 // wave.
+template <int Q>
 __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int64_t ks, Lds& lds,
-                                          int st, int q) {
+                                          int st) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kstep = static_cast<int>(ks);
-  if (q < 8) {
-    const int i = q >> 1, r0 = (w * 4 + i) * 16;
-    if ((q & 1) == 0)
-      load_lds16(la.values, lds_at(&lds.a[st][r0 * BK]), la.voff[i], kstep * la.chunk_stride);
+  if (Q < 8) {
+    constexpr int i = Q >> 1;
+    const int r0 = w * 64 + i * 16;
+    if ((Q & 1) == 0)
+      load_lds16(la.values, lds_at(&lds.a[st][r0 * BK]), la.voff, kstep * la.chunk_stride + i * 1024);
     else
-      load_lds16(lb.values, lds_at(&lds.b[st][r0 * BK]), lb.voff[i], kstep * lb.chunk_stride);
-  } else if (q == 8) {
+      load_lds16(lb.values, lds_at(&lds.b[st][r0 * BK]), lb.voff, kstep * lb.chunk_stride + i * 1024);
+  } else if (Q == 8) {
     load_lds4(la.scales, lds_at(&lds.as[st][w * 64]), la.soff, (kstep >> 1) * la.word_stride);
   } else {
     load_lds4(lb.scales, lds_at(&lds.bs[st][w * 64]), lb.soff, (kstep >> 1) * lb.word_stride);
@@ -252,8 +256,16 @@ __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int6
 // All the direct loads of K step ks into stage `st`.
 __device__ __forceinline__ void issue(const Loads& la, const Loads& lb, int64_t ks, Lds& lds,
                                       int st) {
-#pragma unroll
-  for (int q = 0; q < LOADS_A_STEP; ++q) issue_one(la, lb, ks, lds, st, q);
+  issue_one<0>(la, lb, ks, lds, st);
+  issue_one<1>(la, lb, ks, lds, st);
+  issue_one<2>(la, lb, ks, lds, st);
+  issue_one<3>(la, lb, ks, lds, st);
+  issue_one<4>(la, lb, ks, lds, st);
+  issue_one<5>(la, lb, ks, lds, st);
+  issue_one<6>(la, lb, ks, lds, st);
+  issue_one<7>(la, lb, ks, lds, st);
+  issue_one<8>(la, lb, ks, lds, st);
+  issue_one<9>(la, lb, ks, lds, st);
 }
 
 // The workgroup barrier of the pipeline: this wave's LDS reads and writes are done,
@@ -319,30 +331,80 @@ __device__ __forceinline__ v8i operand(const uint8_t* tile, int row, int half) {
   return v;
 }
 
-// Part p (0..3) of a wave's operands of step ks from stage `st`: A's and B's 32-row
-// block p and their scales.
-__device__ __forceinline__ void read_part(Frag& f, const Lds& lds, int st, int64_t ks, int p) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1, half = lane >> 5;
+// Block p (0..3) of 32 rows of A's (B's) part of a wave's operands of step ks from
+// stage `st`, and its scales. The scale bytes are read one byte each (ds_read_u8), so
+// no instruction touches them before the MFMAs that take them: a read whose value is
+// used at once exposes the LDS latency to the whole wave.
+__device__ __forceinline__ void read_a(Frag& f, const Lds& lds, int st, int64_t ks, int p) {
+  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1, half = lane >> 5;
   // The step's two blocks are bytes 2 (ks % 2) and 2 (ks % 2) + 1 of the scale word;
   // lane half h scales block h.
-  const int shift = 8 * ((static_cast<int>(ks & 1) << 1) + half);
-  const int ra = wm * 128 + p * 32 + (lane & 31), rb = wn * 128 + p * 32 + (lane & 31);
-  f.a[p] = operand(lds.a[st], ra, half);
-  f.b[p] = operand(lds.b[st], rb, half);
-  f.sa[p] = static_cast<int>((lds.as[st][ra] >> shift) & 0xffu);
-  f.sb[p] = static_cast<int>((lds.bs[st][rb] >> shift) & 0xffu);
+  const int byte = (static_cast<int>(ks & 1) << 1) + half;
+  const int r = wm * 128 + p * 32 + (lane & 31);
+  f.a[p] = operand(lds.a[st], r, half);
+  f.sa[p] = reinterpret_cast<const uint8_t*>(lds.as[st])[r * 4 + byte];
+}
+__device__ __forceinline__ void read_b(Frag& f, const Lds& lds, int st, int64_t ks, int p) {
+  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1, half = lane >> 5;
+  const int byte = (static_cast<int>(ks & 1) << 1) + half;
+  const int r = wn * 128 + p * 32 + (lane & 31);
+  f.b[p] = operand(lds.b[st], r, half);
+  f.sb[p] = reinterpret_cast<const uint8_t*>(lds.bs[st])[r * 4 + byte];
 }
 
 __device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, int st, int64_t ks) {
 #pragma unroll
-  for (int p = 0; p < 4; ++p) read_part(f, lds, st, ks, p);
+  for (int p = 0; p < 4; ++p) {
+    read_a(f, lds, st, ks, p);
+    read_b(f, lds, st, ks, p);
+  }
+}
+
+// The 16 MFMAs of one step on `cur`, MFMA q taking A's block q / 4 and B's block q % 4,
+// each after a slice of the memory work: with LOAD, one of the next loads (step
+// ks_load into stage st_load) before each of the first 10; with READ, the next step's
+// blocks into `nxt` in the order its MFMAs take them (a0 b0, b1, b2, b3, then a1, a2,
+// a3 four MFMAs apart), so that each lands a dozen MFMAs before its first use.
+template <bool LOAD, bool READ>
+__device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la, const Loads& lb,
+                                     Lds& lds, int64_t ks_load, int st_load, int64_t ks_next,
+                                     int st_next, v16f acc[4][4]) {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int i = q >> 2, j = q & 3;
+    if (LOAD) {
+      switch (q) {
+        case 0: issue_one<0>(la, lb, ks_load, lds, st_load); break;
+        case 1: issue_one<1>(la, lb, ks_load, lds, st_load); break;
+        case 2: issue_one<2>(la, lb, ks_load, lds, st_load); break;
+        case 3: issue_one<3>(la, lb, ks_load, lds, st_load); break;
+        case 4: issue_one<4>(la, lb, ks_load, lds, st_load); break;
+        case 5: issue_one<5>(la, lb, ks_load, lds, st_load); break;
+        case 6: issue_one<6>(la, lb, ks_load, lds, st_load); break;
+        case 7: issue_one<7>(la, lb, ks_load, lds, st_load); break;
+        case 8: issue_one<8>(la, lb, ks_load, lds, st_load); break;
+        case 9: issue_one<9>(la, lb, ks_load, lds, st_load); break;
+        default: break;
+      }
+    }
+    if (READ) {
+      if (q == 0) read_a(nxt, lds, st_next, ks_next, 0);
+      if (q < 4) read_b(nxt, lds, st_next, ks_next, q);
+      if (q == 4 || q == 8 || q == 12) read_a(nxt, lds, st_next, ks_next, q >> 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.b[j], cur.a[i], acc[i][j], 0,
+                                                               0, 0, cur.sb[j], 0, cur.sa[i]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // acc += A[a_row0 + r] . B[b_row0 + c] over K steps [ks_begin, ks_end) of 64 bytes;
 // with `mask`, A's bytes of K outside [mlo, mhi) count as 0 (in the first and last
 // steps). Step k: wait for this wave's loads of step k + 1 and pass the barrier; then
-// the 16 MFMAs of step k on `cur`, each after a slice of the memory work.
+// the 16 MFMAs of step k on `cur`, each after a slice of the memory work. The steady
+// loop (every step with a load 4 steps ahead) has no branches in it; the last 4 steps
+// follow.
 __device__ __forceinline__ void mainloop(const Operand& A, int64_t a_row0, const Operand& B,
                                          int64_t b_row0, int64_t ks_begin, int64_t ks_end,
                                          bool mask, int64_t mlo, int64_t mhi, Lds& lds,
@@ -360,32 +422,42 @@ __device__ __forceinline__ void mainloop(const Operand& A, int64_t a_row0, const
   }
   Frag cur, nxt;
   read_frag(cur, lds, 0, ks_begin);
-  for (int64_t k = 0; k < n; ++k) {
-    const bool more = k + 1 < n, load = k + 4 < n;
-    if (more) {
-      const int64_t later = n - 2 - k;
-      wait_loads(later < 2 ? later : 2);
-    }
+  int64_t k = 0;
+  // Steps with a load 4 ahead, two at a time so that the operand sets swap roles
+  // without a copy; step k + 1 < n - 1 is never an edge here.
+  for (; k + 5 < n; k += 2) {
+    wait_loads(2);
     // Step k + 1's stage is whole; every wave has read step k's, which step k + 4's
     // loads take.
     barrier_lds();
-    if (more && edge(k + 1)) {
+    step<true, true>(cur, nxt, la, lb, lds, ks_begin + k + 4, static_cast<int>(k % STAGES),
+                     ks_begin + k + 1, static_cast<int>((k + 1) % STAGES), acc);
+    wait_loads(2);
+    barrier_lds();
+    step<true, true>(nxt, cur, la, lb, lds, ks_begin + k + 5, static_cast<int>((k + 1) % STAGES),
+                     ks_begin + k + 2, static_cast<int>((k + 2) % STAGES), acc);
+  }
+  for (; k + 4 < n; ++k) {
+    wait_loads(2);
+    barrier_lds();
+    step<true, true>(cur, nxt, la, lb, lds, ks_begin + k + 4, static_cast<int>(k % STAGES),
+                     ks_begin + k + 1, static_cast<int>((k + 1) % STAGES), acc);
+    cur = nxt;
+  }
+  for (; k + 1 < n; ++k) {
+    const int64_t later = n - 2 - k;
+    wait_loads(later < 2 ? later : 2);
+    barrier_lds();
+    if (edge(k + 1)) {
       mask_stage(lds, static_cast<int>((k + 1) % STAGES), ks_begin + k + 1, mlo, mhi);
       barrier_lds();
     }
-    const int st_next = static_cast<int>((k + 1) % STAGES), st_load = static_cast<int>(k % STAGES);
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int i = q >> 2, j = q & 3;
-      if (load && q < LOADS_A_STEP) issue_one(la, lb, ks_begin + k + 4, lds, st_load, q);
-      if (more && j == 0) read_part(nxt, lds, st_next, ks_begin + k + 1, i);
-      __builtin_amdgcn_sched_barrier(0);
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.b[j], cur.a[i], acc[i][j], 0,
-                                                                 0, 0, cur.sb[j], 0, cur.sa[i]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    step<false, true>(cur, nxt, la, lb, lds, 0, 0, ks_begin + k + 1,
+                      static_cast<int>((k + 1) % STAGES), acc);
     cur = nxt;
   }
+  // The last step: its operands are in registers already.
+  step<false, false>(cur, nxt, la, lb, lds, 0, 0, 0, 0, acc);
   // Every wave is done with every stage before the LDS is used again.
   __syncthreads();
 }
@@ -479,12 +551,17 @@ __device__ void store_zeros(T* out, int64_t ld, int64_t row_lo, int64_t row_hi, 
   }
 }
 
-// The workgroup's tile in a grid renumbered so that XCD x (workgroup id % 8) takes the
-// contiguous tiles [x per, (x + 1) per); -1 past the tiles.
-__device__ __forceinline__ int64_t xcd_tile(int64_t total) {
-  const int64_t per = (total + 7) / 8;
-  const int64_t logical = static_cast<int64_t>(blockIdx.x % 8) * per + blockIdx.x / 8;
-  return logical < total ? logical : -1;
+// The tiles a workgroup of a persistent grid takes, of `count`: XCD x (workgroup id % 8)
+// takes the contiguous tiles [x per, (x + 1) per), its workgroups one after another, so
+// that the XCD's CUs work on neighbouring tiles at any time (they share A's rows and a
+// group's B in the XCD's L2).
+struct Turns {
+  int64_t first, end, stride;
+};
+__device__ __forceinline__ Turns turns(int64_t count) {
+  const int64_t per = (count + 7) / 8, xcd = blockIdx.x % 8;
+  const int64_t lo = xcd * per, hi = lo + per < count ? lo + per : count;
+  return Turns{lo + blockIdx.x / 8, hi, gridDim.x / 8};
 }
 
 __device__ __forceinline__ void zero_acc(v16f acc[4][4]) {
@@ -496,52 +573,60 @@ __device__ __forceinline__ void zero_acc(v16f acc[4][4]) {
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 }
 
+// One workgroup a CU, each looping over its tiles. A tile's epilogue stores are not
+// waited for: they drain while the next tile's first loads are in flight.
 template <typename T>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_kernel(
-    Operand A, Operand B, int32_t groups, int64_t n, int64_t height, const Tile* __restrict__ tiles,
-    int64_t col_tiles, int64_t total, T* __restrict__ y) {
+    Operand A, Operand B, int32_t groups, int64_t n, int64_t height, const int32_t* __restrict__ starts,
+    const Tile* __restrict__ tiles, int64_t col_tiles, T* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t smem[];
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const int64_t id = xcd_tile(total);
-  if (id < 0) return;
-  const int64_t col0 = (id % col_tiles) * BN;
-  Tile tile = tiles[id / col_tiles];
-  // Rows of y stop at height whatever the sizes say.
-  if (tile.hi > height) tile.hi = static_cast<int32_t>(height);
-  if (tile.lo >= tile.hi) return;
-  if (tile.group >= groups) {  // rows past the groups
-    store_zeros(y, n, tile.lo, tile.hi, col0, n);
-    return;
+  const Turns mine = turns(static_cast<int64_t>(starts[groups + 1]) * col_tiles);
+  for (int64_t id = mine.first; id < mine.end; id += mine.stride) {
+    const int64_t col0 = (id % col_tiles) * BN;
+    Tile tile = tiles[id / col_tiles];
+    // Rows of y stop at height whatever the sizes say.
+    if (tile.hi > height) tile.hi = static_cast<int32_t>(height);
+    if (tile.lo >= tile.hi) continue;
+    if (tile.group >= groups) {  // rows past the groups
+      store_zeros(y, n, tile.lo, tile.hi, col0, n);
+      continue;
+    }
+    Operand b = B;
+    b.values += static_cast<int64_t>(tile.group) * B.rows * B.k;
+    b.scales += static_cast<int64_t>(tile.group) * B.rows * (B.k / 32);
+    v16f acc[4][4];
+    zero_acc(acc);
+    mainloop(A, tile.lo, b, col0, 0, A.k / BK, false, 0, 0, lds, acc);
+    store_tile(acc, y, n, tile.lo, col0, tile.lo, tile.hi, n, lds);
+    // Every wave is done with the LDS the epilogue staged through before the next
+    // tile's loads land there.
+    barrier_lds();
   }
-  Operand b = B;
-  b.values += static_cast<int64_t>(tile.group) * B.rows * B.k;
-  b.scales += static_cast<int64_t>(tile.group) * B.rows * (B.k / 32);
-  v16f acc[4][4];
-  zero_acc(acc);
-  mainloop(A, tile.lo, b, col0, 0, A.k / BK, false, 0, 0, lds, acc);
-  store_tile(acc, y, n, tile.lo, col0, tile.lo, tile.hi, n, lds);
 }
 
 template <typename T>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void contract_kernel(
     Operand A, Operand B, int32_t groups, const int32_t* __restrict__ starts, int64_t d_tiles,
-    int64_t f_tiles, int64_t total, T* __restrict__ dw) {
+    int64_t f_tiles, T* __restrict__ dw) {
   extern __shared__ __align__(16) uint8_t smem[];
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const int64_t id = xcd_tile(total);
-  if (id < 0) return;
   const int64_t per_group = d_tiles * f_tiles;
-  const int64_t g = id / per_group, rest = id % per_group;
-  const int64_t row0 = (rest / f_tiles) * BM, col0 = (rest % f_tiles) * BN;
-  const int64_t start = starts[g], end = starts[g + 1];
-  v16f acc[4][4];
-  zero_acc(acc);
-  if (end > start) {
-    const int64_t ks_begin = start / BK, ks_end = (end + BK - 1) / BK;
-    const bool ragged = (start % BK) != 0 || (end % BK) != 0;
-    mainloop(A, row0, B, col0, ks_begin, ks_end, ragged, start, end, lds, acc);
+  const Turns mine = turns(static_cast<int64_t>(groups) * per_group);
+  for (int64_t id = mine.first; id < mine.end; id += mine.stride) {
+    const int64_t g = id / per_group, rest = id % per_group;
+    const int64_t row0 = (rest / f_tiles) * BM, col0 = (rest % f_tiles) * BN;
+    const int64_t start = starts[g], end = starts[g + 1];
+    v16f acc[4][4];
+    zero_acc(acc);
+    if (end > start) {
+      const int64_t ks_begin = start / BK, ks_end = (end + BK - 1) / BK;
+      const bool ragged = (start % BK) != 0 || (end % BK) != 0;
+      mainloop(A, row0, B, col0, ks_begin, ks_end, ragged, start, end, lds, acc);
+    }
+    store_tile(acc, dw + g * A.rows * B.rows, B.rows, row0, col0, row0, A.rows, B.rows, lds);
+    barrier_lds();
   }
-  store_tile(acc, dw + g * A.rows * B.rows, B.rows, row0, col0, row0, A.rows, B.rows, lds);
 }
 
 // Lets a kernel take sizeof(Lds) (over 64 KiB) of dynamic LDS; gfx950 has 160 KiB a CU.
@@ -560,17 +645,28 @@ int64_t row_slots(int32_t groups, int64_t m, int64_t height) {
   return ceil_div(rows, BM) + groups + 1;
 }
 
+// The persistent grid: one workgroup a CU of the current device (a multiple of 8, one
+// share a XCD), or fewer for fewer tiles.
+int grid_for(int64_t tiles, unsigned* blocks) {
+  int device = 0, cus = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  if (err != hipSuccess) return fail(BUX_E_DEVICE, "the device's compute units: %s", hipGetErrorString(err));
+  const int64_t most = cus >= 8 ? cus / 8 * 8 : 8;
+  const int64_t want = 8 * ceil_div(tiles > 0 ? tiles : 1, 8);
+  *blocks = static_cast<unsigned>(want < most ? want : most);
+  return BUX_OK;
+}
+
 template <typename T>
 int launch_rows(const Operand& A, const Operand& B, int32_t groups, int64_t n, int64_t height,
-                const Tile* tiles, int64_t slots, void* y, hipStream_t s) {
+                const int32_t* starts, const Tile* tiles, int64_t slots, void* y, hipStream_t s) {
   const int64_t col_tiles = ceil_div(n, BN);
-  const int64_t total = slots * col_tiles;
-  const int64_t blocks = 8 * ceil_div(total, 8);
-  if (blocks >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_rows: too many tiles");
+  unsigned blocks = 0;
+  if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
   if (int rc = allow_lds(rows_kernel<T>, "rows_kernel")) return rc;
-  hipLaunchKernelGGL(rows_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(THREADS),
-                     sizeof(Lds), s, A, B, groups, n, height, tiles, col_tiles, total,
-                     static_cast<T*>(y));
+  hipLaunchKernelGGL(rows_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups, n,
+                     height, starts, tiles, col_tiles, static_cast<T*>(y));
   return launched("rows_kernel");
 }
 
@@ -578,13 +674,11 @@ template <typename T>
 int launch_contract(const Operand& A, const Operand& B, int32_t groups, const int32_t* starts,
                     void* dw, hipStream_t s) {
   const int64_t d_tiles = ceil_div(A.rows, BM), f_tiles = ceil_div(B.rows, BN);
-  const int64_t total = static_cast<int64_t>(groups) * d_tiles * f_tiles;
-  const int64_t blocks = 8 * ceil_div(total, 8);
-  if (blocks >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_contract: too many tiles");
+  unsigned blocks = 0;
+  if (int rc = grid_for(static_cast<int64_t>(groups) * d_tiles * f_tiles, &blocks)) return rc;
   if (int rc = allow_lds(contract_kernel<T>, "contract_kernel")) return rc;
-  hipLaunchKernelGGL(contract_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(THREADS),
-                     sizeof(Lds), s, A, B, groups, starts, d_tiles, f_tiles, total,
-                     static_cast<T*>(dw));
+  hipLaunchKernelGGL(contract_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+                     starts, d_tiles, f_tiles, static_cast<T*>(dw));
   return launched("contract_kernel");
 }
 
@@ -599,7 +693,7 @@ bool offsets_fit(int64_t rows, int64_t k) { return (rows + BM) * k < (1LL << 31)
 
 extern "C" size_t bux_mx_grouped_rows_workspace_size(int32_t groups, int64_t m, int64_t height) {
   using namespace bux;
-  return align256(static_cast<size_t>(groups + 1) * sizeof(int32_t)) +
+  return align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)) +
          static_cast<size_t>(row_slots(groups, m, height)) * sizeof(Tile);
 }
 
@@ -633,7 +727,7 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
   hipStream_t s = as_stream(stream);
   int32_t* starts = static_cast<int32_t*>(workspace);
   Tile* tiles = reinterpret_cast<Tile*>(static_cast<uint8_t*>(workspace) +
-                                        align256(static_cast<size_t>(groups + 1) * sizeof(int32_t)));
+                                        align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)));
   const int64_t slots = row_slots(groups, m, height);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
                      starts, tiles);
@@ -642,8 +736,9 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
   // following K chunk's rows: a's m must cover every row the groups hold.
   const Operand A{a_values, a_scales, k, m};
   const Operand B{b_values, b_scales, k, n};
-  return out_dtype == BUX_BF16 ? launch_rows<uint16_t>(A, B, groups, n, height, tiles, slots, y, s)
-                               : launch_rows<float>(A, B, groups, n, height, tiles, slots, y, s);
+  return out_dtype == BUX_BF16
+             ? launch_rows<uint16_t>(A, B, groups, n, height, starts, tiles, slots, y, s)
+             : launch_rows<float>(A, B, groups, n, height, starts, tiles, slots, y, s);
 }
 
 extern "C" size_t bux_mx_grouped_contract_workspace_size(int32_t groups) {
