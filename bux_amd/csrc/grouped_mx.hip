@@ -145,11 +145,13 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
 
 // An operand in the tiled layout: row r's byte k at values[((k / 64) rows + r) 64 +
 // k % 64], the scale byte of its block b (of 32) at scales[((b / 4) rows + r) 4 + b % 4].
+// Sizes are 32-bit: the host checks that an operand's bytes fit (and the kernels'
+// buffer offsets with them).
 struct Operand {
   const uint8_t* values;
   const uint8_t* scales;
-  int64_t k;     // bytes of K a row: whole 128s
-  int64_t rows;  // rows there are
+  int32_t k;     // bytes of K a row: whole 128s
+  int32_t rows;  // rows there are
 };
 
 struct Lds {
@@ -163,7 +165,8 @@ struct Lds {
 // ds_read_b128 16 lanes at a time over 64 banks of 4 bytes; those 16 lanes read one
 // chunk of 16 consecutive rows. Rows r .. r + 3 lie 64 bytes apart and (r / 4) % 4
 // spreads each such four over the 4 chunk places: 16 places of 16 bytes in 256, every
-// bank once.
+// bank once. Rows 16 apart share a swizzle, so blocks of 16 or 32 rows are copies of
+// one another at fixed offsets.
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 
 // A raw buffer resource (stride 0) over `bytes` bytes from `base`; offsets past them
@@ -206,66 +209,74 @@ __device__ __forceinline__ void load_lds4(i32x4 rsrc, uint32_t lds, int voffset,
 // over the operand, and each lane's byte offsets in them: 4 instructions of 16 rows x
 // 64 bytes (each 1 KiB in one run; a lane takes the 16-byte chunk that belongs in its
 // swizzled place) and one of the scale words of 64 rows. Rows past the operand read
-// whatever follows (0 past its end); their outputs are never stored. The 4 slices of a
-// wave are 1 KiB apart in both places (the swizzle of a row, (row / 4) % 4, is the
-// same for row r and r + 16), so one lane offset serves them, the scalar offset adding
-// 0, 1, 2 or 3 KiB.
+// whatever follows (0 past its end); their outputs are never stored. A wave's 4 slices
+// are 1 KiB apart in both places (rows 16 apart share a swizzle), so one lane offset
+// serves them, the scalar offset adding 0, 1, 2 or 3 KiB.
 struct Loads {
   i32x4 values, scales;
-  int voff;
-  int soff;
-  int chunk_stride;  // bytes from one 64-byte K chunk of the rows to the next
-  int word_stride;   // bytes from one 128-byte K chunk's scale words to the next
+  int32_t voff, soff;                 // this lane's
+  int32_t chunk_stride, word_stride;  // bytes from a K chunk (64 / 128 bytes) to the next
 };
 
-__device__ __forceinline__ Loads loads_for(const Operand& op, int64_t row0) {
+__device__ __forceinline__ Loads loads_for(const Operand& op, int32_t row0) {
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   Loads ld;
-  ld.values = resource(op.values, op.k * op.rows);
-  ld.scales = resource(op.scales, op.k / 32 * op.rows);
+  ld.values = resource(op.values, static_cast<int64_t>(op.k) * op.rows);
+  ld.scales = resource(op.scales, static_cast<int64_t>(op.k / 32) * op.rows);
   const int r = w * 64 + (l >> 2);
-  ld.voff = static_cast<int>((row0 + r) * 64 + 16 * ((l & 3) ^ swizzle(r)));
-  ld.soff = static_cast<int>((row0 + w * 64 + l) * 4);
-  ld.chunk_stride = static_cast<int>(op.rows * 64);
-  ld.word_stride = static_cast<int>(op.rows * 4);
+  ld.voff = (row0 + r) * 64 + 16 * ((l & 3) ^ swizzle(r));
+  ld.soff = (row0 + w * 64 + l) * 4;
+  ld.chunk_stride = op.rows * 64;
+  ld.word_stride = op.rows * 4;
   return ld;
 }
 
-// Direct load number q (0..9) of K step ks into stage `st`: q < 8 a 16-row slice of A's
-// (even q) or B's (odd q) tile, 8 and 9 the scale words of A's and B's 64 rows of this
+// The LDS addresses of the parts of stage st, as scalars.
+struct Stage {
+  uint32_t a, b, as, bs;
+};
+__device__ __forceinline__ Stage stage_at(uint32_t lds0, int st) {
+  return Stage{lds0 + static_cast<uint32_t>(offsetof(Lds, a) + st * BM * BK),
+               lds0 + static_cast<uint32_t>(offsetof(Lds, b) + st * BN * BK),
+               lds0 + static_cast<uint32_t>(offsetof(Lds, as) + st * BM * 4),
+               lds0 + static_cast<uint32_t>(offsetof(Lds, bs) + st * BN * 4)};
+}
+
+// Direct load number Q (0..9) of K step ks into stage `st`: Q < 8 a 16-row slice of A's
+// (even Q) or B's (odd Q) tile, 8 and 9 the scale words of A's and B's 64 rows of this
 // wave.
 template <int Q>
-__device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int64_t ks, Lds& lds,
-                                          int st) {
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kstep = static_cast<int>(ks);
+__device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int32_t ks,
+                                          uint32_t lds0, int st) {
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const Stage at = stage_at(lds0, st);
   if (Q < 8) {
     constexpr int i = Q >> 1;
-    const int r0 = w * 64 + i * 16;
+    const uint32_t slice = (w * 4 + i) * 1024;
     if ((Q & 1) == 0)
-      load_lds16(la.values, lds_at(&lds.a[st][r0 * BK]), la.voff, kstep * la.chunk_stride + i * 1024);
+      load_lds16(la.values, at.a + slice, la.voff, ks * la.chunk_stride + i * 1024);
     else
-      load_lds16(lb.values, lds_at(&lds.b[st][r0 * BK]), lb.voff, kstep * lb.chunk_stride + i * 1024);
+      load_lds16(lb.values, at.b + slice, lb.voff, ks * lb.chunk_stride + i * 1024);
   } else if (Q == 8) {
-    load_lds4(la.scales, lds_at(&lds.as[st][w * 64]), la.soff, (kstep >> 1) * la.word_stride);
+    load_lds4(la.scales, at.as + w * 256, la.soff, (ks >> 1) * la.word_stride);
   } else {
-    load_lds4(lb.scales, lds_at(&lds.bs[st][w * 64]), lb.soff, (kstep >> 1) * lb.word_stride);
+    load_lds4(lb.scales, at.bs + w * 256, lb.soff, (ks >> 1) * lb.word_stride);
   }
 }
 
 // All the direct loads of K step ks into stage `st`.
-__device__ __forceinline__ void issue(const Loads& la, const Loads& lb, int64_t ks, Lds& lds,
+__device__ __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks, uint32_t lds0,
                                       int st) {
-  issue_one<0>(la, lb, ks, lds, st);
-  issue_one<1>(la, lb, ks, lds, st);
-  issue_one<2>(la, lb, ks, lds, st);
-  issue_one<3>(la, lb, ks, lds, st);
-  issue_one<4>(la, lb, ks, lds, st);
-  issue_one<5>(la, lb, ks, lds, st);
-  issue_one<6>(la, lb, ks, lds, st);
-  issue_one<7>(la, lb, ks, lds, st);
-  issue_one<8>(la, lb, ks, lds, st);
-  issue_one<9>(la, lb, ks, lds, st);
+  issue_one<0>(la, lb, ks, lds0, st);
+  issue_one<1>(la, lb, ks, lds0, st);
+  issue_one<2>(la, lb, ks, lds0, st);
+  issue_one<3>(la, lb, ks, lds0, st);
+  issue_one<4>(la, lb, ks, lds0, st);
+  issue_one<5>(la, lb, ks, lds0, st);
+  issue_one<6>(la, lb, ks, lds0, st);
+  issue_one<7>(la, lb, ks, lds0, st);
+  issue_one<8>(la, lb, ks, lds0, st);
+  issue_one<9>(la, lb, ks, lds0, st);
 }
 
 // The workgroup barrier of the pipeline: this wave's LDS reads and writes are done,
@@ -276,14 +287,14 @@ __device__ __forceinline__ void barrier_lds() {
 }
 
 // Waits until at most `steps` steps' loads of this wave are in flight.
-__device__ __forceinline__ void wait_loads(int64_t steps) {
+__device__ __forceinline__ void wait_loads(int32_t steps) {
   if (steps >= 3) asm volatile("s_waitcnt vmcnt(30)" ::: "memory");
   else if (steps == 2) asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
   else if (steps == 1) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-__device__ __forceinline__ uint4 zero_outside(uint4 v, int64_t k0, int64_t lo, int64_t hi) {
+__device__ __forceinline__ uint4 zero_outside(uint4 v, int32_t k0, int32_t lo, int32_t hi) {
   if (k0 >= lo && k0 + 16 <= hi) return v;
   if (k0 + 16 <= lo || k0 >= hi) return make_uint4(0, 0, 0, 0);
   uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -292,7 +303,7 @@ __device__ __forceinline__ uint4 zero_outside(uint4 v, int64_t k0, int64_t lo, i
     uint32_t keep = 0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const int64_t k = k0 + 4 * q + b;
+      const int32_t k = k0 + 4 * q + b;
       if (k >= lo && k < hi) keep |= 0xffu << (8 * b);
     }
     w[q] &= keep;
@@ -302,11 +313,11 @@ __device__ __forceinline__ uint4 zero_outside(uint4 v, int64_t k0, int64_t lo, i
 
 // Zeroes A's bytes of K outside [lo, hi) in stage `st`, step ks (a wgrad's edge steps):
 // lane t takes row t.
-__device__ __forceinline__ void mask_stage(Lds& lds, int st, int64_t ks, int64_t lo, int64_t hi) {
+__device__ __forceinline__ void mask_stage(Lds& lds, int st, int32_t ks, int32_t lo, int32_t hi) {
   const int r = threadIdx.x;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const int64_t k0 = ks * BK + 16 * c;
+    const int32_t k0 = ks * BK + 16 * c;
     if (k0 >= lo && k0 + 16 <= hi) continue;
     uint4* at = reinterpret_cast<uint4*>(&lds.a[st][r * BK + ((c ^ swizzle(r)) << 4)]);
     *at = zero_outside(*at, k0, lo, hi);
@@ -319,15 +330,27 @@ struct Frag {
   int sa[4], sb[4];
 };
 
-// 32 bytes of row `row` for lane half `half`: K chunks half and 2 + half of the step,
-// the MFMA's two blocks of 32.
-__device__ __forceinline__ v8i operand(const uint8_t* tile, int row, int half) {
-  const int sw = swizzle(row);
-  const uint4 lo = *reinterpret_cast<const uint4*>(tile + row * BK + ((half ^ sw) << 4));
-  const uint4 hi = *reinterpret_cast<const uint4*>(tile + row * BK + (((2 + half) ^ sw) << 4));
+// This lane's byte offsets in a stage, computed once: its two 16-byte chunks of A's
+// (B's) 32-row block 0 (K chunks h and 2 + h of the step for lane half h, the MFMA's two
+// blocks of 32), and its scale byte of block 0 in an even step. Block p is 2048 bytes
+// further (128 for the scale), an odd step's scale 2 bytes.
+struct Lanes {
+  int32_t a_lo, a_hi, b_lo, b_hi, sa, sb;
+};
+__device__ __forceinline__ Lanes lanes_of() {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, row = lane & 31, sw = swizzle(row);
+  const int ra = (wave >> 1) * 128 + row, rb = (wave & 1) * 128 + row;
+  const int lo = (half ^ sw) << 4, hi = ((2 + half) ^ sw) << 4;
+  return Lanes{ra * BK + lo, ra * BK + hi, rb * BK + lo, rb * BK + hi, ra * 4 + half, rb * 4 + half};
+}
+
+__device__ __forceinline__ v8i chunks(const uint8_t* lo, const uint8_t* hi) {
+  const uint4 x = *reinterpret_cast<const uint4*>(lo);
+  const uint4 y = *reinterpret_cast<const uint4*>(hi);
   v8i v;
-  v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-  v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+  v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
   return v;
 }
 
@@ -335,28 +358,25 @@ __device__ __forceinline__ v8i operand(const uint8_t* tile, int row, int half) {
 // stage `st`, and its scales. The scale bytes are read one byte each (ds_read_u8), so
 // no instruction touches them before the MFMAs that take them: a read whose value is
 // used at once exposes the LDS latency to the whole wave.
-__device__ __forceinline__ void read_a(Frag& f, const Lds& lds, int st, int64_t ks, int p) {
-  const int lane = threadIdx.x & 63, wm = (threadIdx.x >> 6) >> 1, half = lane >> 5;
-  // The step's two blocks are bytes 2 (ks % 2) and 2 (ks % 2) + 1 of the scale word;
-  // lane half h scales block h.
-  const int byte = (static_cast<int>(ks & 1) << 1) + half;
-  const int r = wm * 128 + p * 32 + (lane & 31);
-  f.a[p] = operand(lds.a[st], r, half);
-  f.sa[p] = reinterpret_cast<const uint8_t*>(lds.as[st])[r * 4 + byte];
+__device__ __forceinline__ void read_a(Frag& f, const Lds& lds, const Lanes& ln, int st,
+                                       int32_t ks, int p) {
+  const uint8_t* t = lds.a[st] + p * 2048;
+  f.a[p] = chunks(t + ln.a_lo, t + ln.a_hi);
+  f.sa[p] = (reinterpret_cast<const uint8_t*>(lds.as[st]) + ((ks & 1) << 1) + p * 128)[ln.sa];
 }
-__device__ __forceinline__ void read_b(Frag& f, const Lds& lds, int st, int64_t ks, int p) {
-  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1, half = lane >> 5;
-  const int byte = (static_cast<int>(ks & 1) << 1) + half;
-  const int r = wn * 128 + p * 32 + (lane & 31);
-  f.b[p] = operand(lds.b[st], r, half);
-  f.sb[p] = reinterpret_cast<const uint8_t*>(lds.bs[st])[r * 4 + byte];
+__device__ __forceinline__ void read_b(Frag& f, const Lds& lds, const Lanes& ln, int st,
+                                       int32_t ks, int p) {
+  const uint8_t* t = lds.b[st] + p * 2048;
+  f.b[p] = chunks(t + ln.b_lo, t + ln.b_hi);
+  f.sb[p] = (reinterpret_cast<const uint8_t*>(lds.bs[st]) + ((ks & 1) << 1) + p * 128)[ln.sb];
 }
 
-__device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, int st, int64_t ks) {
+__device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& ln, int st,
+                                          int32_t ks) {
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    read_a(f, lds, st, ks, p);
-    read_b(f, lds, st, ks, p);
+    read_a(f, lds, ln, st, ks, p);
+    read_b(f, lds, ln, st, ks, p);
   }
 }
 
@@ -367,30 +387,31 @@ __device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, int st, int64
 // a3 four MFMAs apart), so that each lands a dozen MFMAs before its first use.
 template <bool LOAD, bool READ>
 __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la, const Loads& lb,
-                                     Lds& lds, int64_t ks_load, int st_load, int64_t ks_next,
-                                     int st_next, v16f acc[4][4]) {
+                                     const Lds& lds, uint32_t lds0, const Lanes& ln,
+                                     int32_t ks_load, int st_load, int32_t ks_next, int st_next,
+                                     v16f acc[4][4]) {
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int i = q >> 2, j = q & 3;
     if (LOAD) {
       switch (q) {
-        case 0: issue_one<0>(la, lb, ks_load, lds, st_load); break;
-        case 1: issue_one<1>(la, lb, ks_load, lds, st_load); break;
-        case 2: issue_one<2>(la, lb, ks_load, lds, st_load); break;
-        case 3: issue_one<3>(la, lb, ks_load, lds, st_load); break;
-        case 4: issue_one<4>(la, lb, ks_load, lds, st_load); break;
-        case 5: issue_one<5>(la, lb, ks_load, lds, st_load); break;
-        case 6: issue_one<6>(la, lb, ks_load, lds, st_load); break;
-        case 7: issue_one<7>(la, lb, ks_load, lds, st_load); break;
-        case 8: issue_one<8>(la, lb, ks_load, lds, st_load); break;
-        case 9: issue_one<9>(la, lb, ks_load, lds, st_load); break;
+        case 0: issue_one<0>(la, lb, ks_load, lds0, st_load); break;
+        case 1: issue_one<1>(la, lb, ks_load, lds0, st_load); break;
+        case 2: issue_one<2>(la, lb, ks_load, lds0, st_load); break;
+        case 3: issue_one<3>(la, lb, ks_load, lds0, st_load); break;
+        case 4: issue_one<4>(la, lb, ks_load, lds0, st_load); break;
+        case 5: issue_one<5>(la, lb, ks_load, lds0, st_load); break;
+        case 6: issue_one<6>(la, lb, ks_load, lds0, st_load); break;
+        case 7: issue_one<7>(la, lb, ks_load, lds0, st_load); break;
+        case 8: issue_one<8>(la, lb, ks_load, lds0, st_load); break;
+        case 9: issue_one<9>(la, lb, ks_load, lds0, st_load); break;
         default: break;
       }
     }
     if (READ) {
-      if (q == 0) read_a(nxt, lds, st_next, ks_next, 0);
-      if (q < 4) read_b(nxt, lds, st_next, ks_next, q);
-      if (q == 4 || q == 8 || q == 12) read_a(nxt, lds, st_next, ks_next, q >> 2);
+      if (q == 0) read_a(nxt, lds, ln, st_next, ks_next, 0);
+      if (q < 4) read_b(nxt, lds, ln, st_next, ks_next, q);
+      if (q == 4 || q == 8 || q == 12) read_a(nxt, lds, ln, st_next, ks_next, q >> 2);
     }
     __builtin_amdgcn_sched_barrier(0);
     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.b[j], cur.a[i], acc[i][j], 0,
@@ -399,21 +420,22 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
   }
 }
 
-// acc += A[a_row0 + r] . B[b_row0 + c] over K steps [ks_begin, ks_end) of 64 bytes;
-// with `mask`, A's bytes of K outside [mlo, mhi) count as 0 (in the first and last
-// steps). Step k: wait for this wave's loads of step k + 1 and pass the barrier; then
-// the 16 MFMAs of step k on `cur`, each after a slice of the memory work. The steady
-// loop (every step with a load 4 steps ahead) has no branches in it; the last 4 steps
-// follow.
-__device__ __forceinline__ void mainloop(const Operand& A, int64_t a_row0, const Operand& B,
-                                         int64_t b_row0, int64_t ks_begin, int64_t ks_end,
-                                         bool mask, int64_t mlo, int64_t mhi, Lds& lds,
-                                         v16f acc[4][4]) {
-  const int64_t n = ks_end - ks_begin;
+// acc += A[a_row0 + r] . B[b_row0 + c] over K steps [ks_begin, ks_begin + n) of 64
+// bytes; with `mask`, A's bytes of K outside [mlo, mhi) count as 0 (in the first and
+// last steps). Step k: wait for this wave's loads of step k + 1 and pass the barrier;
+// then the 16 MFMAs of step k on `cur`, each after a slice of the memory work. The
+// steady loop (every step with a load 4 steps ahead) has no branches in it, and takes
+// two steps a turn so that the operand sets swap roles without a copy; the last 4
+// steps follow.
+__device__ __forceinline__ void mainloop(const Operand& A, int32_t a_row0, const Operand& B,
+                                         int32_t b_row0, int32_t ks_begin, int32_t n, bool mask,
+                                         int32_t mlo, int32_t mhi, Lds& lds, v16f acc[4][4]) {
   if (n <= 0) return;
+  const uint32_t lds0 = lds_at(&lds);
+  const Lanes ln = lanes_of();
   const Loads la = loads_for(A, a_row0), lb = loads_for(B, b_row0);
-  auto edge = [&](int64_t k) { return mask && (k == 0 || k == n - 1); };
-  for (int64_t s = 0; s < STAGES && s < n; ++s) issue(la, lb, ks_begin + s, lds, static_cast<int>(s));
+  auto edge = [&](int32_t k) { return mask && (k == 0 || k == n - 1); };
+  for (int32_t s = 0; s < STAGES && s < n; ++s) issue(la, lb, ks_begin + s, lds0, s);
   wait_loads(n - 1 < 3 ? n - 1 : 3);
   barrier_lds();
   if (edge(0)) {
@@ -421,131 +443,146 @@ __device__ __forceinline__ void mainloop(const Operand& A, int64_t a_row0, const
     barrier_lds();
   }
   Frag cur, nxt;
-  read_frag(cur, lds, 0, ks_begin);
-  int64_t k = 0;
-  // Steps with a load 4 ahead, two at a time so that the operand sets swap roles
-  // without a copy; step k + 1 < n - 1 is never an edge here.
+  read_frag(cur, lds, ln, 0, ks_begin);
+  int32_t k = 0;
+  // Steps with a load 4 ahead; step k + 1 < n - 1 is never an edge here.
   for (; k + 5 < n; k += 2) {
     wait_loads(2);
     // Step k + 1's stage is whole; every wave has read step k's, which step k + 4's
     // loads take.
     barrier_lds();
-    step<true, true>(cur, nxt, la, lb, lds, ks_begin + k + 4, static_cast<int>(k % STAGES),
-                     ks_begin + k + 1, static_cast<int>((k + 1) % STAGES), acc);
+    step<true, true>(cur, nxt, la, lb, lds, lds0, ln, ks_begin + k + 4, k % STAGES,
+                     ks_begin + k + 1, (k + 1) % STAGES, acc);
     wait_loads(2);
     barrier_lds();
-    step<true, true>(nxt, cur, la, lb, lds, ks_begin + k + 5, static_cast<int>((k + 1) % STAGES),
-                     ks_begin + k + 2, static_cast<int>((k + 2) % STAGES), acc);
+    step<true, true>(nxt, cur, la, lb, lds, lds0, ln, ks_begin + k + 5, (k + 1) % STAGES,
+                     ks_begin + k + 2, (k + 2) % STAGES, acc);
   }
   for (; k + 4 < n; ++k) {
     wait_loads(2);
     barrier_lds();
-    step<true, true>(cur, nxt, la, lb, lds, ks_begin + k + 4, static_cast<int>(k % STAGES),
-                     ks_begin + k + 1, static_cast<int>((k + 1) % STAGES), acc);
+    step<true, true>(cur, nxt, la, lb, lds, lds0, ln, ks_begin + k + 4, k % STAGES,
+                     ks_begin + k + 1, (k + 1) % STAGES, acc);
     cur = nxt;
   }
   for (; k + 1 < n; ++k) {
-    const int64_t later = n - 2 - k;
+    const int32_t later = n - 2 - k;
     wait_loads(later < 2 ? later : 2);
     barrier_lds();
     if (edge(k + 1)) {
-      mask_stage(lds, static_cast<int>((k + 1) % STAGES), ks_begin + k + 1, mlo, mhi);
+      mask_stage(lds, (k + 1) % STAGES, ks_begin + k + 1, mlo, mhi);
       barrier_lds();
     }
-    step<false, true>(cur, nxt, la, lb, lds, 0, 0, ks_begin + k + 1,
-                      static_cast<int>((k + 1) % STAGES), acc);
+    step<false, true>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, ks_begin + k + 1, (k + 1) % STAGES,
+                      acc);
     cur = nxt;
   }
   // The last step: its operands are in registers already.
-  step<false, false>(cur, nxt, la, lb, lds, 0, 0, 0, 0, acc);
+  step<false, false>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, 0, 0, acc);
   // Every wave is done with every stage before the LDS is used again.
   __syncthreads();
 }
 
 // --- the epilogue ----------------------------------------------------------------------
 
-// Stores rows [row_lo, row_hi) and columns below n_cols (a multiple of 4) of the tile
-// at (row0, col0) as float32: lane l holds row l % 32 of each 32-row block and, in
-// register run g, columns 8 g + 4 (l / 32) .. + 3 of each 32-column block.
-__device__ void store_f32(const v16f acc[4][4], float* out, int64_t ld, int64_t row0, int64_t col0,
-                          int64_t row_lo, int64_t row_hi, int64_t n_cols) {
+// The epilogues address a tile from its corner (a 64-bit pointer, the same for the
+// workgroup) with 32-bit offsets: rows [0, rows) and columns [0, cols) of it are stored
+// (cols a multiple of 4), at row pitch ld.
+
+// float32: lane l holds row l % 32 of each 32-row block and, in register run g, columns
+// 8 g + 4 (l / 32) .. + 3 of each 32-column block.
+__device__ void store_f32(const v16f acc[4][4], float* tile, int32_t ld, int32_t rows, int32_t cols) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t row = row0 + wm * 128 + i * 32 + (lane & 31);
-    if (row < row_lo || row >= row_hi) continue;
+    const int32_t row = wm * 128 + i * 32 + (lane & 31);
+    if (row >= rows) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int64_t col = col0 + wn * 128 + j * 32 + 8 * g + 4 * (lane >> 5);
+        const int32_t col = wn * 128 + j * 32 + 8 * g + 4 * (lane >> 5);
         const v16f& a = acc[i][j];
-        if (col < n_cols)
-          *reinterpret_cast<float4*>(out + row * ld + col) =
+        if (col < cols)
+          *reinterpret_cast<float4*>(tile + row * ld + col) =
               make_float4(a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
       }
   }
 }
 
-// Stores the tile as bfloat16 through LDS, so that each store instruction writes whole
-// rows: each wave puts its 128 x 128 outputs (32 KiB) in a region of its own, row r's
-// 16 chunks of 16 bytes at chunk ^ (r % 16), then reads them back 16 bytes a lane, 16
-// lanes a row: 4 runs of 256 bytes an instruction.
-__device__ void store_bf16(const v16f acc[4][4], uint16_t* out, int64_t ld, int64_t row0,
-                           int64_t col0, int64_t row_lo, int64_t row_hi, int64_t n_cols, Lds& lds) {
+// bfloat16 through LDS, so that each store instruction writes whole rows: each wave
+// puts its 128 x 128 outputs in a region of its own, rows 272 bytes apart (256 and a
+// pad, so that the 16 lanes that read one row, and rows 4 apart, use different banks;
+// the four regions fill the LDS exactly), then reads them back 16 bytes a lane, 16
+// lanes a row: 4 runs of 256 bytes an instruction. Every LDS address is a lane's base
+// plus a constant.
+constexpr int PITCH = 272;
+static_assert(4 * 128 * PITCH <= sizeof(Lds), "the epilogue's regions fit the LDS");
+
+__device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int32_t rows,
+                           int32_t cols, Lds& lds) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  uint8_t* region = reinterpret_cast<uint8_t*>(&lds) + wave * 128 * 256;
+  uint8_t* region = reinterpret_cast<uint8_t*>(&lds) + wave * 128 * PITCH;
+  // Lane l writes row 32 i + l % 32, its 4 columns of each 8 at byte 8 (l / 32).
+  uint8_t* mine = region + (lane & 31) * PITCH + 8 * (lane >> 5);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = i * 32 + (lane & 31);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int cc = j * 4 + g;  // 16-byte chunk (8 columns) of the wave's 128 columns
         const v16f& a = acc[i][j];
-        *reinterpret_cast<uint2*>(region + r * 256 + ((cc ^ (r & 15)) << 4) + 8 * (lane >> 5)) =
-            make_uint2(pack_bf16x2(a[4 * g], a[4 * g + 1]), pack_bf16x2(a[4 * g + 2], a[4 * g + 3]));
+        // v_cvt_pk_bf16_f32: two floats to two bfloat16, nearest even
+        const bf16x2 lo = __builtin_convertvector((f32x2{a[4 * g], a[4 * g + 1]}), bf16x2);
+        const bf16x2 hi = __builtin_convertvector((f32x2{a[4 * g + 2], a[4 * g + 3]}), bf16x2);
+        *reinterpret_cast<uint2*>(mine + i * 32 * PITCH + (j * 4 + g) * 16) =
+            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
       }
+    // One block of accumulators at a time: hoisting them all would need more registers
+    // than there are.
+    __builtin_amdgcn_sched_barrier(0);
   }
   // The wave reads back only its own region.
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
-#pragma unroll 4
+  const int cc = lane & 15;  // the lane's 16-byte chunk (8 columns) of a row
+  const int32_t col = wn * 128 + 8 * cc;
+  if (col >= cols) return;
+  const uint8_t* from = region + (lane >> 4) * PITCH + cc * 16;
+  uint16_t* out = tile + (wm * 128 + (lane >> 4)) * ld + col;
+#pragma unroll 8
   for (int it = 0; it < 32; ++it) {
-    const int r = it * 4 + (lane >> 4), cc = lane & 15;
-    const uint4 v = *reinterpret_cast<const uint4*>(region + r * 256 + ((cc ^ (r & 15)) << 4));
-    const int64_t row = row0 + wm * 128 + r, col = col0 + wn * 128 + 8 * cc;
-    if (row >= row_lo && row < row_hi && col < n_cols) {
-      if (col + 8 <= n_cols) {
-        *reinterpret_cast<uint4*>(out + row * ld + col) = v;
-      } else {  // n_cols is a multiple of 4: half a chunk
-        *reinterpret_cast<uint2*>(out + row * ld + col) = make_uint2(v.x, v.y);
+    const int r = it * 4 + (lane >> 4);
+    const uint4 v = *reinterpret_cast<const uint4*>(from + it * 4 * PITCH);
+    if (wm * 128 + r < rows) {
+      if (col + 8 <= cols) {
+        *reinterpret_cast<uint4*>(out + it * 4 * ld) = v;
+      } else {  // cols is a multiple of 4: half a chunk
+        *reinterpret_cast<uint2*>(out + it * 4 * ld) = make_uint2(v.x, v.y);
       }
     }
   }
 }
 
-__device__ __forceinline__ void store_tile(const v16f acc[4][4], uint16_t* out, int64_t ld,
-                                           int64_t row0, int64_t col0, int64_t row_lo,
-                                           int64_t row_hi, int64_t n_cols, Lds& lds) {
-  store_bf16(acc, out, ld, row0, col0, row_lo, row_hi, n_cols, lds);
+__device__ __forceinline__ void store_tile(const v16f acc[4][4], uint16_t* tile, int32_t ld,
+                                           int32_t rows, int32_t cols, Lds& lds) {
+  store_bf16(acc, tile, ld, rows, cols, lds);
 }
-__device__ __forceinline__ void store_tile(const v16f acc[4][4], float* out, int64_t ld,
-                                           int64_t row0, int64_t col0, int64_t row_lo,
-                                           int64_t row_hi, int64_t n_cols, Lds&) {
-  store_f32(acc, out, ld, row0, col0, row_lo, row_hi, n_cols);
+__device__ __forceinline__ void store_tile(const v16f acc[4][4], float* tile, int32_t ld,
+                                           int32_t rows, int32_t cols, Lds&) {
+  store_f32(acc, tile, ld, rows, cols);
 }
 
-// Zeroes rows [row_lo, row_hi) of the tile's columns from col0 (n_cols a multiple of 4).
+// Zeroes rows [0, rows) and columns [0, cols) of a tile (cols a multiple of 4).
 template <typename T>
-__device__ void store_zeros(T* out, int64_t ld, int64_t row_lo, int64_t row_hi, int64_t col0,
-                            int64_t n_cols) {
-  const int64_t width = ((col0 + BN < n_cols ? col0 + BN : n_cols) - col0) / 4;
-  for (int64_t i = threadIdx.x; i < (row_hi - row_lo) * width; i += THREADS) {
-    T* at = out + (row_lo + i / width) * ld + col0 + 4 * (i % width);
+__device__ void store_zeros(T* tile, int32_t ld, int32_t rows, int32_t cols) {
+  const int32_t width = cols / 4;
+  for (int32_t i = threadIdx.x; i < rows * width; i += THREADS) {
+    T* at = tile + (i / width) * ld + 4 * (i % width);
     if (sizeof(T) == 2) *reinterpret_cast<uint2*>(at) = make_uint2(0, 0);
     else *reinterpret_cast<uint4*>(at) = make_uint4(0, 0, 0, 0);
   }
@@ -556,12 +593,12 @@ __device__ void store_zeros(T* out, int64_t ld, int64_t row_lo, int64_t row_hi, 
 // that the XCD's CUs work on neighbouring tiles at any time (they share A's rows and a
 // group's B in the XCD's L2).
 struct Turns {
-  int64_t first, end, stride;
+  int32_t first, end, stride;
 };
-__device__ __forceinline__ Turns turns(int64_t count) {
-  const int64_t per = (count + 7) / 8, xcd = blockIdx.x % 8;
-  const int64_t lo = xcd * per, hi = lo + per < count ? lo + per : count;
-  return Turns{lo + blockIdx.x / 8, hi, gridDim.x / 8};
+__device__ __forceinline__ Turns turns(int32_t count) {
+  const int32_t per = (count + 7) / 8, xcd = blockIdx.x % 8;
+  const int32_t lo = xcd * per, hi = lo + per < count ? lo + per : count;
+  return Turns{lo + static_cast<int32_t>(blockIdx.x / 8), hi, static_cast<int32_t>(gridDim.x / 8)};
 }
 
 __device__ __forceinline__ void zero_acc(v16f acc[4][4]) {
@@ -573,23 +610,27 @@ __device__ __forceinline__ void zero_acc(v16f acc[4][4]) {
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 }
 
+__device__ __forceinline__ int32_t smaller(int32_t a, int32_t b) { return a < b ? a : b; }
+
 // One workgroup a CU, each looping over its tiles. A tile's epilogue stores are not
 // waited for: they drain while the next tile's first loads are in flight.
 template <typename T>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_kernel(
-    Operand A, Operand B, int32_t groups, int64_t n, int64_t height, const int32_t* __restrict__ starts,
-    const Tile* __restrict__ tiles, int64_t col_tiles, T* __restrict__ y) {
+    Operand A, Operand B, int32_t groups, int32_t n, int32_t height,
+    const int32_t* __restrict__ starts, const Tile* __restrict__ tiles, int32_t col_tiles,
+    T* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t smem[];
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const Turns mine = turns(static_cast<int64_t>(starts[groups + 1]) * col_tiles);
-  for (int64_t id = mine.first; id < mine.end; id += mine.stride) {
-    const int64_t col0 = (id % col_tiles) * BN;
-    Tile tile = tiles[id / col_tiles];
+  const Turns mine = turns(starts[groups + 1] * col_tiles);
+  for (int32_t id = mine.first; id < mine.end; id += mine.stride) {
+    const int32_t col0 = (id % col_tiles) * BN, cols = smaller(n - col0, BN);
+    const Tile tile = tiles[id / col_tiles];
     // Rows of y stop at height whatever the sizes say.
-    if (tile.hi > height) tile.hi = static_cast<int32_t>(height);
-    if (tile.lo >= tile.hi) continue;
+    const int32_t rows = smaller(tile.hi, height) - tile.lo;
+    if (rows <= 0) continue;
+    T* corner = y + static_cast<int64_t>(tile.lo) * n + col0;
     if (tile.group >= groups) {  // rows past the groups
-      store_zeros(y, n, tile.lo, tile.hi, col0, n);
+      store_zeros(corner, n, rows, cols);
       continue;
     }
     Operand b = B;
@@ -598,7 +639,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
     v16f acc[4][4];
     zero_acc(acc);
     mainloop(A, tile.lo, b, col0, 0, A.k / BK, false, 0, 0, lds, acc);
-    store_tile(acc, y, n, tile.lo, col0, tile.lo, tile.hi, n, lds);
+    store_tile(acc, corner, n, rows, cols, lds);
     // Every wave is done with the LDS the epilogue staged through before the next
     // tile's loads land there.
     barrier_lds();
@@ -607,24 +648,25 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 
 template <typename T>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void contract_kernel(
-    Operand A, Operand B, int32_t groups, const int32_t* __restrict__ starts, int64_t d_tiles,
-    int64_t f_tiles, T* __restrict__ dw) {
+    Operand A, Operand B, int32_t groups, const int32_t* __restrict__ starts, int32_t d_tiles,
+    int32_t f_tiles, T* __restrict__ dw) {
   extern __shared__ __align__(16) uint8_t smem[];
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const int64_t per_group = d_tiles * f_tiles;
-  const Turns mine = turns(static_cast<int64_t>(groups) * per_group);
-  for (int64_t id = mine.first; id < mine.end; id += mine.stride) {
-    const int64_t g = id / per_group, rest = id % per_group;
-    const int64_t row0 = (rest / f_tiles) * BM, col0 = (rest % f_tiles) * BN;
-    const int64_t start = starts[g], end = starts[g + 1];
+  const int32_t per_group = d_tiles * f_tiles;
+  const Turns mine = turns(groups * per_group);
+  for (int32_t id = mine.first; id < mine.end; id += mine.stride) {
+    const int32_t g = id / per_group, rest = id % per_group;
+    const int32_t row0 = (rest / f_tiles) * BM, col0 = (rest % f_tiles) * BN;
+    const int32_t start = starts[g], end = starts[g + 1];
     v16f acc[4][4];
     zero_acc(acc);
     if (end > start) {
-      const int64_t ks_begin = start / BK, ks_end = (end + BK - 1) / BK;
+      const int32_t ks_begin = start / BK, ks_end = (end + BK - 1) / BK;
       const bool ragged = (start % BK) != 0 || (end % BK) != 0;
-      mainloop(A, row0, B, col0, ks_begin, ks_end, ragged, start, end, lds, acc);
+      mainloop(A, row0, B, col0, ks_begin, ks_end - ks_begin, ragged, start, end, lds, acc);
     }
-    store_tile(acc, dw + g * A.rows * B.rows, B.rows, row0, col0, row0, A.rows, B.rows, lds);
+    T* corner = dw + (static_cast<int64_t>(g) * A.rows + row0) * B.rows + col0;
+    store_tile(acc, corner, B.rows, smaller(A.rows - row0, BM), smaller(B.rows - col0, BN), lds);
     barrier_lds();
   }
 }
@@ -662,11 +704,13 @@ template <typename T>
 int launch_rows(const Operand& A, const Operand& B, int32_t groups, int64_t n, int64_t height,
                 const int32_t* starts, const Tile* tiles, int64_t slots, void* y, hipStream_t s) {
   const int64_t col_tiles = ceil_div(n, BN);
+  if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_rows: too many tiles");
   unsigned blocks = 0;
   if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
   if (int rc = allow_lds(rows_kernel<T>, "rows_kernel")) return rc;
-  hipLaunchKernelGGL(rows_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups, n,
-                     height, starts, tiles, col_tiles, static_cast<T*>(y));
+  hipLaunchKernelGGL(rows_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+                     static_cast<int32_t>(n), static_cast<int32_t>(height), starts, tiles,
+                     static_cast<int32_t>(col_tiles), static_cast<T*>(y));
   return launched("rows_kernel");
 }
 
@@ -674,11 +718,14 @@ template <typename T>
 int launch_contract(const Operand& A, const Operand& B, int32_t groups, const int32_t* starts,
                     void* dw, hipStream_t s) {
   const int64_t d_tiles = ceil_div(A.rows, BM), f_tiles = ceil_div(B.rows, BN);
+  const int64_t tiles = static_cast<int64_t>(groups) * d_tiles * f_tiles;
+  if (tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_contract: too many tiles");
   unsigned blocks = 0;
-  if (int rc = grid_for(static_cast<int64_t>(groups) * d_tiles * f_tiles, &blocks)) return rc;
+  if (int rc = grid_for(tiles, &blocks)) return rc;
   if (int rc = allow_lds(contract_kernel<T>, "contract_kernel")) return rc;
   hipLaunchKernelGGL(contract_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
-                     starts, d_tiles, f_tiles, static_cast<T*>(dw));
+                     starts, static_cast<int32_t>(d_tiles), static_cast<int32_t>(f_tiles),
+                     static_cast<T*>(dw));
   return launched("contract_kernel");
 }
 
@@ -734,8 +781,8 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
   if (int rc = launched("prologue_kernel")) return rc;
   // Rows of the groups past a's m rows read 0 (the resource ends there) or the
   // following K chunk's rows: a's m must cover every row the groups hold.
-  const Operand A{a_values, a_scales, k, m};
-  const Operand B{b_values, b_scales, k, n};
+  const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(m)};
+  const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};
   return out_dtype == BUX_BF16
              ? launch_rows<uint16_t>(A, B, groups, n, height, starts, tiles, slots, y, s)
              : launch_rows<float>(A, B, groups, n, height, starts, tiles, slots, y, s);
@@ -775,8 +822,8 @@ extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a
                      nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   // The operands' K is m: each of a's d rows (b's f rows) is m bytes.
-  const Operand A{a_values, a_scales, m, d};
-  const Operand B{b_values, b_scales, m, f};
+  const Operand A{a_values, a_scales, static_cast<int32_t>(m), static_cast<int32_t>(d)};
+  const Operand B{b_values, b_scales, static_cast<int32_t>(m), static_cast<int32_t>(f)};
   return out_dtype == BUX_BF16 ? launch_contract<uint16_t>(A, B, groups, starts, dw, s)
                                : launch_contract<float>(A, B, groups, starts, dw, s);
 }
