@@ -3,16 +3,18 @@
 // argsort of the flat picks with those outside [0, E) as E, bincount, argsort of the
 // order; the offsets cumsum(sizes) - sizes of grouped_mxfp8.py:142).
 //
-// A counting sort in three launches over segments of 256 picks (one wave a segment):
+// A counting sort over segments of 256 picks (one wave a segment):
 //   1. count:   each wave counts its segment's picks per bin (E bins and one for the
 //               picks outside) in LDS; counts[bin][segment] goes to the workspace.
-//   2. scan:    one workgroup scans counts bin-major, exclusively: entry (b, s) becomes
-//               where bin b's picks of segment s start in `order`. The scan's values at
-//               each bin's first segment are the offsets; their differences the sizes.
-//   3. scatter: each wave walks its segment 64 picks at a time, in order. A pick's rank
-//               among the same bin's picks of those 64 comes from ballots over its bin's
-//               bits (the lanes that agree on every bit), and the lowest lane of each
-//               bin moves the bin's running position on by the count: a stable order.
+//   2. rows:    a workgroup a bin scans its row of counts exclusively, in place, and
+//               leaves the bin's total.
+//   3. bases:   one workgroup scans the bins' totals: where each bin starts in `order`
+//               (the offsets; the totals are the sizes).
+//   4. scatter: each wave walks its segment 64 picks at a time, in order, from its
+//               bins' starts (base + row prefix). A pick's rank among the same bin's
+//               picks of those 64 comes from ballots over its bin's bits (the lanes that
+//               agree on every bit), and the lowest lane of each bin moves the bin's
+//               running position on by the count: a stable order.
 // All integer work: bit-exact by construction.
 
 #include "common.h"
@@ -22,7 +24,7 @@ namespace {
 
 constexpr int SEGMENT = 256;  // picks a wave takes
 constexpr int WAVES = 4;      // waves a workgroup
-constexpr int MAX_BINS = 8192;  // experts + 1 the scan's LDS holds offsets for
+constexpr int MAX_BINS = 8192;  // experts + 1 (the LDS of count and scatter limits them further)
 
 __device__ __forceinline__ int bin_of(int32_t expert, int32_t num_experts) {
   return (expert >= 0 && expert < num_experts) ? expert : num_experts;
@@ -51,60 +53,89 @@ __global__ __launch_bounds__(64 * WAVES) void count_kernel(const int32_t* __rest
   }
 }
 
-constexpr int SCAN_THREADS = 1024;
+constexpr int SCAN_THREADS = 256;
 
-__global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(int32_t* __restrict__ counts,
-                                                            int64_t segments, int32_t num_experts,
-                                                            int64_t n, int32_t* __restrict__ sizes,
-                                                            int32_t* __restrict__ offsets) {
-  __shared__ int32_t partial[SCAN_THREADS];
-  __shared__ int32_t starts[MAX_BINS + 1];
-  const int t = threadIdx.x;
-  const int bins = num_experts + 1;
-  const int64_t total = static_cast<int64_t>(bins) * segments;
-  const int64_t per = (total + SCAN_THREADS - 1) / SCAN_THREADS;
-  const int64_t lo = t * per, hi = lo + per < total ? lo + per : total;
-  int32_t sum = 0;
-  for (int64_t i = lo; i < hi; ++i) sum += counts[i];
-  partial[t] = sum;
+// Exclusive scan of one value a thread over the workgroup (SCAN_THREADS lanes), by
+// wave prefix sums and one pass over the waves' totals; returns the workgroup's total.
+__device__ __forceinline__ int32_t block_exclusive(int32_t v, int32_t& prefix, int32_t* wave_sums) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int32_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wave_sums[wave] = x;
   __syncthreads();
-  // Inclusive Hillis-Steele scan of the 1024 partial sums.
-  for (int step = 1; step < SCAN_THREADS; step <<= 1) {
-    const int32_t add = t >= step ? partial[t - step] : 0;
-    __syncthreads();
-    partial[t] += add;
-    __syncthreads();
+  int32_t before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < SCAN_THREADS / 64; ++w) {
+    const int32_t t = wave_sums[w];
+    if (w < wave) before += t;
+    total += t;
   }
-  int32_t run = t > 0 ? partial[t - 1] : 0;
-  for (int64_t i = lo; i < hi; ++i) {
-    const int32_t c = counts[i];
-    counts[i] = run;
-    if (i % segments == 0) starts[i / segments] = run;
-    run += c;
-  }
-  if (segments == 0) {
-    for (int b = t; b < bins; b += SCAN_THREADS) starts[b] = 0;
-  }
-  if (t == 0) starts[bins] = static_cast<int32_t>(n);
   __syncthreads();
-  for (int b = t; b < num_experts; b += SCAN_THREADS) {
-    sizes[b] = starts[b + 1] - starts[b];
-    offsets[b] = starts[b];
+  prefix = before + x - v;
+  return total;
+}
+
+// Workgroup b scans counts[b][0 .. segments) exclusively in place; totals[b] = the sum.
+__global__ __launch_bounds__(SCAN_THREADS) void rows_kernel(int32_t* __restrict__ counts,
+                                                            int64_t segments,
+                                                            int32_t* __restrict__ totals) {
+  __shared__ int32_t wave_sums[SCAN_THREADS / 64];
+  int32_t* row = counts + static_cast<int64_t>(blockIdx.x) * segments;
+  int32_t carry = 0;
+  for (int64_t base = 0; base < segments; base += SCAN_THREADS) {
+    const int64_t i = base + threadIdx.x;
+    const int32_t v = i < segments ? row[i] : 0;
+    int32_t prefix;
+    const int32_t total = block_exclusive(v, prefix, wave_sums);
+    if (i < segments) row[i] = carry + prefix;
+    carry += total;
   }
-  if (t == 0) offsets[num_experts] = starts[num_experts];  // the picks of experts: filled
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+}
+
+// One workgroup: bases[b] = the totals of the bins before b; sizes and offsets of the
+// experts (offsets[E] = the picks of experts: `filled`).
+__global__ __launch_bounds__(SCAN_THREADS) void bases_kernel(const int32_t* __restrict__ totals,
+                                                             int32_t bins,
+                                                             int32_t* __restrict__ bases,
+                                                             int32_t* __restrict__ sizes,
+                                                             int32_t* __restrict__ offsets) {
+  __shared__ int32_t wave_sums[SCAN_THREADS / 64];
+  int32_t carry = 0;
+  for (int32_t base = 0; base < bins; base += SCAN_THREADS) {
+    const int32_t b = base + threadIdx.x;
+    const int32_t v = b < bins ? totals[b] : 0;
+    int32_t prefix;
+    const int32_t total = block_exclusive(v, prefix, wave_sums);
+    if (b < bins) {
+      bases[b] = carry + prefix;
+      if (b < bins - 1) {
+        sizes[b] = v;
+        offsets[b] = carry + prefix;
+      } else {
+        offsets[b] = carry + prefix;  // past the last expert: the sum of their sizes
+      }
+    }
+    carry += total;
+  }
 }
 
 __global__ __launch_bounds__(64 * WAVES) void scatter_kernel(
     const int32_t* __restrict__ idx, int64_t n, int32_t num_experts, int32_t bits,
-    int64_t segments, const int32_t* __restrict__ base, int32_t* __restrict__ order,
-    int32_t* __restrict__ inverse) {
+    int64_t segments, const int32_t* __restrict__ base, const int32_t* __restrict__ bases,
+    int32_t* __restrict__ order, int32_t* __restrict__ inverse) {
   extern __shared__ int32_t lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int bins = num_experts + 1;
   int32_t* running = lds + wave * bins;
   const int64_t seg = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
   if (seg >= segments) return;  // whole waves leave; no workgroup barrier follows
-  for (int b = lane; b < bins; b += 64) running[b] = base[static_cast<int64_t>(b) * segments + seg];
+  for (int b = lane; b < bins; b += 64)
+    running[b] = bases[b] + base[static_cast<int64_t>(b) * segments + seg];
   __builtin_amdgcn_wave_barrier();
   const uint64_t below = (1ull << lane) - 1ull;
   for (int i = 0; i < SEGMENT; i += 64) {
@@ -134,8 +165,9 @@ __global__ __launch_bounds__(64 * WAVES) void scatter_kernel(
 }  // namespace bux
 
 extern "C" size_t bux_moe_permute_workspace_size(int64_t n_picks, int32_t num_experts) {
+  // counts[bins][segments], then the bins' totals and bases
   const int64_t segments = (n_picks + bux::SEGMENT - 1) / bux::SEGMENT;
-  return static_cast<size_t>(segments) * static_cast<size_t>(num_experts + 1) * sizeof(int32_t);
+  return static_cast<size_t>(segments + 2) * static_cast<size_t>(num_experts + 1) * sizeof(int32_t);
 }
 
 extern "C" int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_experts,
@@ -151,7 +183,7 @@ extern "C" int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_
   BUX_CHECK(n_picks == 0 || (idx && order && inverse),
             "bux_moe_permute: idx, order and inverse are needed");
   const size_t need = bux_moe_permute_workspace_size(n_picks, num_experts);
-  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+  if (workspace_bytes < need || workspace == nullptr)
     return fail(BUX_E_WORKSPACE, "bux_moe_permute: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
   const int64_t segments = ceil_div(n_picks, SEGMENT);
@@ -169,12 +201,16 @@ extern "C" int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_
                        num_experts, segments, counts);
     if (int rc = launched("count_kernel")) return rc;
   }
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(SCAN_THREADS), 0, s, counts, segments,
-                     num_experts, n_picks, sizes, offsets);
-  if (int rc = launched("scan_kernel")) return rc;
+  int32_t* totals = counts + segments * bins;
+  int32_t* bases = totals + bins;
+  hipLaunchKernelGGL(rows_kernel, dim3(bins), dim3(SCAN_THREADS), 0, s, counts, segments, totals);
+  if (int rc = launched("rows_kernel")) return rc;
+  hipLaunchKernelGGL(bases_kernel, dim3(1), dim3(SCAN_THREADS), 0, s, totals, bins, bases, sizes,
+                     offsets);
+  if (int rc = launched("bases_kernel")) return rc;
   if (segments > 0) {
     hipLaunchKernelGGL(scatter_kernel, dim3(blocks), dim3(64 * WAVES), lds, s, idx, n_picks,
-                       num_experts, bits, segments, counts, order, inverse);
+                       num_experts, bits, segments, counts, bases, order, inverse);
     if (int rc = launched("scatter_kernel")) return rc;
   }
   return BUX_OK;

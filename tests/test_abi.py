@@ -41,8 +41,9 @@ def test_version(lib):
 
 
 def test_workspace_sizes(lib):
-    assert lib.bux_moe_permute_workspace_size(131072, 128) == 512 * 129 * 4
-    assert lib.bux_moe_permute_workspace_size(0, 8) == 0
+    # counts of each bin in each segment of 256 picks, then the bins' totals and bases
+    assert lib.bux_moe_permute_workspace_size(131072, 128) == (512 + 2) * 129 * 4
+    assert lib.bux_moe_permute_workspace_size(0, 8) == 2 * 9 * 4
     # group starts, then a tile list: tiles of 256 rows, one more a group at most
     assert lib.bux_mx_grouped_rows_workspace_size(128, 131072, 131072) >= (512 + 128) * 12
     assert lib.bux_mx_grouped_contract_workspace_size(128) == 129 * 4
