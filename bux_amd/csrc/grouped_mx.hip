@@ -141,7 +141,7 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
   if (t == 0) starts_out[groups + 1] = used < slots ? used : static_cast<int32_t>(slots);
 }
 
-// --- the mainloop --------------------------------------------------------------------
+// --- the pipeline --------------------------------------------------------------------
 
 // An operand in the tiled layout: row r's byte k at values[((k / 64) rows + r) 64 +
 // k % 64], the scale byte of its block b (of 32) at scales[((b / 4) rows + r) 4 + b % 4].
@@ -154,11 +154,16 @@ struct Operand {
   int32_t rows;  // rows there are
 };
 
+// One K step's operands in LDS: 256 rows of A and of B, 64 bytes each, and their rows'
+// scale words of the 128 bytes of K the step is in.
+struct Stage {
+  uint8_t a[BM * BK];
+  uint8_t b[BN * BK];
+  uint32_t as[BM];
+  uint32_t bs[BN];
+};
 struct Lds {
-  uint8_t a[STAGES][BM * BK];
-  uint8_t b[STAGES][BN * BK];
-  uint32_t as[STAGES][BM];  // each row's scale word of the 128 bytes of K the step is in
-  uint32_t bs[STAGES][BN];
+  Stage st[STAGES];
 };
 
 // Where a 64-byte LDS row's 16-byte chunk c sits: c ^ swizzle(row). gfx950's LDS serves
@@ -194,8 +199,7 @@ __device__ __forceinline__ uint32_t lds_at(const void* p) {
 // soffset land in LDS at M0 + 4 (16) i. Written as inline assembly so that the compiler
 // does not track these loads: left to itself it waits for every load in flight
 // (vmcnt(0)) before any LDS read that might alias their destinations, which undoes the
-// pipeline. The mainloop counts them itself (wait_loads), and nothing else in it
-// touches vector memory.
+// pipeline. The waves count them themselves (wait_loads).
 __device__ __forceinline__ void load_lds16(i32x4 rsrc, uint32_t lds, int voffset, int soffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory", "m0");
@@ -205,13 +209,13 @@ __device__ __forceinline__ void load_lds4(i32x4 rsrc, uint32_t lds, int voffset,
                :: "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory", "m0");
 }
 
-// What a workgroup's lanes load for one operand's 256 rows from `row0` on: resources
-// over the operand, and each lane's byte offsets in them: 4 instructions of 16 rows x
-// 64 bytes (each 1 KiB in one run; a lane takes the 16-byte chunk that belongs in its
-// swizzled place) and one of the scale words of 64 rows. Rows past the operand read
-// whatever follows (0 past its end); their outputs are never stored. A wave's 4 slices
-// are 1 KiB apart in both places (rows 16 apart share a swizzle), so one lane offset
-// serves them, the scalar offset adding 0, 1, 2 or 3 KiB.
+// What a wave w loads of one operand's 256 rows from `row0` on: rows [64 w, 64 w + 64)
+// of the tile, as 4 slices of 16 rows x 64 bytes (each 1 KiB in one run; a lane takes
+// the 16-byte chunk that belongs in its swizzled place) and the scale words of those
+// rows. Slices are 1 KiB apart in memory and in LDS alike (rows 16 apart share a
+// swizzle), so one lane offset serves them all, the scalar offset adding 1 KiB a slice.
+// Rows past the operand read whatever follows (0 past its end); their outputs are never
+// stored.
 struct Loads {
   i32x4 values, scales;
   int32_t voff, soff;                 // this lane's
@@ -231,62 +235,51 @@ __device__ __forceinline__ Loads loads_for(const Operand& op, int32_t row0) {
   return ld;
 }
 
-// The LDS addresses of the parts of stage st, as scalars.
-struct Stage {
-  uint32_t a, b, as, bs;
-};
-__device__ __forceinline__ Stage stage_at(uint32_t lds0, int st) {
-  return Stage{lds0 + static_cast<uint32_t>(offsetof(Lds, a) + st * BM * BK),
-               lds0 + static_cast<uint32_t>(offsetof(Lds, b) + st * BN * BK),
-               lds0 + static_cast<uint32_t>(offsetof(Lds, as) + st * BM * 4),
-               lds0 + static_cast<uint32_t>(offsetof(Lds, bs) + st * BN * 4)};
-}
-
-// Direct load number Q (0..9) of K step ks into stage `st`: Q < 8 a 16-row slice of A's
-// (even Q) or B's (odd Q) tile, 8 and 9 the scale words of A's and B's 64 rows of this
-// wave.
+// Direct load Q (0..9) of K step ks into stage `st`: Q < 8 a 16-row slice of A's (even
+// Q) or B's (odd Q) rows of this wave; 8 and 9 the scale words of its A and B rows.
 template <int Q>
 __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int32_t ks,
                                           uint32_t lds0, int st) {
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const Stage at = stage_at(lds0, st);
+  const uint32_t at = lds0 + static_cast<uint32_t>(st * sizeof(Stage));
   if (Q < 8) {
     constexpr int i = Q >> 1;
-    const uint32_t slice = (w * 4 + i) * 1024;
+    const uint32_t slice = w * 4096 + i * 1024;
     if ((Q & 1) == 0)
-      load_lds16(la.values, at.a + slice, la.voff, ks * la.chunk_stride + i * 1024);
+      load_lds16(la.values, at + offsetof(Stage, a) + slice, la.voff, ks * la.chunk_stride + i * 1024);
     else
-      load_lds16(lb.values, at.b + slice, lb.voff, ks * lb.chunk_stride + i * 1024);
+      load_lds16(lb.values, at + offsetof(Stage, b) + slice, lb.voff, ks * lb.chunk_stride + i * 1024);
   } else if (Q == 8) {
-    load_lds4(la.scales, at.as + w * 256, la.soff, (ks >> 1) * la.word_stride);
+    load_lds4(la.scales, at + offsetof(Stage, as) + w * 256, la.soff, (ks >> 1) * la.word_stride);
   } else {
-    load_lds4(lb.scales, at.bs + w * 256, lb.soff, (ks >> 1) * lb.word_stride);
+    load_lds4(lb.scales, at + offsetof(Stage, bs) + w * 256, lb.soff, (ks >> 1) * lb.word_stride);
   }
 }
 
-// All the direct loads of K step ks into stage `st`.
+template <int Q>
+__device__ __forceinline__ void issue_from(const Loads& la, const Loads& lb, int32_t ks,
+                                           uint32_t lds0, int st) {
+  issue_one<Q>(la, lb, ks, lds0, st);
+  if constexpr (Q + 1 < LOADS_A_STEP) issue_from<Q + 1>(la, lb, ks, lds0, st);
+}
+
+// All of a wave's direct loads of K step ks into stage `st`.
 __device__ __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks, uint32_t lds0,
                                       int st) {
-  issue_one<0>(la, lb, ks, lds0, st);
-  issue_one<1>(la, lb, ks, lds0, st);
-  issue_one<2>(la, lb, ks, lds0, st);
-  issue_one<3>(la, lb, ks, lds0, st);
-  issue_one<4>(la, lb, ks, lds0, st);
-  issue_one<5>(la, lb, ks, lds0, st);
-  issue_one<6>(la, lb, ks, lds0, st);
-  issue_one<7>(la, lb, ks, lds0, st);
-  issue_one<8>(la, lb, ks, lds0, st);
-  issue_one<9>(la, lb, ks, lds0, st);
+  issue_from<0>(la, lb, ks, lds0, st);
 }
 
 // The workgroup barrier of the pipeline: this wave's LDS reads and writes are done,
-// then s_barrier. Unlike __syncthreads it does not wait for the direct loads in flight
-// (a fence would: vmcnt(0)), which wait_loads() waits for step by step.
+// then s_barrier. Unlike __syncthreads it does not wait for vector memory in flight
+// (a fence would: vmcnt(0)).
 __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Waits until at most `steps` steps' loads of this wave are in flight.
+// Waits until at most `steps` steps' loads of this wave are in flight. A wave's loads
+// complete in the order they were issued, so a step is complete once no more than the
+// loads issued after it are outstanding; stores of its own in flight only make the
+// count stricter (the epilogue keeps them out of the way: see run_tiles).
 __device__ __forceinline__ void wait_loads(int32_t steps) {
   if (steps >= 3) asm volatile("s_waitcnt vmcnt(30)" ::: "memory");
   else if (steps == 2) asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
@@ -319,7 +312,7 @@ __device__ __forceinline__ void mask_stage(Lds& lds, int st, int32_t ks, int32_t
   for (int c = 0; c < 4; ++c) {
     const int32_t k0 = ks * BK + 16 * c;
     if (k0 >= lo && k0 + 16 <= hi) continue;
-    uint4* at = reinterpret_cast<uint4*>(&lds.a[st][r * BK + ((c ^ swizzle(r)) << 4)]);
+    uint4* at = reinterpret_cast<uint4*>(&lds.st[st].a[r * BK + ((c ^ swizzle(r)) << 4)]);
     *at = zero_outside(*at, k0, lo, hi);
   }
 }
@@ -360,15 +353,15 @@ __device__ __forceinline__ v8i chunks(const uint8_t* lo, const uint8_t* hi) {
 // used at once exposes the LDS latency to the whole wave.
 __device__ __forceinline__ void read_a(Frag& f, const Lds& lds, const Lanes& ln, int st,
                                        int32_t ks, int p) {
-  const uint8_t* t = lds.a[st] + p * 2048;
+  const uint8_t* t = lds.st[st].a + p * 2048;
   f.a[p] = chunks(t + ln.a_lo, t + ln.a_hi);
-  f.sa[p] = (reinterpret_cast<const uint8_t*>(lds.as[st]) + ((ks & 1) << 1) + p * 128)[ln.sa];
+  f.sa[p] = (reinterpret_cast<const uint8_t*>(lds.st[st].as) + ((ks & 1) << 1) + p * 128)[ln.sa];
 }
 __device__ __forceinline__ void read_b(Frag& f, const Lds& lds, const Lanes& ln, int st,
                                        int32_t ks, int p) {
-  const uint8_t* t = lds.b[st] + p * 2048;
+  const uint8_t* t = lds.st[st].b + p * 2048;
   f.b[p] = chunks(t + ln.b_lo, t + ln.b_hi);
-  f.sb[p] = (reinterpret_cast<const uint8_t*>(lds.bs[st]) + ((ks & 1) << 1) + p * 128)[ln.sb];
+  f.sb[p] = (reinterpret_cast<const uint8_t*>(lds.st[st].bs) + ((ks & 1) << 1) + p * 128)[ln.sb];
 }
 
 __device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& ln, int st,
@@ -381,10 +374,11 @@ __device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& 
 }
 
 // The 16 MFMAs of one step on `cur`, MFMA q taking A's block q / 4 and B's block q % 4,
-// each after a slice of the memory work: with LOAD, one of the next loads (step
-// ks_load into stage st_load) before each of the first 10; with READ, the next step's
-// blocks into `nxt` in the order its MFMAs take them (a0 b0, b1, b2, b3, then a1, a2,
-// a3 four MFMAs apart), so that each lands a dozen MFMAs before its first use.
+// each after a slice of the memory work: with LOAD, the next loads (step ks_load into
+// stage st_load), one before each of the first 10; with READ, the next step's blocks
+// into `nxt` in the order its MFMAs take them
+// (a0 b0, b1, b2, b3, then a1, a2, a3 four MFMAs apart), so that each lands a dozen
+// MFMAs before its first use.
 template <bool LOAD, bool READ>
 __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la, const Loads& lb,
                                      const Lds& lds, uint32_t lds0, const Lanes& ln,
@@ -420,77 +414,12 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
   }
 }
 
-// acc += A[a_row0 + r] . B[b_row0 + c] over K steps [ks_begin, ks_begin + n) of 64
-// bytes; with `mask`, A's bytes of K outside [mlo, mhi) count as 0 (in the first and
-// last steps). Step k: wait for this wave's loads of step k + 1 and pass the barrier;
-// then the 16 MFMAs of step k on `cur`, each after a slice of the memory work. The
-// steady loop (every step with a load 4 steps ahead) has no branches in it, and takes
-// two steps a turn so that the operand sets swap roles without a copy; the last 4
-// steps follow.
-__device__ __forceinline__ void mainloop(const Operand& A, int32_t a_row0, const Operand& B,
-                                         int32_t b_row0, int32_t ks_begin, int32_t n, bool mask,
-                                         int32_t mlo, int32_t mhi, Lds& lds, v16f acc[4][4]) {
-  if (n <= 0) return;
-  const uint32_t lds0 = lds_at(&lds);
-  const Lanes ln = lanes_of();
-  const Loads la = loads_for(A, a_row0), lb = loads_for(B, b_row0);
-  auto edge = [&](int32_t k) { return mask && (k == 0 || k == n - 1); };
-  for (int32_t s = 0; s < STAGES && s < n; ++s) issue(la, lb, ks_begin + s, lds0, s);
-  wait_loads(n - 1 < 3 ? n - 1 : 3);
-  barrier_lds();
-  if (edge(0)) {
-    mask_stage(lds, 0, ks_begin, mlo, mhi);
-    barrier_lds();
-  }
-  Frag cur, nxt;
-  read_frag(cur, lds, ln, 0, ks_begin);
-  int32_t k = 0;
-  // Steps with a load 4 ahead; step k + 1 < n - 1 is never an edge here.
-  for (; k + 5 < n; k += 2) {
-    wait_loads(2);
-    // Step k + 1's stage is whole; every wave has read step k's, which step k + 4's
-    // loads take.
-    barrier_lds();
-    step<true, true>(cur, nxt, la, lb, lds, lds0, ln, ks_begin + k + 4, k % STAGES,
-                     ks_begin + k + 1, (k + 1) % STAGES, acc);
-    wait_loads(2);
-    barrier_lds();
-    step<true, true>(nxt, cur, la, lb, lds, lds0, ln, ks_begin + k + 5, (k + 1) % STAGES,
-                     ks_begin + k + 2, (k + 2) % STAGES, acc);
-  }
-  for (; k + 4 < n; ++k) {
-    wait_loads(2);
-    barrier_lds();
-    step<true, true>(cur, nxt, la, lb, lds, lds0, ln, ks_begin + k + 4, k % STAGES,
-                     ks_begin + k + 1, (k + 1) % STAGES, acc);
-    cur = nxt;
-  }
-  for (; k + 1 < n; ++k) {
-    const int32_t later = n - 2 - k;
-    wait_loads(later < 2 ? later : 2);
-    barrier_lds();
-    if (edge(k + 1)) {
-      mask_stage(lds, (k + 1) % STAGES, ks_begin + k + 1, mlo, mhi);
-      barrier_lds();
-    }
-    step<false, true>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, ks_begin + k + 1, (k + 1) % STAGES,
-                      acc);
-    cur = nxt;
-  }
-  // The last step: its operands are in registers already.
-  step<false, false>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, 0, 0, acc);
-  // Every wave is done with every stage before the LDS is used again.
-  __syncthreads();
-}
-
 // --- the epilogue ----------------------------------------------------------------------
 
-// The epilogues address a tile from its corner (a 64-bit pointer, the same for the
-// workgroup) with 32-bit offsets: rows [0, rows) and columns [0, cols) of it are stored
-// (cols a multiple of 4), at row pitch ld.
-
-// float32: lane l holds row l % 32 of each 32-row block and, in register run g, columns
-// 8 g + 4 (l / 32) .. + 3 of each 32-column block.
+// float32 (for tests), by every wave, straight from the accumulators: lane l holds row
+// l % 32 of each 32-row block and, in register run g, columns 8 g + 4 (l / 32) .. + 3 of
+// each 32-column block. The tile's rows [0, rows) and columns [0, cols) are stored (cols
+// a multiple of 4), at row pitch ld, from its corner.
 __device__ void store_f32(const v16f acc[4][4], float* tile, int32_t ld, int32_t rows, int32_t cols) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -511,24 +440,29 @@ __device__ void store_f32(const v16f acc[4][4], float* tile, int32_t ld, int32_t
   }
 }
 
-// bfloat16 through LDS, so that each store instruction writes whole rows: each wave
-// puts its 128 x 128 outputs in a region of its own, rows 272 bytes apart (256 and a
-// pad, so that the 16 lanes that read one row, and rows 4 apart, use different banks;
-// the four regions fill the LDS exactly), then reads them back 16 bytes a lane, 16
-// lanes a row: 4 runs of 256 bytes an instruction. Every LDS address is a lane's base
-// plus a constant.
+// bfloat16 through one stage of LDS, in 4 rounds of 32 rows: each wave puts its block of
+// 32 x 128 outputs in a region of its own (rows 272 bytes apart, 256 and a pad, so that
+// the 16 lanes that read a row and rows 4 apart use different banks; the four regions
+// fill the stage), reads it back 16 bytes a lane, 16 lanes a row, and stores 4 runs of
+// 256 bytes an instruction. No other wave touches the region: no workgroup barrier.
+// Every LDS address is a lane's base plus a constant.
 constexpr int PITCH = 272;
-static_assert(4 * 128 * PITCH <= sizeof(Lds), "the epilogue's regions fit the LDS");
+static_assert(4 * 32 * PITCH == sizeof(Stage), "the epilogue's regions fill a stage");
 
 __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int32_t rows,
-                           int32_t cols, Lds& lds) {
+                           int32_t cols, Stage& stage) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  uint8_t* region = reinterpret_cast<uint8_t*>(&lds) + wave * 128 * PITCH;
-  // Lane l writes row 32 i + l % 32, its 4 columns of each 8 at byte 8 (l / 32).
+  uint8_t* region = reinterpret_cast<uint8_t*>(&stage) + wave * 32 * PITCH;
+  // Lane l writes row l % 32 of the block, its 4 columns of each 8 at byte 8 (l / 32).
   uint8_t* mine = region + (lane & 31) * PITCH + 8 * (lane >> 5);
+  // ... and reads back chunk l % 16 (8 columns) of row l / 16 (of 4).
+  const int cc = lane & 15;
+  const uint8_t* from = region + (lane >> 4) * PITCH + cc * 16;
+  const int32_t col = wn * 128 + 8 * cc;
+  uint16_t* out = tile + (wm * 128 + (lane >> 4)) * ld + col;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -539,54 +473,39 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
         // v_cvt_pk_bf16_f32: two floats to two bfloat16, nearest even
         const bf16x2 lo = __builtin_convertvector((f32x2{a[4 * g], a[4 * g + 1]}), bf16x2);
         const bf16x2 hi = __builtin_convertvector((f32x2{a[4 * g + 2], a[4 * g + 3]}), bf16x2);
-        *reinterpret_cast<uint2*>(mine + i * 32 * PITCH + (j * 4 + g) * 16) =
+        *reinterpret_cast<uint2*>(mine + (j * 4 + g) * 16) =
             make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
       }
-    // One block of accumulators at a time: hoisting them all would need more registers
-    // than there are.
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // The wave reads back only its own region.
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-  const int cc = lane & 15;  // the lane's 16-byte chunk (8 columns) of a row
-  const int32_t col = wn * 128 + 8 * cc;
-  if (col >= cols) return;
-  const uint8_t* from = region + (lane >> 4) * PITCH + cc * 16;
-  uint16_t* out = tile + (wm * 128 + (lane >> 4)) * ld + col;
-#pragma unroll 8
-  for (int it = 0; it < 32; ++it) {
-    const int r = it * 4 + (lane >> 4);
-    const uint4 v = *reinterpret_cast<const uint4*>(from + it * 4 * PITCH);
-    if (wm * 128 + r < rows) {
-      if (col + 8 <= cols) {
-        *reinterpret_cast<uint4*>(out + it * 4 * ld) = v;
-      } else {  // cols is a multiple of 4: half a chunk
-        *reinterpret_cast<uint2*>(out + it * 4 * ld) = make_uint2(v.x, v.y);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    if (col < cols) {
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int32_t row = wm * 128 + i * 32 + it * 4 + (lane >> 4);
+        const uint4 v = *reinterpret_cast<const uint4*>(from + it * 4 * PITCH);
+        if (row < rows) {
+          uint16_t* at = out + (i * 32 + it * 4) * ld;
+          if (col + 8 <= cols) *reinterpret_cast<uint4*>(at) = v;
+          else *reinterpret_cast<uint2*>(at) = make_uint2(v.x, v.y);  // cols % 4 == 0
+        }
       }
     }
+    // The reads are done before the next round's writes.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
 __device__ __forceinline__ void store_tile(const v16f acc[4][4], uint16_t* tile, int32_t ld,
-                                           int32_t rows, int32_t cols, Lds& lds) {
-  store_bf16(acc, tile, ld, rows, cols, lds);
+                                           int32_t rows, int32_t cols, Stage& stage) {
+  store_bf16(acc, tile, ld, rows, cols, stage);
 }
 __device__ __forceinline__ void store_tile(const v16f acc[4][4], float* tile, int32_t ld,
-                                           int32_t rows, int32_t cols, Lds&) {
+                                           int32_t rows, int32_t cols, Stage&) {
   store_f32(acc, tile, ld, rows, cols);
 }
 
-// Zeroes rows [0, rows) and columns [0, cols) of a tile (cols a multiple of 4).
-template <typename T>
-__device__ void store_zeros(T* tile, int32_t ld, int32_t rows, int32_t cols) {
-  const int32_t width = cols / 4;
-  for (int32_t i = threadIdx.x; i < rows * width; i += THREADS) {
-    T* at = tile + (i / width) * ld + 4 * (i % width);
-    if (sizeof(T) == 2) *reinterpret_cast<uint2*>(at) = make_uint2(0, 0);
-    else *reinterpret_cast<uint4*>(at) = make_uint4(0, 0, 0, 0);
-  }
-}
+// --- the persistent tile loop ----------------------------------------------------------
 
 // The tiles a workgroup of a persistent grid takes, of `count`: XCD x (workgroup id % 8)
 // takes the contiguous tiles [x per, (x + 1) per), its workgroups one after another, so
@@ -601,6 +520,85 @@ __device__ __forceinline__ Turns turns(int32_t count) {
   return Turns{lo + static_cast<int32_t>(blockIdx.x / 8), hi, static_cast<int32_t>(gridDim.x / 8)};
 }
 
+__device__ __forceinline__ int32_t smaller(int32_t a, int32_t b) { return a < b ? a : b; }
+
+// One output tile's work: C[r][c] = sum over K steps [ks_begin, ks_begin + n) of
+// A[a_row0 + r] . B[b_row0 + c] (B of `group`), A's bytes of K outside [mlo, mhi)
+// counting 0 where `mask`; its rows [0, rows) and columns [0, cols) stored at `corner`.
+struct Job {
+  int32_t a_row0, b_row0, group;
+  int32_t ks_begin, n;
+  int32_t mlo, mhi;
+  bool mask;
+  int64_t corner;
+  int32_t rows, cols;
+};
+
+// The rows GEMM's tiles: the tile list's row tiles by 256-column tiles of y.
+struct RowsTiles {
+  const Tile* tiles;
+  int32_t groups, n, height, col_tiles, k_steps;
+  __device__ bool job(int32_t id, Job& j) const {
+    const Tile t = tiles[id / col_tiles];
+    const int32_t col0 = (id % col_tiles) * BN;
+    // Rows of y stop at height whatever the sizes say.
+    j.rows = smaller(t.hi, height) - t.lo;
+    if (j.rows <= 0) return false;
+    j.cols = smaller(n - col0, BN);
+    j.a_row0 = t.lo;
+    j.b_row0 = col0;
+    j.group = t.group < groups ? t.group : 0;
+    j.ks_begin = 0;
+    j.n = t.group < groups ? k_steps : 0;  // rows past the groups: zeros
+    j.mask = false;
+    j.mlo = j.mhi = 0;
+    j.corner = static_cast<int64_t>(t.lo) * n + col0;
+    return true;
+  }
+};
+
+// The contract GEMM's tiles: each group's d x f output in 256 x 256 tiles.
+struct ContractTiles {
+  const int32_t* starts;
+  int32_t d, f, d_tiles, f_tiles;
+  __device__ bool job(int32_t id, Job& j) const {
+    const int32_t per_group = d_tiles * f_tiles;
+    const int32_t g = id / per_group, rest = id % per_group;
+    const int32_t row0 = (rest / f_tiles) * BM, col0 = (rest % f_tiles) * BN;
+    const int32_t start = starts[g], end = starts[g + 1];
+    j.a_row0 = row0;
+    j.b_row0 = col0;
+    j.group = 0;
+    j.ks_begin = start / BK;
+    j.n = end > start ? (end + BK - 1) / BK - j.ks_begin : 0;
+    j.mask = (start % BK) != 0 || (end % BK) != 0;
+    j.mlo = start;
+    j.mhi = end;
+    j.corner = (static_cast<int64_t>(g) * d + row0) * f + col0;
+    j.rows = smaller(d - row0, BM);
+    j.cols = smaller(f - col0, BN);
+    return true;
+  }
+};
+
+template <typename Tiles>
+__device__ __forceinline__ bool next_job(const Tiles& tiles, const Turns& mine, int32_t& id, Job& j) {
+  for (; id < mine.end; id += mine.stride) {
+    if (tiles.job(id, j)) {
+      id += mine.stride;
+      return true;
+    }
+  }
+  return false;
+}
+
+__device__ __forceinline__ Operand group_of(const Operand& B, int32_t group) {
+  Operand b = B;
+  b.values += static_cast<int64_t>(group) * B.rows * B.k;
+  b.scales += static_cast<int64_t>(group) * B.rows * (B.k / 32);
+  return b;
+}
+
 __device__ __forceinline__ void zero_acc(v16f acc[4][4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -610,10 +608,112 @@ __device__ __forceinline__ void zero_acc(v16f acc[4][4]) {
       for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 }
 
-__device__ __forceinline__ int32_t smaller(int32_t a, int32_t b) { return a < b ? a : b; }
+// A workgroup's tiles, one after another through one ring of 4 stages. The K steps of
+// all its tiles form one stream: step g sits in stage g % 4, and the loads of step
+// g + 4 go out during step g, also across tiles, so that a tile's first steps land
+// while the tile before it finishes. The one exception: the last step of a tile leaves
+// its stage to the epilogue, which stages the outputs there; the next tile's step 3 is
+// issued after it.
+//
+// Stores and loads share a wave's vmcnt, and a wait counts only loads: with stores in
+// flight it waits for them too. So the epilogue first waits for every load in flight
+// (the next tile's first steps, issued during this tile's last ones, have landed by
+// then) and the next tile skips its waits for those steps; the first wait left (for
+// step 3) comes a few steps after the stores went out.
+template <typename T, typename Tiles>
+__device__ void run_tiles(const Tiles& tiles, int32_t count, const Operand& A, const Operand& B,
+                          Lds& lds, T* out, int32_t ld) {
+  const Turns mine = turns(count);
+  int32_t id = mine.first;
+  Job job{}, next{};
+  if (!next_job(tiles, mine, id, job)) return;
+  const uint32_t lds0 = lds_at(&lds);
+  const Lanes ln = lanes_of();
+  int32_t base = 0;   // the stage of this tile's step 0
+  int32_t ready = 0;  // this tile's steps known to have landed
+  {
+    const Loads la = loads_for(A, job.a_row0), lb = loads_for(group_of(B, job.group), job.b_row0);
+    for (int32_t s = 0; s < STAGES && s < job.n; ++s) issue(la, lb, job.ks_begin + s, lds0, s);
+  }
+  for (;;) {
+    const bool more = next_job(tiles, mine, id, next);
+    const int32_t n = job.n, nn = more ? next.n : 0;
+    auto stage = [&](int32_t k) { return (base + k) & (STAGES - 1); };
+    const Loads la = loads_for(A, job.a_row0), lb = loads_for(group_of(B, job.group), job.b_row0);
+    const Loads na = loads_for(A, next.a_row0), nb = loads_for(group_of(B, next.group), next.b_row0);
+    // The next tile's steps issued so far; those whose stages this tile does not use go
+    // now.
+    int32_t ahead = 0;
+    for (; ahead < 3 && ahead < nn && n + ahead < STAGES; ++ahead)
+      issue(na, nb, next.ks_begin + ahead, lds0, stage(n + ahead));
+    v16f acc[4][4];
+    zero_acc(acc);
+    if (n > 0) {
+      auto edge = [&](int32_t k) { return job.mask && (k == 0 || k == n - 1); };
+      if (ready < 1) wait_loads(smaller(n, STAGES) - 1 + ahead);
+      barrier_lds();
+      if (edge(0)) {
+        mask_stage(lds, stage(0), job.ks_begin, job.mlo, job.mhi);
+        barrier_lds();
+      }
+      Frag cur, nxt;
+      read_frag(cur, lds, ln, stage(0), job.ks_begin);
+      int32_t k = 0;
+      // Steps with this tile's load 4 ahead, two a turn so that the operand sets swap
+      // roles without a copy; step k + 1 < n - 1 is never an edge here.
+      for (; k + 5 < n; k += 2) {
+        if (k + 1 >= ready) wait_loads(2);
+        // Step k + 1's stage is whole; every wave has read step k's, which step k + 4's
+        // loads take.
+        barrier_lds();
+        step<true, true>(cur, nxt, la, lb, lds, lds0, ln, job.ks_begin + k + 4, stage(k),
+                         job.ks_begin + k + 1, stage(k + 1), acc);
+        if (k + 2 >= ready) wait_loads(2);
+        barrier_lds();
+        step<true, true>(nxt, cur, la, lb, lds, lds0, ln, job.ks_begin + k + 5, stage(k + 1),
+                         job.ks_begin + k + 2, stage(k + 2), acc);
+      }
+      for (; k + 4 < n; ++k) {
+        if (k + 1 >= ready) wait_loads(2);
+        barrier_lds();
+        step<true, true>(cur, nxt, la, lb, lds, lds0, ln, job.ks_begin + k + 4, stage(k),
+                         job.ks_begin + k + 1, stage(k + 1), acc);
+        cur = nxt;
+      }
+      // The last steps: the freed stages take the next tile's first steps.
+      for (; k + 1 < n; ++k) {
+        if (k + 1 >= ready) wait_loads(smaller(n - 2 - k + ahead, 3));
+        barrier_lds();
+        if (edge(k + 1)) {
+          mask_stage(lds, stage(k + 1), job.ks_begin + k + 1, job.mlo, job.mhi);
+          barrier_lds();
+        }
+        if (ahead < 3 && ahead < nn && k + STAGES == n + ahead) {
+          issue(na, nb, next.ks_begin + ahead, lds0, stage(k));
+          ++ahead;
+        }
+        step<false, true>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, job.ks_begin + k + 1,
+                          stage(k + 1), acc);
+        cur = nxt;
+      }
+      step<false, false>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, 0, 0, acc);
+    }
+    // Every load in flight (the next tile's first steps) lands before the stores go out;
+    // every wave is done with this tile's stages, and its last step's (stage n + 3) stages
+    // the outputs.
+    wait_loads(0);
+    barrier_lds();
+    store_tile(acc, out + job.corner, ld, job.rows, job.cols, lds.st[stage(n + 3)]);
+    barrier_lds();
+    if (!more) break;
+    if (nn > 3) issue(na, nb, next.ks_begin + 3, lds0, stage(n + 3));
+    base = stage(n);
+    ready = ahead;
+    job = next;
+  }
+}
 
-// One workgroup a CU, each looping over its tiles. A tile's epilogue stores are not
-// waited for: they drain while the next tile's first loads are in flight.
+// The kernels: one workgroup a CU.
 template <typename T>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_kernel(
     Operand A, Operand B, int32_t groups, int32_t n, int32_t height,
@@ -621,29 +721,9 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
     T* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t smem[];
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const Turns mine = turns(starts[groups + 1] * col_tiles);
-  for (int32_t id = mine.first; id < mine.end; id += mine.stride) {
-    const int32_t col0 = (id % col_tiles) * BN, cols = smaller(n - col0, BN);
-    const Tile tile = tiles[id / col_tiles];
-    // Rows of y stop at height whatever the sizes say.
-    const int32_t rows = smaller(tile.hi, height) - tile.lo;
-    if (rows <= 0) continue;
-    T* corner = y + static_cast<int64_t>(tile.lo) * n + col0;
-    if (tile.group >= groups) {  // rows past the groups
-      store_zeros(corner, n, rows, cols);
-      continue;
-    }
-    Operand b = B;
-    b.values += static_cast<int64_t>(tile.group) * B.rows * B.k;
-    b.scales += static_cast<int64_t>(tile.group) * B.rows * (B.k / 32);
-    v16f acc[4][4];
-    zero_acc(acc);
-    mainloop(A, tile.lo, b, col0, 0, A.k / BK, false, 0, 0, lds, acc);
-    store_tile(acc, corner, n, rows, cols, lds);
-    // Every wave is done with the LDS the epilogue staged through before the next
-    // tile's loads land there.
-    barrier_lds();
-  }
+  const RowsTiles list{tiles, groups, n, height, col_tiles, A.k / BK};
+  const int32_t count = starts[groups + 1] * col_tiles;
+  run_tiles(list, count, A, B, lds, y, n);
 }
 
 template <typename T>
@@ -652,23 +732,9 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
     int32_t f_tiles, T* __restrict__ dw) {
   extern __shared__ __align__(16) uint8_t smem[];
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const int32_t per_group = d_tiles * f_tiles;
-  const Turns mine = turns(groups * per_group);
-  for (int32_t id = mine.first; id < mine.end; id += mine.stride) {
-    const int32_t g = id / per_group, rest = id % per_group;
-    const int32_t row0 = (rest / f_tiles) * BM, col0 = (rest % f_tiles) * BN;
-    const int32_t start = starts[g], end = starts[g + 1];
-    v16f acc[4][4];
-    zero_acc(acc);
-    if (end > start) {
-      const int32_t ks_begin = start / BK, ks_end = (end + BK - 1) / BK;
-      const bool ragged = (start % BK) != 0 || (end % BK) != 0;
-      mainloop(A, row0, B, col0, ks_begin, ks_end - ks_begin, ragged, start, end, lds, acc);
-    }
-    T* corner = dw + (static_cast<int64_t>(g) * A.rows + row0) * B.rows + col0;
-    store_tile(acc, corner, B.rows, smaller(A.rows - row0, BM), smaller(B.rows - col0, BN), lds);
-    barrier_lds();
-  }
+  const ContractTiles list{starts, A.rows, B.rows, d_tiles, f_tiles};
+  const int32_t count = groups * d_tiles * f_tiles;
+  run_tiles(list, count, A, B, lds, dw, B.rows);
 }
 
 // Lets a kernel take sizeof(Lds) (over 64 KiB) of dynamic LDS; gfx950 has 160 KiB a CU.
