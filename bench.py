@@ -71,10 +71,14 @@ def op_bytes(t, m, d, f, e):
     return {
         "quantize x": t * d * 2 + 2 * m * d * q,
         "quantize W_up": e * d * 2 * f * 2 + 2 * e * d * 2 * f * q,
-        "quantize h": m * f * 2 + 2 * m * f * q,
+        # the activation (projected and the row weights in) and both copies of h out
+        "activation + quantize h": m * 2 * f * 2 + m * 2 + 2 * m * f * q,
         "quantize W_down": e * f * d * 2 + 2 * e * f * d * q,
         "quantize dy": t * d * 2 + 2 * m * d * q,
-        "quantize dp": m * 2 * f * 2 + 2 * m * 2 * f * q,
+        # its gradient: projected, dh and the weights in; both copies of d projected
+        # and the row weights' gradient out
+        "activation backward + quantize dp": m * 2 * f * 2 + m * f * 2 + m * 2
+                                             + 2 * m * 2 * f * q + m * 2,
         "combine": m * d * 2 + t * d * 2,
         "combine dx": m * d * 2 + t * d * 2,
     }

@@ -416,6 +416,18 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
 
 // --- the epilogue ----------------------------------------------------------------------
 
+// Output stores are non-temporal: the tile is written once and read by another kernel,
+// and a whole round of tiles' outputs (4 MiB an XCD in bfloat16) passing through the
+// XCD's 4 MiB L2 would evict the operands the other CUs are about to reuse.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void stream16(void* at, uint4 v) {
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(at));
+}
+__device__ __forceinline__ void stream8(void* at, uint32_t x, uint32_t y) {
+  __builtin_nontemporal_store(u32x2{x, y}, reinterpret_cast<u32x2*>(at));
+}
+
 // float32 (for tests), by every wave, straight from the accumulators: lane l holds row
 // l % 32 of each 32-row block and, in register run g, columns 8 g + 4 (l / 32) .. + 3 of
 // each 32-column block. The tile's rows [0, rows) and columns [0, cols) are stored (cols
@@ -434,8 +446,9 @@ __device__ void store_f32(const v16f acc[4][4], float* tile, int32_t ld, int32_t
         const int32_t col = wn * 128 + j * 32 + 8 * g + 4 * (lane >> 5);
         const v16f& a = acc[i][j];
         if (col < cols)
-          *reinterpret_cast<float4*>(tile + row * ld + col) =
-              make_float4(a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
+          stream16(tile + row * ld + col,
+                   make_uint4(__float_as_uint(a[4 * g]), __float_as_uint(a[4 * g + 1]),
+                              __float_as_uint(a[4 * g + 2]), __float_as_uint(a[4 * g + 3])));
       }
   }
 }
@@ -485,8 +498,8 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
         const uint4 v = *reinterpret_cast<const uint4*>(from + it * 4 * PITCH);
         if (row < rows) {
           uint16_t* at = out + (i * 32 + it * 4) * ld;
-          if (col + 8 <= cols) *reinterpret_cast<uint4*>(at) = v;
-          else *reinterpret_cast<uint2*>(at) = make_uint2(v.x, v.y);  // cols % 4 == 0
+          if (col + 8 <= cols) stream16(at, v);
+          else stream8(at, v.x, v.y);  // cols % 4 == 0
         }
       }
     }

@@ -27,8 +27,15 @@
 //     conflicts), and writes its 32 codes of x^T's row l as two 16-byte stores (half
 //     of the row's 64-byte K chunk; the other wave of the pair writes the other half).
 // HBM traffic per element: 2 bytes read, 2 x (1 + 1/32) bytes written.
+//
+// The values come from a source: a matrix (or a stack, or rows read by index), or the
+// experts' activation computed on the fly from its inputs (h of the forward, d projected
+// of the backward), so that the activation's bfloat16 result is quantized without a
+// round trip through HBM; those values are the ones the activation kernels would store
+// (float32 arithmetic, one rounding to bfloat16), and can be stored too.
 
 #include "common.h"
+#include "glu.h"
 
 namespace bux {
 namespace {
@@ -37,11 +44,113 @@ constexpr int TILE_ROWS = 128;
 constexpr int TILE_COLS = 64;
 constexpr int THREADS = 256;
 
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// A matrix of bfloat16 (matrix g of a stack), or its rows read by index.
+struct Matrix {
+  static constexpr bool kPartials = false;
+  const uint16_t* x;
+  const int32_t* index;
+  int32_t index_div;
+  int64_t rows, cols;
+  // Columns [col, col + 8) of row r of matrix g; `live`: r holds values and the
+  // columns are the matrix's (`inside`: the columns are; padding past them is not).
+  __device__ __forceinline__ uint4 load(int64_t g, int64_t r, int64_t col, bool live, bool,
+                                        float*) const {
+    if (!live) return make_uint4(0, 0, 0, 0);
+    int64_t src = r;
+    if (index) {
+      const int32_t at = index[r];
+      if (at < 0) return make_uint4(0, 0, 0, 0);
+      src = at / index_div;
+    }
+    return *reinterpret_cast<const uint4*>((index ? x : x + g * rows * cols) + src * cols + col);
+  }
+  __device__ __forceinline__ void partial(int64_t, int64_t, float) const {}
+};
+
+// h = act(gate) (up + offset) w from projected (m, f, 2) and the rows' weights; columns
+// are units. Rows past `filled` give 0. With `h`, the values are stored there too.
+struct GluForward {
+  static constexpr bool kPartials = false;
+  const uint16_t* projected;
+  const uint16_t* weights;
+  uint16_t* h;
+  Act act;
+  int64_t m, f;
+  __device__ __forceinline__ uint4 load(int64_t, int64_t r, int64_t col, bool live, bool inside,
+                                        float*) const {
+    uint4 out = make_uint4(0, 0, 0, 0);
+    if (live) {
+      const uint4* p = reinterpret_cast<const uint4*>(projected + (r * f + col) * 2);
+      const uint4 lo = p[0], hi = p[1];
+      const float w = bf16_to_f32(weights[r]);
+      const uint32_t q[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = glu_unit(act, bf16_to_f32(static_cast<uint16_t>(q[j] & 0xffffu)),
+                        bf16_to_f32(static_cast<uint16_t>(q[j] >> 16)), w);
+      out = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    }
+    if (h && r < m && inside) *reinterpret_cast<uint4*>(h + r * f + col) = out;
+    return out;
+  }
+  __device__ __forceinline__ void partial(int64_t, int64_t, float) const {}
+};
+
+// d projected (m, f, 2) from projected, the rows' weights and dh (m, f); columns are
+// projected's 2 f. Each workgroup also leaves its 64 columns' share of each row's d
+// weight (the sum of its units' terms) in `partials` (m rows of `tiles`), which
+// glu_weights_kernel sums in order. With `d_projected`, the values are stored there too.
+struct GluBackward {
+  static constexpr bool kPartials = true;
+  const uint16_t* projected;
+  const uint16_t* weights;
+  const uint16_t* dh;
+  uint16_t* d_projected;
+  float* partials;
+  Act act;
+  int64_t m, f, tiles;
+  __device__ __forceinline__ uint4 load(int64_t, int64_t r, int64_t col, bool live, bool inside,
+                                        float* dw) const {
+    uint4 out = make_uint4(0, 0, 0, 0);
+    *dw = 0.0f;
+    if (live) {
+      const uint4 p = *reinterpret_cast<const uint4*>(projected + r * f * 2 + col);
+      const uint2 d = *reinterpret_cast<const uint2*>(dh + r * f + col / 2);
+      const float w = bf16_to_f32(weights[r]);
+      const uint32_t q[4] = {p.x, p.y, p.z, p.w};
+      const float g[4] = {bf16_to_f32(d.x & 0xffffu), bf16_to_f32(d.x >> 16),
+                          bf16_to_f32(d.y & 0xffffu), bf16_to_f32(d.y >> 16)};
+      float v[8], sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float term;
+        glu_unit_grad(act, bf16_to_f32(static_cast<uint16_t>(q[j] & 0xffffu)),
+                      bf16_to_f32(static_cast<uint16_t>(q[j] >> 16)), w, g[j], &v[2 * j],
+                      &v[2 * j + 1], &term);
+        sum += term;
+      }
+      *dw = sum;
+      out = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    }
+    if (d_projected && r < m && inside)
+      *reinterpret_cast<uint4*>(d_projected + r * f * 2 + col) = out;
+    return out;
+  }
+  __device__ __forceinline__ void partial(int64_t r, int64_t tile, float v) const {
+    if (r < m) partials[r * tiles + tile] = v;
+  }
+};
+
+template <typename Source>
 __global__ __launch_bounds__(THREADS) void quantize_kernel(
-    const uint16_t* __restrict__ x, const int32_t* __restrict__ index, int32_t index_div,
-    int64_t rows, int64_t cols, int64_t height, const int32_t* __restrict__ filled_ptr, int flags,
-    uint8_t* __restrict__ values, uint8_t* __restrict__ scales, uint8_t* __restrict__ t_values,
-    uint8_t* __restrict__ t_scales) {
+    Source src, int64_t rows, int64_t cols, int64_t height, const int32_t* __restrict__ filled_ptr,
+    int flags, uint8_t* __restrict__ values, uint8_t* __restrict__ scales,
+    uint8_t* __restrict__ t_values, uint8_t* __restrict__ t_scales) {
   __shared__ uint16_t tile[TILE_ROWS][TILE_COLS];
 
   const int t = threadIdx.x;
@@ -49,11 +158,11 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
   // They cover the K padding of the row copy too (columns read as 0 there).
   const int64_t cols_pad = (cols + 127) / 128 * 128;
   const int64_t col_tiles = cols_pad / TILE_COLS;
-  const int64_t col0 = (static_cast<int64_t>(blockIdx.x) % col_tiles) * TILE_COLS;
+  const int64_t col_tile = static_cast<int64_t>(blockIdx.x) % col_tiles;
+  const int64_t col0 = col_tile * TILE_COLS;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) / col_tiles) * TILE_ROWS;
   const int64_t g = blockIdx.y;
   const int64_t filled = filled_ptr ? static_cast<int64_t>(*filled_ptr) : height;
-  const uint16_t* xg = index ? x : x + g * rows * cols;
 
   const int chunk = t & 7;  // 8 values of columns col0 + 8 chunk
   const int64_t col = col0 + 8 * chunk;
@@ -63,17 +172,15 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t r = row0 + (t >> 3) + 32 * i;
-    int64_t src = -1;
-    if (r < rows && r < filled) {
-      if (index) {
-        const int32_t at = index[r];
-        src = at < 0 ? -1 : at / index_div;
-      } else {
-        src = r;
-      }
+    float part = 0.0f;
+    raw[i] = src.load(g, r, col, r < rows && r < filled && col_in, col_in, &part);
+    if constexpr (Source::kPartials) {
+      // the 8 lanes of the row: a fixed order of additions
+      part += __shfl_xor(part, 1);
+      part += __shfl_xor(part, 2);
+      part += __shfl_xor(part, 4);
+      if (chunk == 0) src.partial(r, col_tile, part);
     }
-    raw[i] = make_uint4(0, 0, 0, 0);
-    if (src >= 0 && col_in) raw[i] = *reinterpret_cast<const uint4*>(xg + src * cols + col);
   }
 
   if (flags & BUX_MX_ROWS) {
@@ -146,6 +253,48 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
       static_cast<uint8_t>(e + 127);
 }
 
+// d weight of each row: its workgroups' partial sums, added in column order, rounded
+// once to bfloat16; rows past `filled` give 0.
+__global__ __launch_bounds__(THREADS) void glu_weights_kernel(const float* __restrict__ partials,
+                                                              int64_t m, int64_t tiles,
+                                                              const int32_t* __restrict__ filled_ptr,
+                                                              uint16_t* __restrict__ d_weights) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
+  if (r >= m) return;
+  const int64_t filled = filled_ptr ? static_cast<int64_t>(*filled_ptr) : m;
+  float sum = 0.0f;
+  if (r < filled)
+    for (int64_t c = 0; c < tiles; ++c) sum += partials[r * tiles + c];
+  d_weights[r] = f32_to_bf16(sum);
+}
+
+// Checks shared by the entry points, then the launch over `groups` matrices.
+template <typename Source>
+int launch_quantize(const char* name, const Source& src, int64_t groups, int64_t rows, int64_t cols,
+                    int64_t height, const int32_t* filled, int flags, uint8_t* values,
+                    uint8_t* scales, uint8_t* t_values, uint8_t* t_scales, hipStream_t s) {
+  BUX_CHECK(groups >= 1 && rows >= 0 && cols > 0 && height >= rows,
+            "%s: bad shape groups=%lld rows=%lld cols=%lld height=%lld", name, (long long)groups,
+            (long long)rows, (long long)cols, (long long)height);
+  BUX_CHECK(cols % 32 == 0, "%s: cols=%lld is not a multiple of 32", name, (long long)cols);
+  BUX_CHECK(height % 32 == 0, "%s: height=%lld is not a multiple of 32", name, (long long)height);
+  BUX_CHECK(flags != 0 && (flags & ~(BUX_MX_ROWS | BUX_MX_COLUMNS)) == 0,
+            "%s: flags=%d must be BUX_MX_ROWS and/or BUX_MX_COLUMNS", name, flags);
+  BUX_CHECK(!(flags & BUX_MX_ROWS) || (values && scales), "%s: BUX_MX_ROWS needs values and scales",
+            name);
+  BUX_CHECK(!(flags & BUX_MX_COLUMNS) || (t_values && t_scales),
+            "%s: BUX_MX_COLUMNS needs t_values and t_scales", name);
+  BUX_CHECK(groups <= 65535, "%s: %lld matrices exceed one launch", name, (long long)groups);
+  if (height == 0) return BUX_OK;
+  const int64_t tiles = ceil_div(height, TILE_ROWS) * (ceil_div(cols, 128) * 128 / TILE_COLS);
+  BUX_CHECK(tiles <= (1LL << 23), "%s: %lld x %lld is too large for one launch", name,
+            (long long)height, (long long)cols);
+  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
+  hipLaunchKernelGGL(quantize_kernel<Source>, grid, dim3(THREADS), 0, s, src, rows, cols, height,
+                     filled, flags, values, scales, t_values, t_scales);
+  return launched(name);
+}
+
 }  // namespace
 }  // namespace bux
 
@@ -156,29 +305,69 @@ extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t 
   using namespace bux;
   clear_error();
   BUX_CHECK(x != nullptr, "bux_mx_quantize: x is NULL");
-  BUX_CHECK(groups >= 1 && rows >= 0 && cols > 0 && height >= rows,
-            "bux_mx_quantize: bad shape groups=%lld rows=%lld cols=%lld height=%lld",
-            (long long)groups, (long long)rows, (long long)cols, (long long)height);
   BUX_CHECK(index == nullptr || index_div >= 1, "bux_mx_quantize: index_div=%d", index_div);
-  BUX_CHECK(cols % 32 == 0, "bux_mx_quantize: cols=%lld is not a multiple of 32", (long long)cols);
-  BUX_CHECK(height % 32 == 0, "bux_mx_quantize: height=%lld is not a multiple of 32",
-            (long long)height);
-  BUX_CHECK(flags != 0 && (flags & ~(BUX_MX_ROWS | BUX_MX_COLUMNS)) == 0,
-            "bux_mx_quantize: flags=%d must be BUX_MX_ROWS and/or BUX_MX_COLUMNS", flags);
-  BUX_CHECK(!(flags & BUX_MX_ROWS) || (values && scales),
-            "bux_mx_quantize: BUX_MX_ROWS needs values and scales");
-  BUX_CHECK(!(flags & BUX_MX_COLUMNS) || (t_values && t_scales),
-            "bux_mx_quantize: BUX_MX_COLUMNS needs t_values and t_scales");
   BUX_CHECK(index == nullptr || groups == 1, "bux_mx_quantize: index takes one matrix, not %lld",
             (long long)groups);
-  BUX_CHECK(groups <= 65535, "bux_mx_quantize: %lld matrices exceed one launch", (long long)groups);
-  if (height == 0) return BUX_OK;
-  const int64_t tiles = ceil_div(height, TILE_ROWS) * (ceil_div(cols, 128) * 128 / TILE_COLS);
-  BUX_CHECK(tiles <= (1LL << 23), "bux_mx_quantize: %lld x %lld is too large for one launch",
-            (long long)height, (long long)cols);
-  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(groups));
-  hipLaunchKernelGGL(quantize_kernel, grid, dim3(THREADS), 0, as_stream(stream), x, index,
-                     index_div, rows, cols, height, filled, flags, values, scales, t_values,
-                     t_scales);
-  return launched("quantize_kernel");
+  return launch_quantize("bux_mx_quantize", Matrix{x, index, index_div, rows, cols}, groups, rows,
+                         cols, height, filled, flags, values, scales, t_values, t_scales,
+                         as_stream(stream));
+}
+
+namespace {
+int check_act(const char* name, int activation) {
+  BUX_CHECK(activation == BUX_SWISH || activation == BUX_QUICK_GELU,
+            "%s: activation %d is neither BUX_SWISH nor BUX_QUICK_GELU", name, activation);
+  return BUX_OK;
+}
+}  // namespace
+
+extern "C" int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights,
+                                const int32_t* filled, int64_t m, int64_t f, int activation,
+                                float limit, float up_offset, int64_t height, uint16_t* h,
+                                uint8_t* values, uint8_t* scales, uint8_t* t_values,
+                                uint8_t* t_scales, void* stream) {
+  using namespace bux;
+  clear_error();
+  if (int rc = check_act("bux_glu_quantize", activation)) return rc;
+  BUX_CHECK(m == 0 || (projected && weights), "bux_glu_quantize: NULL input");
+  const GluForward src{projected, weights, h, Act{activation, limit, up_offset}, m, f};
+  return launch_quantize("bux_glu_quantize", src, 1, m, f, height, filled,
+                         BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales,
+                         as_stream(stream));
+}
+
+extern "C" size_t bux_glu_backward_quantize_workspace_size(int64_t m, int64_t f) {
+  using namespace bux;
+  // a float a row and a 64-column tile of d projected
+  return static_cast<size_t>(m) * static_cast<size_t>(ceil_div(2 * f, 128) * 2) * sizeof(float);
+}
+
+extern "C" int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights,
+                                         const uint16_t* dh, const int32_t* filled, int64_t m,
+                                         int64_t f, int activation, float limit, float up_offset,
+                                         int64_t height, uint16_t* d_projected, uint8_t* values,
+                                         uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
+                                         uint16_t* d_weights, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  using namespace bux;
+  clear_error();
+  if (int rc = check_act("bux_glu_backward_quantize", activation)) return rc;
+  BUX_CHECK(m == 0 || (projected && weights && dh && d_weights),
+            "bux_glu_backward_quantize: NULL input or d_weights");
+  const size_t need = bux_glu_backward_quantize_workspace_size(m, f);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(BUX_E_WORKSPACE, "bux_glu_backward_quantize: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  const int64_t tiles = ceil_div(2 * f, 128) * 2;
+  float* partials = static_cast<float*>(workspace);
+  const GluBackward src{projected, weights, dh, d_projected, partials,
+                        Act{activation, limit, up_offset}, m, f, tiles};
+  hipStream_t s = as_stream(stream);
+  if (int rc = launch_quantize("bux_glu_backward_quantize", src, 1, m, 2 * f, height, filled,
+                               BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales, s))
+    return rc;
+  if (m == 0) return BUX_OK;
+  hipLaunchKernelGGL(glu_weights_kernel, dim3(static_cast<unsigned>(ceil_div(m, THREADS))),
+                     dim3(THREADS), 0, s, partials, m, tiles, filled, d_weights);
+  return launched("glu_weights_kernel");
 }

@@ -12,6 +12,7 @@
 // once to bfloat16 (XLA fuses the elementwise chain and keeps float32 inside).
 
 #include "common.h"
+#include "glu.h"
 
 namespace bux {
 namespace {
@@ -83,21 +84,6 @@ __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __r
   *reinterpret_cast<uint4*>(out + t * width + c) = pack8(acc);
 }
 
-struct Act {
-  int kind;
-  float limit;  // <= 0: no clamp
-  float offset;
-};
-
-// The gate's activation a(g) and its derivative: g sigmoid(alpha g). jax multiplies
-// the bfloat16 gate by quick_gelu's 1.702 as a bfloat16 constant, 1.703125.
-__device__ __forceinline__ void activate(int kind, float g, float* a, float* da) {
-  const float alpha = kind == BUX_QUICK_GELU ? 1.703125f : 1.0f;
-  const float s = 1.0f / (1.0f + expf(-alpha * g));
-  *a = g * s;
-  *da = s + alpha * g * s * (1.0f - s);
-}
-
 __global__ __launch_bounds__(THREADS) void glu_forward_kernel(
     const uint16_t* __restrict__ projected, const uint16_t* __restrict__ weights,
     const int32_t* __restrict__ filled_ptr, int64_t m, int64_t f, Act act,
@@ -116,16 +102,7 @@ __global__ __launch_bounds__(THREADS) void glu_forward_kernel(
     const float w = bf16_to_f32(weights[i]);
     float out[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float up = p[2 * j], gate = p[2 * j + 1];
-      if (act.limit > 0.0f) {
-        up = fminf(fmaxf(up, -act.limit), act.limit);
-        gate = fminf(gate, act.limit);
-      }
-      float a, da;
-      activate(act.kind, gate, &a, &da);
-      out[j] = a * (up + act.offset) * w;
-    }
+    for (int j = 0; j < 4; ++j) out[j] = glu_unit(act, p[2 * j], p[2 * j + 1], w);
     packed.x = f32_to_bf16(out[0]) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
     packed.y = f32_to_bf16(out[2]) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
   }
@@ -157,21 +134,9 @@ __global__ __launch_bounds__(THREADS) void glu_backward_kernel(
     float dp[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float up = p[2 * j], gate = p[2 * j + 1];
-      float up_pass = 1.0f, gate_pass = 1.0f;
-      if (act.limit > 0.0f) {
-        const float au = fabsf(up);
-        up_pass = au < act.limit ? 1.0f : (au == act.limit ? 0.5f : 0.0f);
-        gate_pass = gate < act.limit ? 1.0f : (gate == act.limit ? 0.5f : 0.0f);
-        up = fminf(fmaxf(up, -act.limit), act.limit);
-        gate = fminf(gate, act.limit);
-      }
-      float a, da;
-      activate(act.kind, gate, &a, &da);
-      const float uo = up + act.offset;
-      dp[2 * j] = g[j] * w * a * up_pass;
-      dp[2 * j + 1] = g[j] * w * uo * da * gate_pass;
-      dw += g[j] * a * uo;
+      float term;
+      glu_unit_grad(act, p[2 * j], p[2 * j + 1], w, g[j], &dp[2 * j], &dp[2 * j + 1], &term);
+      dw += term;
     }
     *reinterpret_cast<uint4*>(d_projected + (i * f + u) * 2) = pack8(dp);
   }

@@ -115,6 +115,54 @@ def weighted_units(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
     return h
 
 
+def weighted_units_quantized(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
+                             filled: torch.Tensor | None, height: int, keep: bool = False
+                             ) -> tuple[Tiled, Tiled, torch.Tensor | None]:
+    """Return `weighted_units` in MXFP8 along its rows and, as h^T, along m (both tiled,
+    `height` rows of the copies), computed and quantized in one pass; with `keep`, h
+    itself (bfloat16 (m, f)) too, else None."""
+    require(projected, weights, filled)
+    m, f = projected.shape[0], projected.shape[1]
+    dev = projected.device
+    kf, kh = grouped_mxfp8.whole(f, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
+    vals = torch.empty(kf // 64, height, 64, dtype=torch.uint8, device=dev)
+    scales = torch.empty(kf // 128, height, 4, dtype=torch.uint8, device=dev)
+    t_vals = torch.empty(kh // 64, f, 64, dtype=torch.uint8, device=dev)
+    t_scales = torch.empty(kh // 128, f, 4, dtype=torch.uint8, device=dev)
+    h = torch.empty(m, f, dtype=torch.bfloat16, device=dev) if keep else None
+    kind, limit, offset = ffn.codes()
+    _lib.check(lib().bux_glu_quantize(
+        ptr(projected), ptr(weights), ptr(filled), m, f, kind, limit, offset, height, ptr(h),
+        ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))
+    return Tiled(vals, scales), Tiled(t_vals, t_scales), h
+
+
+def weighted_units_backward_quantized(
+    ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor, dh: torch.Tensor,
+    filled: torch.Tensor | None, height: int, keep: bool = False,
+) -> tuple[Tiled, Tiled, torch.Tensor, torch.Tensor | None]:
+    """Return the gradient of `weighted_units` to projected in MXFP8 along its rows (2f)
+    and, transposed, along m (both tiled, `height` rows of the copies), the gradient to
+    the weights (m,), and with `keep` the bfloat16 gradient to projected (m, f, 2)."""
+    require(projected, weights, dh, filled)
+    m, f = projected.shape[0], projected.shape[1]
+    dev = projected.device
+    kp, kh = grouped_mxfp8.whole(2 * f, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
+    vals = torch.empty(kp // 64, height, 64, dtype=torch.uint8, device=dev)
+    scales = torch.empty(kp // 128, height, 4, dtype=torch.uint8, device=dev)
+    t_vals = torch.empty(kh // 64, 2 * f, 64, dtype=torch.uint8, device=dev)
+    t_scales = torch.empty(kh // 128, 2 * f, 4, dtype=torch.uint8, device=dev)
+    dw = torch.empty(m, dtype=torch.bfloat16, device=dev)
+    dp = torch.empty(m, f, 2, dtype=torch.bfloat16, device=dev) if keep else None
+    ws = workspace(lib().bux_glu_backward_quantize_workspace_size(m, f), dev)
+    kind, limit, offset = ffn.codes()
+    _lib.check(lib().bux_glu_backward_quantize(
+        ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f, kind, limit, offset, height,
+        ptr(dp), ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), ptr(dw), ptr(ws), ws.numel(),
+        stream()))
+    return Tiled(vals, scales), Tiled(t_vals, t_scales), dw, dp
+
+
 def weighted_units_backward(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
                             dh: torch.Tensor, filled: torch.Tensor | None = None
                             ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -141,7 +189,7 @@ class Saved(NamedTuple):
     k: int
     row_weights: torch.Tensor  # bfloat16 (m,)
     projected: torch.Tensor  # bfloat16 (m, 2f)
-    h: torch.Tensor  # bfloat16 (m, f)
+    h: torch.Tensor | None  # bfloat16 (m, f): compute format, or kept for inspection
     x_m: Tiled | None  # x^T along the rows (wgrad of up)
     up_n: Tiled | None  # each W_up along n (dgrad of up)
     h_m: Tiled | None  # h^T along the rows (wgrad of down)
@@ -151,9 +199,11 @@ class Saved(NamedTuple):
 
 def experts_forward(
     z: torch.Tensor, idx: torch.Tensor, weights: torch.Tensor, up: torch.Tensor,
-    down: torch.Tensor, ffn: Ffn = Ffn(), fmt: str = "mxfp8",
+    down: torch.Tensor, ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
 ) -> tuple[torch.Tensor, Saved]:
     """Return the routed experts' output (t, d), bfloat16, and what the backward takes.
+    In MXFP8 the activation goes straight to its quantized copies; with `intermediates`
+    it is kept in bfloat16 too (Saved.h).
 
     Args:
         z: the tokens, bfloat16 (t, d).
@@ -186,16 +236,17 @@ def experts_forward(
             rows = token_rows(z, s.order, k)
         with span("up fprop"):
             projected = grouped.dot(rows, up2, s.sizes)
-    with span("activation"):
-        h = weighted_units(ffn, projected.view(m, f, p), row_weights, filled)
     if fmt == "mxfp8":
-        with span("quantize h"):
-            h_k, h_m = grouped_mxfp8.quantized_twice(h, filled, True, height=height)
+        with span("activation + quantize h"):
+            h_k, h_m, h = weighted_units_quantized(ffn, projected.view(m, f, p), row_weights,
+                                                   filled, height, intermediates)
         with span("quantize W_down"):
             down_n, down_k = grouped_mxfp8.quantized_twice(down)
         with span("down fprop"):
             y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m)
     else:
+        with span("activation"):
+            h = weighted_units(ffn, projected.view(m, f, p), row_weights, filled)
         with span("down fprop"):
             y = grouped.dot(h, down, s.sizes)
     with span("combine"):
@@ -232,18 +283,22 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
             dh = grouped.dot(dy_rows, down, s.sizes, transposed=True)
         with span("down wgrad"):
             d_down = grouped.weight_grad(saved.h, dy_rows, s.sizes)
-    with span("activation backward"):
-        dp, d_rows_w = weighted_units_backward(ffn, saved.projected.view(m, f, p),
-                                               saved.row_weights, dh, filled)
-    dp = dp.view(m, f * p)
     if fmt == "mxfp8":
-        with span("quantize dp"):
-            dp_n, dp_m = grouped_mxfp8.quantized_twice(dp, filled, True, height=height)
+        with span("activation backward + quantize dp"):
+            dp_n, dp_m, d_rows_w, dp = weighted_units_backward_quantized(
+                ffn, saved.projected.view(m, f, p), saved.row_weights, dh, filled, height,
+                intermediates)
+        if dp is not None:
+            dp = dp.view(m, f * p)
         with span("up dgrad"):
             dx = grouped_mxfp8.rows(dp_n, saved.up_n, s.sizes, height=m)
         with span("up wgrad"):
             d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes)
     else:
+        with span("activation backward"):
+            dp, d_rows_w = weighted_units_backward(ffn, saved.projected.view(m, f, p),
+                                                   saved.row_weights, dh, filled)
+        dp = dp.view(m, f * p)
         with span("up dgrad"):
             dx = grouped.dot(dp, up2, s.sizes, transposed=True)
         with span("up wgrad"):

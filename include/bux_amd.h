@@ -203,6 +203,39 @@ int bux_glu_backward(const uint16_t* projected, const uint16_t* weights, const u
                      const int32_t* filled, int64_t m, int64_t f, int activation, float limit,
                      float up_offset, uint16_t* d_projected, uint16_t* d_weights, void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * a-8 with a-4. The activation and its gradient, quantized as they are computed.
+ *
+ * The reference fuses the activation and the weight into its up GEMM's epilogue on
+ * Blackwell (grouped_cudnn.activated / activation_grad, experts/grouped_cudnn.py:
+ * 161-263) and otherwise quantizes the activation's bfloat16 result
+ * (grouped_blockscaled._quantized, grouped_blockscaled.py:296-317); here one kernel
+ * computes the bfloat16 values bux_glu_forward / bux_glu_backward compute and writes
+ * both MXFP8 copies of them as bux_mx_quantize does (rows from *filled on as 0), with no
+ * round trip of the bfloat16 result through memory.
+ *
+ * bux_glu_quantize: h (m, f) of projected (m, f, 2) and the rows' weights (m);
+ *   values/scales: h along its rows (K = f rounded up to 128), height rows;
+ *   t_values/t_scales: h^T along its rows (K = height rounded up to 128), f rows;
+ *   h: NULL, or bfloat16 [m, f] to store h as well. f a multiple of 32.
+ * bux_glu_backward_quantize: d projected (m, f, 2) of projected, the weights and dh
+ *   (m, f); values/scales along its rows (K = 2 f rounded up to 128), t_values/t_scales
+ *   of its transpose; d_projected: NULL, or bfloat16 [m, f, 2] to store it as well;
+ *   d_weights [m] as bux_glu_backward's (its float32 sum taken in another fixed order).
+ *   workspace: bux_glu_backward_quantize_workspace_size(m, f) bytes.
+ */
+int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights, const int32_t* filled,
+                     int64_t m, int64_t f, int activation, float limit, float up_offset,
+                     int64_t height, uint16_t* h, uint8_t* values, uint8_t* scales,
+                     uint8_t* t_values, uint8_t* t_scales, void* stream);
+size_t bux_glu_backward_quantize_workspace_size(int64_t m, int64_t f);
+int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights,
+                              const uint16_t* dh, const int32_t* filled, int64_t m, int64_t f,
+                              int activation, float limit, float up_offset, int64_t height,
+                              uint16_t* d_projected, uint8_t* values, uint8_t* scales,
+                              uint8_t* t_values, uint8_t* t_scales, uint16_t* d_weights,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,50 @@ def test_weighted_units_and_gradients(lib, name):
     assert (got_dw[filled:] == 0).all()
 
 
+@pytest.mark.parametrize("name", list(FFNS))
+def test_activation_quantized_in_one_pass(lib, name):
+    """The fused kernels (activation, then both MXFP8 copies, no bfloat16 round trip)
+    against the separate ones: the same bfloat16 h and d projected bit for bit, their
+    copies bit for bit what the oracle's quantizer makes of those values (rows from
+    `filled` on as 0, padding to whole tiles), d weights within a bfloat16 step."""
+    from bux_amd import moe
+    from oracle import mxfp8 as omx
+    o, g = _ffn(name)
+    rng = np.random.default_rng(42)
+    m, f, filled = 1000, 768, 937
+    height = 1024
+    p = normal_bf16(rng, (m, f, 2), 4.0)
+    p.reshape(-1)[:64] = bf16.to_bf16(np.array([7.0, -7.0, 6.99, 7.01] * 16, np.float32))
+    w = bf16.to_bf16(rng.random(m).astype(np.float32))
+    dh = normal_bf16(rng, (m, f))
+    announce("glu quantized", name)
+    fg = to_gpu(np.array([filled], np.int32))
+    gp, gw, gdh = to_gpu_bf16(p), to_gpu_bf16(w), to_gpu_bf16(dh)
+    h_sep = moe.weighted_units(g, gp, gw, fg)
+    dp_sep, dw_sep = moe.weighted_units_backward(g, gp, gw, gdh, fg)
+    h_k, h_m, h = moe.weighted_units_quantized(g, gp, gw, fg, height, keep=True)
+    dp_n, dp_m, dw, dp = moe.weighted_units_backward_quantized(g, gp, gw, gdh, fg, height, keep=True)
+    _, _, none = moe.weighted_units_quantized(g, gp, gw, fg, height)
+    torch.cuda.synchronize()
+    assert none is None
+    np.testing.assert_array_equal(bf16_bits(h), bf16_bits(h_sep))
+    np.testing.assert_array_equal(bf16_bits(dp), bf16_bits(dp_sep))
+    want_k, want_m = omx.quantized_twice(bf16_bits(h), filled, True, height=height)
+    for got, want, cols in ((h_k, want_k, f), (h_m, want_m, height)):
+        v, sc = untiled(got, cols)
+        np.testing.assert_array_equal(v, want.values)
+        np.testing.assert_array_equal(sc, want.scales)
+    want_n, want_pm = omx.quantized_twice(bf16_bits(dp).reshape(m, 2 * f), filled, True,
+                                          height=height)
+    for got, want, cols in ((dp_n, want_n, 2 * f), (dp_m, want_pm, height)):
+        v, sc = untiled(got, cols)
+        np.testing.assert_array_equal(v, want.values)
+        np.testing.assert_array_equal(sc, want.scales)
+    a, b = bf16.to_f32(bf16_bits(dw)), bf16.to_f32(bf16_bits(dw_sep))
+    assert (np.abs(a - b) <= np.abs(b) * 2.0 ** -7 + 1e-30).all()
+    assert (a[filled:] == 0).all()
+
+
 def _inputs(rng, t, k, e, d, f, skew=None):
     z = normal_bf16(rng, (t, d))
     if skew is None:
@@ -112,7 +156,7 @@ def test_layer_forward_and_backward(lib, name, t, k, e, d, f, act, fmt):
     announce("layer", name)
     gz, gidx, gw, gup, gdown, gdy = (to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up),
                                       to_gpu_bf16(down), to_gpu_bf16(dy))
-    out, saved = moe.experts_forward(gz, gidx, gw, gup, gdown, g, fmt)
+    out, saved = moe.experts_forward(gz, gidx, gw, gup, gdown, g, fmt, intermediates=True)
     grads = moe.experts_backward(saved, gdy, gup, gdown, g, fmt, intermediates=True)
     torch.cuda.synchronize()
 
