@@ -23,9 +23,9 @@
 // 4 steps ahead of their MFMAs. A wave keeps two sets of operand registers: while the
 // MFMAs of step k run on one, its LDS reads of step k + 1 fill the other. The
 // workgroup's one barrier a step comes first (after it step k + 1's stage is whole and
-// every wave has read step k's), then the 16 MFMAs, each after a slice of the memory
-// work (one of step k + 4's loads, a part of step k + 1's reads): a wave issues in
-// order, so a load that waits for the memory pipe waits while an MFMA runs.
+// every wave has read step k's), then the 16 MFMAs, each followed by a slice of the
+// memory work (one of step k + 4's loads, a part of step k + 1's reads): a wave issues in
+// order, so a load that waits for the memory pipe waits while the MFMA before it runs.
 //
 // MFMA lane layout (32 x 32 x 64), measured on the MI355X: lane l holds row l % 32 of
 // its first operand (column l % 32 of its second); lane half h = l / 32 holds 16 bytes
@@ -374,11 +374,12 @@ __device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& 
 }
 
 // The 16 MFMAs of one step on `cur`, MFMA q taking A's block q / 4 and B's block q % 4,
-// each after a slice of the memory work: with LOAD, the next loads (step ks_load into
-// stage st_load), one before each of the first 10; with READ, the next step's blocks
-// into `nxt` in the order its MFMAs take them
-// (a0 b0, b1, b2, b3, then a1, a2, a3 four MFMAs apart), so that each lands a dozen
-// MFMAs before its first use.
+// each followed by a slice of the memory work: with LOAD, the next loads (step ks_load
+// into stage st_load), one after each of the first 10; with READ, the next step's blocks
+// into `nxt` in the order its MFMAs take them (a0 b0, b1, b2, b3, then a1, a2, a3 four
+// MFMAs apart), so that each lands a dozen MFMAs before its first use. The MFMA goes
+// first: a load that waits to issue (the memory pipe full) then waits while the MFMA
+// runs, rather than holding the MFMA back.
 template <bool LOAD, bool READ>
 __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la, const Loads& lb,
                                      const Lds& lds, uint32_t lds0, const Lanes& ln,
@@ -387,6 +388,9 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int i = q >> 2, j = q & 3;
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.b[j], cur.a[i], acc[i][j], 0,
+                                                               0, 0, cur.sb[j], 0, cur.sa[i]);
+    __builtin_amdgcn_sched_barrier(0);
     if (LOAD) {
       switch (q) {
         case 0: issue_one<0>(la, lb, ks_load, lds0, st_load); break;
@@ -408,9 +412,6 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
       if (q == 4 || q == 8 || q == 12) read_a(nxt, lds, ln, st_next, ks_next, q >> 2);
     }
     __builtin_amdgcn_sched_barrier(0);
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.b[j], cur.a[i], acc[i][j], 0,
-                                                               0, 0, cur.sb[j], 0, cur.sa[i]);
-    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -421,6 +422,7 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
 // XCD's 4 MiB L2 would evict the operands the other CUs are about to reuse.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int NT = 2;  // a buffer store's cache policy: non-temporal
 __device__ __forceinline__ void stream16(void* at, uint4 v) {
   __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(at));
 }
@@ -476,6 +478,12 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
   const uint8_t* from = region + (lane >> 4) * PITCH + cc * 16;
   const int32_t col = wn * 128 + 8 * cc;
   uint16_t* out = tile + (wm * 128 + (lane >> 4)) * ld + col;
+  // A whole tile (the common case) stores without bounds checks, through a buffer
+  // resource from its corner: the lane's offset, a scalar one a row of stores.
+  const bool whole = rows >= BM && cols >= BN;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(tile, 0, 0x7fffffff, 0x00020000);
+  const int32_t lane_off = ((wm * 128 + (lane >> 4)) * ld + col) * 2;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -491,15 +499,23 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
       }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    if (col < cols) {
+    // All 8 reads of the round go out before its first store.
+    uint4 v[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) v[it] = *reinterpret_cast<const uint4*>(from + it * 4 * PITCH);
+    if (whole) {
+#pragma unroll
+      for (int it = 0; it < 8; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[it].x, v[it].y, v[it].z, v[it].w}, rsrc,
+                                               lane_off, (i * 32 + it * 4) * ld * 2, NT);
+    } else if (col < cols) {
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int32_t row = wm * 128 + i * 32 + it * 4 + (lane >> 4);
-        const uint4 v = *reinterpret_cast<const uint4*>(from + it * 4 * PITCH);
         if (row < rows) {
           uint16_t* at = out + (i * 32 + it * 4) * ld;
-          if (col + 8 <= cols) stream16(at, v);
-          else stream8(at, v.x, v.y);  // cols % 4 == 0
+          if (col + 8 <= cols) stream16(at, v[it]);
+          else stream8(at, v[it].x, v[it].y);  // cols % 4 == 0
         }
       }
     }

@@ -61,6 +61,10 @@ __global__ __launch_bounds__(THREADS) void token_rows_narrow_kernel(
   rows[e] = z[(order[i] / k) * width + c];
 }
 
+// KMAX > 0: the token's k <= KMAX picks' rows are all requested before the first is
+// added (their indices first, then their rows); KMAX = 0: any k, one pick at a time.
+// The additions are the same either way: picks in order, a row outside y skipped.
+template <int KMAX>
 __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __restrict__ y,
                                                              int64_t y_rows,
                                                              const int32_t* __restrict__ inverse,
@@ -73,13 +77,32 @@ __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __r
   float acc[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) acc[j] = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    const int64_t r = inverse[t * k + j];
-    if (r < 0 || r >= y_rows) continue;
-    float v[VEC];
-    unpack8(*reinterpret_cast<const uint4*>(y + r * width + c), v);
+  if constexpr (KMAX > 0) {
+    int64_t r[KMAX];
 #pragma unroll
-    for (int q = 0; q < VEC; ++q) acc[q] += v[q];
+    for (int j = 0; j < KMAX; ++j) r[j] = j < k ? inverse[t * k + j] : -1;
+    uint4 raw[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      raw[j] = (r[j] >= 0 && r[j] < y_rows) ? *reinterpret_cast<const uint4*>(y + r[j] * width + c)
+                                            : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (r[j] < 0 || r[j] >= y_rows) continue;
+      float v[VEC];
+      unpack8(raw[j], v);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) acc[q] += v[q];
+    }
+  } else {
+    for (int j = 0; j < k; ++j) {
+      const int64_t r = inverse[t * k + j];
+      if (r < 0 || r >= y_rows) continue;
+      float v[VEC];
+      unpack8(*reinterpret_cast<const uint4*>(y + r * width + c), v);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) acc[q] += v[q];
+    }
   }
   *reinterpret_cast<uint4*>(out + t * width + c) = pack8(acc);
 }
@@ -183,8 +206,12 @@ extern "C" int bux_token_sums(const uint16_t* y, int64_t y_rows, const int32_t* 
   BUX_CHECK(y && inverse && out, "bux_token_sums: NULL buffer");
   BUX_CHECK(tokens * ceil_div(width, THREADS * VEC) < (1LL << 31), "bux_token_sums: too large");
   dim3 grid(static_cast<unsigned>(tokens * ceil_div(width, THREADS * VEC)));
-  hipLaunchKernelGGL(token_sums_kernel, grid, dim3(THREADS), 0, as_stream(stream), y, y_rows,
-                     inverse, k, width, out);
+  if (k <= 8)
+    hipLaunchKernelGGL(token_sums_kernel<8>, grid, dim3(THREADS), 0, as_stream(stream), y, y_rows,
+                       inverse, k, width, out);
+  else
+    hipLaunchKernelGGL(token_sums_kernel<0>, grid, dim3(THREADS), 0, as_stream(stream), y, y_rows,
+                       inverse, k, width, out);
   return launched("token_sums_kernel");
 }
 
