@@ -83,6 +83,8 @@ ROW_CASES = [
     ([5], 64, 96, 64),
     ([0, 0, 0], 128, 128, 128),  # no rows at all: every row 0
     ([700, 0, 1, 300, 513, 2000], 512, 640, 3712),  # tiles of 256 from each group's start
+    ([0, 300, 1, 0, 250, 49], 7168, 256, None),  # config 5's d as K: a 112-step K loop
+    ([100, 0, 37], 256, 7168, 160),  # config 5's d as N: 28 column tiles
 ]
 
 
@@ -118,6 +120,7 @@ CONTRACT_CASES = [
     ([128, 0, 384], 128, 256, 512),  # groups on tile edges
     ([0, 0], 64, 64, 64),  # nothing: dW 0
     ([700, 0, 1, 300, 513, 2000], 640, 384, 3584),  # 256-wide tiles, a partial one
+    ([300, 0, 212, 0], 7168, 256, 512),  # config 5's d as the wgrad's rows
 ]
 
 
