@@ -65,6 +65,16 @@ def gemm_flops(m, d, f):
             "down wgrad": down, "up wgrad": up}
 
 
+def gemm_bytes(m, d, f, e):
+    """Algorithmic HBM bytes of each GEMM: both MXFP8 operands (a code and 1/32 of a
+    scale byte an element) read once and the bfloat16 output written once."""
+    q = 1 + 1 / 32
+    rows = {"up fprop": (m * d, e * 2 * f * d, m * 2 * f), "down fprop": (m * f, e * d * f, m * d),
+            "down dgrad": (m * d, e * f * d, m * f), "up dgrad": (m * 2 * f, e * d * 2 * f, m * d),
+            "down wgrad": (m * d, m * f, e * d * f), "up wgrad": (m * 2 * f, m * d, e * 2 * f * d)}
+    return {name: (a + b) * q + 2 * c for name, (a, b, c) in rows.items()}
+
+
 def op_bytes(t, m, d, f, e):
     """Algorithmic HBM bytes of the streaming ops: unique input bytes + output bytes."""
     q = 1 + 1 / 32  # an E4M3 code and its share of a scale byte
@@ -82,6 +92,23 @@ def op_bytes(t, m, d, f, e):
         "combine": m * d * 2 + t * d * 2,
         "combine dx": m * d * 2 + t * d * 2,
     }
+
+
+def measured_traffic(op):
+    """HBM bytes (read + written) of one launch of `op`, as rocprofv3's FETCH_SIZE and
+    WRITE_SIZE counters measured it (scaled by a plain copy of known size), from the
+    summary committed under profiles/; None when that summary has no row for `op`."""
+    path = os.path.join(ROOT, "profiles", "c3_layer_step_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 7 and cells[0] == op:
+            try:
+                return round((float(cells[2]) + float(cells[5])) * 2**20)
+            except ValueError:
+                return None
+    return None
 
 
 def step(z, idx, w, up, down, dy):
@@ -210,7 +237,10 @@ def main():
             "peak": PEAK_MXFP8_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemms[dominant]["frac_of_peak"], 4),
-            "traffic": None,
+            "traffic": measured_traffic(dominant),
+            "traffic_source": "profiles/c3_layer_step_hbm_traffic.md (rocprofv3 --pmc "
+                              "FETCH_SIZE, WRITE_SIZE; bytes a launch)",
+            "algorithmic_bytes": round(gemm_bytes(m, D, F, E)[dominant]),
         },
         "gemms": {n: {k2: round(v2, 4) for k2, v2 in g.items()} for n, g in gemms.items()},
         "streaming": {n: {k2: round(v2, 4) for k2, v2 in g.items()} for n, g in streams.items()},
