@@ -119,6 +119,31 @@ def step(z, idx, w, up, down, dy):
     return out, grads
 
 
+def router_time(z, e, k, reps=20):
+    """Time the router (bux_amd.router.route: logits, softmax, top-k, weights) on the
+    step's tokens `z` with a random-init Qwen3 router kernel (d x E, N(0, 0.02)), outside
+    the timed step: the layer's feed, not part of its GEMM FLOP. Returns its average
+    milliseconds (HIP events on the stream the kernels run on) and algorithmic bytes
+    (the tokens and the kernel read once, idx and weights written once)."""
+    from bux_amd import router
+
+    g = torch.Generator(device=z.device).manual_seed(SEED + 1)
+    kernel = (torch.randn(z.shape[1], e, generator=g, device=z.device) * 0.02).to(torch.bfloat16)
+    for _ in range(3):
+        router.route(z, kernel, top_k=k)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(s)
+    for _ in range(reps):
+        router.route(z, kernel, top_k=k)
+    end.record(s)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    nbytes = z.numel() * 2 + kernel.numel() * 2 + z.shape[0] * k * (4 + 2)
+    return ms, nbytes
+
+
 def cpu_baseline():
     """The CPU oracle (numpy: float64/float32 quantizer, BLAS float32 GEMMs) on a bounded
     sample of config 3: 8 of its 128 experts with the same per-expert shape (1024
@@ -247,6 +272,10 @@ def main():
         "other_ms": {n: round(g["ms"], 4) for n, g in other.items()},
         "gemm_ms_per_step": round(sum(g["ms"] for g in gemms.values()), 4),
     }
+    r_ms, r_bytes = router_time(z, E, K)
+    result["router"] = {"ms": round(r_ms, 4), "bytes": r_bytes,
+                        "gbs": round(r_bytes / (r_ms * 1e-3) / 1e9, 1),
+                        "frac_of_hbm": round(r_bytes / (r_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle on a sample of config 3 ...")
         result["cpu_baseline"] = cpu_baseline()

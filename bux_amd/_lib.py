@@ -45,12 +45,17 @@ SIGNATURES = {
     "bux_glu_backward_quantize": (
         _int, [_p, _p, _p, _p, _i64, _i64, _int, _f32, _f32, _i64, _p, _p, _p, _p, _p, _p, _p,
                _size, _p]),
+    "bux_route_workspace_size": (_size, [_i64, _i32]),
+    "bux_route": (
+        _int, [_p, _p, _p, _i64, _i64, _i32, _f32, _int, _i32, _p, _i32, _i32, _i32, _int, _f32,
+               _p, _p, _p, _p, _p, _p, _size, _p]),
 }
 
 # Constants of include/bux_amd.h.
 MX_ROWS, MX_COLUMNS = 1, 2
 BF16, F32 = 0, 1
 SWISH, QUICK_GELU = 0, 1
+ROUTER_SOFTMAX, ROUTER_SIGMOID, ROUTER_SQRTSOFTPLUS = 0, 1, 2
 
 
 class BuxError(RuntimeError):

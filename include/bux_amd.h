@@ -236,6 +236,38 @@ int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights
                               uint8_t* t_values, uint8_t* t_scales, uint16_t* d_weights,
                               void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * The router (the path's feed: its picks are a-1's idx, its weights a-8's).
+ *
+ * Replaces MoE._route (src/bux/architecture/experts/moe.py:236-273) off training, with
+ * MoE._logits (:275-284) and _limit_groups (:474-483):
+ *   logits = (x @ kernel + bias) * logit_scale: x bfloat16 [t, d], kernel bfloat16
+ *     [d, n_logits] (the router's nnx kernel, [in, out]), bias float32 [n_logits] or
+ *     NULL; products exact, sums in float32 (MFMA);
+ *   scores = softmax over all n_logits logits | sigmoid | sqrt(softplus), float32;
+ *   the first `scored` are the experts' (routed and zero experts), the rest sinks;
+ *   choice = scores[:scored] + choice_bias (float32 [scored] or NULL: the aux-free
+ *     bias), at -inf outside the `keep` best of `groups` equal groups (a group scored by
+ *     the sum of its two best choices, one if it holds one);
+ *   idx = the k largest choices, the largest first, ties to the lower index;
+ *   weights = the picked scores, and sinks = the sinks' scores, each divided by the
+ *     picked scores' sum plus the sinks' sum (float32, in order) if normalize; both
+ *     rounded to bfloat16, then times scaling rounded to bfloat16, the product rounded
+ *     to bfloat16 (a python float times a bfloat16 array in jax).
+ * Outputs: idx int32 [t, k]; weights bfloat16 [t, k]; sinks bfloat16 [t, n_logits -
+ * scored] (NULL when there are none); scores float32 [t, scored] and logits float32
+ * [t, n_logits], each NULL to skip. n_logits <= 1024, k <= 16, keep <= 16, groups <= 64
+ * and dividing scored, d a multiple of 16. workspace: bux_route_workspace_size(d,
+ * n_logits) bytes (the kernel transposed).
+ */
+enum { BUX_ROUTER_SOFTMAX = 0, BUX_ROUTER_SIGMOID = 1, BUX_ROUTER_SQRTSOFTPLUS = 2 };
+size_t bux_route_workspace_size(int64_t d, int32_t n_logits);
+int bux_route(const uint16_t* x, const uint16_t* kernel, const float* bias, int64_t t, int64_t d,
+              int32_t n_logits, float logit_scale, int router, int32_t scored,
+              const float* choice_bias, int32_t groups, int32_t keep, int32_t k, int normalize,
+              float scaling, int32_t* idx, uint16_t* weights, uint16_t* sinks, float* scores,
+              float* logits, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

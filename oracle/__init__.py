@@ -15,6 +15,8 @@ Modules:
   ``grouped.py:42-102``), the ragged tile list (``grouped_mxfp8.py:157-182``), the
   expert activation (``layers/mlp.py:20-35``, ``common/functional.py:12-40``) and the
   MoE layer's forward and backward composed from them;
+- `oracle.router`: the router's forward (``src/bux/architecture/experts/moe.py:236-284,
+  474-483``): logits, scores, group limit, top-k, weights;
 - `oracle.bf16`: bfloat16 as uint16 bits, rounding to nearest even.
 
 What pins each function (golden vectors, exhaustive checks, closed forms, brute force)

@@ -104,6 +104,28 @@ def test_permute_and_token_ops_reject_bad_arguments(lib):
     assert rc == 1 and "activation 9" in _msg(lib)
 
 
+def test_route_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    f = ctypes.c_float
+
+    def route(t=8, d=64, n=16, router=0, scored=16, groups=1, keep=1, k=4, ws=1 << 20, sinks=None):
+        return lib.bux_route(p, p, None, t, d, n, f(1.0), router, scored, None, groups, keep, k,
+                             1, f(1.0), p, p, sinks, None, None, p, ws, None)
+
+    assert lib.bux_route_workspace_size(2048, 128) == 128 * 2048 * 2
+    assert lib.bux_route_workspace_size(64, 20) == 32 * 64 * 2  # experts padded to 32
+    assert route(d=40) == 1 and "d=40" in _msg(lib)
+    assert route(n=1025, scored=1025) == 1 and "n_logits=1025" in _msg(lib)
+    assert route(k=17) == 1 and "k=17" in _msg(lib)
+    assert route(router=3) == 1 and "router=3" in _msg(lib)
+    assert route(groups=3) == 1 and "groups=3" in _msg(lib)
+    assert route(groups=4, keep=5) == 1 and "keep=5" in _msg(lib)
+    assert route(groups=8, keep=1, k=4) == 1 and "fewer than k=4" in _msg(lib)
+    assert route(n=18, scored=16) == 1 and "NULL" in _msg(lib)  # sinks, none given
+    assert route(t=0, n=18, scored=16) == 0  # no tokens: nothing to write
+    assert route(ws=16) == 2 and "workspace" in _msg(lib)
+
+
 def test_a_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "_LIB", None)
     with pytest.raises(_lib.BuxError, match="not built"):
