@@ -119,29 +119,50 @@ def step(z, idx, w, up, down, dy):
     return out, grads
 
 
-def router_time(z, e, k, reps=20):
-    """Time the router (bux_amd.router.route: logits, softmax, top-k, weights) on the
-    step's tokens `z` with a random-init Qwen3 router kernel (d x E, N(0, 0.02)), outside
-    the timed step: the layer's feed, not part of its GEMM FLOP. Returns its average
-    milliseconds (HIP events on the stream the kernels run on) and algorithmic bytes
-    (the tokens and the kernel read once, idx and weights written once)."""
-    from bux_amd import router
-
-    g = torch.Generator(device=z.device).manual_seed(SEED + 1)
-    kernel = (torch.randn(z.shape[1], e, generator=g, device=z.device) * 0.02).to(torch.bfloat16)
+def timed(fn, reps=20):
+    """Average milliseconds of `fn()` over `reps` calls after 3 untimed ones: HIP events
+    on the current stream, which the library's kernels run on."""
     for _ in range(3):
-        router.route(z, kernel, top_k=k)
+        fn()
     torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(s)
     for _ in range(reps):
-        router.route(z, kernel, top_k=k)
+        fn()
     end.record(s)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / reps
-    nbytes = z.numel() * 2 + kernel.numel() * 2 + z.shape[0] * k * (4 + 2)
-    return ms, nbytes
+    return start.elapsed_time(end) / reps
+
+
+def feed_ops(z, idx, e, k):
+    """Time the ops either side of the layer, outside the timed step (they are not part
+    of its GEMM FLOP): the router (bux_amd.router.route: logits, softmax, top-k,
+    weights) on the step's tokens with a random-init Qwen3 router kernel (d x E,
+    N(0, 0.02)), and an expert-parallel dispatch's MXFP8 rows (bux_amd.dispatch: the
+    picks' rows packed from the tokens, then unpacked to bfloat16). Each with its
+    algorithmic bytes (inputs read once, outputs written once) and HBM fraction."""
+    from bux_amd import dispatch, moe, router
+
+    g = torch.Generator(device=z.device).manual_seed(SEED + 1)
+    kernel = (torch.randn(z.shape[1], e, generator=g, device=z.device) * 0.02).to(torch.bfloat16)
+    t, d = z.shape
+    m = t * k
+    row = d + d // 32
+    order = moe.sort_by_expert(idx, e).order
+    packed = dispatch.picked_in_mxfp8(z, order, k)
+    ops = {
+        "router": (lambda: router.route(z, kernel, top_k=k), t * d * 2 + d * e * 2 + t * k * 6),
+        "dispatch pack": (lambda: dispatch.picked_in_mxfp8(z, order, k), t * d * 2 + m * 4 + m * row),
+        "dispatch unpack": (lambda: dispatch.from_mxfp8(packed, d), m * row + m * d * 2),
+    }
+    out = {}
+    for name, (fn, nbytes) in ops.items():
+        ms = timed(fn)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
+                     "frac_of_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    return out
 
 
 def cpu_baseline():
@@ -272,10 +293,7 @@ def main():
         "other_ms": {n: round(g["ms"], 4) for n, g in other.items()},
         "gemm_ms_per_step": round(sum(g["ms"] for g in gemms.values()), 4),
     }
-    r_ms, r_bytes = router_time(z, E, K)
-    result["router"] = {"ms": round(r_ms, 4), "bytes": r_bytes,
-                        "gbs": round(r_bytes / (r_ms * 1e-3) / 1e9, 1),
-                        "frac_of_hbm": round(r_bytes / (r_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    result["feed"] = feed_ops(z, idx, E, K)
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle on a sample of config 3 ...")
         result["cpu_baseline"] = cpu_baseline()

@@ -45,6 +45,8 @@ SIGNATURES = {
     "bux_glu_backward_quantize": (
         _int, [_p, _p, _p, _p, _i64, _i64, _int, _f32, _f32, _i64, _p, _p, _p, _p, _p, _p, _p,
                _size, _p]),
+    "bux_mx_pack_rows": (_int, [_p, _p, _i32, _i64, _i64, _i64, _p, _p]),
+    "bux_mx_unpack_rows": (_int, [_p, _i64, _i64, _p, _p]),
     "bux_route_workspace_size": (_size, [_i64, _i32]),
     "bux_route": (
         _int, [_p, _p, _p, _i64, _i64, _i32, _f32, _int, _i32, _p, _i32, _i32, _i32, _int, _f32,

@@ -268,6 +268,26 @@ int bux_route(const uint16_t* x, const uint16_t* kernel, const float* bias, int6
               float scaling, int32_t* idx, uint16_t* weights, uint16_t* sinks, float* scores,
               float* logits, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * MXFP8 rows of bytes: what an expert-parallel dispatch in MXFP8 sends a token.
+ *
+ * bux_mx_pack_rows replaces parallel/experts._in_mxfp8 (src/bux/parallel/experts.py:
+ * 659-663) = blockscaled.mx_packed(mx_quantize(z)) (src/bux/architecture/precision/
+ * blockscaled.py:372-375, 312-314) with the pick of each sent row, _in_mxfp8(z)[order
+ * // k] (experts.py:624): packed[i] (d + d/32 bytes: the E4M3 codes of the row
+ * quantized in blocks of 32 along d, then its d/32 E8M0 scale bytes) of x[index[i] /
+ * index_div] (x[i] with index NULL), i < m; x bfloat16 [n, d]. A source row outside
+ * [0, n) packs as zeros.
+ * bux_mx_unpack_rows replaces parallel/experts._from_mxfp8 (experts.py:666-672) =
+ * dequantized(mx_unpacked(packed, d)).astype(bfloat16) (blockscaled.py:223-229,
+ * 378-380): out[i][j] = code * 2^(scale byte - 127) in float32, rounded to bfloat16
+ * (exact for products in bfloat16's normal range).
+ * d a multiple of 32.
+ */
+int bux_mx_pack_rows(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t n,
+                     int64_t m, int64_t d, uint8_t* packed, void* stream);
+int bux_mx_unpack_rows(const uint8_t* packed, int64_t m, int64_t d, uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,7 +29,13 @@ Pins, run by ``tests/test_oracle.py``:
   (brute force over exponents on random blocks); dequantization is within half an E4M3
   ulp of each value;
 - `dequantized`: closed form ``value * 2^(byte - 127)`` checked against torch's
-  ``float8_e4m3fn`` -> float32 cast for all 256 codes.
+  ``float8_e4m3fn`` -> float32 cast for all 256 codes, and `e8m0_values` against
+  torch's ``float8_e8m0fnu`` -> float32 cast for all 256 bytes;
+- `mx_packed` / `mx_unpacked` / `in_mxfp8` / `from_mxfp8` (the expert-parallel
+  dispatch's rows of bytes, parallel/experts.py:659-672): the reference's round trip
+  (tests/test_precision.py:344-352: 8 x 64 rows pack to 66 bytes and unpack to the
+  same values), and ``from_mxfp8`` exact (E4M3 codes through torch's float8 cast,
+  times the scale, equal to the bfloat16 result).
 """
 
 from typing import NamedTuple
@@ -136,13 +142,45 @@ def mx_twice(x: np.ndarray) -> tuple[Blocks, Blocks]:
     return mx_quantize(x), mx_quantize(np.ascontiguousarray(x.T))
 
 
+def e8m0_values() -> np.ndarray:
+    """Return the float32 value of each E8M0 byte (``float8_e8m0fnu``): 2^(byte - 127),
+    byte 0 giving 2^-127 (a float32 subnormal) and 255 NaN."""
+    table = np.ldexp(np.float64(1.0), np.arange(255) - 127).astype(np.float32)
+    return np.append(table, np.float32(np.nan)).astype(np.float32)
+
+
 def dequantized(blocks: Blocks) -> np.ndarray:
     """Return the float32 values MXFP8 blocks hold: each code's value times its
-    block's 2^(byte - 127) (blockscaled.py:223-229)."""
+    block's scale, ``scales.astype(float32)`` of E8M0 bytes (blockscaled.py:223-229)."""
     values, scales = blocks
     block = values.shape[-1] // scales.shape[-1]
-    scale = power_of_two(scales.astype(np.int32) - 127)
-    return e4m3_values()[values] * np.repeat(scale, block, axis=-1)
+    scale = e8m0_values()[scales]
+    with np.errstate(over="ignore", invalid="ignore"):  # past float32: inf, as float32 gives
+        return e4m3_values()[values] * np.repeat(scale, block, axis=-1)
+
+
+def mx_packed(blocks: Blocks) -> np.ndarray:
+    """Return each row of `blocks` as one row of bytes, its c codes then its c/32 scale
+    bytes (blockscaled.py:372-375)."""
+    return np.concatenate([blocks.values, blocks.scales], axis=-1).astype(np.uint8)
+
+
+def mx_unpacked(packed: np.ndarray, c: int) -> Blocks:
+    """Return the blocks of rows of `c` values that `mx_packed` made
+    (blockscaled.py:378-380)."""
+    return Blocks(packed[:, :c].copy(), packed[:, c:].copy())
+
+
+def in_mxfp8(z: np.ndarray) -> np.ndarray:
+    """Return each token (bfloat16 bits, n x d) in MXFP8 as a row of d + d/32 bytes
+    (parallel/experts.py:659-663)."""
+    return mx_packed(mx_quantize(z))
+
+
+def from_mxfp8(packed: np.ndarray, d: int) -> np.ndarray:
+    """Return rows of `in_mxfp8` bytes dequantized, as bfloat16 bits
+    (parallel/experts.py:666-672: float32, then ``astype`` the tokens' dtype)."""
+    return bf16.to_bf16(dequantized(mx_unpacked(packed, d)))
 
 
 def quantized_twice(

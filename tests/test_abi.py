@@ -126,6 +126,21 @@ def test_route_rejects_bad_arguments(lib):
     assert route(ws=16) == 2 and "workspace" in _msg(lib)
 
 
+def test_wire_rows_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    rc = lib.bux_mx_pack_rows(p, None, 1, 10, 10, 48, p, None)
+    assert rc == 1 and "d=48" in _msg(lib)
+    rc = lib.bux_mx_pack_rows(p, None, 1, 10, 11, 64, p, None)
+    assert rc == 1 and "without an index" in _msg(lib)
+    rc = lib.bux_mx_pack_rows(p, p, 0, 10, 20, 64, p, None)
+    assert rc == 1 and "index_div=0" in _msg(lib)
+    assert lib.bux_mx_pack_rows(None, None, 1, 0, 0, 64, None, None) == 0  # nothing to pack
+    rc = lib.bux_mx_unpack_rows(p, 10, 40, p, None)
+    assert rc == 1 and "d=40" in _msg(lib)
+    rc = lib.bux_mx_unpack_rows(None, 10, 64, p, None)
+    assert rc == 1 and "NULL" in _msg(lib)
+
+
 def test_a_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "_LIB", None)
     with pytest.raises(_lib.BuxError, match="not built"):

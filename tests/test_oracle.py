@@ -83,6 +83,43 @@ def test_e4m3_values_are_torchs():
     np.testing.assert_array_equal(got[ok], want[ok])
 
 
+def test_e8m0_values_are_torchs():
+    """Every E8M0 byte (byte 0: 2^-127, 255: NaN) as torch's float8_e8m0fnu widens it."""
+    want = torch.arange(256, dtype=torch.uint8).view(torch.float8_e8m0fnu).float().numpy()
+    got = mxfp8.e8m0_values()
+    assert np.array_equal(got[:255], want[:255]) and np.isnan(got[255]) and np.isnan(want[255])
+
+
+def test_mxfp8_rows_pack_into_bytes_and_back():
+    """The reference's round trip (tests/test_precision.py:344-352): 8 rows of 64 pack
+    into 66 bytes each, codes then scale bytes, and unpack to the same values."""
+    x = (np.random.default_rng(8).standard_normal((8, 64)) * 3).astype(np.float32)
+    blocks = mxfp8.mx_quantize(x)
+    packed = mxfp8.mx_packed(blocks)
+    assert packed.dtype == np.uint8 and packed.shape == (8, 64 + 2)
+    assert (packed[:, :64] == blocks.values).all() and (packed[:, 64:] == blocks.scales).all()
+    back = mxfp8.mx_unpacked(packed, 64)
+    assert np.array_equal(mxfp8.dequantized(back), mxfp8.dequantized(blocks))
+
+
+def test_tokens_from_mxfp8_are_exact_bfloat16():
+    """from_mxfp8: each code (torch's float8_e4m3fn cast) times its scale is a bfloat16
+    exactly wherever the product is a normal bfloat16 (4 significant bits), for every
+    byte pattern of a row and every scale byte 0..255; below that, bfloat16's
+    subnormals round it, as the reference's astype does."""
+    rng = np.random.default_rng(9)
+    packed = rng.integers(0, 256, (256, 64 + 2), dtype=np.uint8)
+    packed[:, 64] = np.arange(256, dtype=np.uint8)  # every scale byte
+    got = bf16.to_f32(mxfp8.from_mxfp8(packed, 64)).astype(np.float64)
+    codes = torch.from_numpy(packed[:, :64].copy()).view(torch.float8_e4m3fn).double().numpy()
+    scale = np.repeat(torch.from_numpy(packed[:, 64:].copy()).view(torch.float8_e8m0fnu)
+                      .double().numpy(), 32, axis=-1)
+    want = codes * scale
+    normal = np.isfinite(want) & (np.abs(want) < 3e38) & ((want == 0) | (np.abs(want) >= 2.0**-126))
+    assert np.array_equal(got[normal], want[normal])  # exact: no rounding happened
+    assert np.isnan(got[~np.isfinite(want) & np.isnan(want)]).all()
+
+
 def test_ceil_log2_is_exact_for_every_bf16_block_maximum():
     """e = the least integer with 2^e >= fl32(amax / 448), clipped to [-126, 126],
     computed from the quotient's exact rational value (not from its bits)."""
