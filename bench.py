@@ -136,10 +136,10 @@ def timed(fn, reps=20):
 
 
 def feed_ops(z, idx, e, k):
-    """Time the ops either side of the layer, outside the timed step (they are not part
-    of its GEMM FLOP): the router (bux_amd.router.route: logits, softmax, top-k,
+    """Time the ops either side of the layer, and the mxfp8_2d recipe's weight
+    quantizer, outside the timed step (they are not part of its GEMM FLOP): the router (bux_amd.router.route: logits, softmax, top-k,
     weights) on the step's tokens with a random-init Qwen3 router kernel (d x E,
-    N(0, 0.02)), and an expert-parallel dispatch's MXFP8 rows (bux_amd.dispatch: the
+    N(0, 0.02)), W_up's two copies with a scale per 32 x 32 tile, and an expert-parallel dispatch's MXFP8 rows (bux_amd.dispatch: the
     picks' rows packed from the tokens, then unpacked to bfloat16). Each with its
     algorithmic bytes (inputs read once, outputs written once) and HBM fraction."""
     from bux_amd import dispatch, moe, router
@@ -151,8 +151,14 @@ def feed_ops(z, idx, e, k):
     row = d + d // 32
     order = moe.sort_by_expert(idx, e).order
     packed = dispatch.picked_in_mxfp8(z, order, k)
+    from bux_amd import grouped_mxfp8
+
+    up = (torch.randn(e, d, 2 * F, generator=g, device=z.device) * 0.02).to(torch.bfloat16)
+    q = 1 + 1 / 32
     ops = {
         "router": (lambda: router.route(z, kernel, top_k=k), t * d * 2 + d * e * 2 + t * k * 6),
+        "quantize W_up (mxfp8_2d: 32x32 tiles)": (
+            lambda: grouped_mxfp8.quantized_twice(up, tiles=True), up.numel() * (2 + 2 * q)),
         "dispatch pack": (lambda: dispatch.picked_in_mxfp8(z, order, k), t * d * 2 + m * 4 + m * row),
         "dispatch unpack": (lambda: dispatch.from_mxfp8(packed, d), m * row + m * d * 2),
     }

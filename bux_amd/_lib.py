@@ -54,7 +54,7 @@ SIGNATURES = {
 }
 
 # Constants of include/bux_amd.h.
-MX_ROWS, MX_COLUMNS = 1, 2
+MX_ROWS, MX_COLUMNS, MX_TILES = 1, 2, 4
 BF16, F32 = 0, 1
 SWISH, QUICK_GELU = 0, 1
 ROUTER_SOFTMAX, ROUTER_SIGMOID, ROUTER_SQRTSOFTPLUS = 0, 1, 2

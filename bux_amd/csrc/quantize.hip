@@ -28,6 +28,11 @@
 //     of the row's 64-byte K chunk; the other wave of the pair writes the other half).
 // HBM traffic per element: 2 bytes read, 2 x (1 + 1/32) bytes written.
 //
+// With BUX_MX_TILES the scale is one per 32 x 32 tile of x instead (the mxfp8_2d
+// recipe's weights, blockscaled.py:294-309): the tile is staged in LDS first and each
+// wave reduces its two tiles' largest magnitudes, so both copies take the tile's scale
+// and hold the same codes, transposed.
+//
 // The values come from a source: a matrix (or a stack, or rows read by index), or the
 // experts' activation computed on the fly from its inputs (h of the forward, d projected
 // of the backward), so that the activation's bfloat16 result is quantized without a
@@ -183,6 +188,26 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     }
   }
 
+  // BUX_MX_TILES: a scale per 32 x 32 tile, both copies. The tile goes through LDS
+  // first; wave w takes the 32 rows of slab w, lane l column l, and the 32 lanes of a
+  // tile reduce its largest magnitude by xor-shuffles.
+  __shared__ int tile_e[TILE_ROWS / 32][TILE_COLS / 32];
+  const bool tiles = (flags & BUX_MX_TILES) != 0;
+  if (tiles) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<uint4*>(&tile[(t >> 3) + 32 * i][8 * chunk]) = raw[i];
+    __syncthreads();
+    const int wave = t >> 6, lane = t & 63;
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(bf16_to_f32(tile[32 * wave + j][lane])));
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if ((lane & 31) == 0) tile_e[wave][lane >> 5] = scale_exponent(amax);
+    __syncthreads();
+  }
+
   if (flags & BUX_MX_ROWS) {
     uint8_t* vg = values + g * height * cols_pad;
     uint8_t* sg = scales + g * height * (cols_pad / 32);
@@ -201,7 +226,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
       amax = fmaxf(amax, __shfl_xor(amax, 1));
       amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const int e = scale_exponent(amax);
+      const int e = tiles ? tile_e[i][chunk >> 2] : scale_exponent(amax);
       const float down = power_of_two_down(e);
       uint2 codes;
       codes.x = e4m3x4(clip448(v[0] * down), clip448(v[1] * down), clip448(v[2] * down),
@@ -218,11 +243,13 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
 
   if (!(flags & BUX_MX_COLUMNS)) return;
 
+  if (!tiles) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<uint4*>(&tile[(t >> 3) + 32 * i][8 * chunk]) = raw[i];
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<uint4*>(&tile[(t >> 3) + 32 * i][8 * chunk]) = raw[i];
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -237,7 +264,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     v[j] = bf16_to_f32(tile[32 * wave + j][lane]);
     amax = fmaxf(amax, fabsf(v[j]));
   }
-  const int e = scale_exponent(amax);
+  const int e = tiles ? tile_e[wave][lane >> 5] : scale_exponent(amax);
   const float down = power_of_two_down(e);
   uint32_t w[8];
 #pragma unroll
@@ -278,8 +305,10 @@ int launch_quantize(const char* name, const Source& src, int64_t groups, int64_t
             (long long)rows, (long long)cols, (long long)height);
   BUX_CHECK(cols % 32 == 0, "%s: cols=%lld is not a multiple of 32", name, (long long)cols);
   BUX_CHECK(height % 32 == 0, "%s: height=%lld is not a multiple of 32", name, (long long)height);
-  BUX_CHECK(flags != 0 && (flags & ~(BUX_MX_ROWS | BUX_MX_COLUMNS)) == 0,
-            "%s: flags=%d must be BUX_MX_ROWS and/or BUX_MX_COLUMNS", name, flags);
+  BUX_CHECK((flags & (BUX_MX_ROWS | BUX_MX_COLUMNS)) != 0 &&
+                (flags & ~(BUX_MX_ROWS | BUX_MX_COLUMNS | BUX_MX_TILES)) == 0,
+            "%s: flags=%d must be BUX_MX_ROWS and/or BUX_MX_COLUMNS (with BUX_MX_TILES)", name,
+            flags);
   BUX_CHECK(!(flags & BUX_MX_ROWS) || (values && scales), "%s: BUX_MX_ROWS needs values and scales",
             name);
   BUX_CHECK(!(flags & BUX_MX_COLUMNS) || (t_values && t_scales),

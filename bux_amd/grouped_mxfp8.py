@@ -91,9 +91,11 @@ def quantized_twice(
     index_div: int = 1,
     height: int | None = None,
     rows: bool = True,
+    tiles: bool = False,
 ) -> tuple[Tiled | None, Tiled | None]:
     """Return x in MXFP8 along its rows and, if `columns`, x^T along its rows, in one
-    pass over x, both tiled.
+    pass over x, both tiled; with `tiles`, a scale per 32 x 32 tile shared by both
+    (``blockscaled.mx_tiles_twice``, blockscaled.py:294-309: the mxfp8_2d recipe's W).
 
     Args:
         x: bfloat16, a matrix (r, c) or a stack (g, r, c); with `index`, the matrix
@@ -139,6 +141,8 @@ def quantized_twice(
         kh = whole(h, K_ALIGN)
         t_vals = torch.empty(*lead, kh // 64, c, 64, dtype=torch.uint8, device=dev)
         t_scales = torch.empty(*lead, kh // 128, c, 4, dtype=torch.uint8, device=dev)
+    if tiles:
+        flags |= _lib.MX_TILES
     _lib.check(lib().bux_mx_quantize(
         ptr(x), ptr(index), index_div, groups, r, c, h, ptr(filled), flags,
         ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))

@@ -181,6 +181,15 @@ def weighted_units_backward(ffn: Ffn, projected: torch.Tensor, weights: torch.Te
 # --- The layer: routed -> experts, forward and backward ------------------------------
 
 
+MX_FORMATS = ("mxfp8", "mxfp8_2d")
+
+
+def _check_fmt(fmt: str) -> None:
+    """The grouped GEMMs' formats bux allows (train/config.py:822)."""
+    if fmt not in (*MX_FORMATS, "compute"):
+        raise ValueError(f"the routed experts multiply in compute, mxfp8, mxfp8_2d: not {fmt}")
+
+
 class Saved(NamedTuple):
     """What the layer's backward takes of its forward (grouped_blockscaled.py:84's Saved
     for each GEMM, and the activation's input, which jax.checkpoint recomputes from)."""
@@ -212,7 +221,10 @@ def experts_forward(
         up: the experts' up and gate kernels, bfloat16 (E, d, f, 2).
         down: the experts' down kernels, bfloat16 (E, f, d).
         ffn: the activation.
-        fmt: "mxfp8", or "compute" for bfloat16 GEMMs.
+        fmt: "mxfp8" (Transformer Engine's recipe: every operand in blocks of 32 along
+            what its GEMM contracts), "mxfp8_2d" (the same, but each W with a scale per
+            32 x 32 tile, shared by its two copies: blockscaled.MXFP8_2D,
+            blockscaled.py:306-309), or "compute" for bfloat16 GEMMs.
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -223,12 +235,14 @@ def experts_forward(
         row_weights = picked_weights(weights, s.order)
     up2 = up.reshape(e, d, f * p)
     x_m = up_n = h_m = down_n = rows = None
-    if fmt == "mxfp8":
+    _check_fmt(fmt)
+    mx, tiles = fmt in MX_FORMATS, fmt == "mxfp8_2d"
+    if mx:
         height = grouped_mxfp8.whole(m)
         with span("quantize x"):
             x_k, x_m = grouped_mxfp8.quantized_twice(z, filled, True, s.order, k, height)
         with span("quantize W_up"):
-            up_n, up_k = grouped_mxfp8.quantized_twice(up2)
+            up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
         with span("up fprop"):
             projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m)
     else:
@@ -236,12 +250,12 @@ def experts_forward(
             rows = token_rows(z, s.order, k)
         with span("up fprop"):
             projected = grouped.dot(rows, up2, s.sizes)
-    if fmt == "mxfp8":
+    if mx:
         with span("activation + quantize h"):
             h_k, h_m, h = weighted_units_quantized(ffn, projected.view(m, f, p), row_weights,
                                                    filled, height, intermediates)
         with span("quantize W_down"):
-            down_n, down_k = grouped_mxfp8.quantized_twice(down)
+            down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
         with span("down fprop"):
             y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m)
     else:
@@ -268,7 +282,9 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
     m = t * k
     filled = s.filled
     up2 = up.reshape(e, d, f * p)
-    if fmt == "mxfp8":
+    _check_fmt(fmt)
+    mx = fmt in MX_FORMATS
+    if mx:
         height = grouped_mxfp8.whole(m)
         with span("quantize dy"):
             dy_n, dy_m = grouped_mxfp8.quantized_twice(dy, filled, True, s.order, k, height)
@@ -283,7 +299,7 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
             dh = grouped.dot(dy_rows, down, s.sizes, transposed=True)
         with span("down wgrad"):
             d_down = grouped.weight_grad(saved.h, dy_rows, s.sizes)
-    if fmt == "mxfp8":
+    if mx:
         with span("activation backward + quantize dp"):
             dp_n, dp_m, d_rows_w, dp = weighted_units_backward_quantized(
                 ffn, saved.projected.view(m, f, p), saved.row_weights, dh, filled, height,

@@ -95,9 +95,13 @@ int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_experts, in
  *           [groups, K/128, height, 4]. BUX_MX_COLUMNS: write t_values and t_scales,
  *           x^T (cols, height) likewise with K = height rounded up to 128:
  *           [groups, K/64, cols, 64] and [groups, K/128, cols, 4].
+ *           With BUX_MX_TILES as well, the scale is one per 32 x 32 tile of x, which
+ *           both copies take (so they hold the same codes, transposed): the mxfp8_2d
+ *           recipe's weights, blockscaled.mx_tiles_twice (src/bux/architecture/
+ *           precision/blockscaled.py:294-309).
  *           cols must be a multiple of 32.
  */
-enum { BUX_MX_ROWS = 1, BUX_MX_COLUMNS = 2 };
+enum { BUX_MX_ROWS = 1, BUX_MX_COLUMNS = 2, BUX_MX_TILES = 4 };
 int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t groups,
                     int64_t rows, int64_t cols, int64_t height, const int32_t* filled, int flags,
                     uint8_t* values, uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,

@@ -292,7 +292,8 @@ def layer_forward(
         up: the experts' up and gate kernels, bfloat16 bits (E, d, f, 2).
         down: the experts' down kernels, bfloat16 bits (E, f, d).
         ffn: the activation.
-        fmt: "mxfp8" or "compute".
+        fmt: "mxfp8", "mxfp8_2d" (each W with a scale per 32 x 32 tile shared by its
+            copies, blockscaled.MXFP8_2D, blockscaled.py:306-309) or "compute".
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -305,17 +306,18 @@ def layer_forward(
     row_weights = kept[s.order]
     up2 = np.asarray(up).reshape(e, d, f * p)
     x_m = up_n = h_m = down_n = None
-    if fmt == "mxfp8":
+    mx, tiles = fmt in ("mxfp8", "mxfp8_2d"), fmt == "mxfp8_2d"
+    if mx:
         # rows padded by 0 to whole tiles of 128 (grouped_blockscaled.py:122-128)
         x_k, x_m = mxfp8.quantized_twice(z, filled, True, index=tokens, height=whole(m))
-        up_n, up_k = mxfp8.quantized_twice(up2, d)
+        up_n, up_k = mxfp8.quantized_twice(up2, d, tiles=tiles)
         projected = rows_mx(x_k, up_k, s.sizes, height=m)
     else:
         projected = ragged_dot_bf16(z[tokens], up2, s.sizes)
     h = weighted_units(ffn, projected.reshape(m, f, p), row_weights)
-    if fmt == "mxfp8":
+    if mx:
         h_k, h_m = mxfp8.quantized_twice(h, filled, True, height=whole(m))
-        down_n, down_k = mxfp8.quantized_twice(down, f)
+        down_n, down_k = mxfp8.quantized_twice(down, f, tiles=tiles)
         y = rows_mx(h_k, down_k, s.sizes, height=m)
     else:
         y = ragged_dot_bf16(h, down, s.sizes)
@@ -338,7 +340,8 @@ def layer_backward(
     filled = int(s.sizes.sum())
     tokens = s.order // k
     up2 = np.asarray(up).reshape(e, d, f * p)
-    if fmt == "mxfp8":
+    mx = fmt in ("mxfp8", "mxfp8_2d")  # W's copies come from the forward
+    if mx:
         dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens, height=whole(m))
         dh = rows_mx(dy_n, saved.down_n, s.sizes, height=m)
         d_down = contract_mx(saved.h_m, dy_m, s.sizes)
@@ -348,7 +351,7 @@ def layer_backward(
         d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes)
     dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), saved.row_weights, dh)
     dp = dp.reshape(m, f * p)
-    if fmt == "mxfp8":
+    if mx:
         dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True, height=whole(m))
         dx = rows_mx(dp_n, saved.up_n, s.sizes, height=m)
         d_up = contract_mx(saved.x_m, dp_m, s.sizes)

@@ -31,6 +31,10 @@ Pins, run by ``tests/test_oracle.py``:
 - `dequantized`: closed form ``value * 2^(byte - 127)`` checked against torch's
   ``float8_e4m3fn`` -> float32 cast for all 256 codes, and `e8m0_values` against
   torch's ``float8_e8m0fnu`` -> float32 cast for all 256 bytes;
+- `mx_tiles_twice` (32 x 32 tiles): each tile's scale the least power of two that fits
+  its largest magnitude (brute force over exponents), both copies the same codes
+  transposed, and a matrix whose tiles each hold one magnitude quantizing as the 1 x 32
+  blocks do;
 - `mx_packed` / `mx_unpacked` / `in_mxfp8` / `from_mxfp8` (the expert-parallel
   dispatch's rows of bytes, parallel/experts.py:659-672): the reference's round trip
   (tests/test_precision.py:344-352: 8 x 64 rows pack to 66 bytes and unpack to the
@@ -136,6 +140,18 @@ def mx_quantize(x: np.ndarray) -> Blocks:
     return Blocks(*in_e4m3(x, "rows"))
 
 
+def mx_tiles_twice(w: np.ndarray) -> tuple[Blocks, Blocks]:
+    """Return W and W^T in MXFP8 with a scale per 32 x 32 tile, each copy's blocks of 32
+    along its rows taking its tile's scale, so that both hold the same codes
+    (blockscaled.py:294-309, the mxfp8_2d recipe's weights)."""
+    if w.dtype == np.uint16:
+        w = bf16.to_f32(w)
+    values, exponents = in_e4m3(w, "tiles")
+    rows = np.repeat(exponents, MX_BLOCK, axis=0)
+    columns = np.repeat(exponents.T, MX_BLOCK, axis=0)
+    return Blocks(values, rows), Blocks(np.ascontiguousarray(values.T), np.ascontiguousarray(columns))
+
+
 def mx_twice(x: np.ndarray) -> tuple[Blocks, Blocks]:
     """Return x and x^T in MXFP8, each along its rows (blockscaled.py:282-291, the
     XLA branch)."""
@@ -189,6 +205,7 @@ def quantized_twice(
     columns: bool = True,
     index: np.ndarray | None = None,
     height: int | None = None,
+    tiles: bool = False,
 ) -> tuple[Blocks, Blocks | None]:
     """Return the MXFP8 copies a grouped GEMM's operand takes
     (grouped_blockscaled.py:296-317 off a Blackwell GPU; grouped_triton.py:44-101 for
@@ -203,6 +220,7 @@ def quantized_twice(
             kernel's meaning, grouped_triton.py:208-214); None for x itself.
         height: rows of the copies, padded by 0 past x's (``ragged_dot``'s padding to
             whole tiles of 128, grouped_blockscaled.py:122-128); None for x's own.
+        tiles: a scale per 32 x 32 tile, shared by both copies (`mx_tiles_twice`).
 
     Returns:
         The copies; a stack gives stacks (values (g, r, c) and (g, c, r)).
@@ -220,8 +238,13 @@ def quantized_twice(
     padded = np.zeros((g, h, c), np.float32)
     padded[:, :r] = stack
     kept = np.where((np.arange(h) < filled)[None, :, None], padded, np.float32(0))
-    rows_out = [mx_quantize(m) for m in kept]
-    cols_out = [mx_quantize(np.ascontiguousarray(m.T)) for m in kept] if columns else None
+    if tiles:
+        both = [mx_tiles_twice(m) for m in kept]
+        rows_out = [b[0] for b in both]
+        cols_out = [b[1] for b in both] if columns else None
+    else:
+        rows_out = [mx_quantize(m) for m in kept]
+        cols_out = [mx_quantize(np.ascontiguousarray(m.T)) for m in kept] if columns else None
 
     def stacked(parts: list[Blocks]) -> Blocks:
         if x.ndim == 2:

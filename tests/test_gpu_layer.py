@@ -120,6 +120,7 @@ LAYERS = [
     ("small_mxfp8", 1024, 4, 16, 256, 256, "swiglu", "mxfp8"),
     ("gptoss_like_mxfp8", 256, 4, 8, 1440, 1440, "clamped", "mxfp8"),
     ("empty_experts_mxfp8", 700, 2, 12, 128, 192, "swiglu", "mxfp8"),
+    ("small_mxfp8_2d", 1024, 4, 16, 256, 256, "swiglu", "mxfp8_2d"),
 ]
 
 # End to end, two float implementations of a quantized pipeline differ by more than

@@ -103,6 +103,24 @@ def test_a_stack_of_matrices_one_at_a_time(lib):
     _equal(got_cols, want_cols, "columns")
 
 
+@pytest.mark.parametrize("shape", [(5, 96, 160), (2, 2048, 1536), (3, 768, 2048), (1, 32, 32)])
+def test_weights_with_a_scale_per_32x32_tile(lib, shape):
+    """The mxfp8_2d recipe's W (blockscaled.mx_tiles_twice): each expert's matrix with a
+    scale per 32 x 32 tile, both copies the tile's; c3's W_up and W_down shapes
+    included (two experts of W_up, three of W_down), with outliers that set a tile's
+    scale apart from its row blocks'."""
+    rng = np.random.default_rng(15)
+    w = with_outliers(rng, normal_bf16(rng, shape, 0.02), 1e-3, 1e3)
+    announce("quantize tiles", shape)
+    got_rows, got_cols = _quantize(to_gpu_bf16(w), tiles=True)
+    want_rows, want_cols = mxfp8.quantized_twice(w, shape[1], True, tiles=True)
+    _equal(got_rows, want_rows, "rows")
+    _equal(got_cols, want_cols, "columns")
+    v_rows, _ = untiled(got_rows, shape[2])
+    v_cols, _ = untiled(got_cols, shape[1])
+    assert (v_cols == np.swapaxes(v_rows, -1, -2)).all()  # the same codes, transposed
+
+
 def test_only_the_rows_copy_or_only_the_columns_copy(lib):
     rng = np.random.default_rng(14)
     x = normal_bf16(rng, (64, 128))

@@ -83,6 +83,35 @@ def test_e4m3_values_are_torchs():
     np.testing.assert_array_equal(got[ok], want[ok])
 
 
+def test_a_tile_takes_the_least_power_of_two_that_fits_it():
+    """mx_tiles_twice: brute force over exponents for each 32 x 32 tile; both copies
+    hold the same codes, transposed, and their scale bytes repeat the tile's."""
+    rng = np.random.default_rng(10)
+    w = (rng.standard_normal((96, 64)) * rng.choice([1e-3, 1.0, 50.0], (96, 64))).astype(np.float32)
+    rows, cols = mxfp8.mx_tiles_twice(w)
+    assert (cols.values == rows.values.T).all()
+    for i in range(3):
+        for j in range(2):
+            tile = w[32 * i:32 * i + 32, 32 * j:32 * j + 32]
+            amax = float(np.abs(tile).max())
+            e = min(e for e in range(-126, 127) if amax <= 448.0 * 2.0**e)
+            assert (rows.scales[32 * i:32 * i + 32, j] == e + 127).all()
+            assert (cols.scales[32 * j:32 * j + 32, i] == e + 127).all()
+    deq = mxfp8.dequantized(rows).astype(np.float64)
+    assert np.allclose(deq, w, rtol=2.0**-4, atol=2.0**-9 * np.abs(w).max())
+
+
+def test_tiles_of_one_magnitude_quantize_as_row_blocks_do():
+    """Where every row block of a tile holds the tile's largest magnitude, the tile's
+    scale is each block's: the codes equal the 1 x 32 copies'."""
+    rng = np.random.default_rng(11)
+    w = rng.standard_normal((64, 96)).astype(np.float32)
+    w[:, ::32] = np.abs(w).reshape(64, 3, 32).max(-1).reshape(2, 32, 3).max(1).repeat(32, 0)
+    rows, _ = mxfp8.mx_tiles_twice(w)
+    plain = mxfp8.mx_quantize(w)
+    assert (rows.values == plain.values).all() and (rows.scales == plain.scales).all()
+
+
 def test_e8m0_values_are_torchs():
     """Every E8M0 byte (byte 0: 2^-127, 255: NaN) as torch's float8_e8m0fnu widens it."""
     want = torch.arange(256, dtype=torch.uint8).view(torch.float8_e8m0fnu).float().numpy()
