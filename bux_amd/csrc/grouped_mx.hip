@@ -51,7 +51,6 @@ namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 256;  // rows of a tile (A's)
 constexpr int BN = 256;  // columns of a tile (B's rows)
@@ -173,41 +172,6 @@ struct Lds {
 // bank once. Rows 16 apart share a swizzle, so blocks of 16 or 32 rows are copies of
 // one another at fixed offsets.
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
-
-// A raw buffer resource (stride 0) over `bytes` bytes from `base`; offsets past them
-// read 0.
-__device__ __forceinline__ i32x4 resource(const void* base, int64_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
-  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));
-  r[2] = __builtin_amdgcn_readfirstlane(
-      static_cast<int>(bytes > 0xffffffffLL ? 0xffffffffLL : bytes));
-  r[3] = 0x00020000;
-  return r;
-}
-
-// The LDS address of `p` (a location in the workgroup's LDS), as a scalar: the low word
-// of a flat pointer into the LDS aperture is the LDS address. (An address-space cast
-// would say the same but brings a null check, which hipcc fails to compile in some of
-// these kernels.)
-__device__ __forceinline__ uint32_t lds_at(const void* p) {
-  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
-}
-
-// buffer_load_dword{,x4} ... lds: lane i's 4 (16) bytes at the resource's base + voffset +
-// soffset land in LDS at M0 + 4 (16) i. Written as inline assembly so that the compiler
-// does not track these loads: left to itself it waits for every load in flight
-// (vmcnt(0)) before any LDS read that might alias their destinations, which undoes the
-// pipeline. The waves count them themselves (wait_loads).
-__device__ __forceinline__ void load_lds16(i32x4 rsrc, uint32_t lds, int voffset, int soffset) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :: "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory", "m0");
-}
-__device__ __forceinline__ void load_lds4(i32x4 rsrc, uint32_t lds, int voffset, int soffset) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               :: "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory", "m0");
-}
 
 // What a wave w loads of one operand's 256 rows from `row0` on: rows [64 w, 64 w + 64)
 // of the tile, as 4 slices of 16 rows x 64 bytes (each 1 KiB in one run; a lane takes

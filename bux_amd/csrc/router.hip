@@ -165,117 +165,13 @@ __device__ __forceinline__ float lanes_sum(float v) {
 // banks apart.
 __device__ __host__ __forceinline__ int pitch_of(int npad) { return npad + 8; }
 
-// SPLIT = 4 (at most 256 logits): wave w sums a quarter of K over every 32-column
-//   block, and the four partial sums meet in LDS, added in wave order.
-// SPLIT = 1 (wider): wave w sums all of K over the column blocks w, w + 4, ...
-// BLOCKS: the column blocks a wave holds. TOKS: tokens a workgroup, 32 or (at most 128
-// logits) 64, each row block of 32 taking the same kernel operands: the kernel's
-// bytes a token halve. CAP: the picks a list holds (k at most).
-template <int SPLIT, int BLOCKS, int TOKS, int CAP>
-__global__ __launch_bounds__(THREADS) void route_kernel(Params p) {
-  constexpr int RB = TOKS / 32, LANES = THREADS / TOKS;
-  extern __shared__ __align__(16) float lds[];  // SPLIT tiles of TOKS rows
-  __shared__ uint64_t kept_groups[TOKS];
-  const int pitch = pitch_of(p.npad);
-  float* tile = lds;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = lane & 31, h = lane >> 5;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TOKS;
-  const int nb = p.npad / 32;
-
-  // --- logits: rows past t load the last row (not stored)
-  {
-    constexpr int U = BLOCKS * RB <= 4 ? 4 : 2;  // K chunks of 16 a turn
-    const int64_t chunks = p.d / 16;
-    const int64_t c_lo = SPLIT == 4 ? chunks * wave / 4 : 0;
-    const int64_t c_hi = SPLIT == 4 ? chunks * (wave + 1) / 4 : chunks;
-    const uint16_t* xa[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int64_t tok = t0 + rb * 32 + r < p.t ? t0 + rb * 32 + r : p.t - 1;
-      xa[rb] = p.x + tok * p.d + 8 * h;
-    }
-    const uint16_t* kb[BLOCKS];
-    bool live[BLOCKS];
-#pragma unroll
-    for (int j = 0; j < BLOCKS; ++j) {
-      const int c = SPLIT == 4 ? j : wave + 4 * j;
-      live[j] = c < nb;
-      kb[j] = p.kt + static_cast<int64_t>((live[j] ? c : 0) * 32 + r) * p.d + 8 * h;
-    }
-    v16f acc[RB][BLOCKS];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int j = 0; j < BLOCKS; ++j) acc[rb][j] = v16f{};
-    int64_t c = c_lo;
-    for (; c + U <= c_hi; c += U) {
-      bf16x8 a[RB][U], b[BLOCKS][U];
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int u = 0; u < U; ++u) a[rb][u] = load8(xa[rb] + (c + u) * 16);
-#pragma unroll
-      for (int j = 0; j < BLOCKS; ++j)
-#pragma unroll
-        for (int u = 0; u < U; ++u) b[j][u] = live[j] ? load8(kb[j] + (c + u) * 16) : bf16x8{};
-#pragma unroll
-      for (int j = 0; j < BLOCKS; ++j)
-        if (live[j])
-#pragma unroll
-          for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-              acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb][u], b[j][u], acc[rb][j],
-                                                                   0, 0, 0);
-    }
-    for (; c < c_hi; ++c) {
-#pragma unroll
-      for (int j = 0; j < BLOCKS; ++j) {
-        if (!live[j]) continue;
-        const bf16x8 b = load8(kb[j] + c * 16);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-          acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(load8(xa[rb] + c * 16), b,
-                                                               acc[rb][j], 0, 0, 0);
-      }
-    }
-    // Lane l holds column l % 32 of a block, token rows 8 (q / 4) + 4 h + q % 4.
-    float* dst = SPLIT == 4 ? lds + wave * TOKS * pitch : tile;
-#pragma unroll
-    for (int j = 0; j < BLOCKS; ++j) {
-      const int col = (SPLIT == 4 ? j : wave + 4 * j) * 32 + r;
-      if (!live[j] || col >= p.n) continue;
-      const float bias = SPLIT == 1 && p.bias ? p.bias[col] : 0.0f;
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int row = rb * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
-          dst[row * pitch + col] =
-              SPLIT == 4 ? acc[rb][j][q] : (acc[rb][j][q] + bias) * p.logit_scale;
-        }
-    }
-  }
-  __syncthreads();
-  if (SPLIT == 4) {
-    for (int i = threadIdx.x; i < TOKS * p.n; i += THREADS) {
-      const int at = (i / p.n) * pitch + i % p.n;
-      const float v = ((lds[at] + lds[at + TOKS * pitch]) + lds[at + 2 * TOKS * pitch]) +
-                      lds[at + 3 * TOKS * pitch];
-      tile[at] = (v + (p.bias ? p.bias[i % p.n] : 0.0f)) * p.logit_scale;
-    }
-    __syncthreads();
-  }
-  if (p.logits) {
-    for (int i = threadIdx.x; i < TOKS * p.n; i += THREADS) {
-      const int row = i / p.n, col = i % p.n;
-      if (t0 + row < p.t) p.logits[(t0 + row) * p.n + col] = tile[row * pitch + col];
-    }
-    __syncthreads();  // copied before the scores overwrite them
-  }
-
-  // --- LANES lanes a token: lane s of token q takes the columns s, s + LANES, ...
+// Once the logits sit in `tile` (TOKS rows of `pitch` floats from token t0): the
+// scores, the group limit, the picks and the weights, LANES lanes a token.
+template <int TOKS, int CAP>
+__device__ __forceinline__ void select(const Params& p, float* tile, int pitch, int64_t t0,
+                                       uint64_t* kept_groups) {
+  constexpr int LANES = THREADS / TOKS;
+  // lane s of token q takes the columns s, s + LANES, ...
   const int q = threadIdx.x / LANES, s = threadIdx.x % LANES;
   float* row = tile + q * pitch;
   const int n = p.n, scored = p.scored;
@@ -388,6 +284,248 @@ __global__ __launch_bounds__(THREADS) void route_kernel(Params p) {
   }
 }
 
+// SPLIT = 4 (at most 256 logits): wave w sums a quarter of K over every 32-column
+//   block, and the four partial sums meet in LDS, added in wave order.
+// SPLIT = 1 (wider): wave w sums all of K over the column blocks w, w + 4, ...
+// BLOCKS: the column blocks a wave holds. TOKS: tokens a workgroup, 32 or (at most 128
+// logits) 64, each row block of 32 taking the same kernel operands: the kernel's
+// bytes a token halve. CAP: the picks a list holds (k at most).
+template <int SPLIT, int BLOCKS, int TOKS, int CAP>
+__global__ __launch_bounds__(THREADS) void route_kernel(Params p) {
+  constexpr int RB = TOKS / 32;
+  extern __shared__ __align__(16) float lds[];  // SPLIT tiles of TOKS rows
+  __shared__ uint64_t kept_groups[TOKS];
+  const int pitch = pitch_of(p.npad);
+  float* tile = lds;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TOKS;
+  const int nb = p.npad / 32;
+
+  // --- logits: rows past t load the last row (not stored)
+  {
+    constexpr int U = BLOCKS * RB <= 4 ? 4 : 2;  // K chunks of 16 a turn
+    const int64_t chunks = p.d / 16;
+    const int64_t c_lo = SPLIT == 4 ? chunks * wave / 4 : 0;
+    const int64_t c_hi = SPLIT == 4 ? chunks * (wave + 1) / 4 : chunks;
+    const uint16_t* xa[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int64_t tok = t0 + rb * 32 + r < p.t ? t0 + rb * 32 + r : p.t - 1;
+      xa[rb] = p.x + tok * p.d + 8 * h;
+    }
+    const uint16_t* kb[BLOCKS];
+    bool live[BLOCKS];
+#pragma unroll
+    for (int j = 0; j < BLOCKS; ++j) {
+      const int c = SPLIT == 4 ? j : wave + 4 * j;
+      live[j] = c < nb;
+      kb[j] = p.kt + static_cast<int64_t>((live[j] ? c : 0) * 32 + r) * p.d + 8 * h;
+    }
+    v16f acc[RB][BLOCKS];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int j = 0; j < BLOCKS; ++j) acc[rb][j] = v16f{};
+    int64_t c = c_lo;
+    for (; c + U <= c_hi; c += U) {
+      bf16x8 a[RB][U], b[BLOCKS][U];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int u = 0; u < U; ++u) a[rb][u] = load8(xa[rb] + (c + u) * 16);
+#pragma unroll
+      for (int j = 0; j < BLOCKS; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u) b[j][u] = live[j] ? load8(kb[j] + (c + u) * 16) : bf16x8{};
+#pragma unroll
+      for (int j = 0; j < BLOCKS; ++j)
+        if (live[j])
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+              acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb][u], b[j][u], acc[rb][j],
+                                                                   0, 0, 0);
+    }
+    for (; c < c_hi; ++c) {
+#pragma unroll
+      for (int j = 0; j < BLOCKS; ++j) {
+        if (!live[j]) continue;
+        const bf16x8 b = load8(kb[j] + c * 16);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(load8(xa[rb] + c * 16), b,
+                                                               acc[rb][j], 0, 0, 0);
+      }
+    }
+    // Lane l holds column l % 32 of a block, token rows 8 (q / 4) + 4 h + q % 4.
+    float* dst = SPLIT == 4 ? lds + wave * TOKS * pitch : tile;
+#pragma unroll
+    for (int j = 0; j < BLOCKS; ++j) {
+      const int col = (SPLIT == 4 ? j : wave + 4 * j) * 32 + r;
+      if (!live[j] || col >= p.n) continue;
+      const float bias = SPLIT == 1 && p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int row = rb * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
+          dst[row * pitch + col] =
+              SPLIT == 4 ? acc[rb][j][q] : (acc[rb][j][q] + bias) * p.logit_scale;
+        }
+    }
+  }
+  __syncthreads();
+  if (SPLIT == 4) {
+    for (int i = threadIdx.x; i < TOKS * p.n; i += THREADS) {
+      const int at = (i / p.n) * pitch + i % p.n;
+      const float v = ((lds[at] + lds[at + TOKS * pitch]) + lds[at + 2 * TOKS * pitch]) +
+                      lds[at + 3 * TOKS * pitch];
+      tile[at] = (v + (p.bias ? p.bias[i % p.n] : 0.0f)) * p.logit_scale;
+    }
+    __syncthreads();
+  }
+  if (p.logits) {
+    for (int i = threadIdx.x; i < TOKS * p.n; i += THREADS) {
+      const int row = i / p.n, col = i % p.n;
+      if (t0 + row < p.t) p.logits[(t0 + row) * p.n + col] = tile[row * pitch + col];
+    }
+    __syncthreads();  // copied before the scores overwrite them
+  }
+
+  select<TOKS, CAP>(p, tile, pitch, t0, kept_groups);
+}
+
+// s_waitcnt vmcnt(N) alone (gfx9's encoding: vmcnt's low bits at 3:0 and high bits at
+// 15:14, expcnt and lgkmcnt at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// The K loop staged through LDS (at most 256 logits, d a multiple of 64). A workgroup
+// takes 64 tokens; per step of 64 columns of K, the tokens' 128-byte row pieces (8 KiB)
+// and the transposed kernel's (128 CB rows, 16 CB KiB) go straight from global memory
+// into a stage of LDS (buffer_load ... lds, 1 KiB an instruction), STAGES - 1 steps
+// ahead, one barrier a step; wave w multiplies the 64 tokens by its CB blocks of 32
+// experts from LDS. A stage's rows are 128 bytes, their 16-byte chunk c at c ^ ((row
+// / 2) % 8), so the 16 lanes that read one chunk of 16 rows hit 16 different bank
+// groups; a load's lane i takes the chunk that belongs at its place. After the loop
+// the stages hold the logits tile.
+template <int CB, int CAP>
+__global__ __launch_bounds__(THREADS) void route_staged_kernel(Params p) {
+  constexpr int TOKS = 64;
+  constexpr int NPAD = 128 * CB;
+  constexpr int X_BYTES = TOKS * 128;
+  constexpr int STAGE = X_BYTES + NPAD * 128;
+  constexpr int STAGES = CB == 1 ? 4 : 3;
+  constexpr int LPS = TOKS / 32 + NPAD / 32;  // a wave's loads a step: 2 of x, 4 CB of kernel
+  extern __shared__ __align__(16) float lds[];
+  __shared__ uint64_t kept_groups[TOKS];
+  const int pitch = pitch_of(p.npad);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TOKS;
+  const uint32_t lds0 = lds_at(lds);
+  const int64_t row_bytes = p.d * 2;
+  // x from the workgroup's first token (past t reads 0), the kernel's padded rows
+  // (past npad read 0).
+  const i32x4 xr = resource(p.x + t0 * p.d, (p.t - t0) * row_bytes);
+  const i32x4 kr = resource(p.kt, static_cast<int64_t>(p.npad) * row_bytes);
+  // This lane's place in a 1 KiB slice of 8 rows, and the chunk that belongs there.
+  const int srow = lane >> 3, place = lane & 7;
+  auto voff = [&](int row) { return row * static_cast<int>(row_bytes) + 16 * (place ^ ((row >> 1) & 7)); };
+  int xoff[2], koff[4 * CB];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) xoff[j] = voff((2 * wave + j) * 8 + srow);
+#pragma unroll
+  for (int j = 0; j < 4 * CB; ++j) koff[j] = voff((wave * 4 * CB + j) * 8 + srow);
+  const int steps = static_cast<int>(p.d / 64);
+  auto issue = [&](int ks, int st) {
+    const uint32_t at = lds0 + st * STAGE;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      load_lds16_uniform(xr, at + (2 * wave + j) * 1024, xoff[j], ks * 128);
+#pragma unroll
+    for (int j = 0; j < 4 * CB; ++j)
+      load_lds16_uniform(kr, at + X_BYTES + (wave * 4 * CB + j) * 1024, koff[j], ks * 128);
+  };
+  // Lane offsets of the fragments: row block rb of x, expert block cb of the wave; the
+  // chunk of K sub-step u is 2 u + h.
+  auto frag_at = [&](int row, int u) { return row * 128 + 16 * ((2 * u + h) ^ ((row >> 1) & 7)); };
+  v16f acc[2][CB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
+  for (int s0 = 0; s0 < STAGES - 1 && s0 < steps; ++s0) issue(s0, s0);
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(lds);
+  for (int ks = 0; ks < steps; ++ks) {
+    const int later = steps - 1 - ks;  // steps issued after this one, at most STAGES - 2
+    if (later >= 2 && STAGES > 3) wait_vm<2 * LPS>();
+    else if (later >= 1) wait_vm<LPS>();
+    else wait_vm<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (ks + STAGES - 1 < steps) issue(ks + STAGES - 1, (ks + STAGES - 1) % STAGES);
+    const uint8_t* st = base + (ks % STAGES) * STAGE;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      bf16x8 a[2], b[CB];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+        a[rb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(st + frag_at(rb * 32 + r, u)));
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+        b[cb] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4*>(st + X_BYTES + frag_at((wave * CB + cb) * 32 + r, u)));
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb], b[cb], acc[rb][cb], 0, 0, 0);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every stage read
+  float* tile = lds;
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const int col = (wave * CB + cb) * 32 + r;
+    if (col >= p.n) continue;
+    const float bias = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int row = rb * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
+        tile[row * pitch + col] = (acc[rb][cb][q] + bias) * p.logit_scale;
+      }
+  }
+  __syncthreads();
+  if (p.logits) {
+    for (int i = threadIdx.x; i < TOKS * p.n; i += THREADS) {
+      const int row = i / p.n, col = i % p.n;
+      if (t0 + row < p.t) p.logits[(t0 + row) * p.n + col] = tile[row * pitch + col];
+    }
+    __syncthreads();  // copied before the scores overwrite them
+  }
+  select<TOKS, CAP>(p, tile, pitch, t0, kept_groups);
+}
+
+template <int CB, int CAP>
+int launch_staged(const Params& p, hipStream_t s) {
+  constexpr int STAGE = (64 + 128 * CB) * 128, STAGES = CB == 1 ? 4 : 3;
+  const size_t tile = static_cast<size_t>(64) * pitch_of(p.npad) * sizeof(float);
+  const size_t lds = tile > static_cast<size_t>(STAGES * STAGE) ? tile : STAGES * STAGE;
+  const void* kernel = reinterpret_cast<const void*>(route_staged_kernel<CB, CAP>);
+  hipError_t err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds));
+  if (err != hipSuccess) return fail(BUX_E_LAUNCH, "route_staged_kernel: %s", hipGetErrorString(err));
+  hipLaunchKernelGGL((route_staged_kernel<CB, CAP>), dim3(static_cast<unsigned>(ceil_div(p.t, 64))),
+                     dim3(THREADS), lds, s, p);
+  return launched("route_staged_kernel");
+}
+
 template <int SPLIT, int BLOCKS, int TOKS, int CAP>
 int launch(const Params& p, hipStream_t s) {
   const size_t lds = static_cast<size_t>(SPLIT) * TOKS * pitch_of(p.npad) * sizeof(float);
@@ -403,6 +541,8 @@ int launch(const Params& p, hipStream_t s) {
 template <int CAP>
 int launch_for(const Params& p, hipStream_t s) {
   const int nb = p.npad / 32;
+  if (p.d % 64 == 0 && nb <= 4) return launch_staged<1, CAP>(p, s);
+  if (p.d % 64 == 0 && nb <= 8) return launch_staged<2, CAP>(p, s);
   if (nb <= 1) return launch<4, 1, 64, CAP>(p, s);
   if (nb <= 2) return launch<4, 2, 64, CAP>(p, s);
   if (nb <= 4) return launch<4, 4, 64, CAP>(p, s);
