@@ -15,10 +15,13 @@ struct Act {
 };
 
 // The gate's activation a(g) and its derivative: g sigmoid(alpha g). jax multiplies
-// the bfloat16 gate by quick_gelu's 1.702 as a bfloat16 constant, 1.703125.
+// the bfloat16 gate by quick_gelu's 1.702 as a bfloat16 constant, 1.703125. The sigmoid
+// takes the hardware's 2^x and reciprocal (v_exp_f32, v_rcp_f32: a few float32 ulps,
+// far inside the one rounding to bfloat16 that follows); the precise library exp and
+// an IEEE division made the activation kernels VALU-bound (24% slower forward).
 __device__ __forceinline__ void activate(int kind, float g, float* a, float* da) {
   const float alpha = kind == BUX_QUICK_GELU ? 1.703125f : 1.0f;
-  const float s = 1.0f / (1.0f + expf(-alpha * g));
+  const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-alpha * g * 1.44269504f));
   *a = g * s;
   *da = s + alpha * g * s * (1.0f - s);
 }

@@ -49,9 +49,8 @@ constexpr int TILE_ROWS = 128;
 constexpr int TILE_COLS = 64;
 constexpr int THREADS = 256;
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
-}
+// Two float32 -> two bfloat16 (nearest even) by the hardware's conversion.
+__device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
 
 // A matrix of bfloat16 (matrix g of a stack), or its rows read by index.
 struct Matrix {
