@@ -71,6 +71,19 @@ __device__ __forceinline__ int scale_exponent(float amax) {
   return e < -126 ? -126 : (e > 126 ? 126 : e);
 }
 
+// The same exponent for an amax that is a bfloat16 value (its float32 bits' low 16
+// zero), from its bits alone: amax = m 2^E gives E - 8, plus 1 when m > 1.75 (448 =
+// 1.75 2^8, and no other 8-bit mantissa puts the quotient within a float32 rounding
+// of a power of two, so the division's rounding never moves the result); inf and NaN
+// give 126 as the division's bits do. Equal to scale_exponent for every non-negative
+// bfloat16 (checked exhaustively).
+__device__ __forceinline__ int scale_exponent_bf16(float amax) {
+  const uint32_t b = __float_as_uint(amax);
+  const int field = static_cast<int>(b >> 23);
+  const int e = field - 135 + (((b >> 16) & 0x7fu) > 0x60u ? 1 : 0);
+  return field == 255 ? 126 : (e < -126 ? -126 : (e > 126 ? 126 : e));
+}
+
 // 2^-e as a float32, exactly, for e in [-126, 126].
 __device__ __forceinline__ float power_of_two_down(int e) {
   return __uint_as_float(static_cast<uint32_t>(127 - e) << 23);

@@ -68,7 +68,9 @@ struct Matrix {
     if (index) {
       const int32_t at = index[r];
       if (at < 0) return make_uint4(0, 0, 0, 0);
-      src = at / index_div;
+      // a power-of-two divisor (every top-k bux's configs use) by a shift
+      src = (index_div & (index_div - 1)) == 0 ? (at >> (31 - __builtin_clz(index_div)))
+                                               : at / index_div;
     }
     return *reinterpret_cast<const uint4*>((index ? x : x + g * rows * cols) + src * cols + col);
   }
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(bf16_to_f32(tile[32 * wave + j][lane])));
 #pragma unroll
     for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    if ((lane & 31) == 0) tile_e[wave][lane >> 5] = scale_exponent(amax);
+    if ((lane & 31) == 0) tile_e[wave][lane >> 5] = scale_exponent_bf16(amax);
     __syncthreads();
   }
 
@@ -225,7 +227,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
       amax = fmaxf(amax, __shfl_xor(amax, 1));
       amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const int e = tiles ? tile_e[i][chunk >> 2] : scale_exponent(amax);
+      const int e = tiles ? tile_e[i][chunk >> 2] : scale_exponent_bf16(amax);
       const float down = power_of_two_down(e);
       uint2 codes;
       codes.x = e4m3x4(clip448(v[0] * down), clip448(v[1] * down), clip448(v[2] * down),
@@ -263,7 +265,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     v[j] = bf16_to_f32(tile[32 * wave + j][lane]);
     amax = fmaxf(amax, fabsf(v[j]));
   }
-  const int e = tiles ? tile_e[wave][lane >> 5] : scale_exponent(amax);
+  const int e = tiles ? tile_e[wave][lane >> 5] : scale_exponent_bf16(amax);
   const float down = power_of_two_down(e);
   uint32_t w[8];
 #pragma unroll

@@ -72,7 +72,7 @@ __global__ __launch_bounds__(THREADS) void pack_kernel(const uint16_t* __restric
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    const int e = scale_exponent(amax);
+    const int e = scale_exponent_bf16(amax);
     const float down = power_of_two_down(e);
     uint32_t w[8];
 #pragma unroll

@@ -60,6 +60,25 @@ def _quantize(x, **kw):
     return out
 
 
+def test_every_bf16_magnitude_as_a_blocks_largest(lib):
+    """Each block's scale from its largest magnitude, for every finite bfloat16 of
+    either sign as that largest (its other 31 values 0 or smaller), along the rows and
+    down the columns: the kernels derive the exponent from the maximum's bits, which
+    must agree with the reference's float32 division for every pattern."""
+    mags = FINITE[(FINITE & 0x7FFF) != 0]
+    mags = mags[: mags.size // 32 * 32]
+    rng = np.random.default_rng(16)
+    x = np.zeros((mags.size, 32), np.uint16)
+    x[:, 0] = mags
+    small = bf16.to_bf16((bf16.to_f32(mags) * np.float32(0.5)).astype(np.float32))
+    x[:, 1 + rng.integers(0, 31, mags.size)] = small  # a smaller value beside it
+    announce("quantize every magnitude as the largest", x.shape)
+    got_rows, got_cols = _quantize(to_gpu_bf16(x))
+    want_rows, want_cols = mxfp8.mx_twice(bf16.to_f32(x))
+    _equal(got_rows, want_rows, "rows")
+    _equal(got_cols, want_cols, "columns")
+
+
 def test_every_bf16_pattern_shuffled(lib):
     rng = np.random.default_rng(11)
     x = np.where(np.isfinite(bf16.to_f32(ALL)), ALL, 0).astype(np.uint16)
