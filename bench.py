@@ -2,9 +2,10 @@
 Qwen3-30B-A3B-shaped MXFP8 routed-experts layer, forward and backward.
 
 A step is one forward and backward of the layer (``bux_amd.moe.experts_forward`` then
-``experts_backward``) on synthetic inputs already resident in HBM: the sort by expert,
-12 MXFP8 quantizations, 6 grouped GEMMs, the activation and its gradient, and the
-token sums. `value` is the six GEMMs' algorithmic FLOP (2 M K N each, M = the picks)
+``experts_backward``) on synthetic inputs already resident in HBM, captured in a HIP
+graph and replayed (eager steps, timed too, give the per-op breakdown): the sort by
+expert, 12 MXFP8 quantizations, 6 grouped GEMMs, the activation and its gradient, and
+the token sums. `value` is the six GEMMs' algorithmic FLOP (2 M K N each, M = the picks)
 per second of the whole step. One JSON line on stdout; with `roofline` for the
 dominant kernel (per-op HIP events over the timed steps) and `cpu_baseline` (the CPU
 oracle on a bounded sample of the same layer, on this host's cores).
@@ -117,6 +118,37 @@ def step(z, idx, w, up, down, dy):
     out, saved = moe.experts_forward(z, idx, w, up, down)
     grads = moe.experts_backward(saved, dy, up, down)
     return out, grads
+
+
+def graph_step_ms(z, idx, w, up, down, dy, steps, warmup):
+    """The step captured once in a HIP graph (torch.cuda.CUDAGraph: the same kernels on
+    the same stream, launched without the host in between) and replayed: `warmup`
+    untimed replays, then `steps` timed between two synchronisations. Returns (ms a
+    step, how it was launched); (None, why) if the capture fails, and the eager time
+    stands."""
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step(z, idx, w, up, down, dy)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(z, idx, w, up, down, dy)
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        seconds = time.perf_counter() - start
+        log(f"timed {steps} graph replays in {seconds:.3f} s")
+        return seconds * 1e3 / steps, "hip graph of the whole step (per-op times: eager, HIP events)"
+    except RuntimeError as err:  # no capture here: the eager steps' time stands
+        log(f"graph capture failed ({err}); eager time stands")
+        return None, f"eager (graph capture failed: {str(err)[:120]})"
 
 
 def timed(fn, reps=20):
@@ -249,12 +281,14 @@ def main():
             step(z, idx, w, up, down, dy)
         torch.cuda.synchronize()
         seconds = time.perf_counter() - start
-    log(f"timed {args.steps} steps in {seconds:.3f} s")
+    log(f"timed {args.steps} eager steps in {seconds:.3f} s")
     ms = {name: float(np.mean(v)) for name, v in spans.milliseconds().items()}
     m = T * K
     flops = gemm_flops(m, D, F)
     total_flops = sum(flops.values())
-    ms_per_step = seconds * 1e3 / args.steps
+    eager_ms = seconds * 1e3 / args.steps
+    graph_ms, launch = graph_step_ms(z, idx, w, up, down, dy, args.steps, args.warmup)
+    ms_per_step = graph_ms if graph_ms is not None else eager_ms
     value = total_flops / (ms_per_step * 1e-3) / 1e12
     gemms = {name: {"ms": ms[name], "tflops": flops[name] / (ms[name] * 1e-3) / 1e12,
                     "frac_of_peak": flops[name] / (ms[name] * 1e-3) / 1e12 / PEAK_MXFP8_TFLOPS}
@@ -273,6 +307,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "launch": launch,
+        "ms_per_step_eager": round(eager_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
