@@ -1,5 +1,5 @@
-"""Benchmark of the MoE expert path on one MI355X: config 3 of BASELINE.json, the
-Qwen3-30B-A3B-shaped MXFP8 routed-experts layer, forward and backward.
+"""Benchmark of the MoE expert path on one MI355X: the headline configuration (config
+3), the Qwen3-30B-A3B-shaped MXFP8 routed-experts layer, forward and backward.
 
 A step is one forward and backward of the layer (``bux_amd.moe.experts_forward`` then
 ``experts_backward``) on synthetic inputs already resident in HBM, captured in a HIP
@@ -248,7 +248,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (the MoE expert "
-              "path would shard by expert over RCCL all-to-all; see DESIGN.md)", file=sys.stderr)
+              "path would shard by expert over an RCCL all-to-all of MXFP8 rows)", file=sys.stderr)
         sys.exit(2)
 
     from bux_amd import kernels
