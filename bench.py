@@ -203,6 +203,35 @@ def feed_ops(z, idx, e, k):
     return out
 
 
+def fused_up(z, idx, w, up, e, k):
+    """Time the up GEMM with the activation and h's two MXFP8 copies in its epilogue
+    (grouped_mxfp8.activated, one GEMM kernel and a small fix-up) against the step's
+    unfused pair (the rows GEMM, then the activation's quantizer) on the step's own
+    operands: the two give the same bits, so the faster one belongs in the step."""
+    from bux_amd import grouped_mxfp8, moe
+
+    t, d = z.shape
+    m = t * k
+    f = up.shape[2]
+    s = moe.sort_by_expert(idx, e)
+    height = grouped_mxfp8.whole(m)
+    x_k, _ = grouped_mxfp8.quantized_twice(z, s.filled, False, s.order, k, height)
+    _, up_k = grouped_mxfp8.quantized_twice(up.reshape(e, d, 2 * f))
+    row_weights = moe.picked_weights(w, s.order)
+    ffn = moe.Ffn()
+
+    def unfused():
+        projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m)
+        return moe.weighted_units_quantized(ffn, projected.view(m, f, 2), row_weights, s.filled,
+                                            height)
+
+    def fused():
+        return grouped_mxfp8.activated(x_k, up_k, s.sizes, row_weights, ffn.codes(), m)
+
+    return {"fused_ms": round(timed(fused), 4), "unfused_ms": round(timed(unfused), 4),
+            "used_in_step": "unfused"}
+
+
 def cpu_baseline():
     """The CPU oracle (numpy: float64/float32 quantizer, BLAS float32 GEMMs) on a bounded
     sample of config 3: 8 of its 128 experts with the same per-expert shape (1024
@@ -336,6 +365,7 @@ def main():
         "gemm_ms_per_step": round(sum(g["ms"] for g in gemms.values()), 4),
     }
     result["feed"] = feed_ops(z, idx, E, K)
+    result["fused_up_gemm"] = fused_up(z, idx, w, up, E, K)
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle on a sample of config 3 ...")
         result["cpu_baseline"] = cpu_baseline()

@@ -41,6 +41,10 @@ SIGNATURES = {
     "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _f32, _f32, _p, _p, _p]),
     "bux_glu_quantize": (
         _int, [_p, _p, _p, _i64, _i64, _int, _f32, _f32, _i64, _p, _p, _p, _p, _p, _p]),
+    "bux_mx_grouped_glu_workspace_size": (_size, [_i32, _i64]),
+    "bux_mx_grouped_glu": (
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p, _int, _f32, _f32, _p, _p,
+               _p, _p, _p, _p, _size, _p]),
     "bux_glu_backward_quantize_workspace_size": (_size, [_i64, _i64]),
     "bux_glu_backward_quantize": (
         _int, [_p, _p, _p, _p, _i64, _i64, _int, _f32, _f32, _i64, _p, _p, _p, _p, _p, _p, _p,

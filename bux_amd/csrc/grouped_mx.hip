@@ -45,6 +45,7 @@
 // group's B in its L2.
 
 #include "common.h"
+#include "glu.h"
 
 namespace bux {
 namespace {
@@ -95,12 +96,13 @@ __device__ int32_t block_scan(int32_t* data, int n, int32_t* partial) {
 
 // starts[g] for g <= groups (starts[groups] = sum of sizes), then, if `tiles`, the
 // tile list of `slots` entries: each group's rows in tiles of BM from its first row
-// (the last one partial), then the rows from the sum of sizes to `height` as group
-// `groups`, then empty tiles (0, 0, 0); and the number of tiles listed in
-// starts[groups + 1].
+// rounded down to a multiple of `align` (a power of two; the last tile partial), then
+// the rows from the sum of sizes to `height` as group `groups`, then empty tiles
+// (0, 0, 0); and the number of tiles listed in starts[groups + 1]. A tile (g, lo, hi)
+// computes rows [lo, lo + BM) and holds rows [max(lo, starts[g]), hi) of group g.
 __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __restrict__ sizes,
                                                            int32_t groups, int64_t height,
-                                                           int64_t slots,
+                                                           int64_t slots, int32_t align,
                                                            int32_t* __restrict__ starts_out,
                                                            Tile* __restrict__ tiles) {
   __shared__ int32_t starts[MAX_GROUPS + 2];
@@ -119,19 +121,23 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
     if (g < groups) return sizes[g];
     return height > filled ? height - filled : 0;
   };
-  for (int g = t; g < all; g += THREADS) {
+  // tiles of group g: from its first row rounded down to `align`
+  auto count_of = [&](int g) -> int64_t {
     const int64_t s = size_of(g);
-    before[g] = s > 0 ? static_cast<int32_t>((s + BM - 1) / BM) : 0;
-  }
+    if (s <= 0) return 0;
+    const int64_t start = starts[g], base = start & ~static_cast<int64_t>(align - 1);
+    return (start + s - base + BM - 1) / BM;
+  };
+  for (int g = t; g < all; g += THREADS) before[g] = static_cast<int32_t>(count_of(g));
   __syncthreads();
   const int32_t used = block_scan(before, all, partial);
   for (int g = t; g < all; g += THREADS) {
     const int64_t s = size_of(g), start = starts[g], end = start + s;
-    const int64_t count = s > 0 ? (s + BM - 1) / BM : 0;
+    const int64_t base = start & ~static_cast<int64_t>(align - 1), count = count_of(g);
     // Sizes summing past the rows there are would list more tiles than there are
     // slots: those are dropped, never written past the list.
     for (int64_t j = 0; j < count && before[g] + j < slots; ++j) {
-      const int64_t lo = start + j * BM;
+      const int64_t lo = base + j * BM;
       tiles[before[g] + j] = Tile{g, static_cast<int32_t>(lo),
                                   static_cast<int32_t>(end < lo + BM ? end : lo + BM)};
     }
@@ -428,10 +434,26 @@ __device__ void store_f32(const v16f acc[4][4], float* tile, int32_t ld, int32_t
 constexpr int PITCH = 272;
 static_assert(4 * 32 * PITCH == sizeof(Stage), "the epilogue's regions fill a stage");
 
-__device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int32_t rows,
-                           int32_t cols, Stage& stage) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
+// With LO, only the rows from row_lo on are stored.
+// The accumulators of a 32 x 32 block as bfloat16 pairs: run g's columns 0-1 and 2-3
+// (v_cvt_pk_bf16_f32: two floats to two bfloat16, nearest even).
+struct FromAcc {
+  const v16f (*acc)[4];
+  __device__ __forceinline__ uint2 operator()(int i, int j, int g) const {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const v16f& a = acc[i][j];
+    const bf16x2 lo = __builtin_convertvector((f32x2{a[4 * g], a[4 * g + 1]}), bf16x2);
+    const bf16x2 hi = __builtin_convertvector((f32x2{a[4 * g + 2], a[4 * g + 3]}), bf16x2);
+    return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+  }
+};
+
+// `pairs(i, j, g)`: the bfloat16 pairs of block (i, j), register run g. With LO, only
+// the rows from row_lo on are stored.
+template <bool LO = false, typename Pairs>
+__device__ void store_bf16(const Pairs& pairs, uint16_t* tile, int32_t ld, int32_t rows,
+                           int32_t cols, Stage& stage, int32_t row_lo = 0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   uint8_t* region = reinterpret_cast<uint8_t*>(&stage) + wave * 32 * PITCH;
@@ -444,7 +466,7 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
   uint16_t* out = tile + (wm * 128 + (lane >> 4)) * ld + col;
   // A whole tile (the common case) stores without bounds checks, through a buffer
   // resource from its corner: the lane's offset, a scalar one a row of stores.
-  const bool whole = rows >= BM && cols >= BN;
+  const bool whole = rows >= BM && cols >= BN && (!LO || row_lo <= 0);
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc(tile, 0, 0x7fffffff, 0x00020000);
   const int32_t lane_off = ((wm * 128 + (lane >> 4)) * ld + col) * 2;
@@ -453,14 +475,7 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const v16f& a = acc[i][j];
-        // v_cvt_pk_bf16_f32: two floats to two bfloat16, nearest even
-        const bf16x2 lo = __builtin_convertvector((f32x2{a[4 * g], a[4 * g + 1]}), bf16x2);
-        const bf16x2 hi = __builtin_convertvector((f32x2{a[4 * g + 2], a[4 * g + 3]}), bf16x2);
-        *reinterpret_cast<uint2*>(mine + (j * 4 + g) * 16) =
-            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-      }
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<uint2*>(mine + (j * 4 + g) * 16) = pairs(i, j, g);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
     // All 8 reads of the round go out before its first store.
@@ -476,7 +491,7 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int32_t row = wm * 128 + i * 32 + it * 4 + (lane >> 4);
-        if (row < rows) {
+        if (row < rows && (!LO || row >= row_lo)) {
           uint16_t* at = out + (i * 32 + it * 4) * ld;
           if (col + 8 <= cols) stream16(at, v[it]);
           else stream8(at, v[it].x, v[it].y);  // cols % 4 == 0
@@ -491,7 +506,7 @@ __device__ void store_bf16(const v16f acc[4][4], uint16_t* tile, int32_t ld, int
 
 __device__ __forceinline__ void store_tile(const v16f acc[4][4], uint16_t* tile, int32_t ld,
                                            int32_t rows, int32_t cols, Stage& stage) {
-  store_bf16(acc, tile, ld, rows, cols, stage);
+  store_bf16(FromAcc{acc}, tile, ld, rows, cols, stage);
 }
 __device__ __forceinline__ void store_tile(const v16f acc[4][4], float* tile, int32_t ld,
                                            int32_t rows, int32_t cols, Stage&) {
@@ -525,6 +540,18 @@ struct Job {
   bool mask;
   int64_t corner;
   int32_t rows, cols;
+  int32_t row_lo;  // the first of the tile's rows it stores (the fused epilogue's)
+};
+
+// The plain epilogue: the tile's rows [0, rows) and columns [0, cols) of a row-major
+// output of pitch ld, from its corner.
+template <typename T>
+struct Plain {
+  T* out;
+  int32_t ld;
+  __device__ __forceinline__ void store(const v16f acc[4][4], const Job& j, Stage& stage) const {
+    store_tile(acc, out + j.corner, ld, j.rows, j.cols, stage);
+  }
 };
 
 // The rows GEMM's tiles: the tile list's row tiles by 256-column tiles of y.
@@ -613,9 +640,9 @@ __device__ __forceinline__ void zero_acc(v16f acc[4][4]) {
 // (the next tile's first steps, issued during this tile's last ones, have landed by
 // then) and the next tile skips its waits for those steps; the first wait left (for
 // step 3) comes a few steps after the stores went out.
-template <typename T, typename Tiles>
+template <typename Out, typename Tiles>
 __device__ void run_tiles(const Tiles& tiles, int32_t count, const Operand& A, const Operand& B,
-                          Lds& lds, T* out, int32_t ld) {
+                          Lds& lds, const Out& out) {
   const Turns mine = turns(count);
   int32_t id = mine.first;
   Job job{}, next{};
@@ -696,7 +723,7 @@ __device__ void run_tiles(const Tiles& tiles, int32_t count, const Operand& A, c
     // the outputs.
     wait_loads(0);
     barrier_lds();
-    store_tile(acc, out + job.corner, ld, job.rows, job.cols, lds.st[stage(n + 3)]);
+    out.store(acc, job, lds.st[stage(n + 3)]);
     barrier_lds();
     if (!more) break;
     if (nn > 3) issue(na, nb, next.ks_begin + 3, lds0, stage(n + 3));
@@ -716,7 +743,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const RowsTiles list{tiles, groups, n, height, col_tiles, A.k / BK};
   const int32_t count = starts[groups + 1] * col_tiles;
-  run_tiles(list, count, A, B, lds, y, n);
+  run_tiles(list, count, A, B, lds, Plain<T>{y, n});
 }
 
 template <typename T>
@@ -727,7 +754,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const ContractTiles list{starts, A.rows, B.rows, d_tiles, f_tiles};
   const int32_t count = groups * d_tiles * f_tiles;
-  run_tiles(list, count, A, B, lds, dw, B.rows);
+  run_tiles(list, count, A, B, lds, Plain<T>{dw, B.rows});
 }
 
 // Lets a kernel take sizeof(Lds) (over 64 KiB) of dynamic LDS; gfx950 has 160 KiB a CU.
@@ -794,6 +821,276 @@ size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 // kernels' 32-bit buffer offsets.
 bool offsets_fit(int64_t rows, int64_t k) { return (rows + BM) * k < (1LL << 31); }
 
+// --- the fused activation: the up GEMM's tiles straight to h in MXFP8 ---------------
+//
+// bux_mx_grouped_glu is the rows GEMM of the experts' up projection followed by
+// bux_glu_quantize, in one kernel and a small second one: the epilogue stores the
+// product (bfloat16, which the backward takes), computes h = act(gate) (up + offset) w
+// from the product's bfloat16 values and the row's weight exactly as the activation
+// kernel does, and writes both of h's MXFP8 copies, so that no pass reads the product
+// back. (The reference fuses the same epilogue into its Blackwell up GEMM,
+// grouped_cudnn.activated, grouped_cudnn.py:161-205, for groups padded to 256 rows.)
+//
+// h's column copy takes absolute blocks of 32 rows. Tiles here start at each group's
+// first row rounded down to 32 (the rows before it, another group's, are computed and
+// not stored), so every block of the tile that the tile's group holds whole is
+// quantized in the epilogue. A block with a group's first row strictly inside it is no
+// tile's whole: glu_edges_kernel quantizes those (at most one a group) from the stored
+// product afterwards. The results are bit for bit those of the two unfused kernels.
+
+// The fused GEMM's tiles: the 32-aligned tile list by 256-column tiles of the product.
+struct GluTiles {
+  const Tile* tiles;
+  const int32_t* starts;
+  int32_t groups, n, height, col_tiles, k_steps;
+  __device__ bool job(int32_t id, Job& j) const {
+    const Tile t = tiles[id / col_tiles];
+    const int32_t hi = smaller(t.hi, height);
+    if (hi <= t.lo) return false;
+    const int32_t col0 = (id % col_tiles) * BN;
+    const int32_t first = starts[t.group];  // group `groups`: the groups' end
+    j.rows = hi - t.lo;
+    j.row_lo = first > t.lo ? first - t.lo : 0;
+    j.cols = smaller(n - col0, BN);
+    j.a_row0 = t.lo;
+    j.b_row0 = col0;
+    j.group = t.group < groups ? t.group : 0;
+    j.ks_begin = 0;
+    j.n = t.group < groups ? k_steps : 0;  // rows past the groups: zeros
+    j.mask = false;
+    j.mlo = j.mhi = 0;
+    j.corner = static_cast<int64_t>(t.lo) * n + col0;
+    return true;
+  }
+};
+
+// Two floats to two E4M3 codes in the low 16 bits (v_cvt_pk_fp8_f32).
+__device__ __forceinline__ uint32_t e4m3x2(float a, float b) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xffffu;
+}
+__device__ __forceinline__ float low_bf16(uint32_t p) { return bf16_to_f32(static_cast<uint16_t>(p & 0xffffu)); }
+__device__ __forceinline__ float high_bf16(uint32_t p) { return bf16_to_f32(static_cast<uint16_t>(p >> 16)); }
+
+// The fused epilogue's outputs. The product's columns are (up, gate) pairs of units:
+// unit u's up at column 2u, its gate at 2u + 1 (the experts' (f, 2) kernels flattened).
+struct GluOut {
+  const uint16_t* weights;  // bfloat16 (rows,): each row's weight
+  uint16_t* projected;      // bfloat16 (rows, n): the product
+  uint8_t* values;          // h along its units, tiled: codes (kf/64, height, 64)
+  uint8_t* scales;          //   and scale bytes (kf/128, height, 4)
+  uint8_t* t_values;        // h^T along the rows, tiled: codes (height/64, f, 64)
+  uint8_t* t_scales;        //   and scale bytes (height/128, f, 4)
+  Act act;
+  int32_t rows, n, f, height;
+  int32_t live;  // rows below it have values: min(the groups' end, rows); set on the device
+
+  // A wave's 128 rows x 64 units of the tile, 32 rows at a time: lane l holds row l % 32
+  // and, of each of its four 32-column accumulator blocks jj, units 16 jj + 4 g + 2 (l / 32)
+  // and + 1 (g = 0..3: the accumulator's registers 4 g .. 4 g + 3 are the two units' up
+  // and gate).
+  __device__ void store(const v16f acc[4][4], const Job& j, Stage& stage) const {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, half = lane >> 5, r32 = lane & 31;
+    const int32_t lo = j.a_row0, first = lo + j.row_lo, end = lo + j.rows;
+    float w[4];
+    bool on[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int32_t r = lo + wm * 128 + i * 32 + r32;
+      on[i] = r >= first && r < end && r < live;
+      w[i] = on[i] ? bf16_to_f32(weights[r]) : 0.0f;
+    }
+    // the product as stored, bfloat16 pairs (unit u's up and gate): the accumulators are
+    // read once
+    uint2 pk[4][4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) pk[i][jj][g] = FromAcc{acc}(i, jj, g);
+    // rows [first, min(end, rows))
+    store_bf16<true>([&](int i, int jj, int g) { return pk[i][jj][g]; }, projected + j.corner, n,
+                     smaller(end, rows) - lo, j.cols, stage, j.row_lo);
+    const int32_t u0 = (j.b_row0 >> 1) + wn * 64;  // the wave's first unit
+    // h of 32 rows x 64 units in this wave's part of the stage, a row 33 words apart
+    uint32_t* region = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(&stage) +
+                                                   wave * 32 * PITCH);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // one block of 32 rows at a time: nothing of the next is computed ahead
+      __builtin_amdgcn_sched_barrier(0);
+      const int32_t r0 = lo + wm * 128 + i * 32, r = r0 + r32;
+      uint32_t hp[4][4];  // h of units 16 jj + 4 g + 2 half, + 1: a bfloat16 pair
+      float amax[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t p0 = pk[i][jj][g].x, p1 = pk[i][jj][g].y;
+          const int32_t u = u0 + 16 * jj + 4 * g + 2 * half;
+          float h0 = 0.0f, h1 = 0.0f;
+          if (on[i] && u < f) {
+            h0 = glu_unit(act, low_bf16(p0), high_bf16(p0), w[i]);
+            h1 = glu_unit(act, low_bf16(p1), high_bf16(p1), w[i]);
+          }
+          hp[jj][g] = pack_bf16x2(h0, h1);
+          amax[jj >> 1] = fmaxf(amax[jj >> 1],
+                                fmaxf(fabsf(low_bf16(hp[jj][g])), fabsf(high_bf16(hp[jj][g]))));
+        }
+
+      // h along its units: the wave's blocks of 32 units of row r are jj 0-1 and 2-3,
+      // each half in this lane and half in lane l ^ 32
+#pragma unroll
+      for (int b = 0; b < 2; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 32));
+      const int e0 = scale_exponent_bf16(amax[0]), e1 = scale_exponent_bf16(amax[1]);
+      const float down0 = power_of_two_down(e0), down1 = power_of_two_down(e1);
+      uint32_t piece[4][4];  // the two codes of hp[jj][g]
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float down = jj < 2 ? down0 : down1;
+          piece[jj][g] = e4m3x2(clip448(low_bf16(hp[jj][g]) * down),
+                                clip448(high_bf16(hp[jj][g]) * down));
+        }
+      // Lane half 0 gathers block 0's 32 codes, half 1 block 1's: each sends the other
+      // its pieces of the other's block. Word t of a block is units 4 t .. 4 t + 3, half
+      // 0's piece of (jj, g) = (t / 4, t % 4) then half 1's.
+      uint32_t sent[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t0 = 2 * q, t1 = 2 * q + 1;
+        const uint32_t a0 = half ? piece[t0 >> 2][t0 & 3] : piece[2 + (t0 >> 2)][t0 & 3];
+        const uint32_t a1 = half ? piece[t1 >> 2][t1 & 3] : piece[2 + (t1 >> 2)][t1 & 3];
+        sent[q] = __shfl_xor(a0 | (a1 << 16), 32);
+      }
+      uint32_t word[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t mine = half ? piece[2 + (t >> 2)][t & 3] : piece[t >> 2][t & 3];
+        const uint32_t other = (sent[t >> 1] >> (16 * (t & 1))) & 0xffffu;
+        word[t] = half ? (other | (mine << 16)) : (mine | (other << 16));
+      }
+      if (r >= first && r < end) {
+        uint4* at = reinterpret_cast<uint4*>(
+            values + (static_cast<int64_t>(u0 >> 6) * height + r) * 64 + 32 * half);
+        at[0] = make_uint4(word[0], word[1], word[2], word[3]);
+        at[1] = make_uint4(word[4], word[5], word[6], word[7]);
+        scales[(static_cast<int64_t>(j.b_row0 >> 8) * height + r) * 4 + 2 * wn + half] =
+            static_cast<uint8_t>((half ? e1 : e0) + 127);
+      }
+
+      // h^T along the rows: the 32-row block from r0 if this tile holds all of it.
+      // Through the region: lane (pu, rh) reads units u0 + 2 pu, + 1 of rows 16 rh ..
+      // 16 rh + 15 and writes their 16 codes, half of each unit's 32.
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) region[r32 * 33 + 8 * jj + 2 * g + half] = hp[jj][g];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      if (r0 >= first && r0 + 32 <= end) {
+        const int pu = lane & 31, rh = lane >> 5;
+        uint32_t v[16];
+        float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          v[k] = region[(16 * rh + k) * 33 + pu];
+          m0 = fmaxf(m0, fabsf(low_bf16(v[k])));
+          m1 = fmaxf(m1, fabsf(high_bf16(v[k])));
+        }
+        m0 = fmaxf(m0, __shfl_xor(m0, 32));
+        m1 = fmaxf(m1, __shfl_xor(m1, 32));
+        const int t0 = scale_exponent_bf16(m0), t1 = scale_exponent_bf16(m1);
+        const float d0 = power_of_two_down(t0), d1 = power_of_two_down(t1);
+        uint32_t c0[4], c1[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          c0[q] = e4m3x4(clip448(low_bf16(v[4 * q]) * d0), clip448(low_bf16(v[4 * q + 1]) * d0),
+                         clip448(low_bf16(v[4 * q + 2]) * d0), clip448(low_bf16(v[4 * q + 3]) * d0));
+          c1[q] = e4m3x4(clip448(high_bf16(v[4 * q]) * d1), clip448(high_bf16(v[4 * q + 1]) * d1),
+                         clip448(high_bf16(v[4 * q + 2]) * d1), clip448(high_bf16(v[4 * q + 3]) * d1));
+        }
+        const int32_t u = u0 + 2 * pu;
+        if (u < f) {
+          uint8_t* at = t_values + (static_cast<int64_t>(r0 >> 6) * f + u) * 64 + (r0 & 63) + 16 * rh;
+          *reinterpret_cast<uint4*>(at) = make_uint4(c0[0], c0[1], c0[2], c0[3]);
+          *reinterpret_cast<uint4*>(at + 64) = make_uint4(c1[0], c1[1], c1[2], c1[3]);
+          if (rh == 0) {
+            uint8_t* sc = t_scales + (static_cast<int64_t>(r0 >> 7) * f + u) * 4 + ((r0 >> 5) & 3);
+            sc[0] = static_cast<uint8_t>(t0 + 127);
+            sc[4] = static_cast<uint8_t>(t1 + 127);
+          }
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+};
+
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void glu_kernel(
+    Operand A, Operand B, int32_t groups, int32_t height, const int32_t* __restrict__ starts,
+    const Tile* __restrict__ tiles, int32_t col_tiles, GluOut out) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  Lds& lds = *reinterpret_cast<Lds*>(smem);
+  const GluTiles list{tiles, starts, groups, B.rows, height, col_tiles, A.k / BK};
+  out.live = smaller(starts[groups], out.rows);
+  const int32_t count = starts[groups + 1] * col_tiles;
+  run_tiles(list, count, A, B, lds, out);
+}
+
+// h^T's blocks of 32 rows with a group's first row strictly inside, which no tile holds
+// whole: quantized from the stored product as bux_glu_quantize does (rows from the
+// groups' end, or from `rows`, are 0). Workgroup g takes the block of group g's first
+// row (g = groups: the groups' end), unless group g - 1's first row is inside the same
+// block too.
+__global__ __launch_bounds__(THREADS) void glu_edges_kernel(
+    const int32_t* __restrict__ starts, int32_t groups, const uint16_t* __restrict__ projected,
+    const uint16_t* __restrict__ weights, Act act, int32_t rows, int32_t f, int32_t height,
+    uint8_t* __restrict__ t_values, uint8_t* __restrict__ t_scales) {
+  const int g = blockIdx.x;
+  const int32_t first = starts[g];
+  if ((first & 31) == 0 || first >= height) return;
+  if (g > 0) {
+    const int32_t before = starts[g - 1];
+    if ((before & 31) != 0 && (before >> 5) == (first >> 5)) return;
+  }
+  const int32_t live = smaller(starts[groups], rows), r0 = first & ~31;
+  for (int32_t u = threadIdx.x; u < f; u += THREADS) {
+    float v[32], amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      const int32_t r = r0 + k;
+      float h = 0.0f;
+      if (r < live) {
+        const uint32_t p = *reinterpret_cast<const uint32_t*>(projected + (static_cast<int64_t>(r) * f + u) * 2);
+        h = low_bf16(pack_bf16x2(glu_unit(act, low_bf16(p), high_bf16(p), bf16_to_f32(weights[r])), 0.0f));
+      }
+      v[k] = h;
+      amax = fmaxf(amax, fabsf(h));
+    }
+    const int e = scale_exponent_bf16(amax);
+    const float down = power_of_two_down(e);
+    uint32_t c[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      c[q] = e4m3x4(clip448(v[4 * q] * down), clip448(v[4 * q + 1] * down),
+                    clip448(v[4 * q + 2] * down), clip448(v[4 * q + 3] * down));
+    uint8_t* at = t_values + (static_cast<int64_t>(r0 >> 6) * f + u) * 64 + (r0 & 63);
+    *reinterpret_cast<uint4*>(at) = make_uint4(c[0], c[1], c[2], c[3]);
+    *reinterpret_cast<uint4*>(at + 16) = make_uint4(c[4], c[5], c[6], c[7]);
+    t_scales[(static_cast<int64_t>(r0 >> 7) * f + u) * 4 + ((r0 >> 5) & 3)] = static_cast<uint8_t>(e + 127);
+  }
+}
+
+// Tiles of the 32-aligned list: tiles of the height's rows plus, a group (and the rows
+// past them), one more and the up to 31 rows before its first.
+int64_t glu_slots(int32_t groups, int64_t height) {
+  return ceil_div(height + 32 * static_cast<int64_t>(groups + 1), BM) + groups + 1;
+}
+
 }  // namespace
 }  // namespace bux
 
@@ -836,7 +1133,7 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
                                         align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)));
   const int64_t slots = row_slots(groups, m, height);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
-                     starts, tiles);
+                     1, starts, tiles);
   if (int rc = launched("prologue_kernel")) return rc;
   // Rows of the groups past a's m rows read 0 (the resource ends there) or the
   // following K chunk's rows: a's m must cover every row the groups hold.
@@ -877,12 +1174,78 @@ extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a
                 workspace_bytes, need);
   hipStream_t s = as_stream(stream);
   int32_t* starts = static_cast<int32_t*>(workspace);
-  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, starts,
-                     nullptr);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
+                     starts, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   // The operands' K is m: each of a's d rows (b's f rows) is m bytes.
   const Operand A{a_values, a_scales, static_cast<int32_t>(m), static_cast<int32_t>(d)};
   const Operand B{b_values, b_scales, static_cast<int32_t>(m), static_cast<int32_t>(f)};
   return out_dtype == BUX_BF16 ? launch_contract<uint16_t>(A, B, groups, starts, dw, s)
                                : launch_contract<float>(A, B, groups, starts, dw, s);
+}
+
+extern "C" size_t bux_mx_grouped_glu_workspace_size(int32_t groups, int64_t height) {
+  using namespace bux;
+  return align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)) +
+         static_cast<size_t>(glu_slots(groups, height)) * sizeof(Tile);
+}
+
+extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scales,
+                                  const uint8_t* b_values, const uint8_t* b_scales,
+                                  const int32_t* sizes, int32_t groups, int64_t height, int64_t n,
+                                  int64_t k, int64_t rows, const uint16_t* weights, int activation,
+                                  float limit, float up_offset, uint16_t* projected,
+                                  uint8_t* values, uint8_t* scales, uint8_t* t_values,
+                                  uint8_t* t_scales, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "bux_mx_grouped_glu: groups=%d outside [1, %d]",
+            groups, MAX_GROUPS);
+  BUX_CHECK(height >= 0 && height % 128 == 0 && height < (1LL << 31) && n > 0 && n % 64 == 0 &&
+                k > 0 && k % 128 == 0 && rows >= 0 && rows <= height,
+            "bux_mx_grouped_glu: bad shape height=%lld n=%lld k=%lld rows=%lld (height a "
+            "multiple of 128, n of 64, k of 128, rows at most height)",
+            (long long)height, (long long)n, (long long)k, (long long)rows);
+  BUX_CHECK(offsets_fit(height, k) && offsets_fit(n, k),
+            "bux_mx_grouped_glu: an operand of %lld x %lld bytes exceeds 2 GiB",
+            (long long)(height > n ? height : n), (long long)k);
+  BUX_CHECK(activation == BUX_SWISH || activation == BUX_QUICK_GELU,
+            "bux_mx_grouped_glu: activation %d is neither BUX_SWISH nor BUX_QUICK_GELU", activation);
+  BUX_CHECK(sizes && b_values && b_scales &&
+                (height == 0 || (a_values && a_scales && values && scales && t_values && t_scales)) &&
+                (rows == 0 || (weights && projected)),
+            "bux_mx_grouped_glu: NULL buffer");
+  const size_t need = bux_mx_grouped_glu_workspace_size(groups, height);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(BUX_E_WORKSPACE, "bux_mx_grouped_glu: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  if (height == 0) return BUX_OK;
+  hipStream_t s = as_stream(stream);
+  int32_t* starts = static_cast<int32_t*>(workspace);
+  Tile* tiles = reinterpret_cast<Tile*>(static_cast<uint8_t*>(workspace) +
+                                        align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)));
+  const int64_t slots = glu_slots(groups, height);
+  const int64_t col_tiles = ceil_div(n, BN);
+  if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_glu: too many tiles");
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
+                     32, starts, tiles);
+  if (int rc = launched("prologue_kernel")) return rc;
+  const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(height)};
+  const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};
+  const Act act{activation, limit, up_offset};
+  const int32_t f = static_cast<int32_t>(n / 2);
+  const GluOut out{weights, projected, values, scales, t_values, t_scales, act,
+                   static_cast<int32_t>(rows), static_cast<int32_t>(n), f,
+                   static_cast<int32_t>(height), 0};
+  unsigned blocks = 0;
+  if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
+  if (int rc = allow_lds(glu_kernel, "glu_kernel")) return rc;
+  hipLaunchKernelGGL(glu_kernel, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+                     static_cast<int32_t>(height), starts, tiles, static_cast<int32_t>(col_tiles), out);
+  if (int rc = launched("glu_kernel")) return rc;
+  hipLaunchKernelGGL(glu_edges_kernel, dim3(static_cast<unsigned>(groups + 1)), dim3(THREADS), 0, s,
+                     starts, groups, projected, weights, act, static_cast<int32_t>(rows), f,
+                     static_cast<int32_t>(height), t_values, t_scales);
+  return launched("glu_edges_kernel");
 }

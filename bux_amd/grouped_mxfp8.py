@@ -7,7 +7,9 @@ Mirrors, with the same argument meanings:
   (src/bux/architecture/experts/grouped_triton.py:44-101), the semantics of
   ``blockscaled.mx_twice`` (src/bux/architecture/precision/blockscaled.py:282-356);
 - `rows`: ``grouped_mxfp8.rows`` (src/bux/architecture/experts/grouped_mxfp8.py:116-154);
-- `contract`: ``grouped_mxfp8.contract`` (grouped_mxfp8.py:185-210).
+- `contract`: ``grouped_mxfp8.contract`` (grouped_mxfp8.py:185-210);
+- `activated`: ``grouped_cudnn.activated`` (grouped_cudnn.py:161-205), the up GEMM with
+  the activation and h's two MXFP8 copies in its epilogue.
 
 Operands are `Tiled`: a matrix's MXFP8 blocks along its rows (the reference's
 ``Blocks``, src/bux/architecture/precision/blockscaled.py:43-56) in the layout the
@@ -184,6 +186,51 @@ def rows(
         ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(sizes), groups, m, n, k,
         h, _DTYPES[out], ptr(y), ptr(ws), ws.numel(), stream()))
     return y
+
+
+def activated(
+    a: Tiled, b: Tiled, sizes: torch.Tensor, weights: torch.Tensor, codes: tuple[int, float, float],
+    rows: int,
+) -> tuple[torch.Tensor, Tiled, Tiled]:
+    """Return the up GEMM's product ``a @ b[g]^T`` (rows, n) and h, its activation times
+    each row's weight, in MXFP8 along its units and, as h^T, along the rows: the
+    reference's ``grouped_cudnn.activated`` (grouped_cudnn.py:161-205), for groups as they
+    lie. The same bits as `rows` followed by the activation's quantizer.
+
+    Args:
+        a: the rows (height of K), group 0's first: its height is the copies'.
+        b: the groups' up kernels (g, n, K), columns in (up, gate) pairs.
+        sizes: int32 (g,) on the device.
+        weights: bfloat16 (rows,): each row's weight.
+        codes: the activation (kind, limit, up_offset) as ``Ffn.codes`` gives it.
+        rows: rows of the product (at most a's height).
+    """
+    require(a.values, a.scales, b.values, b.scales, sizes, weights)
+    if a.values.dim() != 3 or b.values.dim() != 4:
+        raise ValueError(f"activated: a {tuple(a.values.shape)} is not one matrix or "
+                         f"b {tuple(b.values.shape)} not a stack")
+    height, k = a.height, a.k
+    groups, n = b.values.shape[0], b.height
+    if b.k != k or sizes.shape != (groups,) or sizes.dtype != torch.int32:
+        raise ValueError(f"activated: a {tuple(a.values.shape)}, b {tuple(b.values.shape)}, "
+                         f"sizes {tuple(sizes.shape)} {sizes.dtype}")
+    if weights.dtype != torch.bfloat16 or weights.numel() < rows:
+        raise ValueError(f"activated: weights {weights.dtype} of {weights.numel()} for {rows} rows")
+    f = n // 2
+    dev = a.values.device
+    kf = whole(f, K_ALIGN)
+    projected = torch.empty(rows, n, dtype=torch.bfloat16, device=dev)
+    vals = torch.empty(kf // 64, height, 64, dtype=torch.uint8, device=dev)
+    scales = torch.empty(kf // 128, height, 4, dtype=torch.uint8, device=dev)
+    t_vals = torch.empty(height // 64, f, 64, dtype=torch.uint8, device=dev)
+    t_scales = torch.empty(height // 128, f, 4, dtype=torch.uint8, device=dev)
+    ws = workspace(lib().bux_mx_grouped_glu_workspace_size(groups, height), dev)
+    kind, limit, offset = codes
+    _lib.check(lib().bux_mx_grouped_glu(
+        ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(sizes), groups, height, n,
+        k, rows, ptr(weights.contiguous()), kind, limit, offset, ptr(projected), ptr(vals),
+        ptr(scales), ptr(t_vals), ptr(t_scales), ptr(ws), ws.numel(), stream()))
+    return projected, Tiled(vals, scales), Tiled(t_vals, t_scales)
 
 
 def contract(

@@ -209,6 +209,7 @@ class Saved(NamedTuple):
 def experts_forward(
     z: torch.Tensor, idx: torch.Tensor, weights: torch.Tensor, up: torch.Tensor,
     down: torch.Tensor, ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
+    fused: bool = False,
 ) -> tuple[torch.Tensor, Saved]:
     """Return the routed experts' output (t, d), bfloat16, and what the backward takes.
     In MXFP8 the activation goes straight to its quantized copies; with `intermediates`
@@ -225,6 +226,9 @@ def experts_forward(
             what its GEMM contracts), "mxfp8_2d" (the same, but each W with a scale per
             32 x 32 tile, shared by its two copies: blockscaled.MXFP8_2D,
             blockscaled.py:306-309), or "compute" for bfloat16 GEMMs.
+        fused: in MXFP8 (without `intermediates`), the activation and h's two copies in
+            the up GEMM's epilogue (`grouped_mxfp8.activated`): the same bits, in one
+            GEMM kernel instead of the GEMM and the activation's quantizer.
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -243,17 +247,24 @@ def experts_forward(
             x_k, x_m = grouped_mxfp8.quantized_twice(z, filled, True, s.order, k, height)
         with span("quantize W_up"):
             up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
-        with span("up fprop"):
-            projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m)
+        if fused and not intermediates:
+            with span("up fprop + activation + quantize h"):
+                projected, h_k, h_m = grouped_mxfp8.activated(x_k, up_k, s.sizes, row_weights,
+                                                              ffn.codes(), m)
+            h = None
+        else:
+            with span("up fprop"):
+                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m)
     else:
         with span("gather x"):
             rows = token_rows(z, s.order, k)
         with span("up fprop"):
             projected = grouped.dot(rows, up2, s.sizes)
     if mx:
-        with span("activation + quantize h"):
-            h_k, h_m, h = weighted_units_quantized(ffn, projected.view(m, f, p), row_weights,
-                                                   filled, height, intermediates)
+        if not (fused and not intermediates):
+            with span("activation + quantize h"):
+                h_k, h_m, h = weighted_units_quantized(ffn, projected.view(m, f, p), row_weights,
+                                                       filled, height, intermediates)
         with span("quantize W_down"):
             down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
         with span("down fprop"):

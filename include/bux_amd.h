@@ -232,6 +232,28 @@ int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights, const i
                      int64_t m, int64_t f, int activation, float limit, float up_offset,
                      int64_t height, uint16_t* h, uint8_t* values, uint8_t* scales,
                      uint8_t* t_values, uint8_t* t_scales, void* stream);
+/* bux_mx_grouped_glu: the experts' up GEMM with the activation and both MXFP8 copies
+ *   of h in its epilogue, the reference's fused up GEMM (grouped_cudnn.activated,
+ *   src/bux/architecture/experts/grouped_cudnn.py:161-205), but for groups as they lie
+ *   (no padding of each to 256 rows). The same outputs, bit for bit, as
+ *   bux_mx_grouped_rows(a, b, sizes, m = height, n, k, height = rows) into projected,
+ *   then bux_glu_quantize(projected, weights, filled = sum(sizes), rows, n / 2, ...,
+ *   height):
+ *   a_values/a_scales  x in MXFP8 along its rows, tiled, height rows of k bytes;
+ *   b_values/b_scales  each expert's (n, k) up kernels, tiled; n = 2 f, columns in
+ *     (up, gate) pairs; f a multiple of 32;
+ *   projected  bfloat16 [rows, n] (rows <= height; past sum(sizes): 0);
+ *   values/scales  h along its units (K = f rounded up to 128), height rows;
+ *   t_values/t_scales  h^T along the rows (K = height, a multiple of 128), f rows;
+ *   workspace  bux_mx_grouped_glu_workspace_size(groups, height) bytes.
+ */
+size_t bux_mx_grouped_glu_workspace_size(int32_t groups, int64_t height);
+int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
+                       const uint8_t* b_scales, const int32_t* sizes, int32_t groups,
+                       int64_t height, int64_t n, int64_t k, int64_t rows,
+                       const uint16_t* weights, int activation, float limit, float up_offset,
+                       uint16_t* projected, uint8_t* values, uint8_t* scales, uint8_t* t_values,
+                       uint8_t* t_scales, void* workspace, size_t workspace_bytes, void* stream);
 size_t bux_glu_backward_quantize_workspace_size(int64_t m, int64_t f);
 int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights,
                               const uint16_t* dh, const int32_t* filled, int64_t m, int64_t f,

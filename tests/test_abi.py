@@ -94,6 +94,25 @@ def test_gemms_reject_bad_shapes_and_small_workspaces(lib):
     assert rc == 1 and "multiples of 8" in _msg(lib)
 
 
+def test_fused_up_gemm_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    ws = lib.bux_mx_grouped_glu_workspace_size(4, 256)
+    # group starts, then tiles of 256 rows with up to 31 more a group, one more a group
+    assert ws >= (-(-(256 + 32 * 5) // 256) + 5) * 12
+
+    def glu(height=256, n=128, k=128, rows=200, act=0, ws_bytes=1 << 20, groups=4):
+        return lib.bux_mx_grouped_glu(p, p, p, p, p, groups, height, n, k, rows, p, act, 0.0, 0.0,
+                                      p, p, p, p, p, p, ws_bytes, None)
+
+    assert glu(height=200) == 1 and "height=200" in _msg(lib)  # whole 128s: h^T's K
+    assert glu(n=96) == 1 and "n=96" in _msg(lib)  # (up, gate) pairs of f, a multiple of 32
+    assert glu(k=64) == 1 and "k=64" in _msg(lib)
+    assert glu(rows=300) == 1 and "rows=300" in _msg(lib)  # the product within the copies
+    assert glu(act=5) == 1 and "activation 5" in _msg(lib)
+    assert glu(groups=0) == 1 and "groups=0" in _msg(lib)
+    assert glu(ws_bytes=8) == 2 and "workspace" in _msg(lib)
+
+
 def test_permute_and_token_ops_reject_bad_arguments(lib):
     p = ctypes.c_void_p(16)
     rc = lib.bux_moe_permute(p, 100, 0, p, p, p, p, p, 1 << 20, None)

@@ -1,0 +1,130 @@
+"""The fused up GEMM (`grouped_mxfp8.activated`, the reference's
+grouped_cudnn.activated, grouped_cudnn.py:161-205) against the unfused kernels it
+replaces: the rows GEMM into the product, then the activation's quantizer. Both run on
+the same GPU operands; the fused kernel must give the same bits in every output (the
+product, h along its units, h^T along the rows). The unfused pair is pinned against
+the oracle by test_gpu_gemm.py and test_gpu_layer.py.
+
+The cases move the groups' first rows off the 32-row blocks of h^T (whose blocks with a
+group's first row inside go through the fix-up kernel), hold empty groups, groups
+smaller than a block and several groups' first rows inside one block, rows past the
+groups (zeros), a hidden width that is not a whole number of 128s (the row copy's K
+padding) and both activations."""
+
+import numpy as np
+import pytest
+import torch
+
+from tests._util import announce
+
+pytestmark = pytest.mark.gpu
+
+# (sizes, rows, d, f, activation)
+CASES = [
+    ([0, 130, 1, 3, 256, 0, 300, 100, 29], 900, 256, 160, "swiglu"),
+    ([33, 31, 64, 0, 0, 517, 2, 2, 2], 700, 128, 32, "clamped"),
+    ([5, 3, 10, 7, 0, 1, 1, 1], 64, 128, 96, "swiglu"),
+    ([512, 256, 0, 768], 1536, 256, 256, "clamped"),
+    ("multinomial", 16 * 1024, 512, 384, "swiglu"),
+]
+
+ACTS = {"swiglu": ("swish", None, 0.0), "clamped": ("quick_gelu", 7.0, 1.0)}
+
+
+def _sizes(spec, rows, groups_if_random, rng):
+    if spec != "multinomial":
+        return np.array(spec, np.int32)
+    s = rng.multinomial(rows - 37, np.ones(groups_if_random) / groups_if_random)
+    return s.astype(np.int32)
+
+
+def _run(sizes_np, rows, d, f, act, seed):
+    from bux_amd import grouped_mxfp8 as gm, moe
+    torch.manual_seed(seed)
+    dev = torch.device("cuda")
+    groups = len(sizes_np)
+    height = gm.whole(rows)
+    filled = int(sizes_np.sum())
+    assert filled <= rows
+    x = (torch.randn(rows, d, device=dev) * 2.0).to(torch.bfloat16)
+    x.view(-1)[torch.randint(0, x.numel(), (max(1, x.numel() // 500),), device=dev)] *= 100
+    w_up = (torch.randn(groups, d, 2 * f, device=dev) * 0.05).to(torch.bfloat16)
+    weights = torch.rand(rows, device=dev).to(torch.bfloat16)
+    sizes = torch.tensor(sizes_np, dtype=torch.int32, device=dev)
+    filled_t = torch.tensor([filled], dtype=torch.int32, device=dev)
+    x_k, _ = gm.quantized_twice(x, filled_t, False, height=height)
+    _, up_k = gm.quantized_twice(w_up)
+    ffn = moe.Ffn(*ACTS[act])
+    # unfused: the rows GEMM, then the activation's quantizer
+    projected = gm.rows(x_k, up_k, sizes, height=rows)
+    h_k, h_m, _ = moe.weighted_units_quantized(ffn, projected.view(rows, f, 2), weights, filled_t,
+                                               height)
+    # fused
+    p2, h_k2, h_m2 = gm.activated(x_k, up_k, sizes, weights, ffn.codes(), rows)
+    torch.cuda.synchronize()
+    return (projected, h_k, h_m), (p2, h_k2, h_m2)
+
+
+def _same(name, a, b):
+    assert a.shape == b.shape, (name, a.shape, b.shape)
+    diff = (a.view(torch.uint8) != b.view(torch.uint8)) if a.dtype != torch.uint8 else (a != b)
+    bad = int(diff.sum())
+    if bad:
+        where = diff.nonzero()[:5].tolist()
+        pytest.fail(f"{name}: {bad} bytes differ, first at {where}")
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_fused_up_gemm_is_the_unfused_pair_bit_for_bit(lib, case):
+    spec, rows, d, f, act = CASES[case]
+    rng = np.random.default_rng(70 + case)
+    sizes = _sizes(spec, rows, 64, rng)
+    announce("glu fused", case, f"groups={len(sizes)} rows={rows} d={d} f={f} {act}")
+    (p, hk, hm), (p2, hk2, hm2) = _run(sizes, rows, d, f, act, 70 + case)
+    _same("product", p, p2)
+    _same("h values", hk.values, hk2.values)
+    _same("h scales", hk.scales, hk2.scales)
+    _same("h^T values", hm.values, hm2.values)
+    _same("h^T scales", hm.scales, hm2.scales)
+
+
+def test_fused_up_gemm_at_config_3(lib):
+    """Qwen3-30B-A3B's experts: 131072 rows, 128 experts, d 2048, f 768."""
+    rng = np.random.default_rng(77)
+    rows = 16384 * 8
+    sizes = rng.multinomial(rows, np.ones(128) / 128).astype(np.int32)
+    announce("glu fused", "config 3")
+    (p, hk, hm), (p2, hk2, hm2) = _run(sizes, rows, 2048, 768, "swiglu", 77)
+    _same("product", p, p2)
+    _same("h values", hk.values, hk2.values)
+    _same("h scales", hk.scales, hk2.scales)
+    _same("h^T values", hm.values, hm2.values)
+    _same("h^T scales", hm.scales, hm2.scales)
+
+
+@pytest.mark.parametrize("t,k,e,d,f,act", [(300, 4, 8, 256, 160, "clamped"),
+                                           (4096, 8, 64, 512, 384, "swiglu")])
+def test_layer_with_the_fused_up_gemm_is_bit_identical(lib, t, k, e, d, f, act):
+    """The whole layer, forward and backward, with and without the fused up GEMM."""
+    from bux_amd import moe
+    torch.manual_seed(t)
+    dev = torch.device("cuda")
+    z = torch.randn(t, d, device=dev).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(e, device=dev)[:k] for _ in range(t)]).to(torch.int32)
+    idx[::7, 0] = e  # picks outside the experts: rows past the groups
+    w = torch.rand(t, k, device=dev).to(torch.bfloat16)
+    up = (torch.randn(e, d, f, 2, device=dev) * 0.05).to(torch.bfloat16)
+    down = (torch.randn(e, f, d, device=dev) * 0.05).to(torch.bfloat16)
+    dy = (torch.randn(t, d, device=dev) * 0.01).to(torch.bfloat16)
+    ffn = moe.Ffn(*ACTS[act])
+    announce("layer fused", t, k, e, d, f, act)
+    results = []
+    for fused in (False, True):
+        out, saved = moe.experts_forward(z, idx, w, up, down, ffn, fused=fused)
+        grads = moe.experts_backward(saved, dy, up, down, ffn)
+        results.append((out, grads))
+    torch.cuda.synchronize()
+    (o0, g0), (o1, g1) = results
+    _same("y", o0, o1)
+    for key in g0:
+        _same(f"d{key}", g0[key], g1[key])
