@@ -30,6 +30,11 @@ SIGNATURES = {
     "bux_mx_grouped_rows_workspace_size": (_size, [_i32, _i64, _i64]),
     "bux_mx_grouped_rows": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
+    "bux_mx_grouped_tiles": (_int, [_p, _i32, _i64, _i64, _p, _size, _p]),
+    "bux_mx_grouped_rows_listed": (
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p]),
+    "bux_mx_grouped_contract_listed": (
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _int, _p, _p]),
     "bux_mx_grouped_contract_workspace_size": (_size, [_i32]),
     "bux_mx_grouped_contract": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _int, _p, _p, _size, _p]),

@@ -1094,10 +1094,104 @@ int64_t glu_slots(int32_t groups, int64_t height) {
 }  // namespace
 }  // namespace bux
 
+namespace bux {
+namespace {
+
+// The checks of a rows GEMM's arguments, `name` its entry point.
+int check_rows(const char* name, const uint8_t* a_values, const uint8_t* a_scales,
+               const uint8_t* b_values, const uint8_t* b_scales, int32_t groups, int64_t m,
+               int64_t n, int64_t k, int64_t height, int out_dtype, const void* y) {
+  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "%s: groups=%d outside [1, %d]", name, groups,
+            MAX_GROUPS);
+  BUX_CHECK(m >= 0 && n > 0 && k > 0 && height >= 0 && height < (1LL << 31) && m < (1LL << 31),
+            "%s: bad shape m=%lld n=%lld k=%lld height=%lld", name, (long long)m, (long long)n,
+            (long long)k, (long long)height);
+  BUX_CHECK(k % 128 == 0, "%s: k=%lld is not a multiple of 128 (the tiled layout's padded K)",
+            name, (long long)k);
+  BUX_CHECK(n % 4 == 0, "%s: n=%lld is not a multiple of 4", name, (long long)n);
+  BUX_CHECK(offsets_fit(m, k) && offsets_fit(n, k), "%s: an operand of %lld x %lld bytes exceeds 2 GiB",
+            name, (long long)(m > n ? m : n), (long long)k);
+  BUX_CHECK(out_dtype == BUX_BF16 || out_dtype == BUX_F32, "%s: out_dtype=%d", name, out_dtype);
+  BUX_CHECK(b_values && b_scales && y && (m == 0 || (a_values && a_scales)), "%s: NULL buffer",
+            name);
+  return BUX_OK;
+}
+
+int check_contract(const char* name, const uint8_t* a_values, const uint8_t* a_scales,
+                   const uint8_t* b_values, const uint8_t* b_scales, int32_t groups, int64_t d,
+                   int64_t f, int64_t m, int out_dtype, const void* dw) {
+  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "%s: groups=%d outside [1, %d]", name, groups,
+            MAX_GROUPS);
+  BUX_CHECK(d > 0 && f > 0 && m >= 0, "%s: bad shape d=%lld f=%lld m=%lld", name, (long long)d,
+            (long long)f, (long long)m);
+  BUX_CHECK(m % 128 == 0, "%s: m=%lld is not a multiple of 128", name, (long long)m);
+  BUX_CHECK(f % 4 == 0, "%s: f=%lld is not a multiple of 4", name, (long long)f);
+  BUX_CHECK(offsets_fit(d, m) && offsets_fit(f, m), "%s: an operand of %lld x %lld bytes exceeds 2 GiB",
+            name, (long long)(d > f ? d : f), (long long)m);
+  BUX_CHECK(out_dtype == BUX_BF16 || out_dtype == BUX_F32, "%s: out_dtype=%d", name, out_dtype);
+  BUX_CHECK(dw && (m == 0 || (a_values && a_scales && b_values && b_scales)), "%s: NULL buffer",
+            name);
+  return BUX_OK;
+}
+
+// A tile list's buffer: the group starts (groups + 2 ints, 256-byte aligned), then the
+// tile records.
+int32_t* starts_in(const void* list) { return static_cast<int32_t*>(const_cast<void*>(list)); }
+Tile* tiles_in(const void* list, int32_t groups) {
+  return reinterpret_cast<Tile*>(static_cast<uint8_t*>(const_cast<void*>(list)) +
+                                 align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)));
+}
+
+int launch_rows_of(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
+                   const uint8_t* b_scales, const void* list, int32_t groups, int64_t m, int64_t n,
+                   int64_t k, int64_t height, int out_dtype, void* y, hipStream_t s) {
+  // Rows of the groups past a's m rows read 0 (the resource ends there) or the
+  // following K chunk's rows: a's m must cover every row the groups hold.
+  const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(m)};
+  const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};
+  const int64_t slots = row_slots(groups, m, height);
+  int32_t* starts = starts_in(list);
+  Tile* tiles = tiles_in(list, groups);
+  return out_dtype == BUX_BF16
+             ? launch_rows<uint16_t>(A, B, groups, n, height, starts, tiles, slots, y, s)
+             : launch_rows<float>(A, B, groups, n, height, starts, tiles, slots, y, s);
+}
+
+int launch_contract_of(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
+                       const uint8_t* b_scales, const void* list, int32_t groups, int64_t d,
+                       int64_t f, int64_t m, int out_dtype, void* dw, hipStream_t s) {
+  // The operands' K is m: each of a's d rows (b's f rows) is m bytes.
+  const Operand A{a_values, a_scales, static_cast<int32_t>(m), static_cast<int32_t>(d)};
+  const Operand B{b_values, b_scales, static_cast<int32_t>(m), static_cast<int32_t>(f)};
+  return out_dtype == BUX_BF16 ? launch_contract<uint16_t>(A, B, groups, starts_in(list), dw, s)
+                               : launch_contract<float>(A, B, groups, starts_in(list), dw, s);
+}
+
+}  // namespace
+}  // namespace bux
+
 extern "C" size_t bux_mx_grouped_rows_workspace_size(int32_t groups, int64_t m, int64_t height) {
   using namespace bux;
   return align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)) +
          static_cast<size_t>(row_slots(groups, m, height)) * sizeof(Tile);
+}
+
+extern "C" int bux_mx_grouped_tiles(const int32_t* sizes, int32_t groups, int64_t m,
+                                    int64_t height, void* list, size_t list_bytes, void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "bux_mx_grouped_tiles: groups=%d outside [1, %d]",
+            groups, MAX_GROUPS);
+  BUX_CHECK(m >= 0 && height >= 0 && height < (1LL << 31) && m < (1LL << 31),
+            "bux_mx_grouped_tiles: bad shape m=%lld height=%lld", (long long)m, (long long)height);
+  BUX_CHECK(sizes != nullptr, "bux_mx_grouped_tiles: NULL sizes");
+  const size_t need = bux_mx_grouped_rows_workspace_size(groups, m, height);
+  if (list == nullptr || list_bytes < need)
+    return fail(BUX_E_WORKSPACE, "bux_mx_grouped_tiles: list of %zu bytes, %zu needed", list_bytes,
+                need);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, as_stream(stream), sizes, groups,
+                     height, row_slots(groups, m, height), 1, starts_in(list), tiles_in(list, groups));
+  return launched("prologue_kernel");
 }
 
 extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_scales,
@@ -1107,41 +1201,38 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
                                    void* workspace, size_t workspace_bytes, void* stream) {
   using namespace bux;
   clear_error();
-  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "bux_mx_grouped_rows: groups=%d outside [1, %d]",
-            groups, MAX_GROUPS);
-  BUX_CHECK(m >= 0 && n > 0 && k > 0 && height >= 0 && height < (1LL << 31) && m < (1LL << 31),
-            "bux_mx_grouped_rows: bad shape m=%lld n=%lld k=%lld height=%lld", (long long)m,
-            (long long)n, (long long)k, (long long)height);
-  BUX_CHECK(k % 128 == 0, "bux_mx_grouped_rows: k=%lld is not a multiple of 128 (the tiled "
-            "layout's padded K)", (long long)k);
-  BUX_CHECK(n % 4 == 0, "bux_mx_grouped_rows: n=%lld is not a multiple of 4", (long long)n);
-  BUX_CHECK(offsets_fit(m, k) && offsets_fit(n, k),
-            "bux_mx_grouped_rows: an operand of %lld x %lld bytes exceeds 2 GiB",
-            (long long)(m > n ? m : n), (long long)k);
-  BUX_CHECK(out_dtype == BUX_BF16 || out_dtype == BUX_F32, "bux_mx_grouped_rows: out_dtype=%d",
-            out_dtype);
-  BUX_CHECK(sizes && b_values && b_scales && y && (m == 0 || (a_values && a_scales)),
-            "bux_mx_grouped_rows: NULL buffer");
+  if (int rc = check_rows("bux_mx_grouped_rows", a_values, a_scales, b_values, b_scales, groups, m,
+                          n, k, height, out_dtype, y))
+    return rc;
+  BUX_CHECK(sizes != nullptr, "bux_mx_grouped_rows: NULL buffer");
   const size_t need = bux_mx_grouped_rows_workspace_size(groups, m, height);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(BUX_E_WORKSPACE, "bux_mx_grouped_rows: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
   if (height == 0) return BUX_OK;
   hipStream_t s = as_stream(stream);
-  int32_t* starts = static_cast<int32_t*>(workspace);
-  Tile* tiles = reinterpret_cast<Tile*>(static_cast<uint8_t*>(workspace) +
-                                        align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)));
-  const int64_t slots = row_slots(groups, m, height);
-  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
-                     1, starts, tiles);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height,
+                     row_slots(groups, m, height), 1, starts_in(workspace),
+                     tiles_in(workspace, groups));
   if (int rc = launched("prologue_kernel")) return rc;
-  // Rows of the groups past a's m rows read 0 (the resource ends there) or the
-  // following K chunk's rows: a's m must cover every row the groups hold.
-  const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(m)};
-  const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};
-  return out_dtype == BUX_BF16
-             ? launch_rows<uint16_t>(A, B, groups, n, height, starts, tiles, slots, y, s)
-             : launch_rows<float>(A, B, groups, n, height, starts, tiles, slots, y, s);
+  return launch_rows_of(a_values, a_scales, b_values, b_scales, workspace, groups, m, n, k, height,
+                        out_dtype, y, s);
+}
+
+extern "C" int bux_mx_grouped_rows_listed(const uint8_t* a_values, const uint8_t* a_scales,
+                                          const uint8_t* b_values, const uint8_t* b_scales,
+                                          const void* list, int32_t groups, int64_t m, int64_t n,
+                                          int64_t k, int64_t height, int out_dtype, void* y,
+                                          void* stream) {
+  using namespace bux;
+  clear_error();
+  if (int rc = check_rows("bux_mx_grouped_rows_listed", a_values, a_scales, b_values, b_scales,
+                          groups, m, n, k, height, out_dtype, y))
+    return rc;
+  BUX_CHECK(list != nullptr, "bux_mx_grouped_rows_listed: NULL list");
+  if (height == 0) return BUX_OK;
+  return launch_rows_of(a_values, a_scales, b_values, b_scales, list, groups, m, n, k, height,
+                        out_dtype, y, as_stream(stream));
 }
 
 extern "C" size_t bux_mx_grouped_contract_workspace_size(int32_t groups) {
@@ -1155,33 +1246,35 @@ extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a
                                        size_t workspace_bytes, void* stream) {
   using namespace bux;
   clear_error();
-  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS,
-            "bux_mx_grouped_contract: groups=%d outside [1, %d]", groups, MAX_GROUPS);
-  BUX_CHECK(d > 0 && f > 0 && m >= 0, "bux_mx_grouped_contract: bad shape d=%lld f=%lld m=%lld",
-            (long long)d, (long long)f, (long long)m);
-  BUX_CHECK(m % 128 == 0, "bux_mx_grouped_contract: m=%lld is not a multiple of 128", (long long)m);
-  BUX_CHECK(f % 4 == 0, "bux_mx_grouped_contract: f=%lld is not a multiple of 4", (long long)f);
-  BUX_CHECK(offsets_fit(d, m) && offsets_fit(f, m),
-            "bux_mx_grouped_contract: an operand of %lld x %lld bytes exceeds 2 GiB",
-            (long long)(d > f ? d : f), (long long)m);
-  BUX_CHECK(out_dtype == BUX_BF16 || out_dtype == BUX_F32, "bux_mx_grouped_contract: out_dtype=%d",
-            out_dtype);
-  BUX_CHECK(sizes && dw && (m == 0 || (a_values && a_scales && b_values && b_scales)),
-            "bux_mx_grouped_contract: NULL buffer");
+  if (int rc = check_contract("bux_mx_grouped_contract", a_values, a_scales, b_values, b_scales,
+                              groups, d, f, m, out_dtype, dw))
+    return rc;
+  BUX_CHECK(sizes != nullptr, "bux_mx_grouped_contract: NULL buffer");
   const size_t need = bux_mx_grouped_contract_workspace_size(groups);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(BUX_E_WORKSPACE, "bux_mx_grouped_contract: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
   hipStream_t s = as_stream(stream);
-  int32_t* starts = static_cast<int32_t*>(workspace);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
-                     starts, nullptr);
+                     static_cast<int32_t*>(workspace), nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
-  // The operands' K is m: each of a's d rows (b's f rows) is m bytes.
-  const Operand A{a_values, a_scales, static_cast<int32_t>(m), static_cast<int32_t>(d)};
-  const Operand B{b_values, b_scales, static_cast<int32_t>(m), static_cast<int32_t>(f)};
-  return out_dtype == BUX_BF16 ? launch_contract<uint16_t>(A, B, groups, starts, dw, s)
-                               : launch_contract<float>(A, B, groups, starts, dw, s);
+  return launch_contract_of(a_values, a_scales, b_values, b_scales, workspace, groups, d, f, m,
+                            out_dtype, dw, s);
+}
+
+extern "C" int bux_mx_grouped_contract_listed(const uint8_t* a_values, const uint8_t* a_scales,
+                                              const uint8_t* b_values, const uint8_t* b_scales,
+                                              const void* list, int32_t groups, int64_t d,
+                                              int64_t f, int64_t m, int out_dtype, void* dw,
+                                              void* stream) {
+  using namespace bux;
+  clear_error();
+  if (int rc = check_contract("bux_mx_grouped_contract_listed", a_values, a_scales, b_values,
+                              b_scales, groups, d, f, m, out_dtype, dw))
+    return rc;
+  BUX_CHECK(list != nullptr, "bux_mx_grouped_contract_listed: NULL list");
+  return launch_contract_of(a_values, a_scales, b_values, b_scales, list, groups, d, f, m,
+                            out_dtype, dw, as_stream(stream));
 }
 
 extern "C" size_t bux_mx_grouped_glu_workspace_size(int32_t groups, int64_t height) {
@@ -1222,9 +1315,8 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
                 workspace_bytes, need);
   if (height == 0) return BUX_OK;
   hipStream_t s = as_stream(stream);
-  int32_t* starts = static_cast<int32_t*>(workspace);
-  Tile* tiles = reinterpret_cast<Tile*>(static_cast<uint8_t*>(workspace) +
-                                        align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)));
+  int32_t* starts = starts_in(workspace);
+  Tile* tiles = tiles_in(workspace, groups);
   const int64_t slots = glu_slots(groups, height);
   const int64_t col_tiles = ceil_div(n, BN);
   if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_glu: too many tiles");

@@ -156,9 +156,33 @@ def quantized_twice(
 _DTYPES = {torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
 
 
+class TileList(NamedTuple):
+    """A rows GEMM's group starts and ragged tile list, made once on the device from the
+    group sizes (the reference's ``tiles_of``, grouped_mxfp8.py:157-182) for every GEMM of
+    a step that takes the same sizes."""
+
+    buffer: torch.Tensor  # uint8: the starts, then the tile records
+    groups: int
+    m: int  # rows of the rows GEMMs' a
+    height: int  # rows of their outputs
+
+
+def tiles_of(sizes: torch.Tensor, m: int, height: int) -> TileList:
+    """Return the tile list of `sizes` (int32 (g,) on the device) for rows GEMMs of a with
+    m rows into outputs of `height` rows; `contract` takes it too (its starts)."""
+    require(sizes)
+    if sizes.dtype != torch.int32 or sizes.dim() != 1:
+        raise ValueError(f"tiles_of: sizes {tuple(sizes.shape)} {sizes.dtype}")
+    groups = sizes.shape[0]
+    buf = workspace(lib().bux_mx_grouped_rows_workspace_size(groups, m, height), sizes.device)
+    _lib.check(lib().bux_mx_grouped_tiles(ptr(sizes), groups, m, height, ptr(buf), buf.numel(),
+                                          stream()))
+    return TileList(buf, groups, m, height)
+
+
 def rows(
     a: Tiled, b: Tiled, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16,
-    height: int | None = None,
+    height: int | None = None, tiles: TileList | None = None,
 ) -> torch.Tensor:
     """Return ``a @ b[g]^T`` for each group g's rows of a, (height, n), the rows past
     the groups 0.
@@ -169,6 +193,8 @@ def rows(
         sizes: int32 (g,) on the device: how many rows each group has.
         out: the output's dtype, bfloat16 or float32.
         height: rows of the output (a's rows past it are not stored); None for m.
+        tiles: `tiles_of(sizes, m, height)`, made once for the step's GEMMs; None to make
+            it here.
     """
     require(a.values, a.scales, b.values, b.scales, sizes)
     if a.values.dim() != 3 or b.values.dim() != 4:
@@ -181,6 +207,14 @@ def rows(
                          f"sizes {tuple(sizes.shape)} {sizes.dtype}")
     h = m if height is None else height
     y = torch.empty(h, n, dtype=out, device=a.values.device)
+    if tiles is not None:
+        if (tiles.groups, tiles.m, tiles.height) != (groups, m, h):
+            raise ValueError(f"rows: a tile list for {tiles.groups} groups, m={tiles.m}, "
+                             f"height={tiles.height}, not {groups}, {m}, {h}")
+        _lib.check(lib().bux_mx_grouped_rows_listed(
+            ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(tiles.buffer), groups,
+            m, n, k, h, _DTYPES[out], ptr(y), stream()))
+        return y
     ws = workspace(lib().bux_mx_grouped_rows_workspace_size(groups, m, h), y.device)
     _lib.check(lib().bux_mx_grouped_rows(
         ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(sizes), groups, m, n, k,
@@ -234,7 +268,8 @@ def activated(
 
 
 def contract(
-    a: Tiled, b: Tiled, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16
+    a: Tiled, b: Tiled, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16,
+    tiles: TileList | None = None,
 ) -> torch.Tensor:
     """Return ``a[:, rows of g] b[:, rows of g]^T`` for each group g, (g, d, f).
 
@@ -243,6 +278,8 @@ def contract(
         b: dy^T (f rows of m) in MXFP8 along m.
         sizes: int32 (g,) on the device, summing to at most m.
         out: the output's dtype.
+        tiles: a `tiles_of` list of the same sizes (its group starts); None to compute
+            the starts here.
     """
     require(a.values, a.scales, b.values, b.scales, sizes)
     if a.values.dim() != 3 or b.values.dim() != 3:
@@ -253,6 +290,13 @@ def contract(
     if b.k != m or sizes.dtype != torch.int32:
         raise ValueError(f"contract: a {tuple(a.values.shape)}, b {tuple(b.values.shape)}")
     dw = torch.empty(groups, d, f, dtype=out, device=a.values.device)
+    if tiles is not None:
+        if tiles.groups != groups:
+            raise ValueError(f"contract: a tile list for {tiles.groups} groups, not {groups}")
+        _lib.check(lib().bux_mx_grouped_contract_listed(
+            ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(tiles.buffer), groups,
+            d, f, m, _DTYPES[out], ptr(dw), stream()))
+        return dw
     ws = workspace(lib().bux_mx_grouped_contract_workspace_size(groups), dw.device)
     _lib.check(lib().bux_mx_grouped_contract(
         ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(sizes), groups, d, f, m,

@@ -204,6 +204,7 @@ class Saved(NamedTuple):
     h_m: Tiled | None  # h^T along the rows (wgrad of down)
     down_n: Tiled | None  # each W_down along n (dgrad of down)
     rows: torch.Tensor | None  # the picks' rows, compute format only
+    tiles: grouped_mxfp8.TileList | None = None  # the MXFP8 GEMMs' tile list, made once
 
 
 def experts_forward(
@@ -241,8 +242,12 @@ def experts_forward(
     x_m = up_n = h_m = down_n = rows = None
     _check_fmt(fmt)
     mx, tiles = fmt in MX_FORMATS, fmt == "mxfp8_2d"
+    tiles = None
     if mx:
         height = grouped_mxfp8.whole(m)
+        with span("tile list"):
+            # one tile list for the step's six GEMMs: a of `height` rows, outputs of m
+            tiles = grouped_mxfp8.tiles_of(s.sizes, height, m)
         with span("quantize x"):
             x_k, x_m = grouped_mxfp8.quantized_twice(z, filled, True, s.order, k, height)
         with span("quantize W_up"):
@@ -254,7 +259,7 @@ def experts_forward(
             h = None
         else:
             with span("up fprop"):
-                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m)
+                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m, tiles=tiles)
     else:
         with span("gather x"):
             rows = token_rows(z, s.order, k)
@@ -268,7 +273,7 @@ def experts_forward(
         with span("quantize W_down"):
             down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
         with span("down fprop"):
-            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m)
+            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=tiles)
     else:
         with span("activation"):
             h = weighted_units(ffn, projected.view(m, f, p), row_weights, filled)
@@ -276,7 +281,7 @@ def experts_forward(
             y = grouped.dot(h, down, s.sizes)
     with span("combine"):
         out = sum_by_token(y, s.inverse.view(t, k))
-    return out, Saved(s, k, row_weights, projected, h, x_m, up_n, h_m, down_n, rows)
+    return out, Saved(s, k, row_weights, projected, h, x_m, up_n, h_m, down_n, rows, tiles)
 
 
 def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: torch.Tensor,
@@ -300,9 +305,9 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         with span("quantize dy"):
             dy_n, dy_m = grouped_mxfp8.quantized_twice(dy, filled, True, s.order, k, height)
         with span("down dgrad"):
-            dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m)
+            dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m, tiles=saved.tiles)
         with span("down wgrad"):
-            d_down = grouped_mxfp8.contract(saved.h_m, dy_m, s.sizes)
+            d_down = grouped_mxfp8.contract(saved.h_m, dy_m, s.sizes, tiles=saved.tiles)
     else:
         with span("gather dy"):
             dy_rows = token_rows(dy, s.order, k)
@@ -318,9 +323,9 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         if dp is not None:
             dp = dp.view(m, f * p)
         with span("up dgrad"):
-            dx = grouped_mxfp8.rows(dp_n, saved.up_n, s.sizes, height=m)
+            dx = grouped_mxfp8.rows(dp_n, saved.up_n, s.sizes, height=m, tiles=saved.tiles)
         with span("up wgrad"):
-            d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes)
+            d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes, tiles=saved.tiles)
     else:
         with span("activation backward"):
             dp, d_rows_w = weighted_units_backward(ffn, saved.projected.view(m, f, p),

@@ -130,6 +130,27 @@ int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_scales, const 
                         int64_t n, int64_t k, int64_t height, int out_dtype, void* y,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* bux_mx_grouped_tiles: the rows GEMM's device prologue on its own, the reference's
+ * tiles_of (grouped_mxfp8.py:157-182), whose result its rows and contract take as
+ * `tiles` and `starts` (:116, :185): the group starts and the ragged tile list of
+ * `sizes` for a of m rows and y of `height` rows, into `list`
+ * (bux_mx_grouped_rows_workspace_size(groups, m, height) bytes).
+ * bux_mx_grouped_rows_listed / bux_mx_grouped_contract_listed: bux_mx_grouped_rows /
+ * bux_mx_grouped_contract on such a list, made from the same sizes (and, for rows, the
+ * same groups, m and height), in place of their own prologue: one list serves every
+ * GEMM of a layer's step.
+ */
+int bux_mx_grouped_tiles(const int32_t* sizes, int32_t groups, int64_t m, int64_t height,
+                         void* list, size_t list_bytes, void* stream);
+int bux_mx_grouped_rows_listed(const uint8_t* a_values, const uint8_t* a_scales,
+                               const uint8_t* b_values, const uint8_t* b_scales, const void* list,
+                               int32_t groups, int64_t m, int64_t n, int64_t k, int64_t height,
+                               int out_dtype, void* y, void* stream);
+int bux_mx_grouped_contract_listed(const uint8_t* a_values, const uint8_t* a_scales,
+                                   const uint8_t* b_values, const uint8_t* b_scales,
+                                   const void* list, int32_t groups, int64_t d, int64_t f,
+                                   int64_t m, int out_dtype, void* dw, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * a-7. Grouped MXFP8 GEMM contracting each group's rows: dw[g] = a[:, g] b[:, g]^T.
  *

@@ -168,3 +168,18 @@ def test_a_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "_LIB", None)
     with pytest.raises(_lib.BuxError, match="not built"):
         _lib.load(str(tmp_path / "libbux_amd.so"))
+
+
+def test_tile_lists_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    need = lib.bux_mx_grouped_rows_workspace_size(4, 256, 200)
+    assert lib.bux_mx_grouped_tiles(p, 4, 256, 200, p, need - 1, None) == 2
+    assert "list of" in _msg(lib)
+    assert lib.bux_mx_grouped_tiles(None, 4, 256, 200, p, need, None) == 1
+    assert lib.bux_mx_grouped_tiles(p, 0, 256, 200, p, need, None) == 1 and "groups=0" in _msg(lib)
+    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, None, 4, 256, 128, 128, 200, 0, p, None)
+    assert rc == 1 and "NULL list" in _msg(lib)
+    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, p, 4, 256, 128, 100, 200, 0, p, None)
+    assert rc == 1 and "k=100" in _msg(lib)
+    rc = lib.bux_mx_grouped_contract_listed(p, p, p, p, p, 4, 64, 64, 100, 0, p, None)
+    assert rc == 1 and "m=100" in _msg(lib)

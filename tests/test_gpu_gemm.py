@@ -248,3 +248,28 @@ def test_bf16_weight_grad(lib):
     got = bf16.to_f32(bf16_bits(dw))
     assert rel_err(got, want) <= 4e-3
     assert (got[1] == 0).all()
+
+
+def test_a_tile_list_made_once_serves_every_gemm(lib):
+    """rows and contract on one `tiles_of` list give the bytes they give on their own
+    prologue (the reference's rows/contract taking `tiles` and `starts`)."""
+    from bux_amd import grouped_mxfp8 as gm
+    rng = np.random.default_rng(31)
+    sizes = np.array([0, 130, 1, 3, 256, 0, 300, 100], np.int32)
+    m, height, k, n = 900, 896, 256, 384
+    a = _gpu(_codes(rng, (m, k)))
+    b = _gpu(_codes(rng, (len(sizes), n, k), 0.05))
+    gs = to_gpu(sizes)
+    announce("gemm tile list", m, height, k, n)
+    tiles = gm.tiles_of(gs, a.height, height)
+    for out in (torch.bfloat16, torch.float32):
+        y0 = gm.rows(a, b, gs, out, height=height)
+        y1 = gm.rows(a, b, gs, out, height=height, tiles=tiles)
+        torch.cuda.synchronize()
+        assert torch.equal(y0.view(torch.uint8), y1.view(torch.uint8))
+    xt = _gpu(_codes(rng, (192, 1024)))
+    dt = _gpu(_codes(rng, (128, 1024)))
+    dw0 = gm.contract(xt, dt, gs)
+    dw1 = gm.contract(xt, dt, gs, tiles=tiles)
+    torch.cuda.synchronize()
+    assert torch.equal(dw0.view(torch.uint8), dw1.view(torch.uint8))
