@@ -1045,7 +1045,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 // whole: quantized from the stored product as bux_glu_quantize does (rows from the
 // groups' end, or from `rows`, are 0). Workgroup g takes the block of group g's first
 // row (g = groups: the groups' end), unless group g - 1's first row is inside the same
-// block too.
+// block too; its lane t unit 256 blockIdx.y + t.
 __global__ __launch_bounds__(THREADS) void glu_edges_kernel(
     const int32_t* __restrict__ starts, int32_t groups, const uint16_t* __restrict__ projected,
     const uint16_t* __restrict__ weights, Act act, int32_t rows, int32_t f, int32_t height,
@@ -1058,7 +1058,8 @@ __global__ __launch_bounds__(THREADS) void glu_edges_kernel(
     if ((before & 31) != 0 && (before >> 5) == (first >> 5)) return;
   }
   const int32_t live = smaller(starts[groups], rows), r0 = first & ~31;
-  for (int32_t u = threadIdx.x; u < f; u += THREADS) {
+  const int32_t u = static_cast<int32_t>(blockIdx.y) * THREADS + threadIdx.x;
+  if (u < f) {
     float v[32], amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
@@ -1336,7 +1337,9 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
   hipLaunchKernelGGL(glu_kernel, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
                      static_cast<int32_t>(height), starts, tiles, static_cast<int32_t>(col_tiles), out);
   if (int rc = launched("glu_kernel")) return rc;
-  hipLaunchKernelGGL(glu_edges_kernel, dim3(static_cast<unsigned>(groups + 1)), dim3(THREADS), 0, s,
+  hipLaunchKernelGGL(glu_edges_kernel,
+                     dim3(static_cast<unsigned>(groups + 1), static_cast<unsigned>(ceil_div(f, THREADS))),
+                     dim3(THREADS), 0, s,
                      starts, groups, projected, weights, act, static_cast<int32_t>(rows), f,
                      static_cast<int32_t>(height), t_values, t_scales);
   return launched("glu_edges_kernel");
