@@ -232,6 +232,95 @@ def fused_up(z, idx, w, up, e, k):
             "used_in_step": "unfused"}
 
 
+# The other configs of BASELINE.json, forward only there: (tokens, width, experts, picks,
+# units, activation (kind, limit, up offset), seed, router skew).
+OTHER_CONFIGS = {
+    "config 2: Qwen3-30B-A3B layer forward": (16384, 2048, 128, 8, 768, ("swish", None, 0.0), 1, None),
+    "config 4: gpt-oss-120b layer forward (clamped SwiGLU)": (
+        8192, 2880, 128, 4, 2880, ("quick_gelu", 7.0, 1.0), 2, "bias"),
+    "config 5: DeepSeek-V3 layer forward (Zipf loads)": (
+        8192, 7168, 256, 8, 2048, ("swish", None, 0.0), 3, "zipf"),
+}
+
+
+def other_config(t, d, e, k, f, act, seed, skew, device, reps=10):
+    """One config's MXFP8 forward (the layer as training runs it: x^T and h^T quantized
+    for the wgrad too), timed as HIP graph replays, with the weights quantized inside
+    (`ms`) and given already in MXFP8 (`ms_weights_given`: the reference's `quantized`,
+    quantized once an optimizer step). Router logits N(0,1), plus a
+    per-expert bias N(0, 0.5) (config 4) or a Zipf(1.2) bias over a permutation of the
+    experts with the last fifth receiving none (config 5); softmax, top-k, normalised."""
+    from bux_amd import moe
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    z = torch.randn(t, d, generator=g, device=device)
+    outliers = torch.randperm(t * d, generator=g, device=device)[: max(1, t * d // 1000)]
+    z.view(-1)[outliers] *= 100
+    logits = torch.randn(t, e, generator=g, device=device)
+    if skew == "bias":
+        logits += torch.randn(e, generator=g, device=device) * 0.5
+    elif skew == "zipf":
+        order = torch.randperm(e, generator=g, device=device)
+        rank = torch.empty(e, device=device)
+        rank[order] = torch.arange(1, e + 1, device=device, dtype=torch.float32)
+        logits += -1.2 * torch.log(rank)
+        logits[:, order[-e // 5:]] = -float("inf")
+    weights, idx = torch.topk(torch.softmax(logits, -1), k, -1)
+    weights = (weights / weights.sum(-1, keepdim=True)).to(torch.bfloat16)
+    idx = idx.to(torch.int32).contiguous()
+    up = (torch.randn(e, d, f, 2, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    down = (torch.randn(e, f, d, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    z = z.to(torch.bfloat16)
+    ffn = moe.Ffn(*act)
+    del logits
+
+    def graph_ms(forward):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            forward()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            forward()
+        graph.replay()
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(reps):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - start) * 1e3 / reps
+
+    ms = graph_ms(lambda: moe.experts_forward(z, idx, weights, up, down, ffn))
+    given = moe.in_mxfp8(up, down)
+    ms_given = graph_ms(lambda: moe.experts_forward(z, idx, weights, up, down, ffn, quantized=given))
+    loads = torch.bincount(idx.view(-1).long(), minlength=e)
+    m = t * k
+    flops = 2 * m * d * 2 * f + 2 * m * f * d
+    return {"ms": round(ms, 4), "gemm_tflop": round(flops / 1e12, 4),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_MXFP8_TFLOPS, 4),
+            "ms_weights_given": round(ms_given, 4),
+            "tflops_weights_given": round(flops / (ms_given * 1e-3) / 1e12, 1),
+            "largest_group_share": round(float(loads.max()) / m, 4),
+            "empty_experts": int((loads == 0).sum())}
+
+
+def other_configs(device):
+    """BASELINE.json's other MXFP8 configs, each timed on its own (an error is recorded,
+    not raised: the headline line stands)."""
+    out = {}
+    for name, cfg in OTHER_CONFIGS.items():
+        try:
+            out[name] = other_config(*cfg, device)
+            log(f"{name}: {out[name]}")
+        except (RuntimeError, torch.OutOfMemoryError) as err:
+            out[name] = {"error": str(err)[:200]}
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline():
     """The CPU oracle (numpy: float64/float32 quantizer, BLAS float32 GEMMs) on a bounded
     sample of config 3: 8 of its 128 experts with the same per-expert shape (1024
@@ -270,6 +359,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the forward timings of configs 2, 4 and 5")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run only a plain device-to-device copy of MIB MiB, 10 times: the "
                          "kernel of known traffic that scales rocprofv3's FETCH_SIZE and "
@@ -366,6 +457,8 @@ def main():
     }
     result["feed"] = feed_ops(z, idx, E, K)
     result["fused_up_gemm"] = fused_up(z, idx, w, up, E, K)
+    if not args.no_other_configs:
+        result["other_configs"] = other_configs(device)
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle on a sample of config 3 ...")
         result["cpu_baseline"] = cpu_baseline()

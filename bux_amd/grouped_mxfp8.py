@@ -119,6 +119,9 @@ def quantized_twice(
     require(x, filled, index)
     if x.dtype != torch.bfloat16:
         raise TypeError(f"quantized_twice takes bfloat16, got {x.dtype}")
+    if not isinstance(tiles, bool):
+        raise TypeError(f"quantized_twice: tiles is a bool (the mxfp8_2d recipe's scales), "
+                        f"not {type(tiles).__name__}")
     stack = x.dim() == 3
     if index is not None:
         if stack:

@@ -190,6 +190,31 @@ def _check_fmt(fmt: str) -> None:
         raise ValueError(f"the routed experts multiply in compute, mxfp8, mxfp8_2d: not {fmt}")
 
 
+class MxWeights(NamedTuple):
+    """The experts' kernels in MXFP8 as the GEMMs take them, each along what its GEMM
+    contracts (the reference's ``grouped_glu.Weights``, grouped_glu.py:78-90, which
+    ``moe.experts`` takes as `quantized`, moe.py:799)."""
+
+    up_n: Tiled  # each W_up along n (the dgrad's)
+    up_k: Tiled  # each W_up^T along d (the forward's)
+    down_n: Tiled  # each W_down along d (the dgrad's)
+    down_k: Tiled  # each W_down^T along f (the forward's)
+
+
+def in_mxfp8(up: torch.Tensor, down: torch.Tensor, fmt: str = "mxfp8") -> MxWeights:
+    """Return the experts' kernels (E, d, f, 2) and (E, f, d) in MXFP8 for `fmt`
+    (the reference's ``grouped_glu.in_mxfp8``, grouped_glu.py:187-203): once per
+    optimizer step, for every forward and backward that step runs."""
+    _check_fmt(fmt)
+    if fmt not in MX_FORMATS:
+        raise ValueError(f"in_mxfp8: {fmt!r} is not an MXFP8 format")
+    e, d, f, p = up.shape
+    tiles = fmt == "mxfp8_2d"
+    up_n, up_k = grouped_mxfp8.quantized_twice(up.reshape(e, d, f * p), tiles=tiles)
+    down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
+    return MxWeights(up_n, up_k, down_n, down_k)
+
+
 class Saved(NamedTuple):
     """What the layer's backward takes of its forward (grouped_blockscaled.py:84's Saved
     for each GEMM, and the activation's input, which jax.checkpoint recomputes from)."""
@@ -210,7 +235,7 @@ class Saved(NamedTuple):
 def experts_forward(
     z: torch.Tensor, idx: torch.Tensor, weights: torch.Tensor, up: torch.Tensor,
     down: torch.Tensor, ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
-    fused: bool = False,
+    fused: bool = False, quantized: MxWeights | None = None,
 ) -> tuple[torch.Tensor, Saved]:
     """Return the routed experts' output (t, d), bfloat16, and what the backward takes.
     In MXFP8 the activation goes straight to its quantized copies; with `intermediates`
@@ -227,6 +252,8 @@ def experts_forward(
             what its GEMM contracts), "mxfp8_2d" (the same, but each W with a scale per
             32 x 32 tile, shared by its two copies: blockscaled.MXFP8_2D,
             blockscaled.py:306-309), or "compute" for bfloat16 GEMMs.
+        quantized: the kernels already in MXFP8 (`in_mxfp8(up, down, fmt)`), as the
+            reference's `quantized` (moe.py:799); None to quantize them here.
         fused: in MXFP8 (without `intermediates`), the activation and h's two copies in
             the up GEMM's epilogue (`grouped_mxfp8.activated`): the same bits, in one
             GEMM kernel instead of the GEMM and the activation's quantizer.
@@ -242,16 +269,19 @@ def experts_forward(
     x_m = up_n = h_m = down_n = rows = None
     _check_fmt(fmt)
     mx, tiles = fmt in MX_FORMATS, fmt == "mxfp8_2d"
-    tiles = None
+    listed = None
     if mx:
         height = grouped_mxfp8.whole(m)
         with span("tile list"):
             # one tile list for the step's six GEMMs: a of `height` rows, outputs of m
-            tiles = grouped_mxfp8.tiles_of(s.sizes, height, m)
+            listed = grouped_mxfp8.tiles_of(s.sizes, height, m)
         with span("quantize x"):
             x_k, x_m = grouped_mxfp8.quantized_twice(z, filled, True, s.order, k, height)
-        with span("quantize W_up"):
-            up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
+        if quantized is not None:
+            up_n, up_k = quantized.up_n, quantized.up_k
+        else:
+            with span("quantize W_up"):
+                up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
         if fused and not intermediates:
             with span("up fprop + activation + quantize h"):
                 projected, h_k, h_m = grouped_mxfp8.activated(x_k, up_k, s.sizes, row_weights,
@@ -259,7 +289,7 @@ def experts_forward(
             h = None
         else:
             with span("up fprop"):
-                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m, tiles=tiles)
+                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m, tiles=listed)
     else:
         with span("gather x"):
             rows = token_rows(z, s.order, k)
@@ -270,10 +300,13 @@ def experts_forward(
             with span("activation + quantize h"):
                 h_k, h_m, h = weighted_units_quantized(ffn, projected.view(m, f, p), row_weights,
                                                        filled, height, intermediates)
-        with span("quantize W_down"):
-            down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
+        if quantized is not None:
+            down_n, down_k = quantized.down_n, quantized.down_k
+        else:
+            with span("quantize W_down"):
+                down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
         with span("down fprop"):
-            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=tiles)
+            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=listed)
     else:
         with span("activation"):
             h = weighted_units(ffn, projected.view(m, f, p), row_weights, filled)
@@ -281,7 +314,7 @@ def experts_forward(
             y = grouped.dot(h, down, s.sizes)
     with span("combine"):
         out = sum_by_token(y, s.inverse.view(t, k))
-    return out, Saved(s, k, row_weights, projected, h, x_m, up_n, h_m, down_n, rows, tiles)
+    return out, Saved(s, k, row_weights, projected, h, x_m, up_n, h_m, down_n, rows, listed)
 
 
 def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: torch.Tensor,

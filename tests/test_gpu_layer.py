@@ -208,3 +208,47 @@ def test_layer_forward_and_backward(lib, name, t, k, e, d, f, act, fmt):
            bf16.to_f32(omoe.contract_mx(x_m, dp_m, s.sizes)))
     d_weights = bf16_bits(grads["d_row_weights"])[s.inverse].reshape(t, k)
     np.testing.assert_array_equal(bf16_bits(grads["weights"]), d_weights)
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp8_2d"])
+def test_the_layer_quantizes_its_weights_by_its_recipe(lib, fmt):
+    """The weights' copies the layer keeps for its backward are exactly its recipe's:
+    1x32 blocks (mxfp8) or one scale per 32 x 32 tile (mxfp8_2d), bit for bit the
+    quantizer's, and the same as `in_mxfp8` gives to callers that quantize once."""
+    from bux_amd import grouped_mxfp8, moe
+    rng = np.random.default_rng(43)
+    z, idx, w, up, down, dy = _inputs(rng, 256, 4, 8, 256, 256, None)
+    gz, gidx, gw, gup, gdown = (to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up),
+                                to_gpu_bf16(down))
+    announce("layer weights", fmt)
+    _, saved = moe.experts_forward(gz, gidx, gw, gup, gdown, fmt=fmt)
+    e, d, f, p = up.shape
+    tiles = fmt == "mxfp8_2d"
+    want_up, _ = grouped_mxfp8.quantized_twice(gup.reshape(e, d, f * p), tiles=tiles)
+    want_down, _ = grouped_mxfp8.quantized_twice(gdown, tiles=tiles)
+    given = moe.in_mxfp8(gup, gdown, fmt)
+    torch.cuda.synchronize()
+    for got, want in ((saved.up_n, want_up), (saved.down_n, want_down),
+                      (given.up_n, want_up), (given.down_n, want_down)):
+        assert torch.equal(got.values, want.values) and torch.equal(got.scales, want.scales)
+    # the two recipes differ: a 1x32 copy is not the tile-scaled one
+    other, _ = grouped_mxfp8.quantized_twice(gup.reshape(e, d, f * p), tiles=not tiles)
+    assert not torch.equal(saved.up_n.scales, other.scales)
+
+
+def test_a_layer_given_its_weights_in_mxfp8_is_the_same_layer(lib):
+    """experts_forward(quantized=in_mxfp8(up, down)) (the reference's `quantized`,
+    moe.py:799) gives the bits of the layer that quantizes them itself."""
+    from bux_amd import moe
+    rng = np.random.default_rng(44)
+    z, idx, w, up, down, dy = _inputs(rng, 300, 4, 8, 256, 192, None)
+    args = (to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up), to_gpu_bf16(down))
+    announce("layer given weights")
+    out0, saved0 = moe.experts_forward(*args)
+    g0 = moe.experts_backward(saved0, to_gpu_bf16(dy), args[3], args[4])
+    out1, saved1 = moe.experts_forward(*args, quantized=moe.in_mxfp8(args[3], args[4]))
+    g1 = moe.experts_backward(saved1, to_gpu_bf16(dy), args[3], args[4])
+    torch.cuda.synchronize()
+    assert torch.equal(out0.view(torch.int16), out1.view(torch.int16))
+    for key in g0:
+        assert torch.equal(g0[key].view(torch.int16), g1[key].view(torch.int16)), key
