@@ -257,41 +257,32 @@ __device__ __forceinline__ void wait_loads(int32_t steps) {
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-__device__ __forceinline__ uint4 zero_outside(uint4 v, int32_t k0, int32_t lo, int32_t hi) {
-  if (k0 >= lo && k0 + 16 <= hi) return v;
-  if (k0 + 16 <= lo || k0 >= hi) return make_uint4(0, 0, 0, 0);
-  uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    uint32_t keep = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int32_t k = k0 + 4 * q + b;
-      if (k >= lo && k < hi) keep |= 0xffu << (8 * b);
-    }
-    w[q] &= keep;
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
-// Zeroes A's bytes of K outside [lo, hi) in stage `st`, step ks (a wgrad's edge steps):
-// lane t takes row t.
-__device__ __forceinline__ void mask_stage(Lds& lds, int st, int32_t ks, int32_t lo, int32_t hi) {
-  const int r = threadIdx.x;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int32_t k0 = ks * BK + 16 * c;
-    if (k0 >= lo && k0 + 16 <= hi) continue;
-    uint4* at = reinterpret_cast<uint4*>(&lds.st[st].a[r * BK + ((c ^ swizzle(r)) << 4)]);
-    *at = zero_outside(*at, k0, lo, hi);
-  }
-}
-
 // A wave's operands of one step: 4 blocks of 32 rows of A and of B, and their scales.
 struct Frag {
   v8i a[4], b[4];
   int sa[4], sb[4];
 };
+
+// Zeroes the bytes of A's operand registers of K step ks whose K lies outside [lo, hi)
+// (a wgrad's edge steps): lane half h holds K bytes 16 h .. 16 h + 15 of the step in
+// dwords 0-3 and 32 + 16 h .. in dwords 4-7, the same for every row it holds.
+__device__ __forceinline__ void mask_frag(Frag& f, int32_t ks, int32_t lo, int32_t hi) {
+  const int h = (threadIdx.x & 63) >> 5;
+  uint32_t keep[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int32_t k0 = ks * BK + (j < 4 ? 16 * h + 4 * j : 32 + 16 * h + 4 * (j - 4));
+    uint32_t m = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if (k0 + b >= lo && k0 + b < hi) m |= 0xffu << (8 * b);
+    keep[j] = m;
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.a[p][j] &= keep[j];
+}
 
 // This lane's byte offsets in a stage, computed once: its two 16-byte chunks of A's
 // (B's) 32-row block 0 (K chunks h and 2 + h of the step for lane half h, the MFMA's two
@@ -672,12 +663,9 @@ __device__ void run_tiles(const Tiles& tiles, int32_t count, const Operand& A, c
       auto edge = [&](int32_t k) { return job.mask && (k == 0 || k == n - 1); };
       if (ready < 1) wait_loads(smaller(n, STAGES) - 1 + ahead);
       barrier_lds();
-      if (edge(0)) {
-        mask_stage(lds, stage(0), job.ks_begin, job.mlo, job.mhi);
-        barrier_lds();
-      }
       Frag cur, nxt;
       read_frag(cur, lds, ln, stage(0), job.ks_begin);
+      if (edge(0)) mask_frag(cur, job.ks_begin, job.mlo, job.mhi);
       int32_t k = 0;
       // Steps with this tile's load 4 ahead, two a turn so that the operand sets swap
       // roles without a copy; step k + 1 < n - 1 is never an edge here.
@@ -704,10 +692,6 @@ __device__ void run_tiles(const Tiles& tiles, int32_t count, const Operand& A, c
       for (; k + 1 < n; ++k) {
         if (k + 1 >= ready) wait_loads(smaller(n - 2 - k + ahead, 3));
         barrier_lds();
-        if (edge(k + 1)) {
-          mask_stage(lds, stage(k + 1), job.ks_begin + k + 1, job.mlo, job.mhi);
-          barrier_lds();
-        }
         if (ahead < 3 && ahead < nn && k + STAGES == n + ahead) {
           issue(na, nb, next.ks_begin + ahead, lds0, stage(k));
           ++ahead;
@@ -716,6 +700,8 @@ __device__ void run_tiles(const Tiles& tiles, int32_t count, const Operand& A, c
                           stage(k + 1), acc);
         cur = nxt;
       }
+      // the last step's operands (read during the step before): its edge, if it has one
+      if (n > 1 && edge(n - 1)) mask_frag(cur, job.ks_begin + n - 1, job.mlo, job.mhi);
       step<false, false>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, 0, 0, acc);
     }
     // Every load in flight (the next tile's first steps) lands before the stores go out;
