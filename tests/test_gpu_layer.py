@@ -252,3 +252,45 @@ def test_a_layer_given_its_weights_in_mxfp8_is_the_same_layer(lib):
     assert torch.equal(out0.view(torch.int16), out1.view(torch.int16))
     for key in g0:
         assert torch.equal(g0[key].view(torch.int16), g1[key].view(torch.int16)), key
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "compute"])
+def test_a_layer_with_no_pick_inside_the_experts_is_zero(lib, fmt):
+    """Every pick outside [0, E) (the reference sorts those last and counts them for no
+    expert, moe.py:776-797): no group holds a row, every GEMM output is 0, and so are y
+    and every gradient."""
+    from bux_amd import moe
+    rng = np.random.default_rng(45)
+    t, k, e, d, f = 64, 2, 4, 128, 64
+    z, idx, w, up, down, dy = _inputs(rng, t, k, e, d, f, None)
+    idx[:] = e + 3
+    announce("layer no picks", fmt)
+    out, saved = moe.experts_forward(to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up),
+                                     to_gpu_bf16(down), fmt=fmt)
+    grads = moe.experts_backward(saved, to_gpu_bf16(dy), to_gpu_bf16(up), to_gpu_bf16(down),
+                                 fmt=fmt)
+    torch.cuda.synchronize()
+    assert int(saved.sorted.sizes.sum()) == 0
+    assert (out.float() == 0).all()
+    for key, g in grads.items():
+        assert (g.float() == 0).all(), key
+
+
+def test_a_layer_of_one_token(lib):
+    """One token, its k picks in k groups of one row each: against the oracle, end to
+    end."""
+    from bux_amd import moe
+    o, g = _ffn("swiglu")
+    rng = np.random.default_rng(46)
+    t, k, e, d, f = 1, 4, 8, 128, 64
+    z, idx, w, up, down, dy = _inputs(rng, t, k, e, d, f, None)
+    announce("layer one token")
+    out, saved = moe.experts_forward(to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up),
+                                     to_gpu_bf16(down), g)
+    grads = moe.experts_backward(saved, to_gpu_bf16(dy), to_gpu_bf16(up), to_gpu_bf16(down), g)
+    torch.cuda.synchronize()
+    want, osaved = omoe.layer_forward(z, idx, w, up, down, o, "mxfp8")
+    wgrads = omoe.layer_backward(osaved, dy, z, up, down, k, o, "mxfp8")
+    _stage("one token y", _f32(out), bf16.to_f32(want), END_TO_END)
+    for key in ("z", "weights", "up", "down"):
+        _stage(f"one token d{key}", _f32(grads[key]), bf16.to_f32(wgrads[key]), END_TO_END)
