@@ -291,8 +291,15 @@ __global__ __launch_bounds__(THREADS) void glu_weights_kernel(const float* __res
   if (r >= m) return;
   const int64_t filled = filled_ptr ? static_cast<int64_t>(*filled_ptr) : m;
   float sum = 0.0f;
-  if (r < filled)
-    for (int64_t c = 0; c < tiles; ++c) sum += partials[r * tiles + c];
+  if (r < filled) {
+    // tiles is even (two 64-column tiles a 128 of d projected): pairs, added in order
+    const float2* row = reinterpret_cast<const float2*>(partials + r * tiles);
+    for (int64_t c = 0; c < tiles / 2; ++c) {
+      const float2 v = row[c];
+      sum += v.x;
+      sum += v.y;
+    }
+  }
   d_weights[r] = f32_to_bf16(sum);
 }
 
