@@ -35,6 +35,8 @@ SIGNATURES = {
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p]),
     "bux_mx_grouped_contract_listed": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _int, _p, _p]),
+    "bux_mx_grouped_rows_noalloc": (
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p]),
     "bux_mx_grouped_contract_workspace_size": (_size, [_i32]),
     "bux_mx_grouped_contract": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
@@ -66,6 +68,7 @@ SIGNATURES = {
 MX_ROWS, MX_COLUMNS, MX_TILES = 1, 2, 4
 BF16, F32 = 0, 1
 SWISH, QUICK_GELU = 0, 1
+NOALLOC_SCRATCH_BYTES = 262144
 ROUTER_SOFTMAX, ROUTER_SIGMOID, ROUTER_SQRTSOFTPLUS = 0, 1, 2
 
 

@@ -44,6 +44,8 @@
 // workgroup's id modulo 8) takes a contiguous run of tiles, which share A's rows and a
 // group's B in its L2.
 
+#include <mutex>
+
 #include "common.h"
 #include "glu.h"
 
@@ -1203,6 +1205,76 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
                      tiles_in(workspace, groups));
   if (int rc = launched("prologue_kernel")) return rc;
   return launch_rows_of(a_values, a_scales, b_values, b_scales, workspace, groups, m, n, k, height,
+                        out_dtype, y, s);
+}
+
+// --- bux_mx_grouped_rows without a workspace -------------------------------------------
+//
+// For callers that cannot allocate (graph capture, serving loops): the rows GEMM's
+// workspace -- the group starts and the tile list its prologue writes in full on every
+// call, so nothing in it needs clearing -- in a static device array of SCRATCH_BYTES,
+// each GPU its own copy, held until the process ends. Every call on a GPU shares that
+// GPU's array: two calls that overlap on one GPU (two streams, two host threads) race.
+namespace bux {
+namespace {
+
+constexpr size_t SCRATCH_BYTES = BUX_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_lock;
+void* scratch_at[MAX_DEVICES] = {};  // each device's address of `scratch`, once known
+
+// The current device's address of `scratch` (host code never passes the array's own
+// name, a host-side stand-in, to a kernel).
+int scratch_of(void** out) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(BUX_E_DEVICE, "the current device: %s", hipGetErrorString(err));
+  if (device < 0 || device >= MAX_DEVICES)
+    return fail(BUX_E_DEVICE, "device %d: the scratch arrays cover devices 0 to %d", device,
+                MAX_DEVICES - 1);
+  std::lock_guard<std::mutex> hold(scratch_lock);
+  if (scratch_at[device] == nullptr) {
+    void* at = nullptr;
+    err = hipGetSymbolAddress(&at, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || at == nullptr)
+      return fail(BUX_E_DEVICE, "device %d: the scratch array's address: %s", device,
+                  hipGetErrorString(err));
+    scratch_at[device] = at;
+  }
+  *out = scratch_at[device];
+  return BUX_OK;
+}
+
+}  // namespace
+}  // namespace bux
+
+extern "C" int bux_mx_grouped_rows_noalloc(const uint8_t* a_values, const uint8_t* a_scales,
+                                           const uint8_t* b_values, const uint8_t* b_scales,
+                                           const int32_t* sizes, int32_t groups, int64_t m,
+                                           int64_t n, int64_t k, int64_t height, int out_dtype,
+                                           void* y, void* stream) {
+  using namespace bux;
+  clear_error();
+  if (int rc = check_rows("bux_mx_grouped_rows_noalloc", a_values, a_scales, b_values, b_scales,
+                          groups, m, n, k, height, out_dtype, y))
+    return rc;
+  BUX_CHECK(sizes != nullptr, "bux_mx_grouped_rows_noalloc: NULL buffer");
+  const size_t need = bux_mx_grouped_rows_workspace_size(groups, m, height);
+  if (need > SCRATCH_BYTES)
+    return fail(BUX_E_WORKSPACE,
+                "bux_mx_grouped_rows_noalloc: groups=%d, m=%lld, height=%lld need a workspace of "
+                "%zu bytes, past its fixed %zu (use bux_mx_grouped_rows with a workspace)",
+                groups, (long long)m, (long long)height, need, SCRATCH_BYTES);
+  if (height == 0) return BUX_OK;
+  void* ws = nullptr;
+  if (int rc = scratch_of(&ws)) return rc;
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height,
+                     row_slots(groups, m, height), 1, starts_in(ws), tiles_in(ws, groups));
+  if (int rc = launched("prologue_kernel")) return rc;
+  return launch_rows_of(a_values, a_scales, b_values, b_scales, ws, groups, m, n, k, height,
                         out_dtype, y, s);
 }
 

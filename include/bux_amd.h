@@ -151,6 +151,23 @@ int bux_mx_grouped_contract_listed(const uint8_t* a_values, const uint8_t* a_sca
                                    const void* list, int32_t groups, int64_t d, int64_t f,
                                    int64_t m, int out_dtype, void* dw, void* stream);
 
+/* bux_mx_grouped_rows_noalloc: bux_mx_grouped_rows with no workspace argument and no
+ * allocation of any kind. It has no counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Its workspace -- the group starts and the tile list -- lives in a
+ * static device array of BUX_NOALLOC_SCRATCH_BYTES on each GPU, held until the process
+ * ends; a call whose bux_mx_grouped_rows_workspace_size(groups, m, height) exceeds it
+ * fails with BUX_E_WORKSPACE (256 KiB: e.g. 1024 groups and 3.5 M rows). Nothing in the
+ * array needs clearing (each call's prologue writes all it reads), but every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (two streams, two host
+ * threads) race. Same outputs as bux_mx_grouped_rows, bit for bit.
+ */
+enum { BUX_NOALLOC_SCRATCH_BYTES = 262144 };
+int bux_mx_grouped_rows_noalloc(const uint8_t* a_values, const uint8_t* a_scales,
+                                const uint8_t* b_values, const uint8_t* b_scales,
+                                const int32_t* sizes, int32_t groups, int64_t m, int64_t n,
+                                int64_t k, int64_t height, int out_dtype, void* y, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * a-7. Grouped MXFP8 GEMM contracting each group's rows: dw[g] = a[:, g] b[:, g]^T.
  *
