@@ -20,6 +20,23 @@ _int = ctypes.c_int
 _f32 = ctypes.c_float
 _size = ctypes.c_size_t
 
+
+class FfnStruct(ctypes.Structure):
+    """``bux_ffn``: an expert FFN's activation settings."""
+
+    _fields_ = [
+        ("activation", ctypes.c_int32),
+        ("gated", ctypes.c_int32),
+        ("clamped", ctypes.c_int32),
+        ("limit", ctypes.c_float),
+        ("capped", ctypes.c_int32),
+        ("up_softcap", ctypes.c_float),
+        ("up_offset", ctypes.c_float),
+    ]
+
+
+_ffn = ctypes.POINTER(FfnStruct)
+
 # name -> (restype, argtypes), as include/bux_amd.h declares them.
 SIGNATURES = {
     "bux_last_error": (ctypes.c_char_p, []),
@@ -44,17 +61,21 @@ SIGNATURES = {
     "bux_bf16_grouped_contract": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p]),
     "bux_token_rows": (_int, [_p, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
-    "bux_glu_forward": (_int, [_p, _p, _p, _i64, _i64, _int, _f32, _f32, _p, _p]),
-    "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _f32, _f32, _p, _p, _p]),
+    "bux_token_sums_biased": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p, _i32, _p, _p, _p]),
+    "bux_expert_bias_add": (_int, [_p, _i64, _i64, _p, _p, _i32, _p]),
+    "bux_expert_sums": (_int, [_p, _p, _i32, _p, _i64, _i64, _p, _i32, _p, _p]),
+    "bux_expert_bias_weight_grad": (_int, [_p, _p, _i32, _i64, _i64, _p, _p, _i32, _p, _p]),
+    "bux_glu_forward": (_int, [_p, _p, _p, _i64, _i64, _ffn, _p, _p]),
+    "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _ffn, _p, _p, _p]),
     "bux_glu_quantize": (
-        _int, [_p, _p, _p, _i64, _i64, _int, _f32, _f32, _i64, _p, _p, _p, _p, _p, _p]),
+        _int, [_p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p]),
     "bux_mx_grouped_glu_workspace_size": (_size, [_i32, _i64]),
     "bux_mx_grouped_glu": (
-        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p, _int, _f32, _f32, _p, _p,
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p, _ffn, _p, _p,
                _p, _p, _p, _p, _size, _p]),
     "bux_glu_backward_quantize_workspace_size": (_size, [_i64, _i64]),
     "bux_glu_backward_quantize": (
-        _int, [_p, _p, _p, _p, _i64, _i64, _int, _f32, _f32, _i64, _p, _p, _p, _p, _p, _p, _p,
+        _int, [_p, _p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p, _p,
                _size, _p]),
     "bux_mx_pack_rows": (_int, [_p, _p, _i32, _i64, _i64, _i64, _p, _p]),
     "bux_mx_unpack_rows": (_int, [_p, _i64, _i64, _p, _p]),
@@ -67,7 +88,9 @@ SIGNATURES = {
 # Constants of include/bux_amd.h.
 MX_ROWS, MX_COLUMNS, MX_TILES = 1, 2, 4
 BF16, F32 = 0, 1
-SWISH, QUICK_GELU = 0, 1
+# the activations, bux_ffn.activation
+ACTIVATIONS = {"swish": 0, "quick_gelu": 1, "relu": 2, "relu2": 3, "gelu": 4, "gelu_tanh": 5,
+               "sigmoid": 6, "tanh": 7, "softplus": 8, "situ": 9}
 NOALLOC_SCRATCH_BYTES = 262144
 ROUTER_SOFTMAX, ROUTER_SIGMOID, ROUTER_SQRTSOFTPLUS = 0, 1, 2
 

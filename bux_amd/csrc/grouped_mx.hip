@@ -861,6 +861,8 @@ __device__ __forceinline__ float high_bf16(uint32_t p) { return bf16_to_f32(stat
 
 // The fused epilogue's outputs. The product's columns are (up, gate) pairs of units:
 // unit u's up at column 2u, its gate at 2u + 1 (the experts' (f, 2) kernels flattened).
+// K: the gated activation (Kind<BUX_SWISH | BUX_QUICK_GELU | BUX_SITU, true>).
+template <typename K>
 struct GluOut {
   const uint16_t* weights;  // bfloat16 (rows,): each row's weight
   uint16_t* projected;      // bfloat16 (rows, n): the product
@@ -919,8 +921,8 @@ struct GluOut {
           const int32_t u = u0 + 16 * jj + 4 * g + 2 * half;
           float h0 = 0.0f, h1 = 0.0f;
           if (on[i] && u < f) {
-            h0 = glu_unit(act, low_bf16(p0), high_bf16(p0), w[i]);
-            h1 = glu_unit(act, low_bf16(p1), high_bf16(p1), w[i]);
+            h0 = glu_unit<K>(act, low_bf16(p0), high_bf16(p0), w[i]);
+            h1 = glu_unit<K>(act, low_bf16(p1), high_bf16(p1), w[i]);
           }
           hp[jj][g] = pack_bf16x2(h0, h1);
           amax[jj >> 1] = fmaxf(amax[jj >> 1],
@@ -1018,9 +1020,10 @@ struct GluOut {
   }
 };
 
+template <typename K>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void glu_kernel(
     Operand A, Operand B, int32_t groups, int32_t height, const int32_t* __restrict__ starts,
-    const Tile* __restrict__ tiles, int32_t col_tiles, GluOut out) {
+    const Tile* __restrict__ tiles, int32_t col_tiles, GluOut<K> out) {
   extern __shared__ __align__(16) uint8_t smem[];
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const GluTiles list{tiles, starts, groups, B.rows, height, col_tiles, A.k / BK};
@@ -1034,6 +1037,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 // groups' end, or from `rows`, are 0). Workgroup g takes the block of group g's first
 // row (g = groups: the groups' end), unless group g - 1's first row is inside the same
 // block too; its lane t unit 256 blockIdx.y + t.
+template <typename K>
 __global__ __launch_bounds__(THREADS) void glu_edges_kernel(
     const int32_t* __restrict__ starts, int32_t groups, const uint16_t* __restrict__ projected,
     const uint16_t* __restrict__ weights, Act act, int32_t rows, int32_t f, int32_t height,
@@ -1055,7 +1059,7 @@ __global__ __launch_bounds__(THREADS) void glu_edges_kernel(
       float h = 0.0f;
       if (r < live) {
         const uint32_t p = *reinterpret_cast<const uint32_t*>(projected + (static_cast<int64_t>(r) * f + u) * 2);
-        h = low_bf16(pack_bf16x2(glu_unit(act, low_bf16(p), high_bf16(p), bf16_to_f32(weights[r])), 0.0f));
+        h = low_bf16(pack_bf16x2(glu_unit<K>(act, low_bf16(p), high_bf16(p), bf16_to_f32(weights[r])), 0.0f));
       }
       v[k] = h;
       amax = fmaxf(amax, fabsf(h));
@@ -1345,8 +1349,8 @@ extern "C" size_t bux_mx_grouped_glu_workspace_size(int32_t groups, int64_t heig
 extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scales,
                                   const uint8_t* b_values, const uint8_t* b_scales,
                                   const int32_t* sizes, int32_t groups, int64_t height, int64_t n,
-                                  int64_t k, int64_t rows, const uint16_t* weights, int activation,
-                                  float limit, float up_offset, uint16_t* projected,
+                                  int64_t k, int64_t rows, const uint16_t* weights,
+                                  const bux_ffn* ffn, uint16_t* projected,
                                   uint8_t* values, uint8_t* scales, uint8_t* t_values,
                                   uint8_t* t_scales, void* workspace, size_t workspace_bytes,
                                   void* stream) {
@@ -1362,8 +1366,11 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
   BUX_CHECK(offsets_fit(height, k) && offsets_fit(n, k),
             "bux_mx_grouped_glu: an operand of %lld x %lld bytes exceeds 2 GiB",
             (long long)(height > n ? height : n), (long long)k);
-  BUX_CHECK(activation == BUX_SWISH || activation == BUX_QUICK_GELU,
-            "bux_mx_grouped_glu: activation %d is neither BUX_SWISH nor BUX_QUICK_GELU", activation);
+  Act act;
+  if (int rc = act_of("bux_mx_grouped_glu", ffn, &act)) return rc;
+  BUX_CHECK(act.gated && (act.kind == BUX_SWISH || act.kind == BUX_QUICK_GELU || act.kind == BUX_SITU),
+            "bux_mx_grouped_glu: the fused epilogue is of a gated BUX_SWISH, BUX_QUICK_GELU or "
+            "BUX_SITU, not activation %d%s", act.kind, act.gated ? "" : " plain");
   BUX_CHECK(sizes && b_values && b_scales &&
                 (height == 0 || (a_values && a_scales && values && scales && t_values && t_scales)) &&
                 (rows == 0 || (weights && projected)),
@@ -1384,21 +1391,27 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
   if (int rc = launched("prologue_kernel")) return rc;
   const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(height)};
   const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};
-  const Act act{activation, limit, up_offset};
   const int32_t f = static_cast<int32_t>(n / 2);
-  const GluOut out{weights, projected, values, scales, t_values, t_scales, act,
-                   static_cast<int32_t>(rows), static_cast<int32_t>(n), f,
-                   static_cast<int32_t>(height), 0};
   unsigned blocks = 0;
   if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
-  if (int rc = allow_lds(glu_kernel, "glu_kernel")) return rc;
-  hipLaunchKernelGGL(glu_kernel, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
-                     static_cast<int32_t>(height), starts, tiles, static_cast<int32_t>(col_tiles), out);
-  if (int rc = launched("glu_kernel")) return rc;
-  hipLaunchKernelGGL(glu_edges_kernel,
-                     dim3(static_cast<unsigned>(groups + 1), static_cast<unsigned>(ceil_div(f, THREADS))),
-                     dim3(THREADS), 0, s,
-                     starts, groups, projected, weights, act, static_cast<int32_t>(rows), f,
-                     static_cast<int32_t>(height), t_values, t_scales);
-  return launched("glu_edges_kernel");
+  auto run = [&](auto kind) {
+    using K = decltype(kind);
+    const GluOut<K> out{weights, projected, values, scales, t_values, t_scales, act,
+                        static_cast<int32_t>(rows), static_cast<int32_t>(n), f,
+                        static_cast<int32_t>(height), 0};
+    if (int rc = allow_lds(glu_kernel<K>, "glu_kernel")) return rc;
+    hipLaunchKernelGGL(glu_kernel<K>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+                       static_cast<int32_t>(height), starts, tiles, static_cast<int32_t>(col_tiles),
+                       out);
+    if (int rc = launched("glu_kernel")) return rc;
+    hipLaunchKernelGGL(glu_edges_kernel<K>,
+                       dim3(static_cast<unsigned>(groups + 1), static_cast<unsigned>(ceil_div(f, THREADS))),
+                       dim3(THREADS), 0, s, starts, groups, projected, weights, act,
+                       static_cast<int32_t>(rows), f, static_cast<int32_t>(height), t_values,
+                       t_scales);
+    return launched("glu_edges_kernel");
+  };
+  if (act.kind == BUX_QUICK_GELU) return run(Kind<BUX_QUICK_GELU, true>{});
+  if (act.kind == BUX_SITU) return run(Kind<BUX_SITU, true>{});
+  return run(Kind<BUX_SWISH, true>{});
 }

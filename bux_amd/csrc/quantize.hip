@@ -77,8 +77,20 @@ struct Matrix {
   __device__ __forceinline__ void partial(int64_t, int64_t, float) const {}
 };
 
-// h = act(gate) (up + offset) w from projected (m, f, 2) and the rows' weights; columns
-// are units. Rows past `filled` give 0. With `h`, the values are stored there too.
+// Eight bfloat16 of a uint4 as floats.
+__device__ __forceinline__ void floats8(const uint4& r, float* v) {
+  const uint32_t q[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = bf16_to_f32(static_cast<uint16_t>(q[j] & 0xffffu));
+    v[2 * j + 1] = bf16_to_f32(static_cast<uint16_t>(q[j] >> 16));
+  }
+}
+
+// h = act(gate) (up + offset) w, or act(up) w, from projected ((m, f, 2) gated, (m, f)
+// plain) and the rows' weights; columns are units. Rows past `filled` give 0. With `h`,
+// the values are stored there too.
+template <typename K>
 struct GluForward {
   static constexpr bool kPartials = false;
   const uint16_t* projected;
@@ -90,15 +102,21 @@ struct GluForward {
                                         float*) const {
     uint4 out = make_uint4(0, 0, 0, 0);
     if (live) {
-      const uint4* p = reinterpret_cast<const uint4*>(projected + (r * f + col) * 2);
-      const uint4 lo = p[0], hi = p[1];
       const float w = bf16_to_f32(weights[r]);
-      const uint32_t q[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       float v[8];
+      if constexpr (K::gated) {
+        const uint4* p = reinterpret_cast<const uint4*>(projected + (r * f + col) * 2);
+        float pair[16];
+        floats8(p[0], pair);
+        floats8(p[1], pair + 8);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        v[j] = glu_unit(act, bf16_to_f32(static_cast<uint16_t>(q[j] & 0xffffu)),
-                        bf16_to_f32(static_cast<uint16_t>(q[j] >> 16)), w);
+        for (int j = 0; j < 8; ++j) v[j] = glu_unit<K>(act, pair[2 * j], pair[2 * j + 1], w);
+      } else {
+        float up[8];
+        floats8(*reinterpret_cast<const uint4*>(projected + r * f + col), up);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = glu_unit<K>(act, up[j], 0.0f, w);
+      }
       out = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
     }
     if (h && r < m && inside) *reinterpret_cast<uint4*>(h + r * f + col) = out;
@@ -107,12 +125,15 @@ struct GluForward {
   __device__ __forceinline__ void partial(int64_t, int64_t, float) const {}
 };
 
-// d projected (m, f, 2) from projected, the rows' weights and dh (m, f); columns are
-// projected's 2 f. Each workgroup also leaves its 64 columns' share of each row's d
-// weight (the sum of its units' terms) in `partials` (m rows of `tiles`), which
-// glu_weights_kernel sums in order. With `d_projected`, the values are stored there too.
+// d projected from projected, the rows' weights and dh (m, f); columns are projected's
+// p f (gated: (up, gate) pairs, p = 2; plain: units, p = 1). Each workgroup also leaves
+// its 64 columns' share of each row's d weight (the sum of its units' terms) in
+// `partials` (m rows of `tiles`), which glu_weights_kernel sums in order. With
+// `d_projected`, the values are stored there too.
+template <typename K>
 struct GluBackward {
   static constexpr bool kPartials = true;
+  static constexpr int P = K::gated ? 2 : 1;
   const uint16_t* projected;
   const uint16_t* weights;
   const uint16_t* dh;
@@ -125,26 +146,34 @@ struct GluBackward {
     uint4 out = make_uint4(0, 0, 0, 0);
     *dw = 0.0f;
     if (live) {
-      const uint4 p = *reinterpret_cast<const uint4*>(projected + r * f * 2 + col);
-      const uint2 d = *reinterpret_cast<const uint2*>(dh + r * f + col / 2);
+      float p[8], v[8], sum = 0.0f;
+      floats8(*reinterpret_cast<const uint4*>(projected + r * f * P + col), p);
       const float w = bf16_to_f32(weights[r]);
-      const uint32_t q[4] = {p.x, p.y, p.z, p.w};
-      const float g[4] = {bf16_to_f32(d.x & 0xffffu), bf16_to_f32(d.x >> 16),
-                          bf16_to_f32(d.y & 0xffffu), bf16_to_f32(d.y >> 16)};
-      float v[8], sum = 0.0f;
+      if constexpr (K::gated) {
+        const uint2 d = *reinterpret_cast<const uint2*>(dh + r * f + col / 2);
+        const float g[4] = {bf16_to_f32(d.x & 0xffffu), bf16_to_f32(d.x >> 16),
+                            bf16_to_f32(d.y & 0xffffu), bf16_to_f32(d.y >> 16)};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float term;
-        glu_unit_grad(act, bf16_to_f32(static_cast<uint16_t>(q[j] & 0xffffu)),
-                      bf16_to_f32(static_cast<uint16_t>(q[j] >> 16)), w, g[j], &v[2 * j],
-                      &v[2 * j + 1], &term);
-        sum += term;
+        for (int j = 0; j < 4; ++j) {
+          float term;
+          glu_unit_grad<K>(act, p[2 * j], p[2 * j + 1], w, g[j], &v[2 * j], &v[2 * j + 1], &term);
+          sum += term;
+        }
+      } else {
+        float g[8];
+        floats8(*reinterpret_cast<const uint4*>(dh + r * f + col), g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float term, none;
+          glu_unit_grad<K>(act, p[j], 0.0f, w, g[j], &v[j], &none, &term);
+          sum += term;
+        }
       }
       *dw = sum;
       out = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
     }
     if (d_projected && r < m && inside)
-      *reinterpret_cast<uint4*>(d_projected + r * f * 2 + col) = out;
+      *reinterpret_cast<uint4*>(d_projected + r * f * P + col) = out;
     return out;
   }
   __device__ __forceinline__ void partial(int64_t r, int64_t tile, float v) const {
@@ -350,60 +379,58 @@ extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t 
                          as_stream(stream));
 }
 
-namespace {
-int check_act(const char* name, int activation) {
-  BUX_CHECK(activation == BUX_SWISH || activation == BUX_QUICK_GELU,
-            "%s: activation %d is neither BUX_SWISH nor BUX_QUICK_GELU", name, activation);
-  return BUX_OK;
-}
-}  // namespace
-
 extern "C" int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights,
-                                const int32_t* filled, int64_t m, int64_t f, int activation,
-                                float limit, float up_offset, int64_t height, uint16_t* h,
-                                uint8_t* values, uint8_t* scales, uint8_t* t_values,
-                                uint8_t* t_scales, void* stream) {
+                                const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
+                                int64_t height, uint16_t* h, uint8_t* values, uint8_t* scales,
+                                uint8_t* t_values, uint8_t* t_scales, void* stream) {
   using namespace bux;
   clear_error();
-  if (int rc = check_act("bux_glu_quantize", activation)) return rc;
+  Act act;
+  if (int rc = act_of("bux_glu_quantize", ffn, &act)) return rc;
   BUX_CHECK(m == 0 || (projected && weights), "bux_glu_quantize: NULL input");
-  const GluForward src{projected, weights, h, Act{activation, limit, up_offset}, m, f};
-  return launch_quantize("bux_glu_quantize", src, 1, m, f, height, filled,
-                         BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales,
-                         as_stream(stream));
+  return with_kind(act, [&](auto kind) {
+    using K = decltype(kind);
+    const GluForward<K> src{projected, weights, h, act, m, f};
+    return launch_quantize("bux_glu_quantize", src, 1, m, f, height, filled,
+                           BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales,
+                           as_stream(stream));
+  });
 }
 
 extern "C" size_t bux_glu_backward_quantize_workspace_size(int64_t m, int64_t f) {
   using namespace bux;
-  // a float a row and a 64-column tile of d projected
+  // a float a row and a 64-column tile of d projected, gated (the wider)
   return static_cast<size_t>(m) * static_cast<size_t>(ceil_div(2 * f, 128) * 2) * sizeof(float);
 }
 
 extern "C" int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights,
                                          const uint16_t* dh, const int32_t* filled, int64_t m,
-                                         int64_t f, int activation, float limit, float up_offset,
-                                         int64_t height, uint16_t* d_projected, uint8_t* values,
-                                         uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
+                                         int64_t f, const bux_ffn* ffn, int64_t height,
+                                         uint16_t* d_projected, uint8_t* values, uint8_t* scales,
+                                         uint8_t* t_values, uint8_t* t_scales,
                                          uint16_t* d_weights, void* workspace,
                                          size_t workspace_bytes, void* stream) {
   using namespace bux;
   clear_error();
-  if (int rc = check_act("bux_glu_backward_quantize", activation)) return rc;
+  Act act;
+  if (int rc = act_of("bux_glu_backward_quantize", ffn, &act)) return rc;
   BUX_CHECK(m == 0 || (projected && weights && dh && d_weights),
             "bux_glu_backward_quantize: NULL input or d_weights");
   const size_t need = bux_glu_backward_quantize_workspace_size(m, f);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(BUX_E_WORKSPACE, "bux_glu_backward_quantize: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
-  const int64_t tiles = ceil_div(2 * f, 128) * 2;
+  const int64_t cols = (act.gated ? 2 : 1) * f;
+  const int64_t tiles = ceil_div(cols, 128) * 2;
   float* partials = static_cast<float*>(workspace);
-  const GluBackward src{projected, weights, dh, d_projected, partials,
-                        Act{activation, limit, up_offset}, m, f, tiles};
   hipStream_t s = as_stream(stream);
-  if (int rc = launch_quantize("bux_glu_backward_quantize", src, 1, m, 2 * f, height, filled,
-                               BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales, s))
-    return rc;
-  if (m == 0) return BUX_OK;
+  const int rc = with_kind(act, [&](auto kind) {
+    using K = decltype(kind);
+    const GluBackward<K> src{projected, weights, dh, d_projected, partials, act, m, f, tiles};
+    return launch_quantize("bux_glu_backward_quantize", src, 1, m, cols, height, filled,
+                           BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales, s);
+  });
+  if (rc != BUX_OK || m == 0) return rc;
   hipLaunchKernelGGL(glu_weights_kernel, dim3(static_cast<unsigned>(ceil_div(m, THREADS))),
                      dim3(THREADS), 0, s, partials, m, tiles, filled, d_weights);
   return launched("glu_weights_kernel");

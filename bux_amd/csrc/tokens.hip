@@ -5,7 +5,9 @@
 //               in float32, picks in order, one rounding to bfloat16; an index outside
 //               y's rows adds 0 (jnp.take's mode="fill").
 //   glu         h = act(gate) (up + offset) w       moe.py:898-926, layers/mlp.py:20-35,
-//               and its gradients                   common/functional.py:12-40
+//               or act(up) w, and its gradients     common/functional.py:12-40
+//   biases      the experts' up and down biases     moe.py:857-870, 876-885, 922-925
+//               by expert, and their gradients
 //
 // All HBM-streaming: a lane moves 16 bytes (8 bfloat16) a load; a workgroup of 256
 // lanes takes 2048 columns of a row. The activation computes in float32 and rounds
@@ -38,6 +40,12 @@ __device__ __forceinline__ uint4 pack8(const float* v) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Four bfloat16 to the low halves of four words (a plain unit's up where a gated
+// unit's pair would be, its gate 0).
+__device__ __forceinline__ uint4 spread4(const uint2& r) {
+  return make_uint4(r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16);
+}
+
 __global__ __launch_bounds__(THREADS) void token_rows_kernel(const uint16_t* __restrict__ z,
                                                              const int32_t* __restrict__ order,
                                                              int32_t k, int64_t width,
@@ -64,11 +72,22 @@ __global__ __launch_bounds__(THREADS) void token_rows_narrow_kernel(
 // KMAX > 0: the token's k <= KMAX picks' rows are all requested before the first is
 // added (their indices first, then their rows); KMAX = 0: any k, one pick at a time.
 // The additions are the same either way: picks in order, a row outside y skipped.
-template <int KMAX>
+// With BIAS, a second sum beside: each pick's bias[e(r)] * weights[r] (rounded to
+// bfloat16), the picks of rows in no expert adding 0; out = the two sums, each rounded
+// to bfloat16, added and rounded.
+struct PickBias {
+  const uint16_t* bias;
+  const int32_t* offsets;
+  int32_t experts;
+  const uint16_t* weights;
+};
+
+template <int KMAX, bool BIAS>
 __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __restrict__ y,
                                                              int64_t y_rows,
                                                              const int32_t* __restrict__ inverse,
                                                              int32_t k, int64_t width,
+                                                             PickBias pb,
                                                              uint16_t* __restrict__ out) {
   const int64_t chunks = (width + THREADS * VEC - 1) / (THREADS * VEC);
   const int64_t t = blockIdx.x / chunks;
@@ -104,14 +123,32 @@ __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __r
       for (int q = 0; q < VEC; ++q) acc[q] += v[q];
     }
   }
+  if constexpr (BIAS) {
+    float bsum[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < k; ++j) {
+      const int64_t r = inverse[t * k + j];
+      if (r < 0 || r >= y_rows) continue;
+      const int32_t e = expert_of(pb.offsets, pb.experts, r);
+      if (e < 0) continue;
+      const float w = bf16_to_f32(pb.weights[r]);
+      float b[VEC];
+      unpack8(*reinterpret_cast<const uint4*>(pb.bias + e * width + c), b);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) bsum[q] += bf16_to_f32(f32_to_bf16(b[q] * w));
+    }
+#pragma unroll
+    for (int q = 0; q < VEC; ++q)
+      acc[q] = bf16_to_f32(f32_to_bf16(acc[q])) + bf16_to_f32(f32_to_bf16(bsum[q]));
+  }
   *reinterpret_cast<uint4*>(out + t * width + c) = pack8(acc);
 }
 
+// A lane takes 4 units of a row: 16 bytes of projected gated (4 up-gate pairs), 8 plain.
+template <typename K>
 __global__ __launch_bounds__(THREADS) void glu_forward_kernel(
     const uint16_t* __restrict__ projected, const uint16_t* __restrict__ weights,
     const int32_t* __restrict__ filled_ptr, int64_t m, int64_t f, Act act,
     uint16_t* __restrict__ h) {
-  // A lane takes 4 units (4 up-gate pairs, 16 bytes) of a row.
   const int64_t chunks = (f + THREADS * 4 - 1) / (THREADS * 4);
   const int64_t i = blockIdx.x / chunks;
   const int64_t u = ((blockIdx.x % chunks) * THREADS + threadIdx.x) * 4;
@@ -119,13 +156,17 @@ __global__ __launch_bounds__(THREADS) void glu_forward_kernel(
   const int64_t filled = filled_ptr ? *filled_ptr : m;
   uint2 packed = make_uint2(0, 0);
   if (i < filled) {
-    const uint4 r = *reinterpret_cast<const uint4*>(projected + (i * f + u) * 2);
     float p[8];
-    unpack8(r, p);
+    if constexpr (K::gated) {
+      unpack8(*reinterpret_cast<const uint4*>(projected + (i * f + u) * 2), p);
+    } else {
+      const uint2 r = *reinterpret_cast<const uint2*>(projected + i * f + u);
+      unpack8(spread4(r), p);  // up j at p[2 j]
+    }
     const float w = bf16_to_f32(weights[i]);
     float out[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = glu_unit(act, p[2 * j], p[2 * j + 1], w);
+    for (int j = 0; j < 4; ++j) out[j] = glu_unit<K>(act, p[2 * j], p[2 * j + 1], w);
     packed.x = f32_to_bf16(out[0]) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
     packed.y = f32_to_bf16(out[2]) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
   }
@@ -133,6 +174,7 @@ __global__ __launch_bounds__(THREADS) void glu_forward_kernel(
 }
 
 // One wave a row: d projected elementwise, d weight summed over the row's units.
+template <typename K>
 __global__ __launch_bounds__(THREADS) void glu_backward_kernel(
     const uint16_t* __restrict__ projected, const uint16_t* __restrict__ weights,
     const uint16_t* __restrict__ dh, const int32_t* __restrict__ filled_ptr, int64_t m, int64_t f,
@@ -147,25 +189,130 @@ __global__ __launch_bounds__(THREADS) void glu_backward_kernel(
   for (int64_t u = 4 * lane; u < f; u += 256) {
     float p[8] = {0, 0, 0, 0, 0, 0, 0, 0}, g[4] = {0, 0, 0, 0};
     if (live) {
-      unpack8(*reinterpret_cast<const uint4*>(projected + (i * f + u) * 2), p);
+      if constexpr (K::gated) {
+        unpack8(*reinterpret_cast<const uint4*>(projected + (i * f + u) * 2), p);
+      } else {
+        const uint2 r = *reinterpret_cast<const uint2*>(projected + i * f + u);
+        unpack8(spread4(r), p);
+      }
       const uint2 d = *reinterpret_cast<const uint2*>(dh + i * f + u);
       g[0] = bf16_to_f32(d.x & 0xffffu);
       g[1] = bf16_to_f32(d.x >> 16);
       g[2] = bf16_to_f32(d.y & 0xffffu);
       g[3] = bf16_to_f32(d.y >> 16);
     }
-    float dp[8];
+    float dp[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // rows past `filled`: +0 (not 0 x offset)
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float term;
-      glu_unit_grad(act, p[2 * j], p[2 * j + 1], w, g[j], &dp[2 * j], &dp[2 * j + 1], &term);
-      dw += term;
+      for (int j = 0; j < 4; ++j) {
+        float term;
+        glu_unit_grad<K>(act, p[2 * j], p[2 * j + 1], w, g[j], &dp[2 * j], &dp[2 * j + 1], &term);
+        dw += term;
+      }
     }
-    *reinterpret_cast<uint4*>(d_projected + (i * f + u) * 2) = pack8(dp);
+    if constexpr (K::gated) {
+      *reinterpret_cast<uint4*>(d_projected + (i * f + u) * 2) = pack8(dp);
+    } else {
+      const uint4 q = pack8(dp);  // d up j in the low half of word j
+      *reinterpret_cast<uint2*>(d_projected + i * f + u) =
+          make_uint2((q.x & 0xffffu) | (q.y << 16), (q.z & 0xffffu) | (q.w << 16));
+    }
   }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) dw += __shfl_xor(dw, s);
   if (lane == 0) d_weights[i] = f32_to_bf16(dw);
+}
+
+// --- The experts' biases --------------------------------------------------------------
+
+// x[i] += bias[e(i)] in place, 8 columns a lane; rows in no expert add 0.
+__global__ __launch_bounds__(THREADS) void expert_bias_add_kernel(
+    uint16_t* __restrict__ x, int64_t width, const uint16_t* __restrict__ bias,
+    const int32_t* __restrict__ offsets, int32_t experts) {
+  const int64_t chunks = (width + THREADS * VEC - 1) / (THREADS * VEC);
+  const int64_t i = blockIdx.x / chunks;
+  const int64_t c = ((blockIdx.x % chunks) * THREADS + threadIdx.x) * VEC;
+  if (c >= width) return;
+  const int32_t e = expert_of(offsets, experts, i);
+  float v[VEC], b[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint4* at = reinterpret_cast<uint4*>(x + i * width + c);
+  unpack8(*at, v);
+  if (e >= 0) unpack8(*reinterpret_cast<const uint4*>(bias + e * width + c), b);
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) v[q] += b[q];
+  *at = pack8(v);
+}
+
+// out[e] = sum over e's rows of v_r (x[src(r)], times weights[r] rounded to bfloat16 if
+// weights). Workgroup (e, column chunk): wave w adds rows w, w + 4, ... of e in order,
+// lanes 8 columns each; the four waves' sums are added in wave order. Deterministic.
+constexpr int SUM_COLS = 64 * VEC;  // a workgroup's columns
+__global__ __launch_bounds__(THREADS) void expert_sums_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ index, int32_t index_div,
+    const uint16_t* __restrict__ weights, int64_t width, const int32_t* __restrict__ offsets,
+    int32_t experts, float* __restrict__ out) {
+  __shared__ float part[THREADS / 64][SUM_COLS];
+  const int64_t chunks = (width + SUM_COLS - 1) / SUM_COLS;
+  const int64_t e = blockIdx.x / chunks;
+  const int64_t c0 = (blockIdx.x % chunks) * SUM_COLS;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t c = c0 + lane * VEC;
+  const int64_t lo = offsets[e], hi = offsets[e + 1];
+  float acc[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (c < width) {
+    for (int64_t r = lo + wave; r < hi; r += THREADS / 64) {
+      const int64_t src = index ? index[r] / index_div : r;
+      float v[VEC];
+      unpack8(*reinterpret_cast<const uint4*>(x + src * width + c), v);
+      if (weights) {
+        const float w = bf16_to_f32(weights[r]);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) v[q] = bf16_to_f32(f32_to_bf16(v[q] * w));
+      }
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) acc[q] += v[q];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) part[wave][lane * VEC + q] = acc[q];
+  __syncthreads();
+  // thread t: column t and t + 256 of the chunk
+  for (int j = threadIdx.x; j < SUM_COLS; j += THREADS) {
+    const int64_t col = c0 + j;
+    if (col >= width) continue;
+    float sum = part[0][j];
+#pragma unroll
+    for (int w = 1; w < THREADS / 64; ++w) sum += part[w][j];
+    out[e * width + col] = sum;
+  }
+}
+
+// d_weights[r] += sum_c dy[src(r)][c] bias[e(r)][c]: one wave a row, lanes 8 columns a
+// step, each lane's products (rounded to bfloat16) in column order, then the lanes by
+// xor-shuffles.
+__global__ __launch_bounds__(THREADS) void expert_bias_weight_grad_kernel(
+    const uint16_t* __restrict__ dy, const int32_t* __restrict__ index, int32_t index_div,
+    int64_t m, int64_t width, const uint16_t* __restrict__ bias,
+    const int32_t* __restrict__ offsets, int32_t experts, uint16_t* __restrict__ d_weights) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (THREADS / 64) + (threadIdx.x >> 6);
+  if (r >= m) return;
+  const int32_t e = expert_of(offsets, experts, r);
+  float sum = 0.0f;
+  if (e >= 0) {
+    const int64_t src = index ? index[r] / index_div : r;
+    for (int64_t c = lane * VEC; c < width; c += 64 * VEC) {
+      float g[VEC], b[VEC];
+      unpack8(*reinterpret_cast<const uint4*>(dy + src * width + c), g);
+      unpack8(*reinterpret_cast<const uint4*>(bias + e * width + c), b);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) sum += bf16_to_f32(f32_to_bf16(g[q] * b[q]));
+    }
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) sum += __shfl_xor(sum, s);
+  if (lane == 0)
+    d_weights[r] = f32_to_bf16(bf16_to_f32(d_weights[r]) + bf16_to_f32(f32_to_bf16(sum)));
 }
 
 }  // namespace
@@ -192,64 +339,162 @@ extern "C" int bux_token_rows(const uint16_t* z, const int32_t* order, int64_t m
   return launched("token_rows_kernel");
 }
 
+namespace bux {
+namespace {
+int token_sums(const char* name, const uint16_t* y, int64_t y_rows, const int32_t* inverse,
+               int64_t tokens, int32_t k, int64_t width, const PickBias* pb, uint16_t* out,
+               void* stream) {
+  BUX_CHECK(tokens >= 0 && tokens <= 2147483647LL && k >= 1 && width > 0 && y_rows >= 0,
+            "%s: bad shape tokens=%lld k=%d width=%lld", name, (long long)tokens, k,
+            (long long)width);
+  BUX_CHECK(width % VEC == 0, "%s: width=%lld is not a multiple of %d", name, (long long)width,
+            VEC);
+  if (tokens == 0) return BUX_OK;
+  BUX_CHECK(y && inverse && out, "%s: NULL buffer", name);
+  BUX_CHECK(tokens * ceil_div(width, THREADS * VEC) < (1LL << 31), "%s: too large", name);
+  dim3 grid(static_cast<unsigned>(tokens * ceil_div(width, THREADS * VEC)));
+  const PickBias none{nullptr, nullptr, 0, nullptr};
+  hipStream_t s = as_stream(stream);
+  if (pb)
+    hipLaunchKernelGGL((token_sums_kernel<0, true>), grid, dim3(THREADS), 0, s, y, y_rows,
+                       inverse, k, width, *pb, out);
+  else if (k <= 8)
+    hipLaunchKernelGGL((token_sums_kernel<8, false>), grid, dim3(THREADS), 0, s, y, y_rows,
+                       inverse, k, width, none, out);
+  else
+    hipLaunchKernelGGL((token_sums_kernel<0, false>), grid, dim3(THREADS), 0, s, y, y_rows,
+                       inverse, k, width, none, out);
+  return launched("token_sums_kernel");
+}
+
+int experts_ok(const char* name, const int32_t* offsets, int32_t experts) {
+  BUX_CHECK(offsets != nullptr && experts >= 1 && experts <= (1 << 20),
+            "%s: offsets of %d experts (1 .. 2^20, not NULL)", name, experts);
+  return BUX_OK;
+}
+}  // namespace
+}  // namespace bux
+
 extern "C" int bux_token_sums(const uint16_t* y, int64_t y_rows, const int32_t* inverse,
                               int64_t tokens, int32_t k, int64_t width, uint16_t* out,
                               void* stream) {
   using namespace bux;
   clear_error();
-  BUX_CHECK(tokens >= 0 && tokens <= 2147483647LL && k >= 1 && width > 0 && y_rows >= 0,
-            "bux_token_sums: bad shape tokens=%lld k=%d width=%lld", (long long)tokens, k,
-            (long long)width);
-  BUX_CHECK(width % VEC == 0, "bux_token_sums: width=%lld is not a multiple of %d",
+  return token_sums("bux_token_sums", y, y_rows, inverse, tokens, k, width, nullptr, out, stream);
+}
+
+extern "C" int bux_token_sums_biased(const uint16_t* y, int64_t y_rows, const int32_t* inverse,
+                                     int64_t tokens, int32_t k, int64_t width,
+                                     const uint16_t* bias, const int32_t* offsets,
+                                     int32_t experts, const uint16_t* weights, uint16_t* out,
+                                     void* stream) {
+  using namespace bux;
+  clear_error();
+  if (int rc = experts_ok("bux_token_sums_biased", offsets, experts)) return rc;
+  BUX_CHECK(tokens == 0 || (bias && weights), "bux_token_sums_biased: NULL bias or weights");
+  const PickBias pb{bias, offsets, experts, weights};
+  return token_sums("bux_token_sums_biased", y, y_rows, inverse, tokens, k, width, &pb, out,
+                    stream);
+}
+
+extern "C" int bux_expert_bias_add(uint16_t* x, int64_t m, int64_t width, const uint16_t* bias,
+                                   const int32_t* offsets, int32_t experts, void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
+            "bux_expert_bias_add: bad shape m=%lld width=%lld (a multiple of %d)", (long long)m,
             (long long)width, VEC);
-  if (tokens == 0) return BUX_OK;
-  BUX_CHECK(y && inverse && out, "bux_token_sums: NULL buffer");
-  BUX_CHECK(tokens * ceil_div(width, THREADS * VEC) < (1LL << 31), "bux_token_sums: too large");
-  dim3 grid(static_cast<unsigned>(tokens * ceil_div(width, THREADS * VEC)));
-  if (k <= 8)
-    hipLaunchKernelGGL(token_sums_kernel<8>, grid, dim3(THREADS), 0, as_stream(stream), y, y_rows,
-                       inverse, k, width, out);
-  else
-    hipLaunchKernelGGL(token_sums_kernel<0>, grid, dim3(THREADS), 0, as_stream(stream), y, y_rows,
-                       inverse, k, width, out);
-  return launched("token_sums_kernel");
+  if (int rc = experts_ok("bux_expert_bias_add", offsets, experts)) return rc;
+  if (m == 0) return BUX_OK;
+  BUX_CHECK(x && bias, "bux_expert_bias_add: NULL buffer");
+  BUX_CHECK(m * ceil_div(width, THREADS * VEC) < (1LL << 31), "bux_expert_bias_add: too large");
+  dim3 grid(static_cast<unsigned>(m * ceil_div(width, THREADS * VEC)));
+  hipLaunchKernelGGL(expert_bias_add_kernel, grid, dim3(THREADS), 0, as_stream(stream), x, width,
+                     bias, offsets, experts);
+  return launched("expert_bias_add_kernel");
+}
+
+extern "C" int bux_expert_sums(const uint16_t* x, const int32_t* index, int32_t index_div,
+                               const uint16_t* weights, int64_t m, int64_t width,
+                               const int32_t* offsets, int32_t experts, float* out,
+                               void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
+            "bux_expert_sums: bad shape m=%lld width=%lld (a multiple of %d)", (long long)m,
+            (long long)width, VEC);
+  BUX_CHECK(index == nullptr || index_div >= 1, "bux_expert_sums: index_div=%d", index_div);
+  if (int rc = experts_ok("bux_expert_sums", offsets, experts)) return rc;
+  BUX_CHECK(out != nullptr && (m == 0 || x != nullptr), "bux_expert_sums: NULL buffer");
+  // every expert's sum is written (0 for none): offsets[experts] <= m is the caller's
+  const int64_t chunks = ceil_div(width, SUM_COLS);
+  BUX_CHECK(experts * chunks < (1LL << 31), "bux_expert_sums: too large");
+  hipLaunchKernelGGL(expert_sums_kernel, dim3(static_cast<unsigned>(experts * chunks)),
+                     dim3(THREADS), 0, as_stream(stream), x, index, index_div, weights, width,
+                     offsets, experts, out);
+  return launched("expert_sums_kernel");
+}
+
+extern "C" int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index,
+                                           int32_t index_div, int64_t m, int64_t width,
+                                           const uint16_t* bias, const int32_t* offsets,
+                                           int32_t experts, uint16_t* d_weights, void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
+            "bux_expert_bias_weight_grad: bad shape m=%lld width=%lld (a multiple of %d)",
+            (long long)m, (long long)width, VEC);
+  BUX_CHECK(index == nullptr || index_div >= 1, "bux_expert_bias_weight_grad: index_div=%d",
+            index_div);
+  if (int rc = experts_ok("bux_expert_bias_weight_grad", offsets, experts)) return rc;
+  if (m == 0) return BUX_OK;
+  BUX_CHECK(dy && bias && d_weights, "bux_expert_bias_weight_grad: NULL buffer");
+  hipLaunchKernelGGL(expert_bias_weight_grad_kernel,
+                     dim3(static_cast<unsigned>(ceil_div(m, THREADS / 64))), dim3(THREADS), 0,
+                     as_stream(stream), dy, index, index_div, m, width, bias, offsets, experts,
+                     d_weights);
+  return launched("expert_bias_weight_grad_kernel");
 }
 
 extern "C" int bux_glu_forward(const uint16_t* projected, const uint16_t* weights,
-                               const int32_t* filled, int64_t m, int64_t f, int activation,
-                               float limit, float up_offset, uint16_t* h, void* stream) {
+                               const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
+                               uint16_t* h, void* stream) {
   using namespace bux;
   clear_error();
   BUX_CHECK(m >= 0 && m <= 2147483647LL && f > 0 && f % 4 == 0,
             "bux_glu_forward: bad shape m=%lld f=%lld (f a multiple of 4)", (long long)m,
             (long long)f);
-  BUX_CHECK(activation == BUX_SWISH || activation == BUX_QUICK_GELU,
-            "bux_glu_forward: activation %d is neither BUX_SWISH nor BUX_QUICK_GELU", activation);
+  Act act;
+  if (int rc = act_of("bux_glu_forward", ffn, &act)) return rc;
   if (m == 0) return BUX_OK;
   BUX_CHECK(projected && weights && h, "bux_glu_forward: NULL buffer");
   BUX_CHECK(m * ceil_div(f, THREADS * 4) < (1LL << 31), "bux_glu_forward: too large");
   dim3 grid(static_cast<unsigned>(m * ceil_div(f, THREADS * 4)));
-  hipLaunchKernelGGL(glu_forward_kernel, grid, dim3(THREADS), 0, as_stream(stream), projected,
-                     weights, filled, m, f, Act{activation, limit, up_offset}, h);
-  return launched("glu_forward_kernel");
+  return with_kind(act, [&](auto kind) {
+    hipLaunchKernelGGL(glu_forward_kernel<decltype(kind)>, grid, dim3(THREADS), 0,
+                       as_stream(stream), projected, weights, filled, m, f, act, h);
+    return launched("glu_forward_kernel");
+  });
 }
 
 extern "C" int bux_glu_backward(const uint16_t* projected, const uint16_t* weights,
                                 const uint16_t* dh, const int32_t* filled, int64_t m, int64_t f,
-                                int activation, float limit, float up_offset,
-                                uint16_t* d_projected, uint16_t* d_weights, void* stream) {
+                                const bux_ffn* ffn, uint16_t* d_projected, uint16_t* d_weights,
+                                void* stream) {
   using namespace bux;
   clear_error();
   BUX_CHECK(m >= 0 && m <= 2147483647LL && f > 0 && f % 4 == 0,
             "bux_glu_backward: bad shape m=%lld f=%lld (f a multiple of 4)", (long long)m,
             (long long)f);
-  BUX_CHECK(activation == BUX_SWISH || activation == BUX_QUICK_GELU,
-            "bux_glu_backward: activation %d is neither BUX_SWISH nor BUX_QUICK_GELU", activation);
+  Act act;
+  if (int rc = act_of("bux_glu_backward", ffn, &act)) return rc;
   if (m == 0) return BUX_OK;
   BUX_CHECK(projected && weights && dh && d_projected && d_weights, "bux_glu_backward: NULL buffer");
   dim3 grid(static_cast<unsigned>(ceil_div(m, THREADS / 64)));
-  hipLaunchKernelGGL(glu_backward_kernel, grid, dim3(THREADS), 0, as_stream(stream), projected,
-                     weights, dh, filled, m, f, Act{activation, limit, up_offset}, d_projected,
-                     d_weights);
-  return launched("glu_backward_kernel");
+  return with_kind(act, [&](auto kind) {
+    hipLaunchKernelGGL(glu_backward_kernel<decltype(kind)>, grid, dim3(THREADS), 0,
+                       as_stream(stream), projected, weights, dh, filled, m, f, act, d_projected,
+                       d_weights);
+    return launched("glu_backward_kernel");
+  });
 }

@@ -20,6 +20,7 @@ convert from and to the row-major ``Blocks`` layout (codes (..., r, c), scale by
 (..., r, c/32)).
 """
 
+import ctypes
 from typing import NamedTuple
 
 import torch
@@ -226,7 +227,7 @@ def rows(
 
 
 def activated(
-    a: Tiled, b: Tiled, sizes: torch.Tensor, weights: torch.Tensor, codes: tuple[int, float, float],
+    a: Tiled, b: Tiled, sizes: torch.Tensor, weights: torch.Tensor, ffn: _lib.FfnStruct,
     rows: int,
 ) -> tuple[torch.Tensor, Tiled, Tiled]:
     """Return the up GEMM's product ``a @ b[g]^T`` (rows, n) and h, its activation times
@@ -239,7 +240,8 @@ def activated(
         b: the groups' up kernels (g, n, K), columns in (up, gate) pairs.
         sizes: int32 (g,) on the device.
         weights: bfloat16 (rows,): each row's weight.
-        codes: the activation (kind, limit, up_offset) as ``Ffn.codes`` gives it.
+        ffn: the activation as ``moe.Ffn.struct`` gives it: gated, of swish,
+            quick_gelu or situ.
         rows: rows of the product (at most a's height).
     """
     require(a.values, a.scales, b.values, b.scales, sizes, weights)
@@ -262,10 +264,9 @@ def activated(
     t_vals = torch.empty(height // 64, f, 64, dtype=torch.uint8, device=dev)
     t_scales = torch.empty(height // 128, f, 4, dtype=torch.uint8, device=dev)
     ws = workspace(lib().bux_mx_grouped_glu_workspace_size(groups, height), dev)
-    kind, limit, offset = codes
     _lib.check(lib().bux_mx_grouped_glu(
         ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(sizes), groups, height, n,
-        k, rows, ptr(weights.contiguous()), kind, limit, offset, ptr(projected), ptr(vals),
+        k, rows, ptr(weights.contiguous()), ctypes.byref(ffn), ptr(projected), ptr(vals),
         ptr(scales), ptr(t_vals), ptr(t_scales), ptr(ws), ws.numel(), stream()))
     return projected, Tiled(vals, scales), Tiled(t_vals, t_scales)
 

@@ -20,6 +20,7 @@ Every op enqueues HIP kernels of ``libbux_amd.so`` on the current stream; torch 
 allocates the buffers.
 """
 
+import ctypes
 from typing import NamedTuple
 
 import torch
@@ -89,29 +90,51 @@ def sum_by_token(y: torch.Tensor, inverse: torch.Tensor) -> torch.Tensor:
 
 
 class Ffn(NamedTuple):
-    """An expert FFN's gated activation (config.py:204-221): ``act(gate) * (up +
-    up_offset)``, `limit` clipping up to [-limit, limit] and the gate from above."""
+    """An expert FFN's activation settings (config.MLPConfig, config.py:204-221):
+    ``act(gate) * (up + up_offset)`` gated, ``act(up)`` plain, `limit` clipping up to
+    [-limit, limit] (and a gate from above), `up_softcap` capping up to ``c tanh(up /
+    c)`` (layers/mlp.py:20-35). Gating follows the projection's shape, (m, f, 2) gated
+    or (m, f, 1) plain, as ``moe.hidden_units`` reads it (moe.py:913-919)."""
 
-    activation: str = "swish"  # or "quick_gelu"
+    activation: str = "swish"  # any of _lib.ACTIVATIONS
     limit: float | None = None
     up_offset: float = 0.0
+    up_softcap: float | None = None
 
-    def codes(self) -> tuple[int, float, float]:
-        kind = {"swish": _lib.SWISH, "quick_gelu": _lib.QUICK_GELU}[self.activation]
-        return kind, (0.0 if self.limit is None else float(self.limit)), float(self.up_offset)
+    def struct(self, gated: bool = True) -> _lib.FfnStruct:
+        """Return the settings as the library's ``bux_ffn``."""
+        if self.activation not in _lib.ACTIVATIONS:
+            raise ValueError(f"no activation {self.activation!r}: one of {list(_lib.ACTIVATIONS)}")
+        return _lib.FfnStruct(
+            _lib.ACTIVATIONS[self.activation], int(gated), int(self.limit is not None),
+            0.0 if self.limit is None else float(self.limit), int(self.up_softcap is not None),
+            0.0 if self.up_softcap is None else float(self.up_softcap), float(self.up_offset))
+
+    def fusable(self, gated: bool) -> bool:
+        """Whether the fused up GEMM (`grouped_mxfp8.activated`) runs these settings: a
+        gated swish, quick_gelu or situ (grouped_glu.epilogue's gated forms,
+        experts/grouped_glu.py:119-136)."""
+        return gated and self.activation in ("swish", "quick_gelu", "situ")
+
+
+def _gating(projected: torch.Tensor) -> tuple[int, int, bool]:
+    """(m, f, gated) of projected (m, f, 2) or (m, f, 1)."""
+    if projected.dim() != 3 or projected.shape[2] not in (1, 2):
+        raise ValueError(f"projected is (m, f, 2) or (m, f, 1), not {tuple(projected.shape)}")
+    return projected.shape[0], projected.shape[1], projected.shape[2] == 2
 
 
 def weighted_units(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
                    filled: torch.Tensor | None = None) -> torch.Tensor:
     """Return each row's hidden units times its weight, (m, f), from projected
-    (m, f, 2) ([..., 0] up, [..., 1] gate) and the rows' weights (m,); rows from
-    `filled` on are 0."""
+    (m, f, 2) ([..., 0] up, [..., 1] gate) or (m, f, 1) (up) and the rows' weights
+    (m,); rows from `filled` on are 0."""
     require(projected, weights, filled)
-    m, f = projected.shape[0], projected.shape[1]
+    m, f, gated = _gating(projected)
     h = torch.empty(m, f, dtype=torch.bfloat16, device=projected.device)
-    kind, limit, offset = ffn.codes()
-    _lib.check(lib().bux_glu_forward(ptr(projected), ptr(weights), ptr(filled), m, f, kind, limit,
-                                     offset, ptr(h), stream()))
+    st = ffn.struct(gated)
+    _lib.check(lib().bux_glu_forward(ptr(projected), ptr(weights), ptr(filled), m, f,
+                                     ctypes.byref(st), ptr(h), stream()))
     return h
 
 
@@ -122,7 +145,7 @@ def weighted_units_quantized(ffn: Ffn, projected: torch.Tensor, weights: torch.T
     `height` rows of the copies), computed and quantized in one pass; with `keep`, h
     itself (bfloat16 (m, f)) too, else None."""
     require(projected, weights, filled)
-    m, f = projected.shape[0], projected.shape[1]
+    m, f, gated = _gating(projected)
     dev = projected.device
     kf, kh = grouped_mxfp8.whole(f, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
     vals = torch.empty(kf // 64, height, 64, dtype=torch.uint8, device=dev)
@@ -130,9 +153,9 @@ def weighted_units_quantized(ffn: Ffn, projected: torch.Tensor, weights: torch.T
     t_vals = torch.empty(kh // 64, f, 64, dtype=torch.uint8, device=dev)
     t_scales = torch.empty(kh // 128, f, 4, dtype=torch.uint8, device=dev)
     h = torch.empty(m, f, dtype=torch.bfloat16, device=dev) if keep else None
-    kind, limit, offset = ffn.codes()
+    st = ffn.struct(gated)
     _lib.check(lib().bux_glu_quantize(
-        ptr(projected), ptr(weights), ptr(filled), m, f, kind, limit, offset, height, ptr(h),
+        ptr(projected), ptr(weights), ptr(filled), m, f, ctypes.byref(st), height, ptr(h),
         ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))
     return Tiled(vals, scales), Tiled(t_vals, t_scales), h
 
@@ -141,23 +164,24 @@ def weighted_units_backward_quantized(
     ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor, dh: torch.Tensor,
     filled: torch.Tensor | None, height: int, keep: bool = False,
 ) -> tuple[Tiled, Tiled, torch.Tensor, torch.Tensor | None]:
-    """Return the gradient of `weighted_units` to projected in MXFP8 along its rows (2f)
+    """Return the gradient of `weighted_units` to projected in MXFP8 along its rows (p f)
     and, transposed, along m (both tiled, `height` rows of the copies), the gradient to
-    the weights (m,), and with `keep` the bfloat16 gradient to projected (m, f, 2)."""
+    the weights (m,), and with `keep` the bfloat16 gradient to projected (m, f, p)."""
     require(projected, weights, dh, filled)
-    m, f = projected.shape[0], projected.shape[1]
+    m, f, gated = _gating(projected)
+    p = projected.shape[2]
     dev = projected.device
-    kp, kh = grouped_mxfp8.whole(2 * f, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
+    kp, kh = grouped_mxfp8.whole(p * f, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
     vals = torch.empty(kp // 64, height, 64, dtype=torch.uint8, device=dev)
     scales = torch.empty(kp // 128, height, 4, dtype=torch.uint8, device=dev)
-    t_vals = torch.empty(kh // 64, 2 * f, 64, dtype=torch.uint8, device=dev)
-    t_scales = torch.empty(kh // 128, 2 * f, 4, dtype=torch.uint8, device=dev)
+    t_vals = torch.empty(kh // 64, p * f, 64, dtype=torch.uint8, device=dev)
+    t_scales = torch.empty(kh // 128, p * f, 4, dtype=torch.uint8, device=dev)
     dw = torch.empty(m, dtype=torch.bfloat16, device=dev)
-    dp = torch.empty(m, f, 2, dtype=torch.bfloat16, device=dev) if keep else None
+    dp = torch.empty(m, f, p, dtype=torch.bfloat16, device=dev) if keep else None
     ws = workspace(lib().bux_glu_backward_quantize_workspace_size(m, f), dev)
-    kind, limit, offset = ffn.codes()
+    st = ffn.struct(gated)
     _lib.check(lib().bux_glu_backward_quantize(
-        ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f, kind, limit, offset, height,
+        ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f, ctypes.byref(st), height,
         ptr(dp), ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), ptr(dw), ptr(ws), ws.numel(),
         stream()))
     return Tiled(vals, scales), Tiled(t_vals, t_scales), dw, dp
@@ -166,16 +190,88 @@ def weighted_units_backward_quantized(
 def weighted_units_backward(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
                             dh: torch.Tensor, filled: torch.Tensor | None = None
                             ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Return the gradients of `weighted_units` to projected (m, f, 2) and to the
+    """Return the gradients of `weighted_units` to projected (m, f, p) and to the
     weights (m,)."""
     require(projected, weights, dh, filled)
-    m, f = projected.shape[0], projected.shape[1]
-    dp = torch.empty(m, f, 2, dtype=torch.bfloat16, device=projected.device)
+    m, f, gated = _gating(projected)
+    dp = torch.empty(projected.shape, dtype=torch.bfloat16, device=projected.device)
     dw = torch.empty(m, dtype=torch.bfloat16, device=projected.device)
-    kind, limit, offset = ffn.codes()
+    st = ffn.struct(gated)
     _lib.check(lib().bux_glu_backward(ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f,
-                                      kind, limit, offset, ptr(dp), ptr(dw), stream()))
+                                      ctypes.byref(st), ptr(dp), ptr(dw), stream()))
     return dp, dw
+
+
+# --- The experts' biases ---------------------------------------------------------------
+
+
+def _experts(offsets: torch.Tensor) -> int:
+    if offsets.dtype != torch.int32 or offsets.dim() != 1 or offsets.numel() < 2:
+        raise ValueError(f"offsets are int32 (E + 1,), not {offsets.dtype} {tuple(offsets.shape)}")
+    return offsets.numel() - 1
+
+
+def add_expert_bias(x: torch.Tensor, bias: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
+    """Add each row's expert's row of `bias` (E, width) to x (m, width) in place and
+    return x: ``x + by_expert(bias, sizes)`` in bfloat16 (moe.py:857-861,876-885)."""
+    require(x, bias, offsets)
+    e = _experts(offsets)
+    m, width = x.shape[0], x.numel() // max(x.shape[0], 1)
+    if bias.dtype != torch.bfloat16 or bias.numel() != e * width:
+        raise ValueError(f"bias {bias.dtype} {tuple(bias.shape)} for {e} experts of {width}")
+    _lib.check(lib().bux_expert_bias_add(ptr(x), m, width, ptr(bias.contiguous()), ptr(offsets), e,
+                                         stream()))
+    return x
+
+
+def expert_sums(x: torch.Tensor, offsets: torch.Tensor, index: torch.Tensor | None = None,
+                index_div: int = 1, weights: torch.Tensor | None = None) -> torch.Tensor:
+    """Return each expert's sum of its rows, float32 (E, width): rows ``x[index[r] //
+    index_div]`` (or ``x[r]``), each times ``weights[r]`` (rounded to bfloat16) if
+    given. The gradient of `add_expert_bias`'s bias, and with the picks' tokens and
+    weights of the down bias (moe.py:866-870)."""
+    require(x, offsets, index, weights)
+    e = _experts(offsets)
+    m = index.numel() if index is not None else x.shape[0]
+    width = x.numel() // x.shape[0] if x.shape[0] else x.shape[-1]
+    if weights is not None and weights.numel() != m:
+        raise ValueError(f"expert_sums: {weights.numel()} weights for {m} rows")
+    out = torch.empty(e, width, dtype=torch.float32, device=x.device)
+    _lib.check(lib().bux_expert_sums(ptr(x), ptr(index), index_div, ptr(weights), m, width,
+                                     ptr(offsets), e, ptr(out), stream()))
+    return out
+
+
+def sum_by_token_biased(y: torch.Tensor, inverse: torch.Tensor, bias: torch.Tensor,
+                        offsets: torch.Tensor, row_weights: torch.Tensor) -> torch.Tensor:
+    """Return `sum_by_token` (y) plus each token's sum of its picks' ``bias[e] * w``:
+    the down bias's forward, ``y + sums_of_tokens(weighted(by_expert(down_bias),
+    weights))`` (moe.py:866-870)."""
+    require(y, inverse, bias, offsets, row_weights)
+    e = _experts(offsets)
+    tokens, k = inverse.shape
+    width = y.shape[-1]
+    if bias.dtype != torch.bfloat16 or bias.numel() != e * width:
+        raise ValueError(f"bias {bias.dtype} {tuple(bias.shape)} for {e} experts of {width}")
+    out = torch.empty(tokens, width, dtype=y.dtype, device=y.device)
+    _lib.check(lib().bux_token_sums_biased(
+        ptr(y), y.shape[0], ptr(inverse), tokens, k, width, ptr(bias.contiguous()), ptr(offsets), e,
+        ptr(row_weights), ptr(out), stream()))
+    return out
+
+
+def add_bias_weight_grad(d_weights: torch.Tensor, dy: torch.Tensor, order: torch.Tensor, k: int,
+                         bias: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
+    """Add the down bias's share of the row weights' gradient to `d_weights` (m,) in
+    place: ``sum_c dy[order[r] // k, c] bias[e(r), c]`` (weighted's VJP,
+    moe.py:922-925)."""
+    require(d_weights, dy, order, bias, offsets)
+    e = _experts(offsets)
+    m, width = order.numel(), dy.shape[-1]
+    _lib.check(lib().bux_expert_bias_weight_grad(ptr(dy), ptr(order), k, m, width,
+                                                 ptr(bias.contiguous()), ptr(offsets), e,
+                                                 ptr(d_weights), stream()))
+    return d_weights
 
 
 # --- The layer: routed -> experts, forward and backward ------------------------------
@@ -215,6 +311,24 @@ def in_mxfp8(up: torch.Tensor, down: torch.Tensor, fmt: str = "mxfp8") -> MxWeig
     return MxWeights(up_n, up_k, down_n, down_k)
 
 
+PASSES = ("fprop", "dgrad", "wgrad")
+
+
+def passes_of(fmt: str, passes=None) -> tuple[bool, bool, bool]:
+    """Return whether (fprop, dgrad, wgrad) multiply in MXFP8: none in "compute", else
+    those named in `passes` (all by default), the reference's ``matmuls.in_force().
+    passes`` (grouped_blockscaled.py:170,189: each GEMM of a pass outside them
+    multiplies its operands as they are, in bfloat16)."""
+    _check_fmt(fmt)
+    if fmt not in MX_FORMATS:
+        return False, False, False
+    chosen = PASSES if passes is None else tuple(passes)
+    unknown = set(chosen) - set(PASSES)
+    if unknown:
+        raise ValueError(f"passes are among {PASSES}, not {sorted(unknown)}")
+    return tuple(q in chosen for q in PASSES)
+
+
 class Saved(NamedTuple):
     """What the layer's backward takes of its forward (grouped_blockscaled.py:84's Saved
     for each GEMM, and the activation's input, which jax.checkpoint recomputes from)."""
@@ -222,20 +336,22 @@ class Saved(NamedTuple):
     sorted: Sorted
     k: int
     row_weights: torch.Tensor  # bfloat16 (m,)
-    projected: torch.Tensor  # bfloat16 (m, 2f)
-    h: torch.Tensor | None  # bfloat16 (m, f): compute format, or kept for inspection
-    x_m: Tiled | None  # x^T along the rows (wgrad of up)
-    up_n: Tiled | None  # each W_up along n (dgrad of up)
-    h_m: Tiled | None  # h^T along the rows (wgrad of down)
-    down_n: Tiled | None  # each W_down along n (dgrad of down)
-    rows: torch.Tensor | None  # the picks' rows, compute format only
+    projected: torch.Tensor  # bfloat16 (m, p f), with the up bias added
+    h: torch.Tensor | None  # bfloat16 (m, f): wgrad in bfloat16, or kept for inspection
+    x_m: Tiled | None  # x^T along the rows (wgrad of up in MXFP8)
+    up_n: Tiled | None  # each W_up along n (dgrad of up in MXFP8)
+    h_m: Tiled | None  # h^T along the rows (wgrad of down in MXFP8)
+    down_n: Tiled | None  # each W_down along n (dgrad of down in MXFP8)
+    rows: torch.Tensor | None  # the picks' rows (wgrad of up in bfloat16)
     tiles: grouped_mxfp8.TileList | None = None  # the MXFP8 GEMMs' tile list, made once
+    passes: tuple[bool, bool, bool] = (True, True, True)  # (fprop, dgrad, wgrad) in MXFP8
 
 
 def experts_forward(
     z: torch.Tensor, idx: torch.Tensor, weights: torch.Tensor, up: torch.Tensor,
     down: torch.Tensor, ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
-    fused: bool = False, quantized: MxWeights | None = None,
+    fused: bool = False, quantized: MxWeights | None = None, passes=None,
+    up_bias: torch.Tensor | None = None, down_bias: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, Saved]:
     """Return the routed experts' output (t, d), bfloat16, and what the backward takes.
     In MXFP8 the activation goes straight to its quantized copies; with `intermediates`
@@ -245,7 +361,8 @@ def experts_forward(
         z: the tokens, bfloat16 (t, d).
         idx: each token's k experts, int32 (t, k).
         weights: their weights, bfloat16 (t, k).
-        up: the experts' up and gate kernels, bfloat16 (E, d, f, 2).
+        up: the experts' up kernels, bfloat16 (E, d, f, p): p = 2 for a gated FFN (up
+            and gate), 1 for a plain one.
         down: the experts' down kernels, bfloat16 (E, f, d).
         ffn: the activation.
         fmt: "mxfp8" (Transformer Engine's recipe: every operand in blocks of 32 along
@@ -255,8 +372,15 @@ def experts_forward(
         quantized: the kernels already in MXFP8 (`in_mxfp8(up, down, fmt)`), as the
             reference's `quantized` (moe.py:799); None to quantize them here.
         fused: in MXFP8 (without `intermediates`), the activation and h's two copies in
-            the up GEMM's epilogue (`grouped_mxfp8.activated`): the same bits, in one
-            GEMM kernel instead of the GEMM and the activation's quantizer.
+            the up GEMM's epilogue (`grouped_mxfp8.activated`) where it runs them (every
+            pass in MXFP8, no bias, `Ffn.fusable`; moe.fused, moe.py:888-895): the same
+            bits, in one GEMM kernel instead of the GEMM and the activation's quantizer.
+        passes: the GEMMs (of "fprop", "dgrad", "wgrad") that multiply in `fmt`; None
+            for all. The others multiply in bfloat16.
+        up_bias: the experts' up biases, bfloat16 (E, f, p), added to the up GEMM's
+            product; None for none (MLPConfig.bias, moe.py:857-861).
+        down_bias: the experts' down biases, bfloat16 (E, d): each pick adds its
+            expert's, times its weight (moe.py:866-870).
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -266,112 +390,139 @@ def experts_forward(
         filled = s.filled
         row_weights = picked_weights(weights, s.order)
     up2 = up.reshape(e, d, f * p)
-    x_m = up_n = h_m = down_n = rows = None
-    _check_fmt(fmt)
-    mx, tiles = fmt in MX_FORMATS, fmt == "mxfp8_2d"
-    listed = None
-    if mx:
-        height = grouped_mxfp8.whole(m)
+    fprop, dgrad, wgrad = passes_of(fmt, passes)
+    tiles = fmt == "mxfp8_2d"
+    height = grouped_mxfp8.whole(m)
+    x_k = x_m = up_n = up_k = h_k = h_m = down_n = down_k = rows = listed = None
+    if fprop or dgrad or wgrad:
         with span("tile list"):
             # one tile list for the step's six GEMMs: a of `height` rows, outputs of m
             listed = grouped_mxfp8.tiles_of(s.sizes, height, m)
+    if fprop or wgrad:
         with span("quantize x"):
             x_k, x_m = grouped_mxfp8.quantized_twice(z, filled, True, s.order, k, height)
-        if quantized is not None:
-            up_n, up_k = quantized.up_n, quantized.up_k
-        else:
-            with span("quantize W_up"):
-                up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
-        if fused and not intermediates:
-            with span("up fprop + activation + quantize h"):
-                projected, h_k, h_m = grouped_mxfp8.activated(x_k, up_k, s.sizes, row_weights,
-                                                              ffn.codes(), m)
-            h = None
-        else:
-            with span("up fprop"):
-                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m, tiles=listed)
-    else:
+    if not (fprop and wgrad):
         with span("gather x"):
             rows = token_rows(z, s.order, k)
-        with span("up fprop"):
-            projected = grouped.dot(rows, up2, s.sizes)
-    if mx:
-        if not (fused and not intermediates):
-            with span("activation + quantize h"):
-                h_k, h_m, h = weighted_units_quantized(ffn, projected.view(m, f, p), row_weights,
-                                                       filled, height, intermediates)
+    if fprop or dgrad:
         if quantized is not None:
+            up_n, up_k = quantized.up_n, quantized.up_k
             down_n, down_k = quantized.down_n, quantized.down_k
         else:
-            with span("quantize W_down"):
+            with span("quantize W"):
+                up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
                 down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
-        with span("down fprop"):
-            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=listed)
+    h = None
+    if (fused and not intermediates and fprop and dgrad and wgrad and up_bias is None
+            and ffn.fusable(p == 2)):
+        with span("up fprop + activation + quantize h"):
+            projected, h_k, h_m = grouped_mxfp8.activated(x_k, up_k, s.sizes, row_weights,
+                                                          ffn.struct(True), m)
     else:
-        with span("activation"):
-            h = weighted_units(ffn, projected.view(m, f, p), row_weights, filled)
-        with span("down fprop"):
+        with span("up fprop"):
+            if fprop:
+                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m, tiles=listed)
+            else:
+                projected = grouped.dot(rows, up2, s.sizes)
+        if up_bias is not None:
+            with span("up bias"):
+                add_expert_bias(projected, up_bias.reshape(e, f * p), s.offsets)
+        pv = projected.view(m, f, p)
+        if fprop or wgrad:
+            with span("activation + quantize h"):
+                h_k, h_m, h = weighted_units_quantized(ffn, pv, row_weights, filled, height,
+                                                       intermediates or not (fprop and wgrad))
+        else:
+            with span("activation"):
+                h = weighted_units(ffn, pv, row_weights, filled)
+    with span("down fprop"):
+        if fprop:
+            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=listed)
+        else:
             y = grouped.dot(h, down, s.sizes)
     with span("combine"):
-        out = sum_by_token(y, s.inverse.view(t, k))
-    return out, Saved(s, k, row_weights, projected, h, x_m, up_n, h_m, down_n, rows, listed)
+        if down_bias is None:
+            out = sum_by_token(y, s.inverse.view(t, k))
+        else:
+            out = sum_by_token_biased(y, s.inverse.view(t, k), down_bias.reshape(e, d), s.offsets,
+                                      row_weights)
+    keep_h = h if (intermediates or not wgrad) else None
+    return out, Saved(s, k, row_weights, projected, keep_h, x_m, up_n, h_m, down_n, rows, listed,
+                      (fprop, dgrad, wgrad))
 
 
 def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: torch.Tensor,
-                     ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False
+                     ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
+                     up_bias: torch.Tensor | None = None, down_bias: torch.Tensor | None = None,
                      ) -> dict[str, torch.Tensor]:
     """Return the gradients of `experts_forward`'s output, dy (t, d), to z, the
-    weights (t, k), up (E, d, f, 2) and down (E, f, d), all bfloat16; with
-    `intermediates`, also the gradients between the GEMMs: "dh" (m, f) of the down
-    GEMM's input, "dp" (m, 2f) of the up GEMM's output, "dx" (m, d) of its input and
-    "d_row_weights" (m,)."""
+    weights (t, k), up (E, d, f, p) and down (E, f, d), all bfloat16, and with biases
+    to "up_bias" (E, f, p) and "down_bias" (E, d), float32 sums; with `intermediates`,
+    also the gradients between the GEMMs: "dh" (m, f) of the down GEMM's input, "dp"
+    (m, p f) of the up GEMM's output, "dx" (m, d) of its input and "d_row_weights"
+    (m,). The passes are the forward's (`saved.passes`); `fmt` is checked against
+    them."""
     s, k = saved.sorted, saved.k
     t = dy.shape[0]
     e, d, f, p = up.shape
     m = t * k
     filled = s.filled
     up2 = up.reshape(e, d, f * p)
-    _check_fmt(fmt)
-    mx = fmt in MX_FORMATS
-    if mx:
-        height = grouped_mxfp8.whole(m)
+    fprop, dgrad, wgrad = saved.passes
+    if (fprop or dgrad or wgrad) != (fmt in MX_FORMATS):
+        raise ValueError(f"experts_backward: fmt {fmt!r} is not the forward's")
+    height = grouped_mxfp8.whole(m)
+    dy_n = dy_m = dp_n = dp_m = dy_rows = None
+    if dgrad or wgrad:
         with span("quantize dy"):
             dy_n, dy_m = grouped_mxfp8.quantized_twice(dy, filled, True, s.order, k, height)
-        with span("down dgrad"):
-            dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m, tiles=saved.tiles)
-        with span("down wgrad"):
-            d_down = grouped_mxfp8.contract(saved.h_m, dy_m, s.sizes, tiles=saved.tiles)
-    else:
+    if not (dgrad and wgrad):
         with span("gather dy"):
             dy_rows = token_rows(dy, s.order, k)
-        with span("down dgrad"):
+    with span("down dgrad"):
+        if dgrad:
+            dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m, tiles=saved.tiles)
+        else:
             dh = grouped.dot(dy_rows, down, s.sizes, transposed=True)
-        with span("down wgrad"):
+    with span("down wgrad"):
+        if wgrad:
+            d_down = grouped_mxfp8.contract(saved.h_m, dy_m, s.sizes, tiles=saved.tiles)
+        else:
             d_down = grouped.weight_grad(saved.h, dy_rows, s.sizes)
-    if mx:
+    pv = saved.projected.view(m, f, p)
+    if dgrad or wgrad:
+        keep = intermediates or up_bias is not None or not (dgrad and wgrad)
         with span("activation backward + quantize dp"):
             dp_n, dp_m, d_rows_w, dp = weighted_units_backward_quantized(
-                ffn, saved.projected.view(m, f, p), saved.row_weights, dh, filled, height,
-                intermediates)
-        if dp is not None:
-            dp = dp.view(m, f * p)
-        with span("up dgrad"):
-            dx = grouped_mxfp8.rows(dp_n, saved.up_n, s.sizes, height=m, tiles=saved.tiles)
-        with span("up wgrad"):
-            d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes, tiles=saved.tiles)
+                ffn, pv, saved.row_weights, dh, filled, height, keep)
     else:
         with span("activation backward"):
-            dp, d_rows_w = weighted_units_backward(ffn, saved.projected.view(m, f, p),
-                                                   saved.row_weights, dh, filled)
+            dp, d_rows_w = weighted_units_backward(ffn, pv, saved.row_weights, dh, filled)
+    if dp is not None:
         dp = dp.view(m, f * p)
-        with span("up dgrad"):
+    with span("up dgrad"):
+        if dgrad:
+            dx = grouped_mxfp8.rows(dp_n, saved.up_n, s.sizes, height=m, tiles=saved.tiles)
+        else:
             dx = grouped.dot(dp, up2, s.sizes, transposed=True)
-        with span("up wgrad"):
+    with span("up wgrad"):
+        if wgrad:
+            d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes, tiles=saved.tiles)
+        else:
             d_up = grouped.weight_grad(saved.rows, dp, s.sizes)
+    grads = {}
+    if up_bias is not None:
+        with span("up bias grad"):
+            grads["up_bias"] = expert_sums(dp, s.offsets).view(e, f, p)
+    if down_bias is not None:
+        with span("down bias grad"):
+            db = down_bias.reshape(e, d)
+            add_bias_weight_grad(d_rows_w, dy, s.order, k, db, s.offsets)
+            grads["down_bias"] = expert_sums(dy, s.offsets, s.order, k, saved.row_weights)
     with span("combine dx"):
         dz = sum_by_token(dx, s.inverse.view(t, k))
         d_weights = token_rows(d_rows_w.view(m, 1), s.inverse, 1).view(t, k)
-    grads = {"z": dz, "weights": d_weights, "up": d_up.view(e, d, f, p), "down": d_down}
+    grads.update(z=dz, weights=d_weights, up=d_up.view(e, d, f, p), down=d_down)
     if intermediates:
         grads.update(dh=dh, dp=dp, dx=dx, d_row_weights=d_rows_w)
     return grads

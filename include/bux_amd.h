@@ -227,23 +227,80 @@ int bux_token_sums(const uint16_t* y, int64_t y_rows, const int32_t* inverse, in
  * a-8. The experts' activation between the two GEMMs, times each row's weight.
  *
  * Replaces moe.weighted_units (moe.py:898-910) = weighted(hidden_units(...))
- * (:913-926) with layers/mlp.py:20-35 and common/functional.py:12-40:
- * h = act(gate) * (up + up_offset) * w, projected (m, f, 2) with [..., 0] up and
- * [..., 1] gate (moe.py:845-846). activation BUX_SWISH: act(g) = g sigmoid(g);
- * BUX_QUICK_GELU: g sigmoid(1.702 g). limit > 0 clamps up to [-limit, limit] and the
- * gate to at most limit (gpt-oss, tests/test_moe.py:519-528); limit <= 0 clamps
- * nothing. Rows from *filled on (if filled is not NULL) give 0.
- * The backward gives d projected (m, f, 2) and d weights (m), the VJP that jax takes
- * of the forward after its jax.checkpoint recompute (moe.py:906-910), with clip's
- * and minimum's gradient 1 inside, 1/2 at the limit, 0 outside.
+ * (:913-926) with layers/mlp.activate (layers/mlp.py:20-35) of
+ * common/functional.activation (functional.py:12-40), settings config.MLPConfig's
+ * (config.py:204-221):
+ *   gated (gated_mlp, projected (m, f, 2): [..., 0] up, [..., 1] gate, moe.py:845):
+ *     h = act(min(gate, limit)) * (cap(clip(up)) + up_offset) * w
+ *   plain (mlp, projected (m, f)):
+ *     h = act(cap(clip(up))) * w
+ * clip(u) = u clipped to [-limit, limit] when `clamped` (limit None in the reference:
+ * clamped 0); cap(u) = up_softcap tanh(u / up_softcap) when `capped`. act one of
+ *   BUX_SWISH       x sigmoid(x)              BUX_QUICK_GELU  x sigmoid(1.702 x)
+ *   BUX_RELU        max(x, 0)                 BUX_RELU2       max(x, 0)^2
+ *   BUX_GELU        x Phi(x) (erf)            BUX_GELU_TANH   gelu's tanh form
+ *   BUX_SIGMOID     sigmoid(x)                BUX_TANH        tanh(x)
+ *   BUX_SOFTPLUS    log(1 + e^x)              BUX_SITU        4 tanh(x / 4) sigmoid(x)
+ * (quick_gelu's 1.702 as jax multiplies a bfloat16 by it: 1.703125). float32 inside,
+ * one rounding to bfloat16. Rows from *filled on (if filled is not NULL) give 0.
+ * The backward gives d projected (projected's shape) and d weights (m), the VJP that
+ * jax takes of the forward after its jax.checkpoint recompute (moe.py:906-910), with
+ * clip's and minimum's gradient 1 inside, 1/2 at the limit, 0 outside, relu's 0 at 0.
+ * f a multiple of 4.
  */
-enum { BUX_SWISH = 0, BUX_QUICK_GELU = 1 };
+enum {
+  BUX_SWISH = 0, BUX_QUICK_GELU = 1, BUX_RELU = 2, BUX_RELU2 = 3, BUX_GELU = 4,
+  BUX_GELU_TANH = 5, BUX_SIGMOID = 6, BUX_TANH = 7, BUX_SOFTPLUS = 8, BUX_SITU = 9
+};
+typedef struct bux_ffn {
+  int32_t activation; /* BUX_SWISH .. BUX_SITU */
+  int32_t gated;      /* 1: gated_mlp, projected (m, f, 2); 0: mlp, projected (m, f) */
+  int32_t clamped;    /* 1: `limit` clips (limit >= 0) */
+  float limit;
+  int32_t capped;     /* 1: `up_softcap` caps up (up_softcap > 0) */
+  float up_softcap;
+  float up_offset;    /* gated only */
+} bux_ffn;
 int bux_glu_forward(const uint16_t* projected, const uint16_t* weights, const int32_t* filled,
-                    int64_t m, int64_t f, int activation, float limit, float up_offset,
-                    uint16_t* h, void* stream);
+                    int64_t m, int64_t f, const bux_ffn* ffn, uint16_t* h, void* stream);
 int bux_glu_backward(const uint16_t* projected, const uint16_t* weights, const uint16_t* dh,
-                     const int32_t* filled, int64_t m, int64_t f, int activation, float limit,
-                     float up_offset, uint16_t* d_projected, uint16_t* d_weights, void* stream);
+                     const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
+                     uint16_t* d_projected, uint16_t* d_weights, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * a-8. The experts' biases (MLPConfig.bias, config.py:214).
+ *
+ * Rows are the picks sorted by expert; offsets (int32 [experts + 1], nondecreasing,
+ * bux_moe_permute's) put row r in the expert e with offsets[e] <= r < offsets[e + 1]
+ * and past offsets[experts] in none.
+ * bux_expert_bias_add replaces moe.by_expert and the add (moe.py:857-861,876-885):
+ *   x[r] = x[r] + bias[e(r)] in place, both bfloat16, one rounding (rows in no expert
+ *   add 0). x [m, width], bias [experts, width]: the up bias ((E, f, p) flattened).
+ * bux_expert_sums replaces by_expert's gradient (the one-hot matmul's transpose,
+ *   moe.py:876-885, and weighted's, :922-925, for the down bias):
+ *   out[e] = sum over rows r of e of v_r, in float32, out float32 [experts, width];
+ *   v_r = x[src(r)], or with weights (bfloat16 [m]) x[src(r)] * weights[r] rounded
+ *   to bfloat16; src(r) = r, or with index index[r] / index_div (a pick's token).
+ * bux_token_sums_biased replaces the down bias's forward (moe.py:866-870):
+ *   out[t] = sum_by_token(y) + sum_by_token(bias[e(r)] * weights[r]), each sum as
+ *   bux_token_sums adds it (the products rounded to bfloat16 first), their sum rounded.
+ * bux_expert_bias_weight_grad adds the down bias's share of the weights' gradient
+ *   (weighted's VJP, moe.py:922-925): d_weights[r] += sum_c dy[src(r)][c] bias[e(r)][c]
+ *   (products rounded to bfloat16, summed in float32, rounded, then added in bfloat16).
+ */
+int bux_expert_bias_add(uint16_t* x, int64_t m, int64_t width, const uint16_t* bias,
+                        const int32_t* offsets, int32_t experts, void* stream);
+int bux_expert_sums(const uint16_t* x, const int32_t* index, int32_t index_div,
+                    const uint16_t* weights, int64_t m, int64_t width, const int32_t* offsets,
+                    int32_t experts, float* out, void* stream);
+int bux_token_sums_biased(const uint16_t* y, int64_t y_rows, const int32_t* inverse,
+                          int64_t tokens, int32_t k, int64_t width, const uint16_t* bias,
+                          const int32_t* offsets, int32_t experts, const uint16_t* weights,
+                          uint16_t* out, void* stream);
+int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index, int32_t index_div,
+                                int64_t m, int64_t width, const uint16_t* bias,
+                                const int32_t* offsets, int32_t experts, uint16_t* d_weights,
+                                void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-8 with a-4. The activation and its gradient, quantized as they are computed.
@@ -256,19 +313,21 @@ int bux_glu_backward(const uint16_t* projected, const uint16_t* weights, const u
  * both MXFP8 copies of them as bux_mx_quantize does (rows from *filled on as 0), with no
  * round trip of the bfloat16 result through memory.
  *
- * bux_glu_quantize: h (m, f) of projected (m, f, 2) and the rows' weights (m);
+ * Any bux_ffn, gated or plain; f a multiple of 32.
+ * bux_glu_quantize: h (m, f) of projected ((m, f, 2) gated, (m, f) plain) and the
+ *   rows' weights (m);
  *   values/scales: h along its rows (K = f rounded up to 128), height rows;
  *   t_values/t_scales: h^T along its rows (K = height rounded up to 128), f rows;
- *   h: NULL, or bfloat16 [m, f] to store h as well. f a multiple of 32.
- * bux_glu_backward_quantize: d projected (m, f, 2) of projected, the weights and dh
- *   (m, f); values/scales along its rows (K = 2 f rounded up to 128), t_values/t_scales
- *   of its transpose; d_projected: NULL, or bfloat16 [m, f, 2] to store it as well;
- *   d_weights [m] as bux_glu_backward's (its float32 sum taken in another fixed order).
- *   workspace: bux_glu_backward_quantize_workspace_size(m, f) bytes.
+ *   h: NULL, or bfloat16 [m, f] to store h as well.
+ * bux_glu_backward_quantize: d projected (m, p f; p = 2 gated, 1 plain) of projected,
+ *   the weights and dh (m, f); values/scales along its rows (K = p f rounded up to
+ *   128), t_values/t_scales of its transpose; d_projected: NULL, or bfloat16 [m, p f]
+ *   to store it as well; d_weights [m] as bux_glu_backward's (its float32 sum taken in
+ *   another fixed order). workspace: bux_glu_backward_quantize_workspace_size(m, f)
+ *   bytes.
  */
 int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights, const int32_t* filled,
-                     int64_t m, int64_t f, int activation, float limit, float up_offset,
-                     int64_t height, uint16_t* h, uint8_t* values, uint8_t* scales,
+                     int64_t m, int64_t f, const bux_ffn* ffn, int64_t height, uint16_t* h, uint8_t* values, uint8_t* scales,
                      uint8_t* t_values, uint8_t* t_scales, void* stream);
 /* bux_mx_grouped_glu: the experts' up GEMM with the activation and both MXFP8 copies
  *   of h in its epilogue, the reference's fused up GEMM (grouped_cudnn.activated,
@@ -284,18 +343,20 @@ int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights, const i
  *   values/scales  h along its units (K = f rounded up to 128), height rows;
  *   t_values/t_scales  h^T along the rows (K = height, a multiple of 128), f rows;
  *   workspace  bux_mx_grouped_glu_workspace_size(groups, height) bytes.
+ *   ffn: gated, of BUX_SWISH, BUX_QUICK_GELU or BUX_SITU (with any clamp, cap and
+ *   offset): the activations of the reference's fused kernels' gated epilogues
+ *   (grouped_glu.epilogue, experts/grouped_glu.py:119-140).
  */
 size_t bux_mx_grouped_glu_workspace_size(int32_t groups, int64_t height);
 int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
                        const uint8_t* b_scales, const int32_t* sizes, int32_t groups,
                        int64_t height, int64_t n, int64_t k, int64_t rows,
-                       const uint16_t* weights, int activation, float limit, float up_offset,
-                       uint16_t* projected, uint8_t* values, uint8_t* scales, uint8_t* t_values,
+                       const uint16_t* weights, const bux_ffn* ffn, uint16_t* projected, uint8_t* values, uint8_t* scales, uint8_t* t_values,
                        uint8_t* t_scales, void* workspace, size_t workspace_bytes, void* stream);
 size_t bux_glu_backward_quantize_workspace_size(int64_t m, int64_t f);
 int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights,
                               const uint16_t* dh, const int32_t* filled, int64_t m, int64_t f,
-                              int activation, float limit, float up_offset, int64_t height,
+                              const bux_ffn* ffn, int64_t height,
                               uint16_t* d_projected, uint8_t* values, uint8_t* scales,
                               uint8_t* t_values, uint8_t* t_scales, uint16_t* d_weights,
                               void* workspace, size_t workspace_bytes, void* stream);

@@ -41,6 +41,7 @@ results are compared to it within tolerances stated in each test.
 from typing import NamedTuple
 
 import numpy as np
+from scipy import special
 
 from oracle import bf16, mxfp8
 from oracle.mxfp8 import Blocks
@@ -190,72 +191,174 @@ def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str 
 
 QUICK_GELU_ALPHA = float(bf16.round_f32(np.array([1.702], np.float32))[0])  # 1.703125
 
+ACTIVATIONS = ("swish", "quick_gelu", "relu", "relu2", "gelu", "gelu_tanh", "sigmoid", "tanh",
+               "softplus", "situ")
+
 
 class Ffn(NamedTuple):
-    """An expert FFN's activation settings (config.py:204-221): the gate's
-    activation, the clamp and the up branch's offset."""
+    """An expert FFN's activation settings (config.py:204-221): the activation, the
+    clamp, the up branch's offset and soft cap. Gated or plain follows the projection's
+    last axis, 2 or 1 (moe.py:913-919)."""
 
-    activation: str = "swish"  # or "quick_gelu" (gpt-oss's x * sigmoid(1.702 x))
+    activation: str = "swish"  # one of ACTIVATIONS
     limit: float | None = None
     up_offset: float = 0.0
+    up_softcap: float | None = None
 
 
 def _sigmoid(x: np.ndarray) -> np.ndarray:
-    return 1.0 / (1.0 + np.exp(-x))
+    return 0.5 * (1.0 + np.tanh(0.5 * x))
 
 
-def _act(name: str, g: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """Return act(g) and act'(g) (functional.py:12-40)."""
-    # functional.py:29 writes ``x * jax.nn.sigmoid(1.702 * x)``: jax casts the weakly
-    # typed 1.702 to x's dtype, bfloat16, whose nearest value is 1.703125.
-    alpha = {"swish": 1.0, "quick_gelu": QUICK_GELU_ALPHA}[name]
-    s = _sigmoid(alpha * g)
-    return g * s, s + alpha * g * s * (1.0 - s)
+def _act(name: str, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Return act(x) and act'(x) in float64 (functional.py:12-40; relu's gradient 0 at
+    0, as jax.nn.relu's)."""
+    if name in ("swish", "quick_gelu"):
+        # functional.py:29 writes ``x * jax.nn.sigmoid(1.702 * x)``: jax casts the weakly
+        # typed 1.702 to x's dtype, bfloat16, whose nearest value is 1.703125.
+        alpha = 1.0 if name == "swish" else QUICK_GELU_ALPHA
+        s = _sigmoid(alpha * x)
+        return x * s, s + alpha * x * s * (1.0 - s)
+    if name == "relu":
+        return np.maximum(x, 0.0), (x > 0).astype(np.float64)
+    if name == "relu2":
+        r = np.maximum(x, 0.0)
+        return r * r, 2.0 * r
+    if name == "gelu":
+        phi = 0.5 * (1.0 + special.erf(x / np.sqrt(2.0)))
+        return x * phi, phi + x * np.exp(-0.5 * x * x) / np.sqrt(2.0 * np.pi)
+    if name == "gelu_tanh":
+        c = np.sqrt(2.0 / np.pi)
+        t = np.tanh(c * (x + 0.044715 * x ** 3))
+        return 0.5 * x * (1.0 + t), 0.5 * (1.0 + t) + 0.5 * x * (1.0 - t * t) * c * (1.0 + 3 * 0.044715 * x * x)
+    if name == "sigmoid":
+        s = _sigmoid(x)
+        return s, s * (1.0 - s)
+    if name == "tanh":
+        t = np.tanh(x)
+        return t, 1.0 - t * t
+    if name == "softplus":
+        return np.logaddexp(x, 0.0), _sigmoid(x)
+    if name == "situ":
+        t, s = np.tanh(x / 4.0), _sigmoid(x)
+        return 4.0 * t * s, (1.0 - t * t) * s + 4.0 * t * s * (1.0 - s)
+    raise ValueError(name)
+
+
+def _up_branch(ffn: Ffn, up: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Return the up branch clipped and capped (mlp.py:28-30), and its derivative (jnp.clip
+    is maximum then minimum, whose gradients split 0.5 / 0.5 at a tie: at a limit of 0
+    an up of 0 ties both, 0.25)."""
+    d = np.ones_like(up)
+    if ffn.limit is not None:
+        tie = 0.25 if ffn.limit == 0 else 0.5
+        d = np.where(np.abs(up) < ffn.limit, 1.0, np.where(np.abs(up) == ffn.limit, tie, 0.0))
+        up = np.clip(up, -ffn.limit, ffn.limit)
+    if ffn.up_softcap is not None:
+        t = np.tanh(up / ffn.up_softcap)
+        d = d * (1.0 - t * t)
+        up = ffn.up_softcap * t
+    return up, d
 
 
 def weighted_units(ffn: Ffn, projected: np.ndarray, weights: np.ndarray) -> np.ndarray:
-    """Return ``act(gate) * (up + offset) * w`` for projected (m, f, 2) [up, gate] and
-    row weights (m,), as bfloat16 bits, computed in float64 and rounded once
-    (mlp.py:20-35, moe.py:898-926)."""
+    """Return ``act(gate) * (up + offset) * w`` for projected (m, f, 2) [up, gate], or
+    ``act(up) * w`` for (m, f, 1) or (m, f), and row weights (m,), as bfloat16 bits,
+    computed in float64 and rounded once (mlp.py:20-35, moe.py:898-926)."""
     p = bf16.to_f32(projected).astype(np.float64)
-    w = bf16.to_f32(weights).astype(np.float64)
-    up, gate = p[..., 0], p[..., 1]
+    if p.ndim == 2:
+        p = p[..., None]
+    w = bf16.to_f32(weights).astype(np.float64)[:, None]
+    up, _ = _up_branch(ffn, p[..., 0])
+    if p.shape[-1] == 1:
+        a, _ = _act(ffn.activation, up)
+        return bf16.to_bf16((a * w).astype(np.float32))
+    gate = p[..., 1]
     if ffn.limit is not None:
-        up = np.clip(up, -ffn.limit, ffn.limit)
         gate = np.minimum(gate, ffn.limit)
     a, _ = _act(ffn.activation, gate)
-    return bf16.to_bf16((a * (up + ffn.up_offset) * w[:, None]).astype(np.float32))
+    return bf16.to_bf16((a * (up + ffn.up_offset) * w).astype(np.float32))
 
 
 def weighted_units_backward(
     ffn: Ffn, projected: np.ndarray, weights: np.ndarray, dh: np.ndarray
 ) -> tuple[np.ndarray, np.ndarray]:
-    """Return the gradients of `weighted_units` to projected (m, f, 2) and to the row
+    """Return the gradients of `weighted_units` to projected (its shape) and to the row
     weights (m,), as bfloat16 bits (the VJP jax takes of it, moe.py:898-910, with
     jax's gradients of clip and minimum: 1 strictly inside, 0.5 at the limit, 0
     outside)."""
     p = bf16.to_f32(projected).astype(np.float64)
+    plain2d = p.ndim == 2
+    if plain2d:
+        p = p[..., None]
     w = bf16.to_f32(weights).astype(np.float64)[:, None]
     g_ = bf16.to_f32(dh).astype(np.float64)
-    up, gate = p[..., 0], p[..., 1]
-    up_pass = np.ones_like(up)
-    gate_pass = np.ones_like(gate)
-    if ffn.limit is not None:
-        # jnp.clip is maximum then minimum, whose gradients split 0.5 / 0.5 at a tie
-        up_pass = np.where(np.abs(up) < ffn.limit, 1.0, np.where(np.abs(up) == ffn.limit, 0.5, 0.0))
-        gate_pass = np.where(gate < ffn.limit, 1.0, np.where(gate == ffn.limit, 0.5, 0.0))
-        up = np.clip(up, -ffn.limit, ffn.limit)
-        gate = np.minimum(gate, ffn.limit)
-    a, da = _act(ffn.activation, gate)
-    u = up + ffn.up_offset
-    d_up = g_ * w * a * up_pass
-    d_gate = g_ * w * u * da * gate_pass
-    d_w = (g_ * a * u).sum(-1)
-    dp = np.stack([d_up, d_gate], -1).astype(np.float32)
-    return bf16.to_bf16(dp), bf16.to_bf16(d_w.astype(np.float32))
+    up, up_pass = _up_branch(ffn, p[..., 0])
+    if p.shape[-1] == 1:
+        a, da = _act(ffn.activation, up)
+        dp = (g_ * w * da * up_pass)[..., None]
+        d_w = (g_ * a).sum(-1)
+    else:
+        gate = p[..., 1]
+        gate_pass = np.ones_like(gate)
+        if ffn.limit is not None:
+            gate_pass = np.where(gate < ffn.limit, 1.0, np.where(gate == ffn.limit, 0.5, 0.0))
+            gate = np.minimum(gate, ffn.limit)
+        a, da = _act(ffn.activation, gate)
+        u = up + ffn.up_offset
+        dp = np.stack([g_ * w * a * up_pass, g_ * w * u * da * gate_pass], -1)
+        d_w = (g_ * a * u).sum(-1)
+    if plain2d:
+        dp = dp[..., 0]
+    return bf16.to_bf16(dp.astype(np.float32)), bf16.to_bf16(d_w.astype(np.float32))
+
+
+# --- The experts' biases ----------------------------------------------------------------
+
+
+def _expert_of_rows(sizes: np.ndarray, m: int) -> np.ndarray:
+    """Each of m sorted rows' expert, -1 past the groups."""
+    sizes = np.asarray(sizes, np.int64)
+    ends = np.cumsum(sizes)
+    r = np.arange(m)
+    e = np.searchsorted(ends, r, side="right")
+    return np.where(r < ends[-1] if ends.size else False, e, -1)
+
+
+def by_expert(bias: np.ndarray, sizes: np.ndarray, m: int) -> np.ndarray:
+    """Return each row's expert's row of `bias` (E, c), 0 past the groups, float32
+    (moe.by_expert, moe.py:876-885: a one-hot product, exact here)."""
+    b = bf16.to_f32(bias).reshape(len(sizes), -1)
+    e = _expert_of_rows(sizes, m)
+    return np.where((e >= 0)[:, None], b[np.maximum(e, 0)], np.float32(0))
+
+
+def add_expert_bias(x: np.ndarray, bias: np.ndarray, sizes: np.ndarray) -> np.ndarray:
+    """Return ``x + by_expert(bias)`` in bfloat16 (moe.py:857-861), bits."""
+    xf = bf16.to_f32(x).reshape(x.shape[0], -1)
+    return bf16.to_bf16(xf + by_expert(bias, sizes, x.shape[0])).reshape(x.shape)
+
+
+def expert_sums(v: np.ndarray, sizes: np.ndarray) -> np.ndarray:
+    """Return each expert's sum of its rows of v (float32 values, (m, c)), in float64:
+    by_expert's gradient, the one-hot product's transpose (moe.py:876-885)."""
+    e = _expert_of_rows(sizes, v.shape[0])
+    out = np.zeros((len(sizes), v.shape[1]), np.float64)
+    np.add.at(out, e[e >= 0], v[e >= 0].astype(np.float64))
+    return out
+
+
+def weighted_bias_rows(bias: np.ndarray, sizes: np.ndarray, row_weights: np.ndarray, m: int) -> np.ndarray:
+    """Return ``weighted(by_expert(down_bias), weights)``, bfloat16 bits (moe.py:869,
+    922-925): each row's expert's bias times the row's weight, rounded."""
+    w = bf16.to_f32(row_weights)[:, None]
+    return bf16.to_bf16(by_expert(bias, sizes, m) * w)
 
 
 # --- The layer: routed -> experts, forward and backward ----------------------------
+
+
+PASSES = ("fprop", "dgrad", "wgrad")
 
 
 class Saved(NamedTuple):
@@ -263,12 +366,20 @@ class Saved(NamedTuple):
 
     sorted: Sorted
     row_weights: np.ndarray
-    projected: np.ndarray  # bf16 bits (m, 2f)
+    projected: np.ndarray  # bf16 bits (m, p f), the up bias added
     h: np.ndarray  # bf16 bits (m, f)
     x_m: Blocks | None
     up_n: Blocks | None
     h_m: Blocks | None
     down_n: Blocks | None
+    passes: tuple[bool, bool, bool] = (True, True, True)
+
+
+def _passes(fmt: str, passes) -> tuple[bool, bool, bool]:
+    if fmt not in ("mxfp8", "mxfp8_2d"):
+        return False, False, False
+    chosen = PASSES if passes is None else tuple(passes)
+    return tuple(q in chosen for q in PASSES)
 
 
 def layer_forward(
@@ -279,21 +390,27 @@ def layer_forward(
     down: np.ndarray,
     ffn: Ffn = Ffn(),
     fmt: str = "mxfp8",
+    passes=None,
+    up_bias: np.ndarray | None = None,
+    down_bias: np.ndarray | None = None,
 ) -> tuple[np.ndarray, Saved]:
     """Return the MoE's routed experts' output (t, d) as bfloat16 bits, and what the
     backward takes: ``routed`` (moe.py:733-773) on one device with picked rows in and
     summed rows out, each grouped GEMM in MXFP8 (`fmt` "mxfp8") or bfloat16
-    ("compute").
+    ("compute"); with `passes`, only those GEMMs in MXFP8 (grouped_blockscaled.py:
+    167-211); with biases, moe.py:857-870.
 
     Args:
         z: tokens, bfloat16 bits (t, d).
         idx: each token's k experts, int (t, k).
         weights: their weights, bfloat16 bits (t, k).
-        up: the experts' up and gate kernels, bfloat16 bits (E, d, f, 2).
+        up: the experts' up kernels, bfloat16 bits (E, d, f, p): p = 2 gated, 1 plain.
         down: the experts' down kernels, bfloat16 bits (E, f, d).
         ffn: the activation.
         fmt: "mxfp8", "mxfp8_2d" (each W with a scale per 32 x 32 tile shared by its
             copies, blockscaled.MXFP8_2D, blockscaled.py:306-309) or "compute".
+        passes: the GEMMs in `fmt`, of PASSES; None for all.
+        up_bias: bfloat16 bits (E, f, p) or None; down_bias: (E, d) or None.
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -306,33 +423,42 @@ def layer_forward(
     row_weights = kept[s.order]
     up2 = np.asarray(up).reshape(e, d, f * p)
     x_m = up_n = h_m = down_n = None
-    mx, tiles = fmt in ("mxfp8", "mxfp8_2d"), fmt == "mxfp8_2d"
-    if mx:
-        # rows padded by 0 to whole tiles of 128 (grouped_blockscaled.py:122-128)
+    fprop, dgrad, wgrad = _passes(fmt, passes)
+    tiles = fmt == "mxfp8_2d"
+    # rows padded by 0 to whole tiles of 128 (grouped_blockscaled.py:122-128)
+    if fprop or wgrad:
         x_k, x_m = mxfp8.quantized_twice(z, filled, True, index=tokens, height=whole(m))
+    if fprop or dgrad:
         up_n, up_k = mxfp8.quantized_twice(up2, d, tiles=tiles)
+        down_n, down_k = mxfp8.quantized_twice(down, f, tiles=tiles)
+    if fprop:
         projected = rows_mx(x_k, up_k, s.sizes, height=m)
     else:
         projected = ragged_dot_bf16(z[tokens], up2, s.sizes)
+    if up_bias is not None:
+        projected = add_expert_bias(projected, up_bias, s.sizes)
     h = weighted_units(ffn, projected.reshape(m, f, p), row_weights)
-    if mx:
+    if fprop or wgrad:
         h_k, h_m = mxfp8.quantized_twice(h, filled, True, height=whole(m))
-        down_n, down_k = mxfp8.quantized_twice(down, f, tiles=tiles)
-        y = rows_mx(h_k, down_k, s.sizes, height=m)
-    else:
-        y = ragged_dot_bf16(h, down, s.sizes)
+    y = rows_mx(h_k, down_k, s.sizes, height=m) if fprop else ragged_dot_bf16(h, down, s.sizes)
     out = sum_by_token(y, s.inverse.reshape(t, k))
-    return out, Saved(s, row_weights, projected, h, x_m, up_n, h_m, down_n)
+    if down_bias is not None:
+        b = weighted_bias_rows(down_bias, s.sizes, row_weights, m)
+        bsum = sum_by_token(b, s.inverse.reshape(t, k))
+        out = bf16.to_bf16(bf16.to_f32(out) + bf16.to_f32(bsum))
+    return out, Saved(s, row_weights, projected, h, x_m, up_n, h_m, down_n, (fprop, dgrad, wgrad))
 
 
 def layer_backward(
     saved: Saved, dy: np.ndarray, z: np.ndarray, up: np.ndarray, down: np.ndarray,
     k: int, ffn: Ffn = Ffn(), fmt: str = "mxfp8",
+    up_bias: np.ndarray | None = None, down_bias: np.ndarray | None = None,
 ) -> dict[str, np.ndarray]:
     """Return the gradients of `layer_forward`'s output, dy (t, d) bfloat16 bits, to
-    z, the weights, up and down (bfloat16 bits): grouped_blockscaled._backward
-    (:191-211) for each GEMM, weighted_units' VJP between them, and the gathers'
-    VJPs (moe.py:1018-1021,1060-1063)."""
+    z, the weights, up and down (bfloat16 bits), and to the biases (float64 sums):
+    grouped_blockscaled._backward (:191-211) for each GEMM, weighted_units' VJP between
+    them, and the gathers' and biases' VJPs (moe.py:857-870,1018-1021,1060-1063). The
+    passes are the forward's."""
     s = saved.sorted
     t = dy.shape[0]
     e, d, f, p = up.shape
@@ -340,24 +466,44 @@ def layer_backward(
     filled = int(s.sizes.sum())
     tokens = s.order // k
     up2 = np.asarray(up).reshape(e, d, f * p)
-    mx = fmt in ("mxfp8", "mxfp8_2d")  # W's copies come from the forward
-    if mx:
+    fprop, dgrad, wgrad = saved.passes
+    if dgrad or wgrad:
         dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens, height=whole(m))
+    dy_rows = dy[tokens]
+    if dgrad:
         dh = rows_mx(dy_n, saved.down_n, s.sizes, height=m)
+    else:
+        dh = ragged_dot_bf16(dy_rows, np.ascontiguousarray(np.swapaxes(down, 1, 2)), s.sizes)
+    if wgrad:
         d_down = contract_mx(saved.h_m, dy_m, s.sizes)
     else:
-        dy_rows = dy[tokens]
-        dh = ragged_dot_bf16(dy_rows, np.ascontiguousarray(np.swapaxes(down, 1, 2)), s.sizes)
         d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes)
     dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), saved.row_weights, dh)
     dp = dp.reshape(m, f * p)
-    if mx:
+    if dgrad or wgrad:
         dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True, height=whole(m))
+    if dgrad:
         dx = rows_mx(dp_n, saved.up_n, s.sizes, height=m)
-        d_up = contract_mx(saved.x_m, dp_m, s.sizes)
     else:
         dx = ragged_dot_bf16(dp, np.ascontiguousarray(np.swapaxes(up2, 1, 2)), s.sizes)
+    if wgrad:
+        d_up = contract_mx(saved.x_m, dp_m, s.sizes)
+    else:
         d_up = weight_grad_bf16(z[tokens], dp, s.sizes)
+    grads = {}
+    if up_bias is not None:
+        grads["up_bias"] = expert_sums(bf16.to_f32(dp), s.sizes).reshape(e, f, p)
+    if down_bias is not None:
+        # weighted(b_rows, w)'s VJP: to b_rows ct * w (bfloat16), to w sum_c ct * b_rows
+        # (products in bfloat16, summed in float32); ct = dy at each row's token
+        g = bf16.to_f32(dy_rows)
+        w = bf16.to_f32(saved.row_weights)[:, None]
+        b_rows = by_expert(down_bias, s.sizes, m)
+        live = (_expert_of_rows(s.sizes, m) >= 0)[:, None]
+        grads["down_bias"] = expert_sums(np.where(live, bf16.round_f32(g * w), 0), s.sizes)
+        extra = bf16.round_f32(bf16.round_f32(g * b_rows).sum(-1, dtype=np.float32))
+        d_rows_w = bf16.to_bf16(bf16.to_f32(d_rows_w) + extra)
     dz = sum_by_token(dx, s.inverse.reshape(t, k))
     d_weights = d_rows_w[s.inverse].reshape(t, k)
-    return {"z": dz, "weights": d_weights, "up": d_up.reshape(e, d, f, p), "down": d_down}
+    grads.update(z=dz, weights=d_weights, up=d_up.reshape(e, d, f, p), down=d_down)
+    return grads

@@ -100,15 +100,18 @@ def test_fused_up_gemm_rejects_bad_arguments(lib):
     # group starts, then tiles of 256 rows with up to 31 more a group, one more a group
     assert ws >= (-(-(256 + 32 * 5) // 256) + 5) * 12
 
-    def glu(height=256, n=128, k=128, rows=200, act=0, ws_bytes=1 << 20, groups=4):
-        return lib.bux_mx_grouped_glu(p, p, p, p, p, groups, height, n, k, rows, p, act, 0.0, 0.0,
-                                      p, p, p, p, p, p, ws_bytes, None)
+    def glu(height=256, n=128, k=128, rows=200, act=0, ws_bytes=1 << 20, groups=4, gated=1):
+        ffn = _lib.FfnStruct(act, gated, 0, 0.0, 0, 0.0, 0.0)
+        return lib.bux_mx_grouped_glu(p, p, p, p, p, groups, height, n, k, rows, p,
+                                      ctypes.byref(ffn), p, p, p, p, p, p, ws_bytes, None)
 
     assert glu(height=200) == 1 and "height=200" in _msg(lib)  # whole 128s: h^T's K
     assert glu(n=96) == 1 and "n=96" in _msg(lib)  # (up, gate) pairs of f, a multiple of 32
     assert glu(k=64) == 1 and "k=64" in _msg(lib)
     assert glu(rows=300) == 1 and "rows=300" in _msg(lib)  # the product within the copies
-    assert glu(act=5) == 1 and "activation 5" in _msg(lib)
+    assert glu(act=5) == 1 and "activation 5" in _msg(lib)  # no fused gelu_tanh epilogue
+    assert glu(act=0, gated=0) == 1 and "plain" in _msg(lib)
+    assert glu(act=10) == 1 and "activation 10" in _msg(lib)
     assert glu(groups=0) == 1 and "groups=0" in _msg(lib)
     assert glu(ws_bytes=8) == 2 and "workspace" in _msg(lib)
 
@@ -121,10 +124,49 @@ def test_permute_and_token_ops_reject_bad_arguments(lib):
     assert rc == 2 and "workspace" in _msg(lib)
     rc = lib.bux_token_sums(p, 10, p, 5, 2, 12, p, None)
     assert rc == 1 and "width=12" in _msg(lib)
-    rc = lib.bux_glu_forward(p, p, None, 10, 6, 0, 0.0, 0.0, p, None)
+    ok = _lib.FfnStruct(0, 1, 0, 0.0, 0, 0.0, 0.0)
+    rc = lib.bux_glu_forward(p, p, None, 10, 6, ctypes.byref(ok), p, None)
     assert rc == 1 and "f=6" in _msg(lib)
-    rc = lib.bux_glu_forward(p, p, None, 10, 8, 9, 0.0, 0.0, p, None)
-    assert rc == 1 and "activation 9" in _msg(lib)
+    for bad, words in (((10, 1, 0, 0.0, 0, 0.0, 0.0), "activation 10"),
+                       ((-1, 1, 0, 0.0, 0, 0.0, 0.0), "activation -1"),
+                       ((0, 1, 1, -1.0, 0, 0.0, 0.0), "limit -1"),
+                       ((0, 1, 1, float("nan"), 0, 0.0, 0.0), "limit nan"),
+                       ((0, 0, 0, 0.0, 1, 0.0, 0.0), "up_softcap 0"),
+                       ((0, 0, 0, 0.0, 1, -2.0, 0.0), "up_softcap -2")):
+        ffn = _lib.FfnStruct(*bad)
+        rc = lib.bux_glu_forward(p, p, None, 10, 8, ctypes.byref(ffn), p, None)
+        assert rc == 1 and words in _msg(lib), (bad, _msg(lib))
+        rc = lib.bux_glu_backward_quantize(p, p, p, None, 10, 32, ctypes.byref(ffn), 128, None, p, p,
+                                           p, p, p, p, 1 << 20, None)
+        assert rc == 1 and words in _msg(lib), (bad, _msg(lib))
+    rc = lib.bux_glu_forward(p, p, None, 10, 8, None, p, None)
+    assert rc == 1 and "NULL ffn" in _msg(lib)
+    # a clamp at 0 clips every up to 0: allowed
+    zero = _lib.FfnStruct(0, 1, 1, 0.0, 0, 0.0, 0.0)
+    assert lib.bux_glu_forward(p, p, None, 0, 8, ctypes.byref(zero), p, None) == 0
+
+
+def test_bias_ops_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    rc = lib.bux_expert_bias_add(p, 10, 12, p, p, 4, None)
+    assert rc == 1 and "width=12" in _msg(lib)
+    rc = lib.bux_expert_bias_add(p, 10, 16, p, None, 4, None)
+    assert rc == 1 and "offsets" in _msg(lib)
+    rc = lib.bux_expert_bias_add(p, 10, 16, p, p, 0, None)
+    assert rc == 1 and "0 experts" in _msg(lib)
+    assert lib.bux_expert_bias_add(None, 0, 16, None, p, 4, None) == 0  # no rows
+    rc = lib.bux_expert_sums(p, p, 0, None, 10, 16, p, 4, p, None)
+    assert rc == 1 and "index_div=0" in _msg(lib)
+    rc = lib.bux_expert_sums(p, None, 1, None, 10, 16, p, 4, None, None)
+    assert rc == 1 and "NULL" in _msg(lib)
+    rc = lib.bux_token_sums_biased(p, 10, p, 5, 2, 16, None, p, 4, p, p, None)
+    assert rc == 1 and "NULL bias" in _msg(lib)
+    rc = lib.bux_token_sums_biased(p, 10, p, 5, 2, 12, p, p, 4, p, p, None)
+    assert rc == 1 and "width=12" in _msg(lib)
+    rc = lib.bux_expert_bias_weight_grad(p, p, 0, 10, 16, p, p, 4, p, None)
+    assert rc == 1 and "index_div=0" in _msg(lib)
+    rc = lib.bux_expert_bias_weight_grad(p, None, 1, 10, 16, p, p, 0, p, None)
+    assert rc == 1 and "0 experts" in _msg(lib)
 
 
 def test_route_rejects_bad_arguments(lib):

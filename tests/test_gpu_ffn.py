@@ -1,0 +1,259 @@
+"""The experts' FFN in all its settings on the GPU, against the oracle: every activation
+of functional.py:12-40, gated (gated_mlp) and plain (mlp), with the clamp, the up
+branch's offset and soft cap (layers/mlp.py:20-35); the experts' up and down biases
+(moe.py:857-870); and the layer with any subset of its GEMMs in MXFP8 (the reference's
+``passes``, grouped_blockscaled.py:167-211).
+
+Bars: the activation and its gradient within one bfloat16 rounding of the oracle's
+float64 values, elementwise (the kernels compute in float32 and round once; XLA's own
+roundings inside its fused chain are not observable without jax, so bit parity is
+unpinned); the bias ops bit for bit where they are a rounding of the same float32
+operations in the same order (the bias add, the biased token sums), else float32 sums
+in another order, within 1e-5 relative; the layer end to end as test_gpu_layer.py holds
+it."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16, moe as omoe, mxfp8 as omx
+from tests._util import announce, bf16_bits, normal_bf16, rel_err, to_gpu, to_gpu_bf16, untiled
+
+pytestmark = pytest.mark.gpu
+
+# (activation, limit, up_offset, up_softcap, p): p = 2 gated, 1 plain
+FFNS = [
+    ("swish", None, 0.0, None, 2),
+    ("quick_gelu", 7.0, 1.0, None, 2),
+    ("situ", None, 0.0, 6.0, 2),
+    ("gelu_tanh", 3.0, 0.5, 5.0, 2),
+    ("gelu", None, 0.0, None, 2),
+    ("relu", 2.0, 0.0, None, 2),
+    ("sigmoid", 0.0, 0.0, None, 2),
+    ("tanh", None, -0.5, 4.0, 2),
+    ("softplus", None, 0.0, None, 2),
+    ("relu2", None, 0.0, None, 2),
+    ("relu2", None, 0.0, None, 1),
+    ("gelu", 4.0, 0.0, 3.0, 1),
+    ("gelu_tanh", None, 0.0, None, 1),
+    ("softplus", None, 0.0, None, 1),
+    ("tanh", None, 0.0, 2.0, 1),
+    ("situ", None, 0.0, None, 1),
+    ("sigmoid", None, 0.0, None, 1),
+    ("swish", 5.0, 0.0, None, 1),
+    ("quick_gelu", None, 0.0, None, 1),
+    ("relu", None, 0.0, None, 1),
+]
+
+
+def _ids(case):
+    act, limit, offset, cap, p = case
+    return f"{act}-{'gated' if p == 2 else 'plain'}" + (f"-clamp{limit}" if limit is not None else "") + \
+        (f"-cap{cap}" if cap is not None else "") + (f"-off{offset}" if offset else "")
+
+
+def _pair(case):
+    from bux_amd import moe
+    act, limit, offset, cap, p = case
+    return omoe.Ffn(act, limit, offset, cap), moe.Ffn(act, limit, offset, cap), p
+
+
+def _within_a_rounding(got_bits, want_bits):
+    """One bfloat16 rounding apart, elementwise; below 2^-20 of the array's largest
+    magnitude, float32 cancellation is allowed too: where a derivative crosses 0 (SiTU's
+    near x = -1.2, swish's near -1.28) its float32 terms cancel to a value far smaller
+    than themselves, and their float32 ulps make the difference."""
+    got, want = bf16.to_f32(got_bits), bf16.to_f32(want_bits)
+    floor = 2.0 ** -20 * float(np.abs(want).max())
+    bad = np.abs(got - want) > np.abs(want) * 2.0 ** -7 + floor
+    assert not bad.any(), (int(bad.sum()), got[bad][:4], want[bad][:4])
+    assert rel_err(got, want) <= 2.0 ** -9
+
+
+@pytest.mark.parametrize("case", FFNS, ids=[_ids(c) for c in FFNS])
+def test_activation_forward_backward_and_their_quantized_copies(lib, case):
+    """Each setting: h and its gradients against the oracle; the one-pass quantizing
+    kernels give the same bfloat16 values bit for bit, and their MXFP8 copies are the
+    oracle quantizer's of those values; rows from `filled` on are 0."""
+    from bux_amd import moe
+    o, g, p = _pair(case)
+    rng = np.random.default_rng(60)
+    m, f, filled, height = 512, 256, 481, 512
+    pr = normal_bf16(rng, (m, f, p), 4.0)
+    if o.limit is not None:  # ties with the clamp, and beyond it
+        pr.reshape(-1)[:64] = bf16.to_bf16(
+            np.array([1, -1, 1.5, -1.5, 0, 0.5, -0.25, 3] * 8, np.float32) * o.limit)
+    w = bf16.to_bf16(rng.random(m).astype(np.float32))
+    dh = normal_bf16(rng, (m, f))
+    announce("ffn activation", _ids(case))
+    fg = to_gpu(np.array([filled], np.int32))
+    gp, gw, gdh = to_gpu_bf16(pr), to_gpu_bf16(w), to_gpu_bf16(dh)
+    h = moe.weighted_units(g, gp, gw, fg)
+    dp, dw = moe.weighted_units_backward(g, gp, gw, gdh, fg)
+    h_k, h_m, h2 = moe.weighted_units_quantized(g, gp, gw, fg, height, keep=True)
+    dp_n, dp_m, dw2, dp2 = moe.weighted_units_backward_quantized(g, gp, gw, gdh, fg, height, keep=True)
+    torch.cuda.synchronize()
+
+    want_h = omoe.weighted_units(o, pr[:filled], w[:filled])
+    want_dp, want_dw = omoe.weighted_units_backward(o, pr[:filled], w[:filled], dh[:filled])
+    got_h, got_dp = bf16_bits(h), bf16_bits(dp)
+    _within_a_rounding(got_h[:filled], want_h)
+    _within_a_rounding(got_dp[:filled], want_dp)
+    assert (got_h[filled:] == 0).all() and (got_dp[filled:] == 0).all()  # +0, bit for bit
+    got_dw = bf16.to_f32(bf16_bits(dw))
+    assert rel_err(got_dw[:filled], bf16.to_f32(want_dw)) <= 1e-3
+    assert (got_dw[filled:] == 0).all()
+
+    np.testing.assert_array_equal(bf16_bits(h2), got_h)
+    np.testing.assert_array_equal(bf16_bits(dp2), got_dp)
+    a, b = bf16.to_f32(bf16_bits(dw2)), got_dw
+    assert (np.abs(a - b) <= np.abs(b) * 2.0 ** -7 + 1e-30).all()
+    want_k, want_m = omx.quantized_twice(got_h, filled, True, height=height)
+    for tiled, want, cols in ((h_k, want_k, f), (h_m, want_m, height)):
+        v, sc = untiled(tiled, cols)
+        np.testing.assert_array_equal(v, want.values)
+        np.testing.assert_array_equal(sc, want.scales)
+    want_n, want_pm = omx.quantized_twice(got_dp.reshape(m, p * f), filled, True, height=height)
+    for tiled, want, cols in ((dp_n, want_n, p * f), (dp_m, want_pm, height)):
+        v, sc = untiled(tiled, cols)
+        np.testing.assert_array_equal(v, want.values)
+        np.testing.assert_array_equal(sc, want.scales)
+
+
+def _sorted_case(rng, t, k, e, skew_empty=True):
+    from oracle import moe as om
+    idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)]).astype(np.int32)
+    if skew_empty:
+        idx[idx % 5 == 3] = (idx[idx % 5 == 3] + 1) % e  # experts 3, 8, ... get no rows
+    idx[::11, 0] = e + 1  # picks outside the experts: rows past the groups
+    return idx, om.sort_by_expert(idx, e)
+
+
+def test_expert_bias_ops(lib):
+    """The bias add (bit for bit), each expert's sums of its rows (plain, and read
+    through the picks' tokens times the row weights), the biased token sums (bit for
+    bit) and the down bias's share of the weights' gradient, against the oracle; empty
+    experts and rows past the groups included."""
+    from bux_amd import moe
+    rng = np.random.default_rng(61)
+    t, k, e, width, d = 700, 4, 16, 384, 256
+    m = t * k
+    idx, s = _sorted_case(rng, t, k, e)
+    filled = int(s.sizes.sum())
+    offsets = np.concatenate([s.offsets, [filled]]).astype(np.int32)
+    x = normal_bf16(rng, (m, width), 2.0)
+    up_bias = normal_bf16(rng, (e, width))
+    down_bias = normal_bf16(rng, (e, d))
+    y = normal_bf16(rng, (m, d))
+    dy = normal_bf16(rng, (t, d))
+    rw = bf16.to_bf16(rng.random(m).astype(np.float32))
+    rw[filled:] = 0
+    announce("bias ops", t, k, e)
+    go, gorder, ginv = to_gpu(offsets), to_gpu(s.order), to_gpu(s.inverse.reshape(t, k))
+    gx = to_gpu_bf16(x)
+    moe.add_expert_bias(gx, to_gpu_bf16(up_bias), go)
+    sums = moe.expert_sums(to_gpu_bf16(x), go)
+    dsums = moe.expert_sums(to_gpu_bf16(dy), go, gorder, k, to_gpu_bf16(rw))
+    out = moe.sum_by_token_biased(to_gpu_bf16(y), ginv, to_gpu_bf16(down_bias), go, to_gpu_bf16(rw))
+    dwg = normal_bf16(rng, (m,), 0.1)
+    gdw = to_gpu_bf16(dwg)
+    moe.add_bias_weight_grad(gdw, to_gpu_bf16(dy), gorder, k, to_gpu_bf16(down_bias), go)
+    torch.cuda.synchronize()
+
+    np.testing.assert_array_equal(bf16_bits(gx), omoe.add_expert_bias(x, up_bias, s.sizes))
+    want = omoe.expert_sums(bf16.to_f32(x), s.sizes)
+    np.testing.assert_allclose(sums.cpu().numpy(), want, rtol=1e-5, atol=1e-5)
+    assert (sums.cpu().numpy()[s.sizes == 0] == 0).all()
+    tokens = s.order // k
+    g = bf16.to_f32(dy[tokens])
+    live = (np.arange(m) < filled)[:, None]
+    wd = np.where(live, bf16.round_f32(g * bf16.to_f32(rw)[:, None]), 0)
+    np.testing.assert_allclose(dsums.cpu().numpy(), omoe.expert_sums(wd, s.sizes), rtol=1e-5, atol=1e-5)
+    b = omoe.weighted_bias_rows(down_bias, s.sizes, rw, m)
+    want_out = bf16.to_bf16(bf16.to_f32(omoe.sum_by_token(y, s.inverse.reshape(t, k)))
+                            + bf16.to_f32(omoe.sum_by_token(b, s.inverse.reshape(t, k))))
+    np.testing.assert_array_equal(bf16_bits(out), want_out)
+    b_rows = omoe.by_expert(down_bias, s.sizes, m)
+    extra = bf16.round_f32(bf16.round_f32(g * b_rows).astype(np.float64).sum(-1))
+    want_dw = bf16.to_f32(bf16.to_bf16(bf16.to_f32(dwg) + extra))
+    got_dw = bf16.to_f32(bf16_bits(gdw))
+    assert (np.abs(got_dw - want_dw) <= np.abs(want_dw) * 2.0 ** -6 + 1e-6).all()
+    np.testing.assert_array_equal(got_dw[filled:], bf16.to_f32(dwg[filled:]) + 0.0)
+
+
+def _layer_inputs(rng, t, k, e, d, f, p, biased):
+    z = normal_bf16(rng, (t, d))
+    idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)]).astype(np.int32)
+    idx[::13, -1] = e  # a pick outside the experts
+    w = bf16.to_bf16(rng.random((t, k)).astype(np.float32) / k)
+    up = normal_bf16(rng, (e, d, f, p), 0.02)
+    down = normal_bf16(rng, (e, f, d), 0.02)
+    dy = normal_bf16(rng, (t, d), 1e-2)
+    ub = normal_bf16(rng, (e, f, p), 0.5) if biased else None
+    db = normal_bf16(rng, (e, d), 0.5) if biased else None
+    return z, idx, w, up, down, dy, ub, db
+
+
+END_TO_END = 1e-2  # as test_gpu_layer.py: a quantized pipeline's float differences
+STAGE = 1e-3
+
+LAYERS = [
+    # name, fmt, passes, (activation, limit, offset, cap), p, biased
+    ("gptoss_biased_mxfp8", "mxfp8", None, ("quick_gelu", 7.0, 1.0, None), 2, True),
+    ("gptoss_biased_compute", "compute", None, ("quick_gelu", 7.0, 1.0, None), 2, True),
+    ("relu2_plain_mxfp8", "mxfp8", None, ("relu2", None, 0.0, None), 1, False),
+    ("gelu_plain_biased_compute", "compute", None, ("gelu", None, 0.0, 3.0), 1, True),
+    ("situglu_mxfp8_2d", "mxfp8_2d", None, ("situ", None, 0.0, 6.0), 2, False),
+] + [
+    (f"passes_{'_'.join(ps)}", "mxfp8", ps, ("swish", None, 0.0, None), 2, False)
+    for ps in (("fprop",), ("dgrad",), ("wgrad",), ("fprop", "dgrad"), ("fprop", "wgrad"),
+               ("dgrad", "wgrad"))
+]
+
+
+@pytest.mark.parametrize("name,fmt,passes,act,p,biased", LAYERS, ids=[c[0] for c in LAYERS])
+def test_layer_in_every_setting(lib, name, fmt, passes, act, p, biased):
+    """The layer forward and backward against the oracle's, end to end, and its
+    float32 bias gradients; with the fused up GEMM asked for, the same bits where it
+    runs (every pass in MXFP8, no bias, a fused activation) and the unfused path
+    elsewhere."""
+    from bux_amd import moe
+    rng = np.random.default_rng(62)
+    t, k, e, d, f = 600, 4, 12, 256, 192
+    z, idx, w, up, down, dy, ub, db = _layer_inputs(rng, t, k, e, d, f, p, biased)
+    o, g = omoe.Ffn(*act), moe.Ffn(*act)
+    announce("ffn layer", name)
+    gz, gidx, gw, gup, gdown, gdy = (to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up),
+                                      to_gpu_bf16(down), to_gpu_bf16(dy))
+    gub = to_gpu_bf16(ub) if biased else None
+    gdb = to_gpu_bf16(db) if biased else None
+    results = []
+    for fused in (False, True):
+        out, saved = moe.experts_forward(gz, gidx, gw, gup, gdown, g, fmt, fused=fused, passes=passes,
+                                         up_bias=gub, down_bias=gdb)
+        grads = moe.experts_backward(saved, gdy, gup, gdown, g, fmt, up_bias=gub, down_bias=gdb)
+        results.append((out, grads))
+    torch.cuda.synchronize()
+    (out, grads), (out_f, grads_f) = results
+    assert torch.equal(out.view(torch.int16), out_f.view(torch.int16))
+    for key in grads:
+        a, b = grads[key], grads_f[key]
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b), key
+
+    want, osaved = omoe.layer_forward(z, idx, w, up, down, o, fmt, passes, ub, db)
+    wgrads = omoe.layer_backward(osaved, dy, z, up, down, k, o, fmt, ub, db)
+    bar = STAGE if fmt == "compute" else END_TO_END
+
+    def f32(x):
+        return bf16.to_f32(bf16_bits(x)).astype(np.float64)
+
+    errs = {"y": rel_err(f32(out), bf16.to_f32(want))}
+    for key in ("z", "weights", "up", "down"):
+        errs[key] = rel_err(f32(grads[key]), bf16.to_f32(wgrads[key]))
+    if biased:
+        for key in ("up_bias", "down_bias"):
+            errs[key] = rel_err(grads[key].cpu().numpy(), wgrads[key])
+    print(f"[err] {name} " + " ".join(f"{k_}={v:.2e}" for k_, v in errs.items()), flush=True)
+    for key, err in errs.items():
+        assert err <= bar, (key, err)

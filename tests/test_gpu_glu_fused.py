@@ -9,7 +9,7 @@ The cases move the groups' first rows off the 32-row blocks of h^T (whose blocks
 group's first row inside go through the fix-up kernel), hold empty groups, groups
 smaller than a block and several groups' first rows inside one block, rows past the
 groups (zeros), a hidden width that is not a whole number of 128s (the row copy's K
-padding) and both activations."""
+padding) and the three gated activations the fused kernel runs."""
 
 import numpy as np
 import pytest
@@ -25,10 +25,14 @@ CASES = [
     ([33, 31, 64, 0, 0, 517, 2, 2, 2], 700, 128, 32, "clamped"),
     ([5, 3, 10, 7, 0, 1, 1, 1], 64, 128, 96, "swiglu"),
     ([512, 256, 0, 768], 1536, 256, 256, "clamped"),
+    ([40, 0, 300, 7, 100], 480, 256, 192, "situglu"),
     ("multinomial", 16 * 1024, 512, 384, "swiglu"),
 ]
 
-ACTS = {"swiglu": ("swish", None, 0.0), "clamped": ("quick_gelu", 7.0, 1.0)}
+# (activation, limit, up_offset, up_softcap): SwiGLU, gpt-oss's clamped GeGLU form, and
+# SiTU-GLU with its soft cap (grouped_glu.epilogue, experts/grouped_glu.py:119-136)
+ACTS = {"swiglu": ("swish", None, 0.0, None), "clamped": ("quick_gelu", 7.0, 1.0, None),
+        "situglu": ("situ", None, 0.0, 6.0)}
 
 
 def _sizes(spec, rows, groups_if_random, rng):
@@ -60,7 +64,7 @@ def _run(sizes_np, rows, d, f, act, seed):
     h_k, h_m, _ = moe.weighted_units_quantized(ffn, projected.view(rows, f, 2), weights, filled_t,
                                                height)
     # fused
-    p2, h_k2, h_m2 = gm.activated(x_k, up_k, sizes, weights, ffn.codes(), rows)
+    p2, h_k2, h_m2 = gm.activated(x_k, up_k, sizes, weights, ffn.struct(True), rows)
     torch.cuda.synchronize()
     return (projected, h_k, h_m), (p2, h_k2, h_m2)
 
@@ -103,7 +107,8 @@ def test_fused_up_gemm_at_config_3(lib):
 
 
 @pytest.mark.parametrize("t,k,e,d,f,act", [(300, 4, 8, 256, 160, "clamped"),
-                                           (4096, 8, 64, 512, 384, "swiglu")])
+                                           (4096, 8, 64, 512, 384, "swiglu"),
+                                           (500, 4, 16, 256, 128, "situglu")])
 def test_layer_with_the_fused_up_gemm_is_bit_identical(lib, t, k, e, d, f, act):
     """The whole layer, forward and backward, with and without the fused up GEMM."""
     from bux_amd import moe

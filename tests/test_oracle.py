@@ -323,62 +323,154 @@ def test_contract_sums_each_groups_rows_and_ignores_rows_past_them():
     np.testing.assert_array_equal(moe.contract_mx(mxfp8.Blocks(junk, a.scales), b, sizes, "f32"), got)
 
 
-@pytest.mark.parametrize("ffn", [moe.Ffn(), moe.Ffn("quick_gelu", 7.0, 1.0)])
-def test_the_activations_gradient_is_autograds(ffn):
-    rng = np.random.default_rng(9)
-    m, f = 64, 48
-    p = bf16.to_bf16((rng.standard_normal((m, f, 2)) * 4).astype(np.float32))
-    w = bf16.to_bf16(rng.random(m).astype(np.float32))
-    dh = bf16.to_bf16(rng.standard_normal((m, f)).astype(np.float32))
-    dp, dw = moe.weighted_units_backward(ffn, p, w, dh)
-    pt = torch.tensor(bf16.to_f32(p), dtype=torch.float64, requires_grad=True)
-    wt = torch.tensor(bf16.to_f32(w), dtype=torch.float64, requires_grad=True)
-    up, gate = pt[..., 0], pt[..., 1]
-    if ffn.limit is not None:  # maximum/minimum: gradient 0.5 at a tie, as jax's
+# torch's own activations (library routines, differentiated by autograd): the oracle's
+# closed forms and hand-derived derivatives are checked against them.
+TORCH_ACTS = {
+    "swish": torch.nn.functional.silu,
+    "quick_gelu": lambda x: x * torch.sigmoid(moe.QUICK_GELU_ALPHA * x),
+    "relu": torch.relu,
+    "relu2": lambda x: torch.relu(x) ** 2,
+    "gelu": torch.nn.functional.gelu,
+    "gelu_tanh": lambda x: torch.nn.functional.gelu(x, approximate="tanh"),
+    "sigmoid": torch.sigmoid,
+    "tanh": torch.tanh,
+    # jax.nn.softplus is logaddexp(x, 0) everywhere; torch's turns linear past its
+    # threshold (20 by default), so the threshold is raised past the range tested
+    "softplus": lambda x: torch.nn.functional.softplus(x, threshold=100.0),
+    "situ": lambda x: 4.0 * torch.tanh(x / 4.0) * torch.sigmoid(x),
+}
+
+
+@pytest.mark.parametrize("name", moe.ACTIVATIONS)
+def test_each_activation_and_its_derivative_are_torchs(name):
+    """functional.py:12-40's activations: the oracle's values and derivatives against
+    torch's functions and autograd in float64, over [-30, 30], at 0 (relu's gradient
+    0 there, as jax.nn.relu's) and at tiny magnitudes."""
+    x = np.concatenate([np.linspace(-30.0, 30.0, 6001), [0.0, 1e-30, -1e-30, 1e-8, -1e-8]])
+    a, da = moe._act(name, x)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    y = TORCH_ACTS[name](xt)
+    y.sum().backward()
+    np.testing.assert_allclose(a, y.detach().numpy(), rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(da, xt.grad.numpy(), rtol=1e-8, atol=1e-14)
+
+
+FFNS = [
+    # (ffn, p): p = 2 gated (gated_mlp), 1 plain (mlp)
+    (moe.Ffn(), 2),
+    (moe.Ffn("quick_gelu", 7.0, 1.0), 2),  # gpt-oss
+    (moe.Ffn("situ", None, 0.0, 6.0), 2),  # SiTU-GLU with its soft cap
+    (moe.Ffn("gelu_tanh", 3.0, 0.5, 5.0), 2),
+    (moe.Ffn("sigmoid", 0.0), 2),  # a clamp at 0: every up at the limit or beyond
+    (moe.Ffn("relu2"), 1),
+    (moe.Ffn("gelu", 4.0, 0.0, 3.0), 1),
+    (moe.Ffn("softplus"), 1),
+    (moe.Ffn("tanh", None, 0.0, 2.0), 1),
+    (moe.Ffn("relu", 2.0), 1),
+]
+
+
+def _torch_units(ffn, pt, wt):
+    """weighted_units in torch float64: mlp.activate (layers/mlp.py:20-35), with
+    maximum/minimum for the clip (their gradients 0.5 at a tie, as jax's)."""
+    up = pt[..., 0]
+    if ffn.limit is not None:
         lim = torch.tensor(ffn.limit, dtype=torch.float64)
         up = torch.minimum(torch.maximum(up, -lim), lim)
-        gate = torch.minimum(gate, lim)
-    alpha = 1.0 if ffn.activation == "swish" else moe.QUICK_GELU_ALPHA
-    h = gate * torch.sigmoid(alpha * gate) * (up + ffn.up_offset) * wt[:, None]
-    np.testing.assert_allclose(bf16.to_f32(moe.weighted_units(ffn, p, w)), h.detach().numpy(), rtol=8e-3, atol=1e-6)
+    if ffn.up_softcap is not None:
+        up = ffn.up_softcap * torch.tanh(up / ffn.up_softcap)
+    act = TORCH_ACTS[ffn.activation]
+    if pt.shape[-1] == 1:
+        return act(up) * wt[:, None]
+    gate = pt[..., 1]
+    if ffn.limit is not None:
+        gate = torch.minimum(gate, torch.tensor(ffn.limit, dtype=torch.float64))
+    return act(gate) * (up + ffn.up_offset) * wt[:, None]
+
+
+@pytest.mark.parametrize("ffn,p", FFNS)
+def test_the_activations_gradient_is_autograds(ffn, p):
+    rng = np.random.default_rng(9)
+    m, f = 64, 48
+    pr = bf16.to_bf16((rng.standard_normal((m, f, p)) * 4).astype(np.float32))
+    if ffn.limit is not None:  # ties with the clamp, both signs
+        pr.reshape(-1)[:8] = bf16.to_bf16(np.array([1, -1, 1, -1, 2, -2, 0.5, 0], np.float32) * ffn.limit)
+    w = bf16.to_bf16(rng.random(m).astype(np.float32))
+    dh = bf16.to_bf16(rng.standard_normal((m, f)).astype(np.float32))
+    dp, dw = moe.weighted_units_backward(ffn, pr, w, dh)
+    pt = torch.tensor(bf16.to_f32(pr), dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(bf16.to_f32(w), dtype=torch.float64, requires_grad=True)
+    h = _torch_units(ffn, pt, wt)
+    np.testing.assert_allclose(bf16.to_f32(moe.weighted_units(ffn, pr, w)), h.detach().numpy(),
+                               rtol=8e-3, atol=1e-6)
     h.backward(torch.tensor(bf16.to_f32(dh), dtype=torch.float64))
     np.testing.assert_allclose(bf16.to_f32(dp), pt.grad.numpy(), rtol=8e-3, atol=1e-5)
     np.testing.assert_allclose(bf16.to_f32(dw), wt.grad.numpy(), rtol=8e-3, atol=1e-4)
 
 
-def test_the_sorted_layer_is_the_dense_one_with_gradients():
+def test_a_plain_ffn_takes_its_projection_with_or_without_the_last_axis():
+    rng = np.random.default_rng(11)
+    pr = bf16.to_bf16(rng.standard_normal((16, 32, 1)).astype(np.float32))
+    w = bf16.to_bf16(rng.random(16).astype(np.float32))
+    dh = bf16.to_bf16(rng.standard_normal((16, 32)).astype(np.float32))
+    ffn = moe.Ffn("relu2")
+    np.testing.assert_array_equal(moe.weighted_units(ffn, pr, w), moe.weighted_units(ffn, pr[..., 0], w))
+    a, b = moe.weighted_units_backward(ffn, pr, w, dh), moe.weighted_units_backward(ffn, pr[..., 0], w, dh)
+    np.testing.assert_array_equal(a[0][..., 0], b[0])
+    np.testing.assert_array_equal(a[1], b[1])
+
+
+DENSE = [
+    # (ffn, p, biased)
+    (moe.Ffn("quick_gelu", 7.0, 1.0), 2, False),
+    (moe.Ffn("quick_gelu", 7.0, 1.0), 2, True),  # gpt-oss: clamped, with biases
+    (moe.Ffn("relu2"), 1, False),
+    (moe.Ffn("gelu", None, 0.0, 3.0), 1, True),
+]
+
+
+@pytest.mark.parametrize("ffn,p,biased", DENSE)
+def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased):
     """``sorted`` equals ``dense`` with gradients (tests/test_moe.py:475-484): the
     oracle's layer, in bfloat16 ("compute"), against every token through each of its
-    experts one by one, differentiated by torch.autograd in float64."""
+    experts one by one, differentiated by torch.autograd in float64; gated or plain,
+    with the experts' up and down biases (moe.py:857-870) or without."""
     rng = np.random.default_rng(10)
     t, k, e, d, f = 48, 2, 5, 32, 24
-    ffn = moe.Ffn("quick_gelu", 7.0, 1.0)
     z = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
     idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)])
     w = bf16.to_bf16(rng.random((t, k)).astype(np.float32))
-    up = bf16.to_bf16((rng.standard_normal((e, d, f, 2)) * 0.3).astype(np.float32))
+    up = bf16.to_bf16((rng.standard_normal((e, d, f, p)) * 0.3).astype(np.float32))
     down = bf16.to_bf16((rng.standard_normal((e, f, d)) * 0.3).astype(np.float32))
     dy = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
-    y, saved = moe.layer_forward(z, idx, w, up, down, ffn, fmt="compute")
-    grads = moe.layer_backward(saved, dy, z, up, down, k, ffn, fmt="compute")
+    ub = bf16.to_bf16((rng.standard_normal((e, f, p))).astype(np.float32)) if biased else None
+    db = bf16.to_bf16((rng.standard_normal((e, d))).astype(np.float32)) if biased else None
+    y, saved = moe.layer_forward(z, idx, w, up, down, ffn, fmt="compute", up_bias=ub, down_bias=db)
+    grads = moe.layer_backward(saved, dy, z, up, down, k, ffn, fmt="compute", up_bias=ub,
+                               down_bias=db)
 
     def tensor(a):
         return torch.tensor(bf16.to_f32(a), dtype=torch.float64, requires_grad=True)
 
     zt, wt, upt, downt = tensor(z), tensor(w), tensor(up), tensor(down)
+    ubt, dbt = (tensor(ub), tensor(db)) if biased else (None, None)
     out = torch.zeros(t, d, dtype=torch.float64)
     for tok in range(t):
         for j in range(k):
             g = int(idx[tok, j])
-            p = zt[tok] @ upt[g].reshape(d, 2 * f)
-            u, gate = p.reshape(f, 2)[:, 0], p.reshape(f, 2)[:, 1]
-            u, gate = torch.clamp(u, -7.0, 7.0), torch.clamp(gate, max=7.0)
-            h = gate * torch.sigmoid(moe.QUICK_GELU_ALPHA * gate) * (u + 1.0) * wt[tok, j]
-            out = out.index_add(0, torch.tensor([tok]), (h @ downt[g])[None])
+            pr = zt[tok] @ upt[g].reshape(d, p * f)
+            if biased:
+                pr = pr + ubt[g].reshape(p * f)
+            h = _torch_units(ffn, pr.reshape(1, f, p), wt[tok, j].reshape(1))[0]
+            row = h @ downt[g]
+            if biased:
+                row = row + dbt[g] * wt[tok, j]
+            out = out.index_add(0, torch.tensor([tok]), row[None])
     out.backward(torch.tensor(bf16.to_f32(dy), dtype=torch.float64))
 
     def close(got, want, rtol):
-        got, want = bf16.to_f32(got).astype(np.float64), want.detach().numpy()
+        got = bf16.to_f32(got).astype(np.float64) if got.dtype == np.uint16 else got
+        want = want.detach().numpy()
         err = np.linalg.norm(got - want) / np.linalg.norm(want)
         assert err < rtol, err
 
@@ -387,3 +479,31 @@ def test_the_sorted_layer_is_the_dense_one_with_gradients():
     close(grads["weights"], wt.grad, 2e-2)
     close(grads["up"], upt.grad, 2e-2)
     close(grads["down"], downt.grad, 2e-2)
+    if biased:
+        close(grads["up_bias"], ubt.grad, 2e-2)
+        close(grads["down_bias"], dbt.grad, 2e-2)
+
+
+def test_the_layer_with_no_pass_in_mxfp8_is_the_compute_layer_and_all_passes_the_default():
+    """passes=() multiplies everything in bfloat16: fmt "compute", bit for bit; all
+    three passes are the default (grouped_blockscaled.py:167-211)."""
+    rng = np.random.default_rng(12)
+    t, k, e, d, f = 40, 2, 4, 64, 32
+    z = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
+    idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)])
+    w = bf16.to_bf16(rng.random((t, k)).astype(np.float32))
+    up = bf16.to_bf16((rng.standard_normal((e, d, f, 2)) * 0.3).astype(np.float32))
+    down = bf16.to_bf16((rng.standard_normal((e, f, d)) * 0.3).astype(np.float32))
+    dy = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
+    runs = {}
+    for name, fmt, passes in (("compute", "compute", None), ("none", "mxfp8", ()),
+                              ("all", "mxfp8", moe.PASSES), ("default", "mxfp8", None)):
+        y, saved = moe.layer_forward(z, idx, w, up, down, fmt=fmt, passes=passes)
+        runs[name] = (y, moe.layer_backward(saved, dy, z, up, down, k, fmt=fmt))
+    for a, b in (("compute", "none"), ("all", "default")):
+        np.testing.assert_array_equal(runs[a][0], runs[b][0])
+        for key in runs[a][1]:
+            np.testing.assert_array_equal(runs[a][1][key], runs[b][1][key])
+    assert not np.array_equal(runs["none"][0], runs["all"][0])
+
+
