@@ -58,6 +58,39 @@ def inputs(t, d, e, k, f, device, seed=SEED):
             dy.to(bf))
 
 
+def zipf_picks(t, e, k, seed, s=1.2, empty=0.2):
+    """Config 5's picks, built from their loads: Zipf(s) shares over a seeded permutation
+    of the experts, the last `empty` fraction of the ranks given none; each expert's
+    load is its share of the t k picks, capped at t (a token picks k distinct experts,
+    so no expert holds more than 1/k of them: 12.5% at k = 8), the cut spread over the
+    others by their shares, rounded by largest remainders to sum to t k. The picks are
+    laid out expert after expert and dealt to tokens round-robin (pick j to token j mod
+    t), which gives every token k distinct experts since no load exceeds t; the tokens
+    are then shuffled. Returns idx (t, k) int32 and the loads (e,)."""
+    rng = np.random.default_rng(seed)
+    ranked = rng.permutation(e)
+    live = e - int(round(e * empty))
+    share = np.zeros(e)
+    share[ranked[:live]] = np.arange(1, live + 1, dtype=np.float64) ** -s
+    total, capped = t * k, np.zeros(e, bool)
+    while True:  # cap the experts whose share of what is left passes t; repeat
+        scale = (total - t * capped.sum()) / share[~capped].sum()
+        over = ~capped & (share * scale > t)
+        if not over.any():
+            break
+        capped |= over
+    want = np.where(capped, float(t), share * scale)
+    loads = np.floor(want).astype(np.int64)
+    short = total - int(loads.sum())
+    loads[np.argsort(-(want - loads), kind="stable")[:short]] += 1
+    assert loads.sum() == total and loads.max() <= t
+    seq = np.repeat(np.arange(e), loads)
+    idx = np.empty((t, k), np.int64)
+    idx[np.arange(total) % t, np.arange(total) // t] = seq
+    idx = idx[rng.permutation(t)]
+    return idx.astype(np.int32), loads
+
+
 def gemm_flops(m, d, f):
     """The six GEMMs' algorithmic FLOP of one fwd+bwd: 2 M K N each."""
     up = 2 * m * d * 2 * f
@@ -232,47 +265,54 @@ def fused_up(z, idx, w, up, e, k):
             "used_in_step": "unfused"}
 
 
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bfloat16 MFMA
+
 # The other configs of BASELINE.json, forward only there: (tokens, width, experts, picks,
-# units, activation (kind, limit, up offset), seed, router skew).
+# units, activation (kind, limit, up offset), seed, router skew, format, the CPU
+# oracle's sample (tokens, experts): None for the whole config).
 OTHER_CONFIGS = {
-    "config 2: Qwen3-30B-A3B layer forward": (16384, 2048, 128, 8, 768, ("swish", None, 0.0), 1, None),
+    "config 1: tiny bf16 layer forward": (
+        4096, 256, 8, 2, 512, ("swish", None, 0.0), 0, None, "compute", None),
+    "config 2: Qwen3-30B-A3B layer forward": (
+        16384, 2048, 128, 8, 768, ("swish", None, 0.0), 1, None, "mxfp8", (1024, 8)),
     "config 4: gpt-oss-120b layer forward (clamped SwiGLU)": (
-        8192, 2880, 128, 4, 2880, ("quick_gelu", 7.0, 1.0), 2, "bias"),
+        8192, 2880, 128, 4, 2880, ("quick_gelu", 7.0, 1.0), 2, "bias", "mxfp8", (256, 4)),
     "config 5: DeepSeek-V3 layer forward (Zipf loads)": (
-        8192, 7168, 256, 8, 2048, ("swish", None, 0.0), 3, "zipf"),
+        8192, 7168, 256, 8, 2048, ("swish", None, 0.0), 3, "zipf", "mxfp8", (128, 8)),
 }
 
 
-def other_config(t, d, e, k, f, act, seed, skew, device, reps=10):
+def other_config(t, d, e, k, f, act, seed, skew, fmt, sample, device, reps=10):
     """One config's MXFP8 forward (the layer as training runs it: x^T and h^T quantized
     for the wgrad too), timed as HIP graph replays, with the weights quantized inside
     (`ms`) and given already in MXFP8 (`ms_weights_given`: the reference's `quantized`,
     quantized once an optimizer step). Router logits N(0,1), plus a
-    per-expert bias N(0, 0.5) (config 4) or a Zipf(1.2) bias over a permutation of the
-    experts with the last fifth receiving none (config 5); softmax, top-k, normalised."""
+    per-expert bias N(0, 0.5) (config 4), softmax, top-k, normalised; config 5's picks
+    built from Zipf(1.2) loads (`zipf_picks`), each token's k weights a softmax of
+    N(0, 1) draws."""
     from bux_amd import moe
 
     g = torch.Generator(device=device).manual_seed(seed)
     z = torch.randn(t, d, generator=g, device=device)
     outliers = torch.randperm(t * d, generator=g, device=device)[: max(1, t * d // 1000)]
     z.view(-1)[outliers] *= 100
-    logits = torch.randn(t, e, generator=g, device=device)
-    if skew == "bias":
-        logits += torch.randn(e, generator=g, device=device) * 0.5
-    elif skew == "zipf":
-        order = torch.randperm(e, generator=g, device=device)
-        rank = torch.empty(e, device=device)
-        rank[order] = torch.arange(1, e + 1, device=device, dtype=torch.float32)
-        logits += -1.2 * torch.log(rank)
-        logits[:, order[-e // 5:]] = -float("inf")
-    weights, idx = torch.topk(torch.softmax(logits, -1), k, -1)
-    weights = (weights / weights.sum(-1, keepdim=True)).to(torch.bfloat16)
+    if skew == "zipf":
+        picks, _ = zipf_picks(t, e, k, seed)
+        idx = torch.from_numpy(picks).to(device)
+        weights = torch.softmax(torch.randn(t, k, generator=g, device=device), -1)
+    else:
+        logits = torch.randn(t, e, generator=g, device=device)
+        if skew == "bias":
+            logits += torch.randn(e, generator=g, device=device) * 0.5
+        weights, idx = torch.topk(torch.softmax(logits, -1), k, -1)
+        weights = weights / weights.sum(-1, keepdim=True)
+        del logits
+    weights = weights.to(torch.bfloat16)
     idx = idx.to(torch.int32).contiguous()
     up = (torch.randn(e, d, f, 2, generator=g, device=device) * 0.02).to(torch.bfloat16)
     down = (torch.randn(e, f, d, generator=g, device=device) * 0.02).to(torch.bfloat16)
     z = z.to(torch.bfloat16)
     ffn = moe.Ffn(*act)
-    del logits
 
     def graph_ms(forward):
         side = torch.cuda.Stream()
@@ -292,19 +332,23 @@ def other_config(t, d, e, k, f, act, seed, skew, device, reps=10):
         torch.cuda.synchronize()
         return (time.perf_counter() - start) * 1e3 / reps
 
-    ms = graph_ms(lambda: moe.experts_forward(z, idx, weights, up, down, ffn))
-    given = moe.in_mxfp8(up, down)
-    ms_given = graph_ms(lambda: moe.experts_forward(z, idx, weights, up, down, ffn, quantized=given))
+    ms = graph_ms(lambda: moe.experts_forward(z, idx, weights, up, down, ffn, fmt))
     loads = torch.bincount(idx.view(-1).long(), minlength=e)
     m = t * k
     flops = 2 * m * d * 2 * f + 2 * m * f * d
-    return {"ms": round(ms, 4), "gemm_tflop": round(flops / 1e12, 4),
-            "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
-            "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_MXFP8_TFLOPS, 4),
-            "ms_weights_given": round(ms_given, 4),
-            "tflops_weights_given": round(flops / (ms_given * 1e-3) / 1e12, 1),
-            "largest_group_share": round(float(loads.max()) / m, 4),
-            "empty_experts": int((loads == 0).sum())}
+    peak = PEAK_MXFP8_TFLOPS if fmt != "compute" else PEAK_BF16_TFLOPS
+    out = {"format": fmt, "ms": round(ms, 4), "gemm_tflop": round(flops / 1e12, 4),
+           "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+           "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / peak, 4), "peak_tflops": peak}
+    if fmt != "compute":
+        given = moe.in_mxfp8(up, down)
+        ms_given = graph_ms(lambda: moe.experts_forward(z, idx, weights, up, down, ffn, fmt,
+                                                        quantized=given))
+        out.update(ms_weights_given=round(ms_given, 4),
+                   tflops_weights_given=round(flops / (ms_given * 1e-3) / 1e12, 1))
+    out.update(largest_group_share=round(float(loads.max()) / m, 4),
+               empty_experts=int((loads == 0).sum()))
+    return out
 
 
 def other_configs(device):
@@ -318,6 +362,38 @@ def other_configs(device):
         except (RuntimeError, torch.OutOfMemoryError) as err:
             out[name] = {"error": str(err)[:200]}
         torch.cuda.empty_cache()
+    return out
+
+
+def config_cpu_baselines():
+    """The CPU oracle's forward on each other config: the whole of config 1, and for the
+    others a bounded sample of the same per-expert shape (a few experts, their share of
+    the tokens), timed on this host's cores."""
+    from oracle import bf16, moe as omoe
+
+    out = {}
+    for name, (t, d, e, k, f, act, seed, _, fmt, sample) in OTHER_CONFIGS.items():
+        ts, es = (t, e) if sample is None else sample
+        rng = np.random.default_rng(seed)
+
+        def bits(shape, scale):
+            return bf16.to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+        z, up, down = bits((ts, d), 1.0), bits((es, d, f, 2), 0.02), bits((es, f, d), 0.02)
+        idx = np.stack([rng.choice(es, k, replace=False) for _ in range(ts)]).astype(np.int32)
+        w = bf16.to_bf16((rng.random((ts, k)) / k).astype(np.float32))
+        start = time.perf_counter()
+        omoe.layer_forward(z, idx, w, up, down, omoe.Ffn(*act), fmt)
+        seconds = time.perf_counter() - start
+        m = ts * k
+        flops = 2 * m * d * 2 * f + 2 * m * f * d
+        out[name] = {"value": round(flops / seconds / 1e12, 5), "unit": "TFLOP/s",
+                     "cores": len(os.sched_getaffinity(0)), "kind": "port",
+                     "sample": ("the whole config" if sample is None else
+                                f"{ts} tokens x top-{k} over {es} experts of d={d} f={f}")
+                               + f", oracle forward ({fmt}), {flops / 1e9:.1f} GFLOP in "
+                                 f"{seconds:.2f} s"}
+        log(f"cpu {name}: {out[name]}")
     return out
 
 
@@ -462,6 +538,9 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline: oracle on a sample of config 3 ...")
         result["cpu_baseline"] = cpu_baseline()
+        if "other_configs" in result:
+            for name, cpu in config_cpu_baselines().items():
+                result["other_configs"][name]["cpu_baseline"] = cpu
     print(json.dumps(result), flush=True)
 
 

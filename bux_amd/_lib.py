@@ -49,9 +49,9 @@ SIGNATURES = {
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
     "bux_mx_grouped_tiles": (_int, [_p, _i32, _i64, _i64, _p, _size, _p]),
     "bux_mx_grouped_rows_listed": (
-        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p]),
+        _int, [_p, _p, _p, _p, _p, _size, _i32, _i64, _i64, _i64, _i64, _int, _p, _p]),
     "bux_mx_grouped_contract_listed": (
-        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _int, _p, _p]),
+        _int, [_p, _p, _p, _p, _p, _size, _i32, _i64, _i64, _i64, _int, _p, _p]),
     "bux_mx_grouped_rows_noalloc": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p]),
     "bux_mx_grouped_contract_workspace_size": (_size, [_i32]),
@@ -92,6 +92,7 @@ BF16, F32 = 0, 1
 ACTIVATIONS = {"swish": 0, "quick_gelu": 1, "relu": 2, "relu2": 3, "gelu": 4, "gelu_tanh": 5,
                "sigmoid": 6, "tanh": 7, "softplus": 8, "situ": 9}
 NOALLOC_SCRATCH_BYTES = 262144
+LIST_MAGIC, LIST_REFUSED = 0x54585542, 1
 ROUTER_SOFTMAX, ROUTER_SIGMOID, ROUTER_SQRTSOFTPLUS = 0, 1, 2
 
 

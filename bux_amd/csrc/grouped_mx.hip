@@ -96,17 +96,34 @@ __device__ int32_t block_scan(int32_t* data, int n, int32_t* partial) {
   return total;
 }
 
+// A tile list (bux_mx_grouped_tiles) opens with a header of LIST_HEADER bytes: LIST_MAGIC,
+// the groups, m and height it was made for, and a status word (LIST_REFUSED once a
+// listed GEMM was called with other dimensions); its group starts follow.
+constexpr int LIST_HEADER = 64;
+constexpr int32_t LIST_MAGIC = BUX_LIST_MAGIC;  // "BUXT"
+constexpr int32_t LIST_REFUSED = BUX_LIST_REFUSED;
+
 // starts[g] for g <= groups (starts[groups] = sum of sizes), then, if `tiles`, the
 // tile list of `slots` entries: each group's rows in tiles of BM from its first row
 // rounded down to a multiple of `align` (a power of two; the last tile partial), then
 // the rows from the sum of sizes to `height` as group `groups`, then empty tiles
 // (0, 0, 0); and the number of tiles listed in starts[groups + 1]. A tile (g, lo, hi)
 // computes rows [lo, lo + BM) and holds rows [max(lo, starts[g]), hi) of group g.
+//
+// With `header` (a tile list's, LIST_HEADER bytes before its starts), the list's
+// dimensions go there too: LIST_MAGIC, groups, m, height, and a 0 status word.
 __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __restrict__ sizes,
                                                            int32_t groups, int64_t height,
                                                            int64_t slots, int32_t align,
                                                            int32_t* __restrict__ starts_out,
-                                                           Tile* __restrict__ tiles) {
+                                                           Tile* __restrict__ tiles,
+                                                           int32_t* __restrict__ header,
+                                                           int64_t m) {
+  if (header != nullptr && threadIdx.x < LIST_HEADER / 4) {
+    const int32_t i = threadIdx.x;
+    header[i] = i == 0 ? LIST_MAGIC : i == 1 ? groups : i == 2 ? static_cast<int32_t>(m)
+              : i == 3 ? static_cast<int32_t>(height) : 0;
+  }
   __shared__ int32_t starts[MAX_GROUPS + 2];
   __shared__ int32_t before[MAX_GROUPS + 2];
   __shared__ int32_t partial[THREADS];
@@ -1127,12 +1144,38 @@ int check_contract(const char* name, const uint8_t* a_values, const uint8_t* a_s
   return BUX_OK;
 }
 
-// A tile list's buffer: the group starts (groups + 2 ints, 256-byte aligned), then the
-// tile records.
-int32_t* starts_in(const void* list) { return static_cast<int32_t*>(const_cast<void*>(list)); }
+// A tile list's buffer: the header (LIST_HEADER bytes), the group starts (groups + 2
+// ints; header and starts 256-byte aligned together), then the tile records.
+int32_t* header_in(const void* list) { return static_cast<int32_t*>(const_cast<void*>(list)); }
+int32_t* starts_in(const void* list) {
+  return reinterpret_cast<int32_t*>(static_cast<uint8_t*>(const_cast<void*>(list)) + LIST_HEADER);
+}
+size_t starts_bytes(int32_t groups) {
+  return align256(LIST_HEADER + static_cast<size_t>(groups + 2) * sizeof(int32_t));
+}
 Tile* tiles_in(const void* list, int32_t groups) {
   return reinterpret_cast<Tile*>(static_cast<uint8_t*>(const_cast<void*>(list)) +
-                                 align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)));
+                                 starts_bytes(groups));
+}
+
+// A listed GEMM's check of its list, one wave before the GEMM: a list made for other
+// dimensions (`m` < 0: any m and height, the contract's) gets the status LIST_REFUSED
+// and is emptied so that the GEMM computes nothing from it: no tiles for the rows GEMM
+// (which then writes nothing), every group empty for the contract (which then writes
+// zeros).
+__global__ __launch_bounds__(64) void list_check_kernel(int32_t* __restrict__ list, int32_t groups,
+                                                        int64_t m, int64_t height) {
+  const bool same = list[0] == LIST_MAGIC && list[1] == groups &&
+                    (m < 0 || (list[2] == static_cast<int32_t>(m) &&
+                               list[3] == static_cast<int32_t>(height)));
+  if (same) return;
+  int32_t* starts = list + LIST_HEADER / 4;
+  if (threadIdx.x == 0) list[4] = LIST_REFUSED;
+  if (m >= 0) {
+    if (threadIdx.x == 0) starts[groups + 1] = 0;  // the rows GEMM's tile count
+  } else {
+    for (int g = threadIdx.x; g <= groups; g += 64) starts[g] = 0;
+  }
 }
 
 int launch_rows_of(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
@@ -1151,13 +1194,13 @@ int launch_rows_of(const uint8_t* a_values, const uint8_t* a_scales, const uint8
 }
 
 int launch_contract_of(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
-                       const uint8_t* b_scales, const void* list, int32_t groups, int64_t d,
+                       const uint8_t* b_scales, const int32_t* starts, int32_t groups, int64_t d,
                        int64_t f, int64_t m, int out_dtype, void* dw, hipStream_t s) {
   // The operands' K is m: each of a's d rows (b's f rows) is m bytes.
   const Operand A{a_values, a_scales, static_cast<int32_t>(m), static_cast<int32_t>(d)};
   const Operand B{b_values, b_scales, static_cast<int32_t>(m), static_cast<int32_t>(f)};
-  return out_dtype == BUX_BF16 ? launch_contract<uint16_t>(A, B, groups, starts_in(list), dw, s)
-                               : launch_contract<float>(A, B, groups, starts_in(list), dw, s);
+  return out_dtype == BUX_BF16 ? launch_contract<uint16_t>(A, B, groups, starts, dw, s)
+                               : launch_contract<float>(A, B, groups, starts, dw, s);
 }
 
 }  // namespace
@@ -1165,8 +1208,7 @@ int launch_contract_of(const uint8_t* a_values, const uint8_t* a_scales, const u
 
 extern "C" size_t bux_mx_grouped_rows_workspace_size(int32_t groups, int64_t m, int64_t height) {
   using namespace bux;
-  return align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)) +
-         static_cast<size_t>(row_slots(groups, m, height)) * sizeof(Tile);
+  return starts_bytes(groups) + static_cast<size_t>(row_slots(groups, m, height)) * sizeof(Tile);
 }
 
 extern "C" int bux_mx_grouped_tiles(const int32_t* sizes, int32_t groups, int64_t m,
@@ -1183,7 +1225,8 @@ extern "C" int bux_mx_grouped_tiles(const int32_t* sizes, int32_t groups, int64_
     return fail(BUX_E_WORKSPACE, "bux_mx_grouped_tiles: list of %zu bytes, %zu needed", list_bytes,
                 need);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, as_stream(stream), sizes, groups,
-                     height, row_slots(groups, m, height), 1, starts_in(list), tiles_in(list, groups));
+                     height, row_slots(groups, m, height), 1, starts_in(list), tiles_in(list, groups),
+                     header_in(list), m);
   return launched("prologue_kernel");
 }
 
@@ -1206,7 +1249,7 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height,
                      row_slots(groups, m, height), 1, starts_in(workspace),
-                     tiles_in(workspace, groups));
+                     tiles_in(workspace, groups), header_in(workspace), m);
   if (int rc = launched("prologue_kernel")) return rc;
   return launch_rows_of(a_values, a_scales, b_values, b_scales, workspace, groups, m, n, k, height,
                         out_dtype, y, s);
@@ -1276,7 +1319,8 @@ extern "C" int bux_mx_grouped_rows_noalloc(const uint8_t* a_values, const uint8_
   if (int rc = scratch_of(&ws)) return rc;
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height,
-                     row_slots(groups, m, height), 1, starts_in(ws), tiles_in(ws, groups));
+                     row_slots(groups, m, height), 1, starts_in(ws), tiles_in(ws, groups),
+                     header_in(ws), m);
   if (int rc = launched("prologue_kernel")) return rc;
   return launch_rows_of(a_values, a_scales, b_values, b_scales, ws, groups, m, n, k, height,
                         out_dtype, y, s);
@@ -1284,18 +1328,26 @@ extern "C" int bux_mx_grouped_rows_noalloc(const uint8_t* a_values, const uint8_
 
 extern "C" int bux_mx_grouped_rows_listed(const uint8_t* a_values, const uint8_t* a_scales,
                                           const uint8_t* b_values, const uint8_t* b_scales,
-                                          const void* list, int32_t groups, int64_t m, int64_t n,
-                                          int64_t k, int64_t height, int out_dtype, void* y,
-                                          void* stream) {
+                                          void* list, size_t list_bytes, int32_t groups,
+                                          int64_t m, int64_t n, int64_t k, int64_t height,
+                                          int out_dtype, void* y, void* stream) {
   using namespace bux;
   clear_error();
   if (int rc = check_rows("bux_mx_grouped_rows_listed", a_values, a_scales, b_values, b_scales,
                           groups, m, n, k, height, out_dtype, y))
     return rc;
   BUX_CHECK(list != nullptr, "bux_mx_grouped_rows_listed: NULL list");
+  const size_t need = bux_mx_grouped_rows_workspace_size(groups, m, height);
+  if (list_bytes < need)
+    return fail(BUX_E_WORKSPACE,
+                "bux_mx_grouped_rows_listed: a list of %zu bytes, not one for groups=%d m=%lld "
+                "height=%lld (%zu bytes)", list_bytes, groups, (long long)m, (long long)height, need);
   if (height == 0) return BUX_OK;
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(list_check_kernel, dim3(1), dim3(64), 0, s, header_in(list), groups, m, height);
+  if (int rc = launched("list_check_kernel")) return rc;
   return launch_rows_of(a_values, a_scales, b_values, b_scales, list, groups, m, n, k, height,
-                        out_dtype, y, as_stream(stream));
+                        out_dtype, y, s);
 }
 
 extern "C" size_t bux_mx_grouped_contract_workspace_size(int32_t groups) {
@@ -1319,31 +1371,39 @@ extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a
                 workspace_bytes, need);
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
-                     static_cast<int32_t*>(workspace), nullptr);
+                     static_cast<int32_t*>(workspace), nullptr, nullptr, 0);
   if (int rc = launched("prologue_kernel")) return rc;
-  return launch_contract_of(a_values, a_scales, b_values, b_scales, workspace, groups, d, f, m,
+  return launch_contract_of(a_values, a_scales, b_values, b_scales,
+                            static_cast<const int32_t*>(workspace), groups, d, f, m,
                             out_dtype, dw, s);
 }
 
 extern "C" int bux_mx_grouped_contract_listed(const uint8_t* a_values, const uint8_t* a_scales,
                                               const uint8_t* b_values, const uint8_t* b_scales,
-                                              const void* list, int32_t groups, int64_t d,
-                                              int64_t f, int64_t m, int out_dtype, void* dw,
-                                              void* stream) {
+                                              void* list, size_t list_bytes, int32_t groups,
+                                              int64_t d, int64_t f, int64_t m, int out_dtype,
+                                              void* dw, void* stream) {
   using namespace bux;
   clear_error();
   if (int rc = check_contract("bux_mx_grouped_contract_listed", a_values, a_scales, b_values,
                               b_scales, groups, d, f, m, out_dtype, dw))
     return rc;
   BUX_CHECK(list != nullptr, "bux_mx_grouped_contract_listed: NULL list");
-  return launch_contract_of(a_values, a_scales, b_values, b_scales, list, groups, d, f, m,
-                            out_dtype, dw, as_stream(stream));
+  if (list_bytes < starts_bytes(groups))
+    return fail(BUX_E_WORKSPACE,
+                "bux_mx_grouped_contract_listed: a list of %zu bytes, not one for groups=%d",
+                list_bytes, groups);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(list_check_kernel, dim3(1), dim3(64), 0, s, header_in(list), groups,
+                     static_cast<int64_t>(-1), static_cast<int64_t>(0));
+  if (int rc = launched("list_check_kernel")) return rc;
+  return launch_contract_of(a_values, a_scales, b_values, b_scales, starts_in(list), groups, d, f,
+                            m, out_dtype, dw, s);
 }
 
 extern "C" size_t bux_mx_grouped_glu_workspace_size(int32_t groups, int64_t height) {
   using namespace bux;
-  return align256(static_cast<size_t>(groups + 2) * sizeof(int32_t)) +
-         static_cast<size_t>(glu_slots(groups, height)) * sizeof(Tile);
+  return starts_bytes(groups) + static_cast<size_t>(glu_slots(groups, height)) * sizeof(Tile);
 }
 
 extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scales,
@@ -1387,7 +1447,7 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
   const int64_t col_tiles = ceil_div(n, BN);
   if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_glu: too many tiles");
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
-                     32, starts, tiles);
+                     32, starts, tiles, nullptr, 0);
   if (int rc = launched("prologue_kernel")) return rc;
   const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(height)};
   const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};

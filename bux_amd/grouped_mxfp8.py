@@ -165,7 +165,7 @@ class TileList(NamedTuple):
     group sizes (the reference's ``tiles_of``, grouped_mxfp8.py:157-182) for every GEMM of
     a step that takes the same sizes."""
 
-    buffer: torch.Tensor  # uint8: the starts, then the tile records
+    buffer: torch.Tensor  # uint8: a header of the dimensions, the starts, the tile records
     groups: int
     m: int  # rows of the rows GEMMs' a
     height: int  # rows of their outputs
@@ -216,8 +216,8 @@ def rows(
             raise ValueError(f"rows: a tile list for {tiles.groups} groups, m={tiles.m}, "
                              f"height={tiles.height}, not {groups}, {m}, {h}")
         _lib.check(lib().bux_mx_grouped_rows_listed(
-            ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(tiles.buffer), groups,
-            m, n, k, h, _DTYPES[out], ptr(y), stream()))
+            ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(tiles.buffer),
+            tiles.buffer.numel(), groups, m, n, k, h, _DTYPES[out], ptr(y), stream()))
         return y
     ws = workspace(lib().bux_mx_grouped_rows_workspace_size(groups, m, h), y.device)
     _lib.check(lib().bux_mx_grouped_rows(
@@ -298,8 +298,8 @@ def contract(
         if tiles.groups != groups:
             raise ValueError(f"contract: a tile list for {tiles.groups} groups, not {groups}")
         _lib.check(lib().bux_mx_grouped_contract_listed(
-            ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(tiles.buffer), groups,
-            d, f, m, _DTYPES[out], ptr(dw), stream()))
+            ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(tiles.buffer),
+            tiles.buffer.numel(), groups, d, f, m, _DTYPES[out], ptr(dw), stream()))
         return dw
     ws = workspace(lib().bux_mx_grouped_contract_workspace_size(groups), dw.device)
     _lib.check(lib().bux_mx_grouped_contract(

@@ -295,6 +295,19 @@ class MxWeights(NamedTuple):
     up_k: Tiled  # each W_up^T along d (the forward's)
     down_n: Tiled  # each W_down along d (the dgrad's)
     down_k: Tiled  # each W_down^T along f (the forward's)
+    fmt: str = "mxfp8"  # the recipe they were quantized by
+    up_shape: tuple = ()  # the kernels they came from: (E, d, f, p)
+    down_shape: tuple = ()  # and (E, f, d)
+
+    def check(self, fmt: str, up: torch.Tensor, down: torch.Tensor) -> None:
+        """Raise unless these are `up` and `down` (by shape) quantized by `fmt`'s recipe."""
+        if fmt not in MX_FORMATS:
+            raise ValueError(f"kernels given in MXFP8, but the GEMMs multiply in {fmt!r}")
+        if self.fmt != fmt:
+            raise ValueError(f"kernels quantized by the {self.fmt!r} recipe, not {fmt!r}'s")
+        if self.up_shape != tuple(up.shape) or self.down_shape != tuple(down.shape):
+            raise ValueError(f"kernels quantized from {self.up_shape} and {self.down_shape}, "
+                             f"not {tuple(up.shape)} and {tuple(down.shape)}")
 
 
 def in_mxfp8(up: torch.Tensor, down: torch.Tensor, fmt: str = "mxfp8") -> MxWeights:
@@ -308,7 +321,7 @@ def in_mxfp8(up: torch.Tensor, down: torch.Tensor, fmt: str = "mxfp8") -> MxWeig
     tiles = fmt == "mxfp8_2d"
     up_n, up_k = grouped_mxfp8.quantized_twice(up.reshape(e, d, f * p), tiles=tiles)
     down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
-    return MxWeights(up_n, up_k, down_n, down_k)
+    return MxWeights(up_n, up_k, down_n, down_k, fmt, tuple(up.shape), tuple(down.shape))
 
 
 PASSES = ("fprop", "dgrad", "wgrad")
@@ -385,12 +398,14 @@ def experts_forward(
     t, k = idx.shape
     e, d, f, p = up.shape
     m = t * k
+    fprop, dgrad, wgrad = passes_of(fmt, passes)
+    if quantized is not None:
+        quantized.check(fmt, up, down)
     with span("permute"):
         s = sort_by_expert(idx, e)
         filled = s.filled
         row_weights = picked_weights(weights, s.order)
     up2 = up.reshape(e, d, f * p)
-    fprop, dgrad, wgrad = passes_of(fmt, passes)
     tiles = fmt == "mxfp8_2d"
     height = grouped_mxfp8.whole(m)
     x_k = x_m = up_n = up_k = h_k = h_m = down_n = down_k = rows = listed = None
@@ -409,8 +424,9 @@ def experts_forward(
             up_n, up_k = quantized.up_n, quantized.up_k
             down_n, down_k = quantized.down_n, quantized.down_k
         else:
-            with span("quantize W"):
+            with span("quantize W_up"):
                 up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
+            with span("quantize W_down"):
                 down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
     h = None
     if (fused and not intermediates and fprop and dgrad and wgrad and up_bias is None

@@ -134,21 +134,27 @@ int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_scales, const 
  * tiles_of (grouped_mxfp8.py:157-182), whose result its rows and contract take as
  * `tiles` and `starts` (:116, :185): the group starts and the ragged tile list of
  * `sizes` for a of m rows and y of `height` rows, into `list`
- * (bux_mx_grouped_rows_workspace_size(groups, m, height) bytes).
+ * (bux_mx_grouped_rows_workspace_size(groups, m, height) bytes). The list opens with a
+ * header of its dimensions: int32 words BUX_LIST_MAGIC, groups, m, height and a status
+ * word, 0 when made.
  * bux_mx_grouped_rows_listed / bux_mx_grouped_contract_listed: bux_mx_grouped_rows /
- * bux_mx_grouped_contract on such a list, made from the same sizes (and, for rows, the
- * same groups, m and height), in place of their own prologue: one list serves every
- * GEMM of a layer's step.
+ * bux_mx_grouped_contract on such a list (`list_bytes` its size), made from the same
+ * sizes (and, for rows, the same groups, m and height), in place of their own
+ * prologue: one list serves every GEMM of a layer's step. A list shorter than those
+ * dimensions need is refused on the host (BUX_E_WORKSPACE); one whose header names
+ * other dimensions is refused on the device: its status word becomes BUX_LIST_REFUSED
+ * and it is emptied, so that the rows GEMM writes nothing and the contract zeros.
  */
+enum { BUX_LIST_MAGIC = 0x54585542, BUX_LIST_REFUSED = 1 };
 int bux_mx_grouped_tiles(const int32_t* sizes, int32_t groups, int64_t m, int64_t height,
                          void* list, size_t list_bytes, void* stream);
 int bux_mx_grouped_rows_listed(const uint8_t* a_values, const uint8_t* a_scales,
-                               const uint8_t* b_values, const uint8_t* b_scales, const void* list,
-                               int32_t groups, int64_t m, int64_t n, int64_t k, int64_t height,
-                               int out_dtype, void* y, void* stream);
+                               const uint8_t* b_values, const uint8_t* b_scales, void* list,
+                               size_t list_bytes, int32_t groups, int64_t m, int64_t n, int64_t k,
+                               int64_t height, int out_dtype, void* y, void* stream);
 int bux_mx_grouped_contract_listed(const uint8_t* a_values, const uint8_t* a_scales,
-                                   const uint8_t* b_values, const uint8_t* b_scales,
-                                   const void* list, int32_t groups, int64_t d, int64_t f,
+                                   const uint8_t* b_values, const uint8_t* b_scales, void* list,
+                                   size_t list_bytes, int32_t groups, int64_t d, int64_t f,
                                    int64_t m, int out_dtype, void* dw, void* stream);
 
 /* bux_mx_grouped_rows_noalloc: bux_mx_grouped_rows with no workspace argument and no

@@ -455,7 +455,8 @@ def layer_backward(
     up_bias: np.ndarray | None = None, down_bias: np.ndarray | None = None,
 ) -> dict[str, np.ndarray]:
     """Return the gradients of `layer_forward`'s output, dy (t, d) bfloat16 bits, to
-    z, the weights, up and down (bfloat16 bits), and to the biases (float64 sums):
+    z, the weights, up and down (bfloat16 bits), to the biases (float64 sums), and
+    between the GEMMs "dh" (m, f) and "dp" (m, p f) (bfloat16 bits):
     grouped_blockscaled._backward (:191-211) for each GEMM, weighted_units' VJP between
     them, and the gathers' and biases' VJPs (moe.py:857-870,1018-1021,1060-1063). The
     passes are the forward's."""
@@ -505,5 +506,5 @@ def layer_backward(
         d_rows_w = bf16.to_bf16(bf16.to_f32(d_rows_w) + extra)
     dz = sum_by_token(dx, s.inverse.reshape(t, k))
     d_weights = d_rows_w[s.inverse].reshape(t, k)
-    grads.update(z=dz, weights=d_weights, up=d_up.reshape(e, d, f, p), down=d_down)
+    grads.update(z=dz, weights=d_weights, up=d_up.reshape(e, d, f, p), down=d_down, dh=dh, dp=dp)
     return grads

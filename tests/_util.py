@@ -72,3 +72,47 @@ def to_gpu_tiled(blocks):
     """Return row-major MXFP8 blocks (the oracle's) on cuda:0, tiled for the GEMMs."""
     from bux_amd import grouped_mxfp8
     return grouped_mxfp8.tiled(to_gpu(blocks.values), to_gpu(blocks.scales))
+
+
+def ulps_apart(got_bits: np.ndarray, want_bits: np.ndarray) -> np.ndarray:
+    """How many bfloat16 steps apart two arrays of bfloat16 bits are, elementwise (±0
+    one value; steps counted through 0 across a sign change)."""
+    def rank(bits):
+        b = bits.astype(np.int64)
+        mag = b & 0x7FFF
+        return np.where(b & 0x8000, -mag, mag)
+    return np.abs(rank(np.asarray(got_bits)) - rank(np.asarray(want_bits)))
+
+
+def e4m3_steps_apart(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """How many E4M3 codes apart two arrays of codes are in value order, elementwise."""
+    def rank(codes):
+        c = codes.astype(np.int64)
+        mag = c & 0x7F
+        return np.where(c & 0x80, -mag, mag)
+    return np.abs(rank(got) - rank(want))
+
+
+def attribute_codes(got_codes, got_scales, want_codes, want_scales, got_bits, want_bits):
+    """Attribute the differences between two MXFP8 copies (row-major codes (r, c) and
+    scale bytes (r, c/32)) of two bfloat16 arrays (r, c) to the differences between those
+    arrays. Returns counts; raises AssertionError on a difference with no cause:
+    - a block's scale byte differs only if one of its 32 values differs;
+    - where the scale agrees, a code differs only where its value differs, and then by
+      at most as many codes as its value by bfloat16 steps (E4M3 keeps fewer mantissa
+      bits than bfloat16, so neighbouring values round to the same or neighbouring
+      codes)."""
+    r, c = got_codes.shape
+    val_diff = ulps_apart(got_bits, want_bits)
+    block_diff = (val_diff.reshape(r, c // 32, 32) > 0).any(-1)
+    scale_diff = got_scales != want_scales
+    assert not (scale_diff & ~block_diff).any(), "a scale differs in a block of equal values"
+    same_scale = np.repeat(~scale_diff, 32, axis=1)
+    steps = e4m3_steps_apart(got_codes, want_codes)
+    code_diff = (steps > 0) & same_scale
+    assert not (code_diff & (val_diff == 0)).any(), "a code differs where its value does not"
+    assert (steps[code_diff] <= np.maximum(val_diff[code_diff], 1)).all(), \
+        "a code differs by more steps than its value"
+    return {"values": int((val_diff > 0).sum()), "codes": int(code_diff.sum()),
+            "scales": int(scale_diff.sum()), "max_value_steps": int(val_diff.max(initial=0)),
+            "max_code_steps": int(steps[same_scale].max(initial=0)), "of": int(r * c)}

@@ -219,9 +219,16 @@ def test_tile_lists_reject_bad_arguments(lib):
     assert "list of" in _msg(lib)
     assert lib.bux_mx_grouped_tiles(None, 4, 256, 200, p, need, None) == 1
     assert lib.bux_mx_grouped_tiles(p, 0, 256, 200, p, need, None) == 1 and "groups=0" in _msg(lib)
-    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, None, 4, 256, 128, 128, 200, 0, p, None)
+    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, None, need, 4, 256, 128, 128, 200, 0, p, None)
     assert rc == 1 and "NULL list" in _msg(lib)
-    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, p, 4, 256, 128, 100, 200, 0, p, None)
+    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, p, need, 4, 256, 128, 100, 200, 0, p, None)
     assert rc == 1 and "k=100" in _msg(lib)
-    rc = lib.bux_mx_grouped_contract_listed(p, p, p, p, p, 4, 64, 64, 100, 0, p, None)
+    # a list too short for the dimensions asked: refused before any launch
+    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, p, need, 4, 256, 128, 128, 4096, 0, p, None)
+    assert rc == 2 and "height=4096" in _msg(lib)
+    rc = lib.bux_mx_grouped_rows_listed(p, p, p, p, p, need, 64, 256, 128, 128, 200, 0, p, None)
+    assert rc == 2 and "groups=64" in _msg(lib)
+    rc = lib.bux_mx_grouped_contract_listed(p, p, p, p, p, need, 4, 64, 64, 100, 0, p, None)
     assert rc == 1 and "m=100" in _msg(lib)
+    rc = lib.bux_mx_grouped_contract_listed(p, p, p, p, p, 16, 4, 64, 64, 128, 0, p, None)
+    assert rc == 2 and "16 bytes" in _msg(lib)

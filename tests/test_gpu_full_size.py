@@ -15,14 +15,13 @@ whatever the size.
 
 Inputs follow the configs: config 4's router logits carry a per-expert bias of
 N(0, 0.5) and its activation is the clamped SwiGLU (limit 7, up offset 1); config 5's
-loads are skewed by a Zipf(1.2) bias over a permutation of the experts, with a fifth of
-them receiving no tokens."""
-
-import math
+picks are built from Zipf(1.2) loads over a permutation of the experts, a fifth of them
+(51) receiving none and none more than 1/k of the picks (bench.zipf_picks)."""
 
 import pytest
 import torch
 
+from bench import zipf_picks
 from tests._util import announce
 
 pytestmark = pytest.mark.gpu
@@ -42,18 +41,18 @@ def _inputs(cfg, seed):
     z = torch.randn(t, d, generator=g, device=dev)
     hot = torch.randint(0, z.numel(), (z.numel() // 1000,), generator=g, device=dev)
     z.view(-1)[hot] *= 100
-    logits = torch.randn(t, e, generator=g, device=dev)
-    if cfg["skew"] == "bias":
-        logits += torch.randn(e, generator=g, device=dev) * 0.5
-    elif cfg["skew"] == "zipf":
-        order = torch.randperm(e, generator=g, device=dev)
-        rank = torch.empty(e, device=dev)
-        rank[order] = torch.arange(1, e + 1, device=dev, dtype=torch.float32)
-        logits += -1.2 * torch.log(rank)
-        logits[:, order[-e // 5:]] = -math.inf  # the last fifth receive nothing
-    top = torch.topk(torch.softmax(logits, -1), k, -1)
-    idx = top.indices.to(torch.int32)
-    w = (top.values / top.values.sum(-1, keepdim=True)).to(torch.bfloat16)
+    if cfg["skew"] == "zipf":  # the loads built directly, as bench.py builds them
+        picks, loads = zipf_picks(t, e, k, seed)
+        assert (loads == 0).sum() == e // 5 and loads.max() <= t
+        idx = torch.from_numpy(picks).to(dev)
+        w = torch.softmax(torch.randn(t, k, generator=g, device=dev), -1).to(torch.bfloat16)
+    else:
+        logits = torch.randn(t, e, generator=g, device=dev)
+        if cfg["skew"] == "bias":
+            logits += torch.randn(e, generator=g, device=dev) * 0.5
+        top = torch.topk(torch.softmax(logits, -1), k, -1)
+        idx = top.indices.to(torch.int32)
+        w = (top.values / top.values.sum(-1, keepdim=True)).to(torch.bfloat16)
     up = (torch.randn(e, d, f, 2, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     down = (torch.randn(e, f, d, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     dy = (torch.randn(t, d, generator=g, device=dev) * 0.01).to(torch.bfloat16)

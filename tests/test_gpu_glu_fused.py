@@ -133,3 +133,54 @@ def test_layer_with_the_fused_up_gemm_is_bit_identical(lib, t, k, e, d, f, act):
     _same("y", o0, o1)
     for key in g0:
         _same(f"d{key}", g0[key], g1[key])
+
+
+@pytest.mark.parametrize("case", [0, 1, 5])
+def test_fused_up_gemm_against_the_oracle(lib, case):
+    """The fused kernel's outputs against the oracle run on its own from the same bits
+    (x and the kernels quantized by the oracle's quantizer, which the GPU's matches bit
+    for bit): the product within the north star's bar; h's copies E4M3 code for code,
+    every code or scale that differs attributed to a bfloat16 step between the GPU's h
+    (the unfused kernels', bit for bit the fused kernel's) and the oracle's."""
+    from bux_amd import grouped_mxfp8 as gm, moe
+    from oracle import bf16, moe as omoe, mxfp8 as omx
+    from tests._util import attribute_codes, bf16_bits, rel_err, untiled
+    spec, rows, d, f, act = CASES[case]
+    rng = np.random.default_rng(80 + case)
+    sizes_np = _sizes(spec, rows, 64, rng)
+    announce("glu fused vs oracle", case)
+    torch.manual_seed(80 + case)
+    dev = torch.device("cuda")
+    groups, height, filled = len(sizes_np), gm.whole(rows), int(sizes_np.sum())
+    x = (torch.randn(rows, d, device=dev) * 2.0).to(torch.bfloat16)
+    w_up = (torch.randn(groups, d, 2 * f, device=dev) * 0.05).to(torch.bfloat16)
+    weights = torch.rand(rows, device=dev).to(torch.bfloat16)
+    sizes = torch.tensor(sizes_np, dtype=torch.int32, device=dev)
+    filled_t = torch.tensor([filled], dtype=torch.int32, device=dev)
+    x_k, _ = gm.quantized_twice(x, filled_t, False, height=height)
+    _, up_k = gm.quantized_twice(w_up)
+    ffn = moe.Ffn(*ACTS[act])
+    product, h_k, h_m = gm.activated(x_k, up_k, sizes, weights, ffn.struct(True), rows)
+    _, _, h = moe.weighted_units_quantized(ffn, product.view(rows, f, 2), weights, filled_t, height,
+                                           keep=True)
+    torch.cuda.synchronize()
+    xb, wb, rw = bf16_bits(x), bf16_bits(w_up), bf16_bits(weights)
+    ox_k, _ = omx.quantized_twice(xb, filled, True, height=height)
+    _, oup_k = omx.quantized_twice(wb, d)
+    want = omoe.rows_mx(ox_k, oup_k, sizes_np, height=rows)
+    err = rel_err(bf16.to_f32(bf16_bits(product)), bf16.to_f32(want))
+    o = omoe.Ffn(*ACTS[act])
+    oh = np.zeros((rows, f), np.uint16)
+    oh[:filled] = omoe.weighted_units(o, want[:filled].reshape(filled, f, 2), rw[:filled])
+    gh = bf16_bits(h)
+    want_k, want_m = omx.quantized_twice(oh, filled, True, height=height)
+    gpad, opad = np.zeros((height, f), np.uint16), np.zeros((height, f), np.uint16)
+    gpad[:rows], opad[:rows] = gh, oh
+    v, sc = untiled(h_k, f)
+    along = attribute_codes(v, sc, want_k.values, want_k.scales, gpad, opad)
+    v, sc = untiled(h_m, height)
+    across = attribute_codes(v, sc, want_m.values, want_m.scales, gpad.T, opad.T)
+    print(f"[fused] case {case} product {err:.2e} h codes {along} h^T codes {across}", flush=True)
+    assert err <= 1e-3
+    for c in (along, across):
+        assert c["codes"] <= 0.02 * c["of"], c

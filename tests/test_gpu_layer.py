@@ -6,14 +6,15 @@ and rounds once: the two agree to a bfloat16 rounding (XLA's own rounding inside
 fused chain is not observable without jax: parity at bit level is unpinned). In the
 layer, every GEMM meets the north star's bar, ||y - y_ref|| / ||y_ref|| <= 1e-3, on the
 GPU's own inputs to it, and the quantizer is bit-exact on the GPU's own activations;
-end to end, see END_TO_END."""
+end to end, see END_TO_END and the attribution test."""
 
 import numpy as np
 import pytest
 import torch
 
 from oracle import bf16, moe as omoe
-from tests._util import announce, bf16_bits, normal_bf16, rel_err, to_gpu, to_gpu_bf16, untiled
+from tests._util import (announce, attribute_codes, bf16_bits, normal_bf16, rel_err, to_gpu,
+                         to_gpu_bf16, ulps_apart, untiled)
 
 pytestmark = pytest.mark.gpu
 
@@ -126,11 +127,22 @@ LAYERS = [
 # End to end, two float implementations of a quantized pipeline differ by more than
 # their GEMMs do: a GEMM's float32 sum that differs in its last bits (the block-scaled
 # MFMA does not add in IEEE float32 order) flips, now and then, the bfloat16 rounding of
-# an activation, and that flips its E4M3 code downstream, a step of 1/16. Measured
-# end-to-end differences are a few 1e-3; the stage-wise checks below hold each GEMM to
-# the 1e-3 bar on identical inputs.
-END_TO_END = 1e-2
+# an activation, and that flips its E4M3 code downstream, a step of 1/16.
+# test_the_layers_drift_from_the_oracle_is_attributed checks that chain link by link
+# and measures 1.1e-3 to 2.3e-3 end to end; the stage-wise checks below hold each GEMM
+# to the 1e-3 bar on identical inputs.
+END_TO_END = 3e-3
 STAGE = 1e-3
+# The attribution test's bounds, from its measured values with margin: the share of
+# elements that differ (measured 1.1-1.2% for the GEMM outputs, 1.2-2.1% for h and dp),
+# a GEMM output by at most a bfloat16 step of itself or FLOOR of the array's largest
+# magnitude (near 0 a float32 sum's last bits flip signs and bfloat16 steps are tiny);
+# the share of E4M3 codes that differ (measured 0.15-0.18%); and the end-to-end error
+# those leave (measured 1.1e-3 to 2.3e-3).
+SHARE_APART = {"projected": 0.02, "h": 0.03, "dh": 0.02, "dp": 0.03}
+FLOOR = 2.0 ** -12
+CODE_SHARE = 0.005
+END_TO_END_ATTRIBUTED = 3e-3
 
 
 def _f32(t):
@@ -294,3 +306,93 @@ def test_a_layer_of_one_token(lib):
     _stage("one token y", _f32(out), bf16.to_f32(want), END_TO_END)
     for key in ("z", "weights", "up", "down"):
         _stage(f"one token d{key}", _f32(grads[key]), bf16.to_f32(wgrads[key]), END_TO_END)
+
+
+@pytest.mark.parametrize("name,t,k,e,d,f,act", [
+    ("small", 1024, 4, 16, 256, 256, "swiglu"), ("gptoss_like", 256, 4, 8, 1440, 1440, "clamped"),
+    ("config3_slice", 2048, 8, 16, 2048, 768, "swiglu")])
+def test_the_layers_drift_from_the_oracle_is_attributed(lib, name, t, k, e, d, f, act):
+    """The GPU layer and the oracle's, each run on its own, drift apart end to end by
+    more than one GEMM does: a float32 sum that differs in its last bits flips the
+    bfloat16 rounding of a product, that moves an activation by a bfloat16 step, that
+    moves its E4M3 code by one, a step of 1/16 downstream. Here each link is checked: the
+    GEMM outputs (projected, dh) differ at a bounded share of elements, each by a
+    rounding; the activation and its gradient (h, dp) by more than a rounding only where
+    their unit's inputs differ; every E4M3 code or scale that differs (h^T's as the GPU
+    wrote it, h's and dp's as the quantizer, bit-exact to the GPU's, makes them) sits at
+    a value that differs, by no more codes than steps; and with those shares, y and every
+    gradient
+    stay within END_TO_END_ATTRIBUTED (3e-3, where a flat bar would need 1e-2 to hold
+without this account of its cause)."""
+    from bux_amd import moe
+    from oracle import mxfp8 as omx
+    o, g = _ffn(act)
+    rng = np.random.default_rng(47)
+    z, idx, w, up, down, dy = _inputs(rng, t, k, e, d, f, None)
+    announce("layer attribution", name)
+    gz, gidx, gw, gup, gdown, gdy = (to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up),
+                                      to_gpu_bf16(down), to_gpu_bf16(dy))
+    out, saved = moe.experts_forward(gz, gidx, gw, gup, gdown, g, intermediates=True)
+    grads = moe.experts_backward(saved, gdy, gup, gdown, g, intermediates=True)
+    torch.cuda.synchronize()
+    want, osaved = omoe.layer_forward(z, idx, w, up, down, o)
+    wgrads = omoe.layer_backward(osaved, dy, z, up, down, k, o)
+    m, filled = t * k, int(osaved.sorted.sizes.sum())
+    hp = -(-m // 128) * 128
+    p = up.shape[-1]
+
+    def apart(got, ref, shape):
+        return ulps_apart(got.reshape(shape)[:filled], ref.reshape(shape)[:filled])
+
+    report = {}
+    # the GEMM outputs: float32 sums in another order, rounded: a bfloat16 step apart
+    # or, near 0 (signs flip, steps are tiny), FLOOR of the largest magnitude
+    steps = {}
+    for what, got, ref, shape in (("projected", bf16_bits(saved.projected), osaved.projected, (m, f, p)),
+                                  ("dh", bf16_bits(grads["dh"]), wgrads["dh"], (m, f))):
+        steps[what] = apart(got, ref, shape)
+        a = bf16.to_f32(got.reshape(shape)[:filled]).astype(np.float64)
+        b = bf16.to_f32(ref.reshape(shape)[:filled]).astype(np.float64)
+        beyond = np.abs(a - b) > np.maximum(np.abs(b) * 2.0 ** -7, FLOOR * np.abs(b).max())
+        report[what] = (float((steps[what] > 0).mean()), int(beyond.sum()))
+    # the activation and its gradient, elementwise from their unit's inputs: more than a
+    # rounding apart only where an input of the unit is apart (up or gate; for dp dh
+    # too), with float32 cancellation allowed below 2^-20 of the largest |dp|
+    unit = (steps["projected"] > 0).any(-1)
+    for what, got, ref, shape, cause in (
+            ("h", bf16_bits(saved.h), osaved.h, (m, f), unit),
+            ("dp", bf16_bits(grads["dp"]), wgrads["dp"], (m, f, p),
+             (unit | (steps["dh"] > 0))[..., None])):
+        st = apart(got, ref, shape)
+        a = bf16.to_f32(got.reshape(shape)[:filled]).astype(np.float64)
+        b = bf16.to_f32(ref.reshape(shape)[:filled]).astype(np.float64)
+        rounding = (st <= 1) | (np.abs(a - b) <= 2.0 ** -20 * np.abs(b).max())
+        report[what] = (float((st > 0).mean()), int((~rounding & ~cause).sum()))
+    # h^T's column copy as the GPU wrote it, against the oracle's
+    hm_v, hm_s = untiled(saved.h_m, hp)
+    _, want_hm = omx.quantized_twice(osaved.h, filled, True, height=hp)
+    h_t = np.zeros((hp, f), np.uint16)
+    h_t[:filled] = bf16_bits(saved.h)[:filled]
+    oh_t = np.zeros((hp, f), np.uint16)
+    oh_t[:filled] = osaved.h[:filled]
+    codes = {"h^T": attribute_codes(hm_v, hm_s, want_hm.values, want_hm.scales, h_t.T, oh_t.T)}
+    for what, got, ref in (("h", bf16_bits(saved.h), osaved.h),
+                           ("dp", bf16_bits(grads["dp"]), wgrads["dp"].reshape(m, -1))):
+        a, _ = omx.quantized_twice(got, filled, True, height=hp)
+        b, _ = omx.quantized_twice(ref, filled, True, height=hp)
+        gb = np.zeros((hp, got.shape[1]), np.uint16)
+        gb[:filled] = got[:filled]
+        rb = np.zeros((hp, got.shape[1]), np.uint16)
+        rb[:filled] = ref[:filled]
+        codes[what] = attribute_codes(a.values, a.scales, b.values, b.scales, gb, rb)
+    errs = {"y": rel_err(_f32(out), bf16.to_f32(want))}
+    for key in ("z", "weights", "up", "down"):
+        errs[key] = rel_err(_f32(grads[key]), bf16.to_f32(wgrads[key]))
+    print(f"[attribution] {name} steps {report} codes {codes} "
+          + " ".join(f"{k_}={v:.2e}" for k_, v in errs.items()), flush=True)
+    for what, (share, beyond) in report.items():
+        assert share <= SHARE_APART[what] and beyond == 0, (what, share, beyond)
+    for what, c in codes.items():
+        assert c["codes"] <= CODE_SHARE * c["of"], (what, c)
+    for key, err in errs.items():
+        assert err <= END_TO_END_ATTRIBUTED, (key, err)
