@@ -739,12 +739,26 @@ __device__ void run_tiles(const Tiles& tiles, int32_t count, const Operand& A, c
 }
 
 // The kernels: one workgroup a CU.
+// Whether the list whose starts are `starts` (its header LIST_HEADER bytes before them)
+// was made for these groups (and, m >= 0, this m and height); if not, workgroup 0 sets
+// its status word to LIST_REFUSED and the caller computes nothing from it.
+__device__ __forceinline__ bool list_fits(const int32_t* starts, int32_t groups, int32_t m,
+                                          int32_t height) {
+  const int32_t* header = starts - LIST_HEADER / 4;
+  const bool fits = header[0] == LIST_MAGIC && header[1] == groups &&
+                    (m < 0 || (header[2] == m && header[3] == height));
+  if (!fits && blockIdx.x == 0 && threadIdx.x == 0)
+    const_cast<int32_t*>(header)[4] = LIST_REFUSED;
+  return fits;
+}
+
 template <typename T>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_kernel(
     Operand A, Operand B, int32_t groups, int32_t n, int32_t height,
     const int32_t* __restrict__ starts, const Tile* __restrict__ tiles, int32_t col_tiles,
     T* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t smem[];
+  if (!list_fits(starts, groups, A.rows, height)) return;
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const RowsTiles list{tiles, groups, n, height, col_tiles, A.k / BK};
   const int32_t count = starts[groups + 1] * col_tiles;
@@ -756,6 +770,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
     Operand A, Operand B, int32_t groups, const int32_t* __restrict__ starts, int32_t d_tiles,
     int32_t f_tiles, T* __restrict__ dw) {
   extern __shared__ __align__(16) uint8_t smem[];
+  if (!list_fits(starts, groups, -1, 0)) return;
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const ContractTiles list{starts, A.rows, B.rows, d_tiles, f_tiles};
   const int32_t count = groups * d_tiles * f_tiles;
@@ -1158,25 +1173,6 @@ Tile* tiles_in(const void* list, int32_t groups) {
                                  starts_bytes(groups));
 }
 
-// A listed GEMM's check of its list, one wave before the GEMM: a list made for other
-// dimensions (`m` < 0: any m and height, the contract's) gets the status LIST_REFUSED
-// and is emptied so that the GEMM computes nothing from it: no tiles for the rows GEMM
-// (which then writes nothing), every group empty for the contract (which then writes
-// zeros).
-__global__ __launch_bounds__(64) void list_check_kernel(int32_t* __restrict__ list, int32_t groups,
-                                                        int64_t m, int64_t height) {
-  const bool same = list[0] == LIST_MAGIC && list[1] == groups &&
-                    (m < 0 || (list[2] == static_cast<int32_t>(m) &&
-                               list[3] == static_cast<int32_t>(height)));
-  if (same) return;
-  int32_t* starts = list + LIST_HEADER / 4;
-  if (threadIdx.x == 0) list[4] = LIST_REFUSED;
-  if (m >= 0) {
-    if (threadIdx.x == 0) starts[groups + 1] = 0;  // the rows GEMM's tile count
-  } else {
-    for (int g = threadIdx.x; g <= groups; g += 64) starts[g] = 0;
-  }
-}
 
 int launch_rows_of(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
                    const uint8_t* b_scales, const void* list, int32_t groups, int64_t m, int64_t n,
@@ -1343,15 +1339,13 @@ extern "C" int bux_mx_grouped_rows_listed(const uint8_t* a_values, const uint8_t
                 "bux_mx_grouped_rows_listed: a list of %zu bytes, not one for groups=%d m=%lld "
                 "height=%lld (%zu bytes)", list_bytes, groups, (long long)m, (long long)height, need);
   if (height == 0) return BUX_OK;
-  hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(list_check_kernel, dim3(1), dim3(64), 0, s, header_in(list), groups, m, height);
-  if (int rc = launched("list_check_kernel")) return rc;
   return launch_rows_of(a_values, a_scales, b_values, b_scales, list, groups, m, n, k, height,
-                        out_dtype, y, s);
+                        out_dtype, y, as_stream(stream));
 }
 
 extern "C" size_t bux_mx_grouped_contract_workspace_size(int32_t groups) {
-  return static_cast<size_t>(groups + 1) * sizeof(int32_t);
+  using namespace bux;
+  return starts_bytes(groups);  // a list of the group starts alone: header, starts
 }
 
 extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a_scales,
@@ -1371,10 +1365,10 @@ extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a
                 workspace_bytes, need);
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
-                     static_cast<int32_t*>(workspace), nullptr, nullptr, 0);
+                     starts_in(workspace), nullptr, header_in(workspace), 0);
   if (int rc = launched("prologue_kernel")) return rc;
-  return launch_contract_of(a_values, a_scales, b_values, b_scales,
-                            static_cast<const int32_t*>(workspace), groups, d, f, m,
+  return launch_contract_of(a_values, a_scales, b_values, b_scales, starts_in(workspace), groups,
+                            d, f, m,
                             out_dtype, dw, s);
 }
 
@@ -1393,12 +1387,8 @@ extern "C" int bux_mx_grouped_contract_listed(const uint8_t* a_values, const uin
     return fail(BUX_E_WORKSPACE,
                 "bux_mx_grouped_contract_listed: a list of %zu bytes, not one for groups=%d",
                 list_bytes, groups);
-  hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(list_check_kernel, dim3(1), dim3(64), 0, s, header_in(list), groups,
-                     static_cast<int64_t>(-1), static_cast<int64_t>(0));
-  if (int rc = launched("list_check_kernel")) return rc;
   return launch_contract_of(a_values, a_scales, b_values, b_scales, starts_in(list), groups, d, f,
-                            m, out_dtype, dw, s);
+                            m, out_dtype, dw, as_stream(stream));
 }
 
 extern "C" size_t bux_mx_grouped_glu_workspace_size(int32_t groups, int64_t height) {

@@ -422,12 +422,9 @@ def experts_forward(
     if fprop or dgrad:
         if quantized is not None:
             up_n, up_k = quantized.up_n, quantized.up_k
-            down_n, down_k = quantized.down_n, quantized.down_k
         else:
             with span("quantize W_up"):
                 up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
-            with span("quantize W_down"):
-                down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
     h = None
     if (fused and not intermediates and fprop and dgrad and wgrad and up_bias is None
             and ffn.fusable(p == 2)):
@@ -451,6 +448,12 @@ def experts_forward(
         else:
             with span("activation"):
                 h = weighted_units(ffn, pv, row_weights, filled)
+    if fprop or dgrad:
+        if quantized is not None:
+            down_n, down_k = quantized.down_n, quantized.down_k
+        else:
+            with span("quantize W_down"):
+                down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
     with span("down fprop"):
         if fprop:
             y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=listed)

@@ -142,8 +142,8 @@ int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_scales, const 
  * sizes (and, for rows, the same groups, m and height), in place of their own
  * prologue: one list serves every GEMM of a layer's step. A list shorter than those
  * dimensions need is refused on the host (BUX_E_WORKSPACE); one whose header names
- * other dimensions is refused on the device: its status word becomes BUX_LIST_REFUSED
- * and it is emptied, so that the rows GEMM writes nothing and the contract zeros.
+ * other dimensions is refused by the GEMM kernel itself as it starts: it writes nothing
+ * and sets the list's status word to BUX_LIST_REFUSED.
  */
 enum { BUX_LIST_MAGIC = 0x54585542, BUX_LIST_REFUSED = 1 };
 int bux_mx_grouped_tiles(const int32_t* sizes, int32_t groups, int64_t m, int64_t height,

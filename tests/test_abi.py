@@ -46,7 +46,8 @@ def test_workspace_sizes(lib):
     assert lib.bux_moe_permute_workspace_size(0, 8) == 2 * 9 * 4
     # group starts, then a tile list: tiles of 256 rows, one more a group at most
     assert lib.bux_mx_grouped_rows_workspace_size(128, 131072, 131072) >= (512 + 128) * 12
-    assert lib.bux_mx_grouped_contract_workspace_size(128) == 129 * 4
+    # a list of the group starts alone: a 64-byte header, then groups + 2 starts
+    assert lib.bux_mx_grouped_contract_workspace_size(128) == 768
 
 
 def _msg(lib) -> str:

@@ -292,9 +292,9 @@ def test_a_tile_list_made_once_serves_every_gemm(lib):
 
 def test_a_tile_list_made_for_other_dimensions_is_refused_on_the_device(lib):
     """A list whose header names other dimensions than the call's (but long enough for
-    them, so the host lets it by) is refused by the listed GEMMs' check: its status word
-    becomes BUX_LIST_REFUSED, the rows GEMM writes nothing (the output keeps what it
-    held) and the contract writes zeros; a matching list's status stays 0."""
+    them, so the host lets it by) is refused by the GEMM kernel as it starts: its status
+    word becomes BUX_LIST_REFUSED and nothing is written (the output keeps what it
+    held); a matching list's status stays 0."""
     from bux_amd import _lib, grouped_mxfp8 as gm
     from bux_amd.kernels import ptr, stream
     rng = np.random.default_rng(32)
@@ -318,7 +318,7 @@ def test_a_tile_list_made_for_other_dimensions_is_refused_on_the_device(lib):
     torch.cuda.synchronize()
     assert int(other.buffer[16:20].view(torch.int32).item()) == _lib.LIST_REFUSED
     assert (kept.float() == 7.0).all()
-    # the contract, called for 4 groups on an 8-group list: zeros
+    # the contract, called for 4 groups on an 8-group list
     third = gm.tiles_of(gs, a.height, height)
     xt = _gpu(_codes(rng, (192, 1024)))
     dt = _gpu(_codes(rng, (128, 1024)))
@@ -328,7 +328,7 @@ def test_a_tile_list_made_for_other_dimensions_is_refused_on_the_device(lib):
         third.buffer.numel(), 4, 192, 128, 1024, _lib.BF16, ptr(dw), stream()))
     torch.cuda.synchronize()
     assert int(third.buffer[16:20].view(torch.int32).item()) == _lib.LIST_REFUSED
-    assert (dw.float() == 0).all()
+    assert (dw.float() == 7.0).all()
     # the good list still serves, its status 0
     y2 = gm.rows(a, b, gs, height=height, tiles=good)
     torch.cuda.synchronize()
