@@ -37,6 +37,22 @@ class FfnStruct(ctypes.Structure):
 
 _ffn = ctypes.POINTER(FfnStruct)
 
+
+class NormStruct(ctypes.Structure):
+    """``bux_norm``: the experts' output norm's settings."""
+
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("affine", ctypes.c_int32),
+        ("zero_centered", ctypes.c_int32),
+        ("scale_input", ctypes.c_int32),
+        ("bias", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+    ]
+
+
+_norm = ctypes.POINTER(NormStruct)
+
 # name -> (restype, argtypes), as include/bux_amd.h declares them.
 SIGNATURES = {
     "bux_last_error": (ctypes.c_char_p, []),
@@ -65,6 +81,11 @@ SIGNATURES = {
     "bux_expert_bias_add": (_int, [_p, _i64, _i64, _p, _p, _i32, _p]),
     "bux_expert_sums": (_int, [_p, _p, _i32, _p, _i64, _i64, _p, _i32, _p, _p]),
     "bux_expert_bias_weight_grad": (_int, [_p, _p, _i32, _i64, _i64, _p, _p, _i32, _p, _p]),
+    "bux_expert_norm_forward": (_int, [_p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p]),
+    "bux_expert_norm_backward_workspace_size": (_size, [_i64, _i64]),
+    "bux_expert_norm_backward": (
+        _int, [_p, _p, _i32, _p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p, _p, _p, _p,
+               _size, _p]),
     "bux_glu_forward": (_int, [_p, _p, _p, _i64, _i64, _ffn, _p, _p]),
     "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _ffn, _p, _p, _p]),
     "bux_glu_quantize": (
@@ -93,6 +114,7 @@ ACTIVATIONS = {"swish": 0, "quick_gelu": 1, "relu": 2, "relu2": 3, "gelu": 4, "g
                "sigmoid": 6, "tanh": 7, "softplus": 8, "situ": 9}
 NOALLOC_SCRATCH_BYTES = 262144
 LIST_MAGIC, LIST_REFUSED = 0x54585542, 1
+LAYERNORM, RMSNORM = 0, 1
 ROUTER_SOFTMAX, ROUTER_SIGMOID, ROUTER_SQRTSOFTPLUS = 0, 1, 2
 
 

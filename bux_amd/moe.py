@@ -274,6 +274,74 @@ def add_bias_weight_grad(d_weights: torch.Tensor, dy: torch.Tensor, order: torch
     return d_weights
 
 
+# --- The experts' output norm ------------------------------------------------------
+
+
+class ExpertNorm(NamedTuple):
+    """The norm of each expert's output rows (MoEConfig.expert_norm, config.py:306): a
+    NormalizationConfig (config.py:71-92) of layernorm or rmsnorm, its gain (`scale`)
+    and bias given as bfloat16 (d,) tensors, as the model casts its parameters for the
+    forward (train/trainer.py:129-140)."""
+
+    kind: str = "rmsnorm"  # or "layernorm"
+    eps: float = 1e-6
+    affine: bool = True
+    bias: bool = False
+    zero_centered: bool = False
+    scale_input: bool = False
+
+    def struct(self) -> _lib.NormStruct:
+        kinds = {"layernorm": _lib.LAYERNORM, "rmsnorm": _lib.RMSNORM}
+        if self.kind not in kinds:
+            raise ValueError(f"no norm {self.kind!r}: layernorm or rmsnorm")
+        return _lib.NormStruct(kinds[self.kind], int(self.affine), int(self.zero_centered),
+                               int(self.scale_input), int(self.bias), float(self.eps))
+
+
+def expert_norm_forward(y: torch.Tensor, offsets: torch.Tensor, norm: ExpertNorm,
+                        scale: torch.Tensor | None, bias: torch.Tensor | None,
+                        row_weights: torch.Tensor, down_bias: torch.Tensor | None = None
+                        ) -> torch.Tensor:
+    """Return ``weighted(norm(y + down_bias), weights)`` of the down GEMM's rows y
+    (m, d) (moe.py:871-872), bfloat16 (m, d); rows in no expert 0."""
+    require(y, offsets, scale, bias, row_weights, down_bias)
+    e = _experts(offsets)
+    m, d = y.shape
+    out = torch.empty_like(y)
+    st = norm.struct()
+    _lib.check(lib().bux_expert_norm_forward(
+        ptr(y), m, d, ptr(down_bias), ptr(offsets), e, ctypes.byref(st), ptr(scale), ptr(bias),
+        ptr(row_weights), ptr(out), stream()))
+    return out
+
+
+def expert_norm_backward(dy: torch.Tensor, order: torch.Tensor, k: int, y: torch.Tensor,
+                         offsets: torch.Tensor, norm: ExpertNorm, scale: torch.Tensor | None,
+                         bias: torch.Tensor | None, row_weights: torch.Tensor,
+                         down_bias: torch.Tensor | None = None
+                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None,
+                                    torch.Tensor | None]:
+    """Return the VJP of `expert_norm_forward` given the tokens' gradient dy (t, d):
+    the gradient to y (m, d) bfloat16 (the down bias's, by expert), to the row weights
+    (m,) bfloat16, and to the norm's scale and bias (d,) float32 (None where it has
+    none)."""
+    require(dy, order, y, offsets, scale, bias, row_weights, down_bias)
+    e = _experts(offsets)
+    m, d = y.shape
+    dev = y.device
+    dv = torch.empty_like(y)
+    dw = torch.empty(m, dtype=torch.bfloat16, device=dev)
+    d_scale = torch.empty(d, dtype=torch.float32, device=dev) if norm.affine else None
+    d_bias = torch.empty(d, dtype=torch.float32, device=dev) if norm.bias else None
+    ws = workspace(lib().bux_expert_norm_backward_workspace_size(m, d), dev)
+    st = norm.struct()
+    _lib.check(lib().bux_expert_norm_backward(
+        ptr(dy), ptr(order), k, ptr(y), m, d, ptr(down_bias), ptr(offsets), e, ctypes.byref(st),
+        ptr(scale), ptr(bias), ptr(row_weights), ptr(dv), ptr(dw), ptr(d_scale), ptr(d_bias),
+        ptr(ws), ws.numel(), stream()))
+    return dv, dw, d_scale, d_bias
+
+
 # --- The layer: routed -> experts, forward and backward ------------------------------
 
 
@@ -358,6 +426,7 @@ class Saved(NamedTuple):
     rows: torch.Tensor | None  # the picks' rows (wgrad of up in bfloat16)
     tiles: grouped_mxfp8.TileList | None = None  # the MXFP8 GEMMs' tile list, made once
     passes: tuple[bool, bool, bool] = (True, True, True)  # (fprop, dgrad, wgrad) in MXFP8
+    y: torch.Tensor | None = None  # with an expert norm: the down GEMM's rows (m, d)
 
 
 def experts_forward(
@@ -365,6 +434,8 @@ def experts_forward(
     down: torch.Tensor, ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
     fused: bool = False, quantized: MxWeights | None = None, passes=None,
     up_bias: torch.Tensor | None = None, down_bias: torch.Tensor | None = None,
+    norm: ExpertNorm | None = None, norm_scale: torch.Tensor | None = None,
+    norm_bias: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, Saved]:
     """Return the routed experts' output (t, d), bfloat16, and what the backward takes.
     In MXFP8 the activation goes straight to its quantized copies; with `intermediates`
@@ -394,6 +465,10 @@ def experts_forward(
             product; None for none (MLPConfig.bias, moe.py:857-861).
         down_bias: the experts' down biases, bfloat16 (E, d): each pick adds its
             expert's, times its weight (moe.py:866-870).
+        norm: a norm of each expert's output rows (MoEConfig.expert_norm), with its
+            gain `norm_scale` and bias `norm_bias` (bfloat16 (d,)): the activation is
+            then unweighted and each row is ``weighted(norm(y + down_bias), w)``
+            (moe.py:871-872).
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -407,6 +482,8 @@ def experts_forward(
         row_weights = picked_weights(weights, s.order)
     up2 = up.reshape(e, d, f * p)
     tiles = fmt == "mxfp8_2d"
+    # with a norm, the activation is not weighted: the norm's output is (moe.py:871)
+    act_weights = row_weights if norm is None else torch.ones_like(row_weights)
     height = grouped_mxfp8.whole(m)
     x_k = x_m = up_n = up_k = h_k = h_m = down_n = down_k = rows = listed = None
     if fprop or dgrad or wgrad:
@@ -427,7 +504,7 @@ def experts_forward(
                 up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
     h = None
     if (fused and not intermediates and fprop and dgrad and wgrad and up_bias is None
-            and ffn.fusable(p == 2)):
+            and norm is None and ffn.fusable(p == 2)):
         with span("up fprop + activation + quantize h"):
             projected, h_k, h_m = grouped_mxfp8.activated(x_k, up_k, s.sizes, row_weights,
                                                           ffn.struct(True), m)
@@ -443,11 +520,11 @@ def experts_forward(
         pv = projected.view(m, f, p)
         if fprop or wgrad:
             with span("activation + quantize h"):
-                h_k, h_m, h = weighted_units_quantized(ffn, pv, row_weights, filled, height,
+                h_k, h_m, h = weighted_units_quantized(ffn, pv, act_weights, filled, height,
                                                        intermediates or not (fprop and wgrad))
         else:
             with span("activation"):
-                h = weighted_units(ffn, pv, row_weights, filled)
+                h = weighted_units(ffn, pv, act_weights, filled)
     if fprop or dgrad:
         if quantized is not None:
             down_n, down_k = quantized.down_n, quantized.down_k
@@ -459,27 +536,36 @@ def experts_forward(
             y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=listed)
         else:
             y = grouped.dot(h, down, s.sizes)
+    y_rows = None
+    if norm is not None:
+        with span("expert norm"):
+            y_rows = y
+            y = expert_norm_forward(y_rows, s.offsets, norm, norm_scale, norm_bias, row_weights,
+                                    None if down_bias is None else down_bias.reshape(e, d))
     with span("combine"):
-        if down_bias is None:
+        if down_bias is None or norm is not None:
             out = sum_by_token(y, s.inverse.view(t, k))
         else:
             out = sum_by_token_biased(y, s.inverse.view(t, k), down_bias.reshape(e, d), s.offsets,
                                       row_weights)
     keep_h = h if (intermediates or not wgrad) else None
     return out, Saved(s, k, row_weights, projected, keep_h, x_m, up_n, h_m, down_n, rows, listed,
-                      (fprop, dgrad, wgrad))
+                      (fprop, dgrad, wgrad), y_rows)
 
 
 def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: torch.Tensor,
                      ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
                      up_bias: torch.Tensor | None = None, down_bias: torch.Tensor | None = None,
+                     norm: ExpertNorm | None = None, norm_scale: torch.Tensor | None = None,
+                     norm_bias: torch.Tensor | None = None,
                      ) -> dict[str, torch.Tensor]:
     """Return the gradients of `experts_forward`'s output, dy (t, d), to z, the
     weights (t, k), up (E, d, f, p) and down (E, f, d), all bfloat16, and with biases
-    to "up_bias" (E, f, p) and "down_bias" (E, d), float32 sums; with `intermediates`,
+    to "up_bias" (E, f, p) and "down_bias" (E, d), float32 sums, and with a norm to
+    "norm_scale" and "norm_bias" (d,), float32 sums; with `intermediates`,
     also the gradients between the GEMMs: "dh" (m, f) of the down GEMM's input, "dp"
-    (m, p f) of the up GEMM's output, "dx" (m, d) of its input and "d_row_weights"
-    (m,). The passes are the forward's (`saved.passes`); `fmt` is checked against
+    (m, p f) of the up GEMM's output, "dx" (m, d) of its input, "d_row_weights" (m,),
+    and with a norm "dv" (m, d) of the down GEMM's output. The passes are the forward's (`saved.passes`); `fmt` is checked against
     them."""
     s, k = saved.sorted, saved.k
     t = dy.shape[0]
@@ -492,12 +578,31 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         raise ValueError(f"experts_backward: fmt {fmt!r} is not the forward's")
     height = grouped_mxfp8.whole(m)
     dy_n = dy_m = dp_n = dp_m = dy_rows = None
-    if dgrad or wgrad:
-        with span("quantize dy"):
-            dy_n, dy_m = grouped_mxfp8.quantized_twice(dy, filled, True, s.order, k, height)
-    if not (dgrad and wgrad):
-        with span("gather dy"):
-            dy_rows = token_rows(dy, s.order, k)
+    grads = {}
+    if norm is not None:
+        if saved.y is None:
+            raise ValueError("experts_backward: a norm, but the forward ran without one")
+        with span("expert norm backward"):
+            db = None if down_bias is None else down_bias.reshape(e, d)
+            dv, d_norm_w, d_scale, d_nbias = expert_norm_backward(
+                dy, s.order, k, saved.y, s.offsets, norm, norm_scale, norm_bias,
+                saved.row_weights, db)
+        grads.update({"norm_scale": d_scale, "norm_bias": d_nbias})
+        if down_bias is not None:
+            with span("down bias grad"):
+                grads["down_bias"] = expert_sums(dv, s.offsets)
+        # the down GEMM's upstream is dv, a row each (no longer the tokens' dy)
+        if dgrad or wgrad:
+            with span("quantize dv"):
+                dy_n, dy_m = grouped_mxfp8.quantized_twice(dv, filled, True, height=height)
+        dy_rows = dv
+    else:
+        if dgrad or wgrad:
+            with span("quantize dy"):
+                dy_n, dy_m = grouped_mxfp8.quantized_twice(dy, filled, True, s.order, k, height)
+        if not (dgrad and wgrad):
+            with span("gather dy"):
+                dy_rows = token_rows(dy, s.order, k)
     with span("down dgrad"):
         if dgrad:
             dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m, tiles=saved.tiles)
@@ -509,14 +614,17 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         else:
             d_down = grouped.weight_grad(saved.h, dy_rows, s.sizes)
     pv = saved.projected.view(m, f, p)
+    act_weights = saved.row_weights if norm is None else torch.ones_like(saved.row_weights)
     if dgrad or wgrad:
         keep = intermediates or up_bias is not None or not (dgrad and wgrad)
         with span("activation backward + quantize dp"):
             dp_n, dp_m, d_rows_w, dp = weighted_units_backward_quantized(
-                ffn, pv, saved.row_weights, dh, filled, height, keep)
+                ffn, pv, act_weights, dh, filled, height, keep)
     else:
         with span("activation backward"):
-            dp, d_rows_w = weighted_units_backward(ffn, pv, saved.row_weights, dh, filled)
+            dp, d_rows_w = weighted_units_backward(ffn, pv, act_weights, dh, filled)
+    if norm is not None:
+        d_rows_w = d_norm_w  # the unweighted activation's is not the weights'
     if dp is not None:
         dp = dp.view(m, f * p)
     with span("up dgrad"):
@@ -529,11 +637,10 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
             d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes, tiles=saved.tiles)
         else:
             d_up = grouped.weight_grad(saved.rows, dp, s.sizes)
-    grads = {}
     if up_bias is not None:
         with span("up bias grad"):
             grads["up_bias"] = expert_sums(dp, s.offsets).view(e, f, p)
-    if down_bias is not None:
+    if down_bias is not None and norm is None:
         with span("down bias grad"):
             db = down_bias.reshape(e, d)
             add_bias_weight_grad(d_rows_w, dy, s.order, k, db, s.offsets)
@@ -544,4 +651,6 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
     grads.update(z=dz, weights=d_weights, up=d_up.view(e, d, f, p), down=d_down)
     if intermediates:
         grads.update(dh=dh, dp=dp, dx=dx, d_row_weights=d_rows_w)
+        if norm is not None:
+            grads["dv"] = dy_rows
     return grads

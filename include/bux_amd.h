@@ -309,6 +309,50 @@ int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index, int32_
                                 void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * a-8. The per-expert norm of the experts' outputs (MoEConfig.expert_norm,
+ * config.py:306).
+ *
+ * bux_expert_norm_forward replaces moe.experts' norm path (moe.py:871-872):
+ *   out[r] = weighted(norm(y[r] + down_bias[e(r)]), weights[r]), bfloat16 [m, d];
+ * y the down GEMM's rows (not summed, not weighted: the activation before it runs with
+ * weights of 1, moe.py:871), down_bias [experts, d] or NULL, offsets/experts as the
+ * biases' above; rows in no expert give 0. The norm is layers/norm.Norm
+ * (layers/norm.py:14-78) of `bux_norm` in bfloat16 compute: gain = scale (1 + scale if
+ * zero_centered), applied before the normalization with scale_input, else after it;
+ * statistics in float32 (layernorm: centred, then over the root of the mean square plus
+ * eps; rmsnorm: the latter alone); the result rounded to bfloat16, each later product
+ * and sum rounded as the reference's bfloat16 ops round. scale [d] (affine) and bias
+ * [d] (bias) bfloat16, else NULL. d a multiple of 8, at most 8192.
+ * bux_expert_norm_backward: its VJP, given the tokens' gradient dy read through
+ * index / index_div (the sort's order and k): dv [m, d], the gradient to y (and, by
+ * expert, to the down bias: bux_expert_sums of it); d_weights [m] (written: the norm
+ * path's only use of the weights); d_scale and d_bias [d] float32 sums over the rows
+ * (NULL where the norm has none). workspace:
+ * bux_expert_norm_backward_workspace_size(m, d) bytes.
+ */
+enum { BUX_LAYERNORM = 0, BUX_RMSNORM = 1 };
+typedef struct bux_norm {
+  int32_t kind;          /* BUX_LAYERNORM or BUX_RMSNORM */
+  int32_t affine;        /* a learned gain, `scale` */
+  int32_t zero_centered; /* the gain is 1 + scale */
+  int32_t scale_input;   /* the gain multiplies before the normalization */
+  int32_t bias;          /* a learned bias, added last */
+  float eps;
+} bux_norm;
+int bux_expert_norm_forward(const uint16_t* y, int64_t m, int64_t d, const uint16_t* down_bias,
+                            const int32_t* offsets, int32_t experts, const bux_norm* norm,
+                            const uint16_t* scale, const uint16_t* bias, const uint16_t* weights,
+                            uint16_t* out, void* stream);
+size_t bux_expert_norm_backward_workspace_size(int64_t m, int64_t d);
+int bux_expert_norm_backward(const uint16_t* dy, const int32_t* index, int32_t index_div,
+                             const uint16_t* y, int64_t m, int64_t d, const uint16_t* down_bias,
+                             const int32_t* offsets, int32_t experts, const bux_norm* norm,
+                             const uint16_t* scale, const uint16_t* bias,
+                             const uint16_t* weights, uint16_t* dv, uint16_t* d_weights,
+                             float* d_scale, float* d_bias, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
  * a-8 with a-4. The activation and its gradient, quantized as they are computed.
  *
  * The reference fuses the activation and the weight into its up GEMM's epilogue on

@@ -355,6 +355,93 @@ def weighted_bias_rows(bias: np.ndarray, sizes: np.ndarray, row_weights: np.ndar
     return bf16.to_bf16(by_expert(bias, sizes, m) * w)
 
 
+# --- The experts' output norm -------------------------------------------------------
+
+
+class Norm(NamedTuple):
+    """The norm of each expert's output (MoEConfig.expert_norm, config.py:306): a
+    NormalizationConfig (config.py:71-92)."""
+
+    kind: str = "rmsnorm"  # or "layernorm"
+    eps: float = 1e-6
+    affine: bool = True
+    bias: bool = False
+    zero_centered: bool = False
+    scale_input: bool = False
+
+
+def _norm_parts(norm: Norm, v: np.ndarray, scale, nbias):
+    """The forward's pieces in float64 with the reference's bfloat16 roundings
+    (layers/norm.py:55-78 in bfloat16 compute): gain, x (the normalization's input), u,
+    rs, xn (its rounded output) and n (the norm's output)."""
+    r = bf16.round_f32
+    d = v.shape[-1]
+    gain = np.ones(d)
+    if norm.affine:
+        s_ = bf16.to_f32(scale).astype(np.float64)
+        gain = r(1.0 + s_).astype(np.float64) if norm.zero_centered else s_
+    x = r(v * gain).astype(np.float64) if norm.affine and norm.scale_input else v
+    u = x - x.mean(-1, keepdims=True) if norm.kind == "layernorm" else x
+    rs = 1.0 / np.sqrt((u * u).mean(-1, keepdims=True) + norm.eps)
+    xn = r(u * rs).astype(np.float64)
+    n = xn
+    if norm.affine and not norm.scale_input:
+        n = r(n * gain).astype(np.float64)
+    if norm.bias:
+        n = r(n + bf16.to_f32(nbias).astype(np.float64)).astype(np.float64)
+    return gain, x, u, rs, xn, n
+
+
+def _norm_input(y: np.ndarray, sizes: np.ndarray, down_bias) -> np.ndarray:
+    v = bf16.to_f32(y).astype(np.float64)
+    if down_bias is not None:
+        v = bf16.round_f32(v + by_expert(down_bias, sizes, y.shape[0])).astype(np.float64)
+    return v
+
+
+def expert_norm_forward(norm: Norm, y: np.ndarray, sizes: np.ndarray, row_weights: np.ndarray,
+                        scale=None, nbias=None, down_bias=None) -> np.ndarray:
+    """Return ``weighted(norm(y + down_bias), weights)`` of the down GEMM's rows y (m, d)
+    (moe.py:871-872), bfloat16 bits; rows past the groups 0."""
+    v = _norm_input(y, sizes, down_bias)
+    *_, n = _norm_parts(norm, v, scale, nbias)
+    w = bf16.to_f32(row_weights).astype(np.float64)[:, None]
+    live = (_expert_of_rows(sizes, y.shape[0]) >= 0)[:, None]
+    return bf16.to_bf16(np.where(live, n * w, 0.0).astype(np.float32))
+
+
+def expert_norm_backward(norm: Norm, g: np.ndarray, y: np.ndarray, sizes: np.ndarray,
+                         row_weights: np.ndarray, scale=None, nbias=None, down_bias=None):
+    """Return the VJP of `expert_norm_forward` given each row's upstream gradient g
+    (m, d) bfloat16 bits (its token's dy): dv (m, d) and d weights (m,) as bfloat16
+    bits, d scale and d bias (d,) as float64 sums (None where the norm has none); jax's
+    VJP of the bfloat16 chain, the normalization's in float32 (here float64)."""
+    r = bf16.round_f32
+    v = _norm_input(y, sizes, down_bias)
+    gain, x, u, rs, xn, n = _norm_parts(norm, v, scale, nbias)
+    gf = bf16.to_f32(g).astype(np.float64)
+    w = bf16.to_f32(row_weights).astype(np.float64)[:, None]
+    live = (_expert_of_rows(sizes, y.shape[0]) >= 0)[:, None]
+    gf = np.where(live, gf, 0.0)
+    d_w = r(r(gf * n).sum(-1)).astype(np.float64)
+    dn = r(gf * w).astype(np.float64)
+    d_bias = dn.sum(0) if norm.bias else None
+    d_scale = None
+    dxn = dn
+    if norm.affine and not norm.scale_input:
+        d_scale = r(dn * xn).sum(0)
+        dxn = r(dn * gain).astype(np.float64)
+    mean_dx = dxn.mean(-1, keepdims=True) if norm.kind == "layernorm" else 0.0
+    mean_dxu = (dxn * u).mean(-1, keepdims=True)
+    dx = r(rs * (dxn - mean_dx - u * rs * rs * mean_dxu)).astype(np.float64)
+    if norm.affine and norm.scale_input:
+        d_scale = r(dx * v).sum(0)
+        dx = r(dx * gain).astype(np.float64)
+    dv = np.where(live, dx, 0.0)
+    return (bf16.to_bf16(dv.astype(np.float32)), bf16.to_bf16(np.where(live[:, 0], d_w, 0.0).astype(np.float32)),
+            d_scale, d_bias)
+
+
 # --- The layer: routed -> experts, forward and backward ----------------------------
 
 
@@ -373,6 +460,7 @@ class Saved(NamedTuple):
     h_m: Blocks | None
     down_n: Blocks | None
     passes: tuple[bool, bool, bool] = (True, True, True)
+    y: np.ndarray | None = None  # with a norm: the down GEMM's rows, bf16 bits (m, d)
 
 
 def _passes(fmt: str, passes) -> tuple[bool, bool, bool]:
@@ -393,6 +481,9 @@ def layer_forward(
     passes=None,
     up_bias: np.ndarray | None = None,
     down_bias: np.ndarray | None = None,
+    norm: Norm | None = None,
+    norm_scale: np.ndarray | None = None,
+    norm_bias: np.ndarray | None = None,
 ) -> tuple[np.ndarray, Saved]:
     """Return the MoE's routed experts' output (t, d) as bfloat16 bits, and what the
     backward takes: ``routed`` (moe.py:733-773) on one device with picked rows in and
@@ -411,6 +502,8 @@ def layer_forward(
             copies, blockscaled.MXFP8_2D, blockscaled.py:306-309) or "compute".
         passes: the GEMMs in `fmt`, of PASSES; None for all.
         up_bias: bfloat16 bits (E, f, p) or None; down_bias: (E, d) or None.
+        norm: the experts' output norm (moe.py:871-872), with its scale and bias
+            (bfloat16 bits (d,)); the activation is then unweighted.
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -437,22 +530,30 @@ def layer_forward(
         projected = ragged_dot_bf16(z[tokens], up2, s.sizes)
     if up_bias is not None:
         projected = add_expert_bias(projected, up_bias, s.sizes)
-    h = weighted_units(ffn, projected.reshape(m, f, p), row_weights)
+    act_weights = row_weights if norm is None else bf16.to_bf16(np.ones(m, np.float32))
+    h = weighted_units(ffn, projected.reshape(m, f, p), act_weights)
     if fprop or wgrad:
         h_k, h_m = mxfp8.quantized_twice(h, filled, True, height=whole(m))
     y = rows_mx(h_k, down_k, s.sizes, height=m) if fprop else ragged_dot_bf16(h, down, s.sizes)
+    y_rows = None
+    if norm is not None:
+        y_rows = y
+        y = expert_norm_forward(norm, y_rows, s.sizes, row_weights, norm_scale, norm_bias, down_bias)
     out = sum_by_token(y, s.inverse.reshape(t, k))
-    if down_bias is not None:
+    if down_bias is not None and norm is None:
         b = weighted_bias_rows(down_bias, s.sizes, row_weights, m)
         bsum = sum_by_token(b, s.inverse.reshape(t, k))
         out = bf16.to_bf16(bf16.to_f32(out) + bf16.to_f32(bsum))
-    return out, Saved(s, row_weights, projected, h, x_m, up_n, h_m, down_n, (fprop, dgrad, wgrad))
+    return out, Saved(s, row_weights, projected, h, x_m, up_n, h_m, down_n, (fprop, dgrad, wgrad),
+                      y_rows)
 
 
 def layer_backward(
     saved: Saved, dy: np.ndarray, z: np.ndarray, up: np.ndarray, down: np.ndarray,
     k: int, ffn: Ffn = Ffn(), fmt: str = "mxfp8",
     up_bias: np.ndarray | None = None, down_bias: np.ndarray | None = None,
+    norm: Norm | None = None, norm_scale: np.ndarray | None = None,
+    norm_bias: np.ndarray | None = None,
 ) -> dict[str, np.ndarray]:
     """Return the gradients of `layer_forward`'s output, dy (t, d) bfloat16 bits, to
     z, the weights, up and down (bfloat16 bits), to the biases (float64 sums), and
@@ -468,9 +569,20 @@ def layer_backward(
     tokens = s.order // k
     up2 = np.asarray(up).reshape(e, d, f * p)
     fprop, dgrad, wgrad = saved.passes
-    if dgrad or wgrad:
-        dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens, height=whole(m))
-    dy_rows = dy[tokens]
+    grads = {}
+    if norm is not None:
+        dv, d_norm_w, d_scale, d_nbias = expert_norm_backward(
+            norm, dy[tokens], saved.y, s.sizes, saved.row_weights, norm_scale, norm_bias, down_bias)
+        grads.update(norm_scale=d_scale, norm_bias=d_nbias)
+        if down_bias is not None:
+            grads["down_bias"] = expert_sums(bf16.to_f32(dv), s.sizes)
+        dy_rows = dv
+        if dgrad or wgrad:
+            dy_n, dy_m = mxfp8.quantized_twice(dv, filled, True, height=whole(m))
+    else:
+        if dgrad or wgrad:
+            dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens, height=whole(m))
+        dy_rows = dy[tokens]
     if dgrad:
         dh = rows_mx(dy_n, saved.down_n, s.sizes, height=m)
     else:
@@ -479,7 +591,10 @@ def layer_backward(
         d_down = contract_mx(saved.h_m, dy_m, s.sizes)
     else:
         d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes)
-    dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), saved.row_weights, dh)
+    act_weights = saved.row_weights if norm is None else bf16.to_bf16(np.ones(m, np.float32))
+    dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), act_weights, dh)
+    if norm is not None:
+        d_rows_w = d_norm_w
     dp = dp.reshape(m, f * p)
     if dgrad or wgrad:
         dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True, height=whole(m))
@@ -491,10 +606,9 @@ def layer_backward(
         d_up = contract_mx(saved.x_m, dp_m, s.sizes)
     else:
         d_up = weight_grad_bf16(z[tokens], dp, s.sizes)
-    grads = {}
     if up_bias is not None:
         grads["up_bias"] = expert_sums(bf16.to_f32(dp), s.sizes).reshape(e, f, p)
-    if down_bias is not None:
+    if down_bias is not None and norm is None:
         # weighted(b_rows, w)'s VJP: to b_rows ct * w (bfloat16), to w sum_c ct * b_rows
         # (products in bfloat16, summed in float32); ct = dy at each row's token
         g = bf16.to_f32(dy_rows)

@@ -420,17 +420,88 @@ def test_a_plain_ffn_takes_its_projection_with_or_without_the_last_axis():
     np.testing.assert_array_equal(a[1], b[1])
 
 
-DENSE = [
-    # (ffn, p, biased)
-    (moe.Ffn("quick_gelu", 7.0, 1.0), 2, False),
-    (moe.Ffn("quick_gelu", 7.0, 1.0), 2, True),  # gpt-oss: clamped, with biases
-    (moe.Ffn("relu2"), 1, False),
-    (moe.Ffn("gelu", None, 0.0, 3.0), 1, True),
+NORMS = [
+    moe.Norm("rmsnorm"),
+    moe.Norm("layernorm", 1e-5, True, True),
+    moe.Norm("rmsnorm", 1e-6, True, False, True),  # zero-centered gain (Qwen3-Next)
+    moe.Norm("layernorm", 1e-6, True, True, False, True),  # scale_input
+    moe.Norm("layernorm", 1e-6, False, False),  # no gain, no bias
 ]
 
 
-@pytest.mark.parametrize("ffn,p,biased", DENSE)
-def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased):
+def _torch_norm(norm, x, scale, bias):
+    """layers/norm.py:55-78 in torch float64, from torch's own layer_norm / rms_norm."""
+    gain = None
+    if norm.affine:
+        gain = 1 + scale if norm.zero_centered else scale
+    if gain is not None and norm.scale_input:
+        x = x * gain
+    d = x.shape[-1]
+    if norm.kind == "layernorm":
+        x = torch.nn.functional.layer_norm(x, (d,), eps=norm.eps)
+    else:
+        x = torch.nn.functional.rms_norm(x, (d,), eps=norm.eps)
+    if gain is not None and not norm.scale_input:
+        x = x * gain
+    if norm.bias:
+        x = x + bias
+    return x
+
+
+@pytest.mark.parametrize("norm", NORMS)
+def test_the_expert_norm_and_its_gradient_are_torchs(norm):
+    """The oracle's norm (with its bfloat16 roundings) against torch's layer_norm and
+    rms_norm and autograd in float64, with a down bias by expert and row weights; rows
+    past the groups give 0."""
+    rng = np.random.default_rng(13)
+    m, d, sizes = 96, 64, np.array([30, 0, 50, 6])
+    filled = int(sizes.sum())
+    y = bf16.to_bf16((rng.standard_normal((m, d)) * 3 + 0.5).astype(np.float32))
+    db = bf16.to_bf16(rng.standard_normal((4, d)).astype(np.float32))
+    scale = bf16.to_bf16((1 + 0.3 * rng.standard_normal(d)).astype(np.float32))
+    nb = bf16.to_bf16((0.2 * rng.standard_normal(d)).astype(np.float32))
+    w = bf16.to_bf16(rng.random(m).astype(np.float32))
+    g = bf16.to_bf16(rng.standard_normal((m, d)).astype(np.float32))
+    out = moe.expert_norm_forward(norm, y, sizes, w, scale, nb, db)
+    dv, dw, dscale, dbias = moe.expert_norm_backward(norm, g, y, sizes, w, scale, nb, db)
+
+    def t(a, grad=False):
+        return torch.tensor(bf16.to_f32(a), dtype=torch.float64, requires_grad=grad)
+
+    yt, wt, st, bt = t(y[:filled], True), t(w[:filled], True), t(scale, True), t(nb, True)
+    rows = torch.tensor(np.repeat(np.arange(4), sizes))
+    x = yt + t(db)[rows]
+    want = _torch_norm(norm, x, st, bt) * wt[:, None]
+    want.backward(t(g[:filled]))
+
+    def close(got, ref, tol):
+        ref = ref.detach().numpy()
+        err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert err < tol, err
+
+    close(bf16.to_f32(out[:filled]), want, 1e-2)
+    assert (out[filled:] == 0).all() and (dv[filled:] == 0).all() and (dw[filled:] == 0).all()
+    close(bf16.to_f32(dv[:filled]), yt.grad, 2e-2)
+    close(bf16.to_f32(dw[:filled]), wt.grad, 2e-2)
+    if norm.affine:
+        close(dscale, st.grad, 2e-2)
+    if norm.bias:
+        close(dbias, bt.grad, 2e-2)
+
+
+DENSE = [
+    # (ffn, p, biased, norm)
+    (moe.Ffn("quick_gelu", 7.0, 1.0), 2, False, None),
+    (moe.Ffn("quick_gelu", 7.0, 1.0), 2, True, None),  # gpt-oss: clamped, with biases
+    (moe.Ffn("relu2"), 1, False, None),
+    (moe.Ffn("gelu", None, 0.0, 3.0), 1, True, None),
+    (moe.Ffn(), 2, False, moe.Norm("rmsnorm")),
+    (moe.Ffn("quick_gelu", 7.0, 1.0), 2, True, moe.Norm("layernorm", 1e-5, True, True)),
+]
+
+
+@pytest.mark.parametrize("ffn,p,biased,norm", DENSE)
+def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased, norm):
     """``sorted`` equals ``dense`` with gradients (tests/test_moe.py:475-484): the
     oracle's layer, in bfloat16 ("compute"), against every token through each of its
     experts one by one, differentiated by torch.autograd in float64; gated or plain,
@@ -445,15 +516,19 @@ def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased):
     dy = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
     ub = bf16.to_bf16((rng.standard_normal((e, f, p))).astype(np.float32)) if biased else None
     db = bf16.to_bf16((rng.standard_normal((e, d))).astype(np.float32)) if biased else None
-    y, saved = moe.layer_forward(z, idx, w, up, down, ffn, fmt="compute", up_bias=ub, down_bias=db)
+    ns = bf16.to_bf16((1 + 0.3 * rng.standard_normal(d)).astype(np.float32)) if norm else None
+    nb = bf16.to_bf16((0.2 * rng.standard_normal(d)).astype(np.float32)) if norm else None
+    y, saved = moe.layer_forward(z, idx, w, up, down, ffn, fmt="compute", up_bias=ub, down_bias=db,
+                                 norm=norm, norm_scale=ns, norm_bias=nb)
     grads = moe.layer_backward(saved, dy, z, up, down, k, ffn, fmt="compute", up_bias=ub,
-                               down_bias=db)
+                               down_bias=db, norm=norm, norm_scale=ns, norm_bias=nb)
 
     def tensor(a):
         return torch.tensor(bf16.to_f32(a), dtype=torch.float64, requires_grad=True)
 
     zt, wt, upt, downt = tensor(z), tensor(w), tensor(up), tensor(down)
     ubt, dbt = (tensor(ub), tensor(db)) if biased else (None, None)
+    nst, nbt = (tensor(ns), tensor(nb)) if norm else (None, None)
     out = torch.zeros(t, d, dtype=torch.float64)
     for tok in range(t):
         for j in range(k):
@@ -461,10 +536,17 @@ def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased):
             pr = zt[tok] @ upt[g].reshape(d, p * f)
             if biased:
                 pr = pr + ubt[g].reshape(p * f)
-            h = _torch_units(ffn, pr.reshape(1, f, p), wt[tok, j].reshape(1))[0]
-            row = h @ downt[g]
-            if biased:
-                row = row + dbt[g] * wt[tok, j]
+            if norm is None:
+                h = _torch_units(ffn, pr.reshape(1, f, p), wt[tok, j].reshape(1))[0]
+                row = h @ downt[g]
+                if biased:
+                    row = row + dbt[g] * wt[tok, j]
+            else:  # moe.py:871-872: unweighted, biased, normed, then weighted
+                h = _torch_units(ffn, pr.reshape(1, f, p), torch.ones(1, dtype=torch.float64))[0]
+                row = h @ downt[g]
+                if biased:
+                    row = row + dbt[g]
+                row = _torch_norm(norm, row, nst, nbt) * wt[tok, j]
             out = out.index_add(0, torch.tensor([tok]), row[None])
     out.backward(torch.tensor(bf16.to_f32(dy), dtype=torch.float64))
 
@@ -482,6 +564,12 @@ def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased):
     if biased:
         close(grads["up_bias"], ubt.grad, 2e-2)
         close(grads["down_bias"], dbt.grad, 2e-2)
+    if norm is not None:
+        close(grads["norm_scale"], nst.grad, 2e-2)
+        if norm.bias:
+            close(grads["norm_bias"], nbt.grad, 2e-2)
+        else:
+            assert grads["norm_bias"] is None
 
 
 def test_the_layer_with_no_pass_in_mxfp8_is_the_compute_layer_and_all_passes_the_default():
