@@ -63,6 +63,8 @@ SIGNATURES = {
     "bux_mx_grouped_rows_workspace_size": (_size, [_i32, _i64, _i64]),
     "bux_mx_grouped_rows": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
+    "bux_mx_grouped_rows_started": (
+        _int, [_p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
     "bux_mx_grouped_tiles": (_int, [_p, _i32, _i64, _i64, _p, _size, _p]),
     "bux_mx_grouped_rows_listed": (
         _int, [_p, _p, _p, _p, _p, _size, _i32, _i64, _i64, _i64, _i64, _int, _p, _p]),
@@ -107,7 +109,7 @@ SIGNATURES = {
 }
 
 # Constants of include/bux_amd.h.
-MX_ROWS, MX_COLUMNS, MX_TILES = 1, 2, 4
+MX_ROWS, MX_COLUMNS, MX_TILES, MX_HALVES = 1, 2, 4, 8
 BF16, F32 = 0, 1
 # the activations, bux_ffn.activation
 ACTIVATIONS = {"swish": 0, "quick_gelu": 1, "relu": 2, "relu2": 3, "gelu": 4, "gelu_tanh": 5,

@@ -111,14 +111,17 @@ constexpr int32_t LIST_REFUSED = BUX_LIST_REFUSED;
 // computes rows [lo, lo + BM) and holds rows [max(lo, starts[g]), hi) of group g.
 //
 // With `header` (a tile list's, LIST_HEADER bytes before its starts), the list's
-// dimensions go there too: LIST_MAGIC, groups, m, height, and a 0 status word.
+// dimensions go there too: LIST_MAGIC, groups, m, height, and a 0 status word. With
+// `a_starts`, the tiles lie where the groups' rows lie in a (a_starts[g] on), not packed
+// (starts_out stays packed: where their rows lie in y).
 __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __restrict__ sizes,
                                                            int32_t groups, int64_t height,
                                                            int64_t slots, int32_t align,
                                                            int32_t* __restrict__ starts_out,
                                                            Tile* __restrict__ tiles,
                                                            int32_t* __restrict__ header,
-                                                           int64_t m) {
+                                                           int64_t m,
+                                                           const int32_t* __restrict__ a_starts) {
   if (header != nullptr && threadIdx.x < LIST_HEADER / 4) {
     const int32_t i = threadIdx.x;
     header[i] = i == 0 ? LIST_MAGIC : i == 1 ? groups : i == 2 ? static_cast<int32_t>(m)
@@ -140,18 +143,23 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
     if (g < groups) return sizes[g];
     return height > filled ? height - filled : 0;
   };
+  // where group g's rows lie in a: `a_starts` (given), else packed; the rows past the
+  // groups where they lie in y
+  auto first = [&](int g) -> int64_t {
+    return a_starts != nullptr && g < groups ? static_cast<int64_t>(a_starts[g]) : starts[g];
+  };
   // tiles of group g: from its first row rounded down to `align`
   auto count_of = [&](int g) -> int64_t {
     const int64_t s = size_of(g);
     if (s <= 0) return 0;
-    const int64_t start = starts[g], base = start & ~static_cast<int64_t>(align - 1);
+    const int64_t start = first(g), base = start & ~static_cast<int64_t>(align - 1);
     return (start + s - base + BM - 1) / BM;
   };
   for (int g = t; g < all; g += THREADS) before[g] = static_cast<int32_t>(count_of(g));
   __syncthreads();
   const int32_t used = block_scan(before, all, partial);
   for (int g = t; g < all; g += THREADS) {
-    const int64_t s = size_of(g), start = starts[g], end = start + s;
+    const int64_t s = size_of(g), start = first(g), end = start + s;
     const int64_t base = start & ~static_cast<int64_t>(align - 1), count = count_of(g);
     // Sizes summing past the rows there are would list more tiles than there are
     // slots: those are dropped, never written past the list.
@@ -587,6 +595,34 @@ struct RowsTiles {
   }
 };
 
+// The rows GEMM's tiles where each group's rows lie in a from a_starts[g] (tiles from
+// the prologue given those starts) while y's rows stay packed (starts, the prologue's):
+// a tile's rows of a map to y's by the group's shift, packed start less a's.
+struct StartedTiles {
+  const Tile* tiles;
+  const int32_t* starts;    // packed: where each group's rows lie in y
+  const int32_t* a_starts;  // where they lie in a
+  int32_t groups, n, height, col_tiles, k_steps;
+  __device__ bool job(int32_t id, Job& j) const {
+    const Tile t = tiles[id / col_tiles];
+    const int32_t col0 = (id % col_tiles) * BN;
+    const int32_t shift = t.group < groups ? starts[t.group] - a_starts[t.group] : 0;
+    const int32_t lo = t.lo + shift;  // the tile's first row of y
+    j.rows = smaller(t.hi + shift, height) - lo;
+    if (j.rows <= 0) return false;
+    j.cols = smaller(n - col0, BN);
+    j.a_row0 = t.lo;
+    j.b_row0 = col0;
+    j.group = t.group < groups ? t.group : 0;
+    j.ks_begin = 0;
+    j.n = t.group < groups ? k_steps : 0;  // rows past the groups: zeros
+    j.mask = false;
+    j.mlo = j.mhi = 0;
+    j.corner = static_cast<int64_t>(lo) * n + col0;
+    return true;
+  }
+};
+
 // The contract GEMM's tiles: each group's d x f output in 256 x 256 tiles.
 struct ContractTiles {
   const int32_t* starts;
@@ -765,6 +801,20 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   run_tiles(list, count, A, B, lds, Plain<T>{y, n});
 }
 
+// rows_kernel with each group's rows of a from a_starts[g] (the reference's `starts`).
+template <typename T>
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_started_kernel(
+    Operand A, Operand B, int32_t groups, int32_t n, int32_t height,
+    const int32_t* __restrict__ starts, const int32_t* __restrict__ a_starts,
+    const Tile* __restrict__ tiles, int32_t col_tiles, T* __restrict__ y) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  if (!list_fits(starts, groups, A.rows, height)) return;
+  Lds& lds = *reinterpret_cast<Lds*>(smem);
+  const StartedTiles list{tiles, starts, a_starts, groups, n, height, col_tiles, A.k / BK};
+  const int32_t count = starts[groups + 1] * col_tiles;
+  run_tiles(list, count, A, B, lds, Plain<T>{y, n});
+}
+
 template <typename T>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void contract_kernel(
     Operand A, Operand B, int32_t groups, const int32_t* __restrict__ starts, int32_t d_tiles,
@@ -818,6 +868,21 @@ int launch_rows(const Operand& A, const Operand& B, int32_t groups, int64_t n, i
                      static_cast<int32_t>(n), static_cast<int32_t>(height), starts, tiles,
                      static_cast<int32_t>(col_tiles), static_cast<T*>(y));
   return launched("rows_kernel");
+}
+
+template <typename T>
+int launch_rows_started(const Operand& A, const Operand& B, int32_t groups, int64_t n,
+                        int64_t height, const int32_t* starts, const int32_t* a_starts,
+                        const Tile* tiles, int64_t slots, void* y, hipStream_t s) {
+  const int64_t col_tiles = ceil_div(n, BN);
+  if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_rows_started: too many tiles");
+  unsigned blocks = 0;
+  if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
+  if (int rc = allow_lds(rows_started_kernel<T>, "rows_started_kernel")) return rc;
+  hipLaunchKernelGGL(rows_started_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B,
+                     groups, static_cast<int32_t>(n), static_cast<int32_t>(height), starts,
+                     a_starts, tiles, static_cast<int32_t>(col_tiles), static_cast<T*>(y));
+  return launched("rows_started_kernel");
 }
 
 template <typename T>
@@ -1222,7 +1287,7 @@ extern "C" int bux_mx_grouped_tiles(const int32_t* sizes, int32_t groups, int64_
                 need);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, as_stream(stream), sizes, groups,
                      height, row_slots(groups, m, height), 1, starts_in(list), tiles_in(list, groups),
-                     header_in(list), m);
+                     header_in(list), m, nullptr);
   return launched("prologue_kernel");
 }
 
@@ -1245,10 +1310,44 @@ extern "C" int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_sca
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height,
                      row_slots(groups, m, height), 1, starts_in(workspace),
-                     tiles_in(workspace, groups), header_in(workspace), m);
+                     tiles_in(workspace, groups), header_in(workspace), m, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   return launch_rows_of(a_values, a_scales, b_values, b_scales, workspace, groups, m, n, k, height,
                         out_dtype, y, s);
+}
+
+extern "C" int bux_mx_grouped_rows_started(const uint8_t* a_values, const uint8_t* a_scales,
+                                           const uint8_t* b_values, const uint8_t* b_scales,
+                                           const int32_t* sizes, const int32_t* starts,
+                                           int32_t groups, int64_t m, int64_t n, int64_t k,
+                                           int64_t height, int out_dtype, void* y,
+                                           void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+  using namespace bux;
+  clear_error();
+  if (int rc = check_rows("bux_mx_grouped_rows_started", a_values, a_scales, b_values, b_scales,
+                          groups, m, n, k, height, out_dtype, y))
+    return rc;
+  BUX_CHECK(sizes != nullptr && starts != nullptr, "bux_mx_grouped_rows_started: NULL sizes or starts");
+  const size_t need = bux_mx_grouped_rows_workspace_size(groups, m, height);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(BUX_E_WORKSPACE, "bux_mx_grouped_rows_started: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  if (height == 0) return BUX_OK;
+  hipStream_t s = as_stream(stream);
+  const int64_t slots = row_slots(groups, m, height);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
+                     1, starts_in(workspace), tiles_in(workspace, groups), header_in(workspace), m,
+                     starts);
+  if (int rc = launched("prologue_kernel")) return rc;
+  // a's rows past m read 0 (the resource ends there): the groups' rows are the caller's
+  const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(m)};
+  const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};
+  return out_dtype == BUX_BF16
+             ? launch_rows_started<uint16_t>(A, B, groups, n, height, starts_in(workspace), starts,
+                                             tiles_in(workspace, groups), slots, y, s)
+             : launch_rows_started<float>(A, B, groups, n, height, starts_in(workspace), starts,
+                                          tiles_in(workspace, groups), slots, y, s);
 }
 
 // --- bux_mx_grouped_rows without a workspace -------------------------------------------
@@ -1316,7 +1415,7 @@ extern "C" int bux_mx_grouped_rows_noalloc(const uint8_t* a_values, const uint8_
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height,
                      row_slots(groups, m, height), 1, starts_in(ws), tiles_in(ws, groups),
-                     header_in(ws), m);
+                     header_in(ws), m, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   return launch_rows_of(a_values, a_scales, b_values, b_scales, ws, groups, m, n, k, height,
                         out_dtype, y, s);
@@ -1365,7 +1464,7 @@ extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a
                 workspace_bytes, need);
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
-                     starts_in(workspace), nullptr, header_in(workspace), 0);
+                     starts_in(workspace), nullptr, header_in(workspace), 0, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   return launch_contract_of(a_values, a_scales, b_values, b_scales, starts_in(workspace), groups,
                             d, f, m,
@@ -1437,7 +1536,7 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
   const int64_t col_tiles = ceil_div(n, BN);
   if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_glu: too many tiles");
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
-                     32, starts, tiles, nullptr, 0);
+                     32, starts, tiles, nullptr, 0, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(height)};
   const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(n)};

@@ -52,13 +52,17 @@ constexpr int THREADS = 256;
 // Two float32 -> two bfloat16 (nearest even) by the hardware's conversion.
 __device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
 
-// A matrix of bfloat16 (matrix g of a stack), or its rows read by index.
+// A matrix of bfloat16 (matrix g of a stack), or its rows read by index. With
+// `halves`, its columns are read as a GLU's halves (grouped_cudnn.halves_of,
+// grouped_cudnn.py:150-155): column c of the copies is, in each 64, the gate (odd column)
+// of pair c % 32 for c % 64 < 32, else that pair's up (even column).
 struct Matrix {
   static constexpr bool kPartials = false;
   const uint16_t* x;
   const int32_t* index;
   int32_t index_div;
   int64_t rows, cols;
+  bool halves;
   // Columns [col, col + 8) of row r of matrix g; `live`: r holds values and the
   // columns are the matrix's (`inside`: the columns are; padding past them is not).
   __device__ __forceinline__ uint4 load(int64_t g, int64_t r, int64_t col, bool live, bool,
@@ -72,7 +76,19 @@ struct Matrix {
       src = (index_div & (index_div - 1)) == 0 ? (at >> (31 - __builtin_clz(index_div)))
                                                : at / index_div;
     }
-    return *reinterpret_cast<const uint4*>((index ? x : x + g * rows * cols) + src * cols + col);
+    const uint16_t* row = (index ? x : x + g * rows * cols) + src * cols;
+    if (!halves) return *reinterpret_cast<const uint4*>(row + col);
+    // 8 columns of one half: 16 consecutive columns of pairs, every other one
+    const int64_t q = col & 63;
+    const uint4* p = reinterpret_cast<const uint4*>(row + (col - q) + 2 * (q & 31));
+    const uint4 lo = p[0], hi = p[1];
+    const int shift = q < 32 ? 16 : 0;  // a gate is a pair's high half, an up its low
+    const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = ((w[2 * j] >> shift) & 0xffffu) | (((w[2 * j + 1] >> shift) & 0xffffu) << 16);
+    return make_uint4(o[0], o[1], o[2], o[3]);
   }
   __device__ __forceinline__ void partial(int64_t, int64_t, float) const {}
 };
@@ -374,9 +390,12 @@ extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t 
   BUX_CHECK(index == nullptr || index_div >= 1, "bux_mx_quantize: index_div=%d", index_div);
   BUX_CHECK(index == nullptr || groups == 1, "bux_mx_quantize: index takes one matrix, not %lld",
             (long long)groups);
-  return launch_quantize("bux_mx_quantize", Matrix{x, index, index_div, rows, cols}, groups, rows,
-                         cols, height, filled, flags, values, scales, t_values, t_scales,
-                         as_stream(stream));
+  const bool halves = (flags & BUX_MX_HALVES) != 0;
+  BUX_CHECK(!halves || cols % 64 == 0, "bux_mx_quantize: BUX_MX_HALVES needs cols=%lld a multiple of 64",
+            (long long)cols);
+  return launch_quantize("bux_mx_quantize", Matrix{x, index, index_div, rows, cols, halves}, groups,
+                         rows, cols, height, filled, flags & ~BUX_MX_HALVES, values, scales, t_values,
+                         t_scales, as_stream(stream));
 }
 
 extern "C" int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights,

@@ -95,6 +95,7 @@ def quantized_twice(
     height: int | None = None,
     rows: bool = True,
     tiles: bool = False,
+    halves: bool = False,
 ) -> tuple[Tiled | None, Tiled | None]:
     """Return x in MXFP8 along its rows and, if `columns`, x^T along its rows, in one
     pass over x, both tiled; with `tiles`, a scale per 32 x 32 tile shared by both
@@ -112,6 +113,9 @@ def quantized_twice(
         height: rows of the copies, a multiple of 32 (rows past x's are 0); None for
             x's (the index's) rows rounded up to 32.
         rows: whether to return the copy along the rows (False: None in its place).
+        halves: x's columns are a GLU's (up, gate) pairs, read as its halves: in each
+            64 columns the 32 pairs' gates, then their ups (the reference's `halves`,
+            grouped_triton.py:49, grouped_cudnn.halves_of); c a multiple of 64.
 
     Returns:
         (x along rows, x^T along rows): `height` rows of K = c padded to 128, and c
@@ -149,6 +153,8 @@ def quantized_twice(
         t_scales = torch.empty(*lead, kh // 128, c, 4, dtype=torch.uint8, device=dev)
     if tiles:
         flags |= _lib.MX_TILES
+    if halves:
+        flags |= _lib.MX_HALVES
     _lib.check(lib().bux_mx_quantize(
         ptr(x), ptr(index), index_div, groups, r, c, h, ptr(filled), flags,
         ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))
@@ -186,7 +192,7 @@ def tiles_of(sizes: torch.Tensor, m: int, height: int) -> TileList:
 
 def rows(
     a: Tiled, b: Tiled, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16,
-    height: int | None = None, tiles: TileList | None = None,
+    height: int | None = None, tiles: TileList | None = None, starts: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Return ``a @ b[g]^T`` for each group g's rows of a, (height, n), the rows past
     the groups 0.
@@ -199,6 +205,9 @@ def rows(
         height: rows of the output (a's rows past it are not stored); None for m.
         tiles: `tiles_of(sizes, m, height)`, made once for the step's GEMMs; None to make
             it here.
+        starts: int32 (g,) on the device: where each group's rows of a start (the
+            reference's `starts`, grouped_mxfp8.py:116-154); None for packed. y's rows
+            stay packed either way.
     """
     require(a.values, a.scales, b.values, b.scales, sizes)
     if a.values.dim() != 3 or b.values.dim() != 4:
@@ -211,6 +220,16 @@ def rows(
                          f"sizes {tuple(sizes.shape)} {sizes.dtype}")
     h = m if height is None else height
     y = torch.empty(h, n, dtype=out, device=a.values.device)
+    if starts is not None:
+        require(starts)
+        if starts.shape != (groups,) or starts.dtype != torch.int32 or tiles is not None:
+            raise ValueError(f"rows: starts int32 ({groups},), without a tile list, not "
+                             f"{starts.dtype} {tuple(starts.shape)}")
+        ws = workspace(lib().bux_mx_grouped_rows_workspace_size(groups, m, h), y.device)
+        _lib.check(lib().bux_mx_grouped_rows_started(
+            ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(sizes), ptr(starts),
+            groups, m, n, k, h, _DTYPES[out], ptr(y), ptr(ws), ws.numel(), stream()))
+        return y
     if tiles is not None:
         if (tiles.groups, tiles.m, tiles.height) != (groups, m, h):
             raise ValueError(f"rows: a tile list for {tiles.groups} groups, m={tiles.m}, "

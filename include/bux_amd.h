@@ -99,9 +99,13 @@ int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_experts, in
  *           both copies take (so they hold the same codes, transposed): the mxfp8_2d
  *           recipe's weights, blockscaled.mx_tiles_twice (src/bux/architecture/
  *           precision/blockscaled.py:294-309).
+ *           With BUX_MX_HALVES, x's columns are a GLU's (up, gate) pairs, read as its
+ *           halves (quantized_twice's `halves`, grouped_triton.py:49,61-62, and
+ *           grouped_cudnn.halves_of, grouped_cudnn.py:150-155): in each 64 columns of
+ *           the copies, the 32 pairs' gates, then their ups; cols a multiple of 64.
  *           cols must be a multiple of 32.
  */
-enum { BUX_MX_ROWS = 1, BUX_MX_COLUMNS = 2, BUX_MX_TILES = 4 };
+enum { BUX_MX_ROWS = 1, BUX_MX_COLUMNS = 2, BUX_MX_TILES = 4, BUX_MX_HALVES = 8 };
 int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t groups,
                     int64_t rows, int64_t cols, int64_t height, const int32_t* filled, int flags,
                     uint8_t* values, uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
@@ -129,6 +133,21 @@ int bux_mx_grouped_rows(const uint8_t* a_values, const uint8_t* a_scales, const 
                         const uint8_t* b_scales, const int32_t* sizes, int32_t groups, int64_t m,
                         int64_t n, int64_t k, int64_t height, int out_dtype, void* y,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* bux_mx_grouped_rows_started: bux_mx_grouped_rows with each group's rows of a where
+ * `starts` (int32 [groups], on the device) puts them: group g's sizes[g] rows of a from
+ * row starts[g] on (the reference's `starts`, grouped_mxfp8.py:116-154, for groups laid
+ * out apart, e.g. at whole tiles as grouped_glu.padded lays them, grouped_glu.py:
+ * 239-272); y's rows stay packed (group g's from sum(sizes[:g])), and rows past the
+ * groups are 0. m: a's rows, past every group's last; the same workspace as
+ * bux_mx_grouped_rows. a's rows between the groups are read where a group's last tile
+ * reaches over them, and never reach y.
+ */
+int bux_mx_grouped_rows_started(const uint8_t* a_values, const uint8_t* a_scales,
+                                const uint8_t* b_values, const uint8_t* b_scales,
+                                const int32_t* sizes, const int32_t* starts, int32_t groups,
+                                int64_t m, int64_t n, int64_t k, int64_t height, int out_dtype,
+                                void* y, void* workspace, size_t workspace_bytes, void* stream);
 
 /* bux_mx_grouped_tiles: the rows GEMM's device prologue on its own, the reference's
  * tiles_of (grouped_mxfp8.py:157-182), whose result its rows and contract take as

@@ -128,18 +128,21 @@ def _cast(y: np.ndarray, out: str) -> np.ndarray:
     return bf16.to_bf16(y) if out == "bf16" else y.astype(np.float32)
 
 
-def rows_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16", height: int | None = None) -> np.ndarray:
+def rows_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16", height: int | None = None,
+            starts: np.ndarray | None = None) -> np.ndarray:
     """Return each group's rows of a times its matrix b[g]^T: a (m, k) and b
     (g, n, k) in MXFP8 along k, dequantized and multiplied in float32; rows past the
-    groups are 0 (grouped_blockscaled.py:220-233, grouped_mxfp8.py:116-154)."""
+    groups are 0 (grouped_blockscaled.py:220-233, grouped_mxfp8.py:116-154). With
+    `starts`, group g's rows of a start at starts[g], y's stay packed."""
     x = mxfp8.dequantized(a)
     w = mxfp8.dequantized(b)
     m = x.shape[0] if height is None else height
     y = np.zeros((m, w.shape[1]), np.float32)
     start = 0
     for g, size in enumerate(np.asarray(sizes).tolist()):
+        at = start if starts is None else int(starts[g])
         if size:
-            y[start:start + size] = x[start:start + size] @ w[g].T
+            y[start:start + size] = x[at:at + size] @ w[g].T
         start += size
     return _cast(y, out)
 

@@ -199,6 +199,21 @@ def from_mxfp8(packed: np.ndarray, d: int) -> np.ndarray:
     return bf16.to_bf16(dequantized(mx_unpacked(packed, d)))
 
 
+def halves_of(pairs: np.ndarray) -> np.ndarray:
+    """Where columns of (up, gate) pairs (unit u's up at 2u, its gate at 2u + 1) lie in a
+    GLU's halves: each 32 units take 64 columns, their gates first, then their ups
+    (grouped_cudnn.halves_of, grouped_cudnn.py:150-155)."""
+    unit, gate = np.asarray(pairs) // 2, np.asarray(pairs) % 2
+    return unit // 32 * 64 + (1 - gate) * 32 + unit % 32
+
+
+def read_as_halves(c: int) -> np.ndarray:
+    """The column of pairs that each of c columns in halves reads (the Triton
+    quantizer's `read`, grouped_triton.py:216-219)."""
+    cs = np.arange(c)
+    return cs // 64 * 64 + cs % 32 * 2 + (cs % 64 < 32).astype(np.int64)
+
+
 def quantized_twice(
     x: np.ndarray,
     filled: int,
@@ -206,6 +221,7 @@ def quantized_twice(
     index: np.ndarray | None = None,
     height: int | None = None,
     tiles: bool = False,
+    halves: bool = False,
 ) -> tuple[Blocks, Blocks | None]:
     """Return the MXFP8 copies a grouped GEMM's operand takes
     (grouped_blockscaled.py:296-317 off a Blackwell GPU; grouped_triton.py:44-101 for
@@ -221,6 +237,7 @@ def quantized_twice(
         height: rows of the copies, padded by 0 past x's (``ragged_dot``'s padding to
             whole tiles of 128, grouped_blockscaled.py:122-128); None for x's own.
         tiles: a scale per 32 x 32 tile, shared by both copies (`mx_tiles_twice`).
+        halves: x's columns, (up, gate) pairs, read as a GLU's halves (`read_as_halves`).
 
     Returns:
         The copies; a stack gives stacks (values (g, r, c) and (g, c, r)).
@@ -228,6 +245,8 @@ def quantized_twice(
     if x.dtype == np.uint16:
         x = bf16.to_f32(x)
     x = np.asarray(x, np.float32)
+    if halves:
+        x = x[..., read_as_halves(x.shape[-1])]
     if index is not None:
         index = np.asarray(index)
         rows = x[np.maximum(index, 0)]

@@ -64,8 +64,10 @@ def test_quantize_rejects_bad_shapes_and_flags(lib):
     assert rc == 1 and "flags" in _msg(lib)
     rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 4, p, p, p, p, None)
     assert rc == 1 and "flags=4" in _msg(lib)  # tiles alone: no copy asked for
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 8 | 1, p, p, p, p, None)
-    assert rc == 1 and "flags=9" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 16 | 1, p, p, p, p, None)
+    assert rc == 1 and "flags=17" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 96, 64, None, 8 | 1, p, p, p, p, None)
+    assert rc == 1 and "BUX_MX_HALVES" in _msg(lib)  # halves: whole 64s of columns
     rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 2, p, p, None, None, None)
     assert rc == 1 and "t_values" in _msg(lib)
     rc = lib.bux_mx_quantize(p, p, 1, 2, 64, 64, 64, None, 1, p, p, None, None, None)

@@ -383,3 +383,43 @@ def test_the_block_scaled_mfma_sum_is_within_its_error_bound(lib, kind, k):
           flush=True)
     assert ratio.max() <= SUM_ERROR[kind]
     assert float((ratio * scale).max()) <= MAX_OF_MAX * top
+
+
+@pytest.mark.parametrize("align", [256, 128])
+def test_rows_with_groups_apart_in_a(lib, align):
+    """`starts` (the reference's, grouped_mxfp8.py:116-154): each group's rows of a
+    laid out apart, at whole tiles as grouped_glu.padded lays them, with garbage
+    between; y packed. Against the oracle (float32 out, the GEMM bars) and bit for bit
+    against the packed GEMM on the packed rows (each row's tile position is the same)."""
+    from bux_amd import grouped_mxfp8 as gm
+    rng = np.random.default_rng(37 + align)
+    sizes = np.array([0, 130, 1, 3, 256, 0, 300, 100, 29], np.int32)
+    k, n = 256, 384
+    starts = np.zeros_like(sizes)
+    at = 0
+    for g, size in enumerate(sizes):
+        starts[g] = at
+        at += -(-int(size) // align) * align + align  # a spare tile between groups too
+    m = at
+    packed = _codes(rng, (int(sizes.sum()), k))
+    a_vals = rng.integers(0, 255, (m, k), dtype=np.uint8)  # garbage between the groups
+    a_scales = rng.integers(100, 140, (m, k // 32), dtype=np.uint8)
+    src = 0
+    for g, size in enumerate(sizes):
+        a_vals[starts[g]:starts[g] + size] = packed.values[src:src + size]
+        a_scales[starts[g]:starts[g] + size] = packed.scales[src:src + size]
+        src += size
+    a = mxfp8.Blocks(a_vals, a_scales)
+    b = _codes(rng, (len(sizes), n, k), 0.05)
+    height = int(sizes.sum()) + 60
+    announce("gemm rows with starts", align)
+    gs = to_gpu(sizes)
+    y = gm.rows(_gpu(a), _gpu(b), gs, torch.float32, height=height, starts=to_gpu(starts))
+    packed_pad = mxfp8.Blocks(np.concatenate([packed.values, np.zeros((60, k), np.uint8)]),
+                              np.concatenate([packed.scales, np.ones((60, k // 32), np.uint8)]))
+    y0 = gm.rows(_gpu(packed_pad), _gpu(b), gs, torch.float32, height=height)
+    torch.cuda.synchronize()
+    want = omoe.rows_mx(a, b, sizes, out="f32", height=height, starts=starts)
+    _close_f32(y.cpu().numpy(), want, f"rows with starts, align {align}")
+    assert torch.equal(y, y0)
+    assert (y[int(sizes.sum()):] == 0).all()

@@ -189,3 +189,33 @@ def test_config2_activations_full_size(lib):
         want = mxfp8.mx_quantize(np.ascontiguousarray(bf16.to_f32(block).T))
         np.testing.assert_array_equal(cols_v[:, 32 * b:32 * b + 32].cpu().numpy(), want.values)
         np.testing.assert_array_equal(cols_s[:, b].cpu().numpy(), want.scales[:, 0])
+
+
+@pytest.mark.parametrize("index", [False, True])
+def test_halves_read_a_glus_pairs_as_its_halves(lib, index):
+    """BUX_MX_HALVES (the reference's `halves`, grouped_triton.py:49): the columns of
+    (up, gate) pairs quantized as a GLU's halves, bit for bit the oracle's, for a stack
+    of kernels and for rows read by index."""
+    from bux_amd import grouped_mxfp8 as gm
+    from oracle import mxfp8 as omx
+    rng = np.random.default_rng(90)
+    announce("quantize halves", index)
+    if index:
+        x = normal_bf16(rng, (300, 384))
+        idx = rng.integers(0, 300 * 4, 1000).astype(np.int32)
+        idx[::17] = -1
+        got_k, got_m = gm.quantized_twice(to_gpu_bf16(x), None, True, to_gpu(idx), 4, 1024,
+                                          halves=True)
+        want_k, want_m = omx.quantized_twice(x, 1000, True, index=np.where(idx >= 0, idx // 4, -1),
+                                             height=1024, halves=True)
+        pairs = [(got_k, want_k, 384), (got_m, want_m, 1024)]
+    else:
+        x = normal_bf16(rng, (3, 256, 512), 0.05)
+        got_k, got_m = gm.quantized_twice(to_gpu_bf16(x), halves=True)
+        want_k, want_m = omx.quantized_twice(x, 256, True, halves=True)
+        pairs = [(got_k, want_k, 512), (got_m, want_m, 256)]
+    torch.cuda.synchronize()
+    for got, want, cols in pairs:
+        v, sc = untiled(got, cols)
+        np.testing.assert_array_equal(v, want.values)
+        np.testing.assert_array_equal(sc, want.scales)

@@ -595,3 +595,22 @@ def test_the_layer_with_no_pass_in_mxfp8_is_the_compute_layer_and_all_passes_the
     assert not np.array_equal(runs["none"][0], runs["all"][0])
 
 
+
+
+def test_the_quantizers_halves_read_is_the_inverse_of_halves_of():
+    """grouped_triton's `read` (which pair column each column in halves takes) and
+    grouped_cudnn.halves_of (where each pair column goes) are inverse permutations: a
+    GLU's halves quantized from pairs are the pairs quantized, permuted by halves_of."""
+    c = 256
+    read = mxfp8.read_as_halves(c)
+    assert sorted(read.tolist()) == list(range(c))
+    np.testing.assert_array_equal(mxfp8.halves_of(read), np.arange(c))
+    # in each 64: the 32 gates (odd pair columns), then the 32 ups
+    np.testing.assert_array_equal(read[:32], np.arange(1, 64, 2))
+    np.testing.assert_array_equal(read[32:64], np.arange(0, 64, 2))
+    rng = np.random.default_rng(14)
+    x = bf16.to_bf16(rng.standard_normal((64, c)).astype(np.float32))
+    a, at = mxfp8.quantized_twice(x, 64, True, halves=True)
+    b, bt = mxfp8.quantized_twice(x[:, read], 64, True)
+    np.testing.assert_array_equal(a.values, b.values)
+    np.testing.assert_array_equal(at.values, bt.values)
