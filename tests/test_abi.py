@@ -235,3 +235,16 @@ def test_tile_lists_reject_bad_arguments(lib):
     assert rc == 1 and "m=100" in _msg(lib)
     rc = lib.bux_mx_grouped_contract_listed(p, p, p, p, p, 16, 4, 64, 64, 128, 0, p, None)
     assert rc == 2 and "16 bytes" in _msg(lib)
+
+
+def test_every_entry_point_has_an_xla_ffi_handler():
+    """bux_amd/xla/xla_ffi.cc binds every compute entry point for jax.ffi (the workspace
+    sizes are trace-time queries through ctypes; the entry point that allocates nothing
+    is for callers outside XLA, which owns every buffer)."""
+    src = open(os.path.join(ROOT, "bux_amd", "xla", "xla_ffi.cc")).read()
+    called = set(re.findall(r"\b(bux_\w+)\(", src)) - {"bux_last_error"}
+    wanted = {n for n in _declared()
+              if not n.endswith("_workspace_size")
+              and n not in ("bux_last_error", "bux_version", "bux_mx_grouped_rows_noalloc")}
+    assert wanted <= called, wanted - called
+    assert len(re.findall(r"XLA_FFI_DEFINE_HANDLER_SYMBOL\(", src)) == len(wanted)
