@@ -75,8 +75,11 @@ SIGNATURES = {
     "bux_mx_grouped_contract_workspace_size": (_size, [_i32]),
     "bux_mx_grouped_contract": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
-    "bux_bf16_grouped_rows": (_int, [_p, _p, _int, _p, _i32, _i64, _i64, _i64, _p, _p]),
-    "bux_bf16_grouped_contract": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p]),
+    "bux_bf16_grouped_rows_workspace_size": (_size, [_i32, _i64]),
+    "bux_bf16_grouped_rows": (
+        _int, [_p, _p, _int, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
+    "bux_bf16_grouped_contract_workspace_size": (_size, [_i32]),
+    "bux_bf16_grouped_contract": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
     "bux_token_rows": (_int, [_p, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums_biased": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p, _i32, _p, _p, _p]),

@@ -1,236 +1,432 @@
 // bfloat16 grouped GEMMs (the experts in "compute" precision) on CDNA4's
-// v_mfma_f32_32x32x16_bf16, float32 accumulation, bfloat16 out.
+// v_mfma_f32_32x32x16_bf16: float32 sums, bfloat16 out.
 //
-//   rows      y[i] = x[i] w[g(i)]   (w [g, k, n]) or x[i] w[g(i)]^T (w [g, n, k])
-//             grouped.dot / jax.lax.ragged_dot, src/bux/architecture/experts/
-//             grouped.py:90-102: rows past sum(sizes) are 0.
+//   rows      y[i] = x[i] w[g(i)]   (w [g, k, n]) or x[i] w[g(i)]^T (w [g, n, k], the
+//             dgrad): grouped.dot / jax.lax.ragged_dot, src/bux/architecture/experts/
+//             grouped.py:90-102; rows past sum(sizes) are 0.
 //   contract  dw[g] = x[rows of g]^T dy[rows of g]   grouped.py:105-146.
 //
-// One mainloop computes C[r][c] = sum_k A(r, k) B(c, k) over a 128 x 128 tile, in steps
-// of 32 of k through LDS ([row][k], rows padded to 80 bytes so that ds_read_b128 of 32
-// consecutive rows spreads over the banks). An operand is "k-major" (A(r, k) at
-// p[r ld + k]) or "mn-major" (p[k ld + r]); an mn-major operand is transposed on its
-// way into LDS. Rows (or ks) outside a window read 0, which is how a tile that several
-// groups share multiplies each group's rows by its own matrix into one accumulator.
-// Not the MXFP8 hot path: it serves the experts' "compute" format (config 1).
+// The schedule is the MXFP8 GEMMs' (tiles.h): a tile list built on the device, a
+// persistent grid split by XCD, 256 x 256 output tiles of 4 waves (each 128 x 128 as
+// 4 x 4 MFMAs of 32 x 32: 256 accumulator registers, one wave a SIMD) and a ring of 4
+// LDS stages that direct loads (buffer_load ... lds) fill 4 steps ahead. A step is 32 of
+// K, 64 bytes of an operand's row: 32 MFMAs a wave, the same MFMA time for the bytes
+// loaded as an MXFP8 step's 16 MFMAs at twice the rate.
+//
+// Operands arrive as the reference holds them, in two layouts, and either sits in a
+// stage as it lies in memory:
+//  - K-major, A(r, k) at p[r ld + k] (x; w of the dgrad): a stage holds 256 rows of 64
+//    bytes, 16-byte chunk c of row r at place c ^ ((r / 4) % 4) (16 lanes of a
+//    ds_read_b128 read one chunk of 16 rows, every bank once); a lane's MFMA operand (row
+//    l % 32, K 8 (l / 32) .. + 7) is one ds_read_b128.
+//  - MN-major, A(r, k) at p[k ld + r] (w of the fprop; x and dy of the wgrad): a stage
+//    holds 32 rows of K of 512 bytes (the tile's 256 r), chunk c of K row k at place
+//    c ^ 4 (k % 4). gfx950's ds_read_b64_tr_b16 transposes on the way out of LDS:
+//    measured on the MI355X, within each 16 lanes, lane j's 16-bit element e is element
+//    j % 4 of the 8 bytes that lane 4 e + j / 4 read. So lane s of a 16 reads K row s / 4
+//    at r = 4 (s % 4) .. + 3 (16 more in the odd 16), and lane j ends up with column
+//    j of 4 consecutive K rows: two such reads make the MFMA's operand. The 32 lanes of
+//    one read touch 4 K rows x 64 bytes, the swizzle putting each row's 64 bytes on
+//    banks of their own.
+//
+// Edges: rows and K rows past an operand read 0 (the buffer resource ends there); a
+// K step that holds K positions that are not the tile's (the wgrad's group boundaries;
+// K past the rows GEMM's k) has both operands' registers of those positions zeroed
+// before its MFMAs, so that nothing past them, NaN included, reaches a sum.
 
-#include "common.h"
+#include "tiles.h"
 
 namespace bux {
 namespace {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef float v16f __attribute__((ext_vector_type(16)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+typedef __attribute__((address_space(3))) uint4 lds_u4;
 
-constexpr int BM = 128, BN = 128, BK = 32, THREADS = 256;
-constexpr int PITCH = 40;  // bfloat16 a row of an LDS tile
-constexpr int MAX_GROUPS = 4096;
+constexpr int BK = 32;     // K a step
+constexpr int LOADS = 8;   // direct loads a wave issues a step: 4 of A, 4 of B
 
+// A matrix: `p` (a group's matrix of B: p + group `stride`), `ld` elements from one row
+// (K-major) or one K row (MN-major) to the next, `bytes` of it readable from there.
 struct Operand {
   const uint16_t* p;
-  int64_t ld;
-  bool k_major;
-  int64_t rows;  // rows r there are
-  int64_t ks;    // ks there are
+  int32_t ld;
+  int32_t bytes;
+  int64_t stride;
 };
 
-struct Window {
-  int64_t lo, hi;  // rows (k_major) or ks of A that read as themselves; others read 0
-  bool on_k;
+struct Stage {
+  uint16_t a[BM * BK];
+  uint16_t b[BN * BK];
+};
+struct Lds {
+  Stage st[STAGES];
+};
+constexpr uint32_t B_AT = offsetof(Stage, b);
+
+// A wave's direct loads of one operand's tile: its lane's offset, and the scalar bytes
+// from one of its 4 loads of a step to the next and from one K step to the next.
+//  K-major: wave w's load i holds rows 64 w + 16 i .. + 15 (1 KiB of LDS), lane l row
+//    l / 4, the chunk that belongs in place l % 4.
+//  MN-major: wave w's load i holds K rows 8 i + 2 w and + 1, lane l K row l / 32 and
+//    the chunk that belongs in place l % 32. (Place ^ chunk depends on the K row mod 4,
+//    the same for every i.)
+struct Loads {
+  i32x4 rsrc;
+  int32_t voff, slice, step;
 };
 
-// Global -> LDS for K step k0 of an operand's 128 rows from row0.
-__device__ __forceinline__ void load_tile(uint16_t* lds, const Operand& op, int64_t row0,
-                                          int64_t k0, const Window* window) {
-  const int t = threadIdx.x;
+template <bool KM>
+__device__ __forceinline__ Loads loads_for(const uint16_t* p, int32_t ld, int32_t bytes, int32_t row0) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  Loads o;
+  o.rsrc = resource(p, bytes);
+  if (KM) {
+    o.voff = (row0 + w * 64 + (l >> 2)) * ld * 2 + 16 * ((l & 3) ^ ((l >> 4) & 3));
+    o.slice = 16 * ld * 2;
+    o.step = BK * 2;
+  } else {
+    const int k = 2 * w + (l >> 5);
+    o.voff = k * ld * 2 + row0 * 2 + 16 * ((l & 31) ^ (4 * (k & 3)));
+    o.slice = 8 * ld * 2;
+    o.step = BK * ld * 2;
+  }
+  return o;
+}
+
+// Where in its operand's part of a stage wave w's load i lands.
+template <bool KM>
+__device__ __forceinline__ uint32_t slice_at(uint32_t w, int i) {
+  return KM ? w * 4096 + i * 1024 : (8 * i + 2 * w) * 512;
+}
+
+// This lane's byte offsets of its MFMA operands in an operand's part of a stage:
+//  K-major: of 32-row block 0, K 0 .. 15 (off[0]) and 16 .. 31 (off[1]); block p 2048
+//    bytes further.
+//  MN-major: of the first of the two reads of block p (off[p]), K 0 .. 15; the second
+//    read 4 K rows (2048 bytes) further, K 16 .. 31 16 K rows (8192 bytes) further.
+template <bool KM>
+__device__ __forceinline__ void lane_offsets(int32_t off[4], int wbase) {
+  const int l = threadIdx.x & 63;
+  if (KM) {
+    const int row = wbase + (l & 31), sw = ((l & 31) >> 2) & 3;
+    off[0] = row * 64 + 16 * ((l >> 5) ^ sw);
+    off[1] = row * 64 + 16 * ((2 + (l >> 5)) ^ sw);
+    off[2] = off[3] = 0;
+  } else {
+    const int s = l & 15, kq = s >> 2;
+    const int k = 8 * (l >> 5) + kq;
+    const int col = 16 * ((l >> 4) & 1) + 4 * (s & 3);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (op.k_major) {
-      const int r = (t >> 2) + 64 * i, chunk = t & 3;
-      const int64_t row = row0 + r, k = k0 + 8 * chunk;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      bool ok = row < op.rows && k < op.ks;
-      if (window && !window->on_k) ok = ok && row >= window->lo && row < window->hi;
-      if (window && window->on_k) ok = ok && k >= window->lo && k + 8 <= window->hi;
-      if (ok) v = *reinterpret_cast<const uint4*>(op.p + row * op.ld + k);
-      if (window && window->on_k && row < op.rows && k < op.ks && !ok) {
-        // a chunk across the window's edge: element by element
-        uint16_t e[8];
+    for (int p = 0; p < 4; ++p)
+      off[p] = k * 512 + 16 * (wbase / 8 + 4 * (p ^ kq) + (col >> 3)) + 8 * ((col >> 2) & 1);
+  }
+}
+
+__device__ __forceinline__ v8bf read16(uint32_t at) {
+  return __builtin_bit_cast(v8bf, *reinterpret_cast<const lds_u4*>(at));
+}
+__device__ __forceinline__ v8bf read_tr(uint32_t at) {
+  const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4s*>(at));
+  const v4s y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4s*>(at + 2048));
+  return __builtin_bit_cast(v8bf, __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Block p's operand registers of K half s (K 16 s .. 16 s + 15 of the step) from an
+// operand's part of a stage at LDS address `at`.
+template <bool KM>
+__device__ __forceinline__ v8bf read_block(uint32_t at, const int32_t off[4], int p, int s) {
+  return KM ? read16(at + p * 2048 + off[s]) : read_tr(at + off[p] + s * 8192);
+}
+
+// Zeroes the 16-bit elements of v whose K (k0 + e for element e) lies outside [lo, hi).
+__device__ __forceinline__ v8bf masked(v8bf v, int32_t k0, int32_t lo, int32_t hi) {
+  u32x4 u = __builtin_bit_cast(u32x4, v);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int64_t kk = k + j;
-          e[j] = (kk >= window->lo && kk < window->hi) ? op.p[row * op.ld + kk] : 0;
+  for (int d = 0; d < 4; ++d) {
+    const int32_t k = k0 + 2 * d;
+    const uint32_t keep = (k >= lo && k < hi ? 0xffffu : 0u) | (k + 1 >= lo && k + 1 < hi ? 0xffff0000u : 0u);
+    u[d] &= keep;
+  }
+  return __builtin_bit_cast(v8bf, u);
+}
+
+// The bfloat16 format's part of the shared pipeline (run_tiles): A K-major or not (AK),
+// B likewise (BKM).
+template <bool AK, bool BKM>
+struct Bf16 {
+  using Operand = bux::Operand;
+  using Lds = bux::Lds;
+  using Loads = bux::Loads;
+  struct Lanes {
+    int32_t a[4], b[4];
+  };
+  // A wave's operands of one step: 4 blocks of 32 rows of A and of B, each in two K
+  // halves of 16.
+  struct Frag {
+    v8bf a[4][2], b[4][2];
+  };
+
+  __device__ static __forceinline__ Loads loads_a(const Operand& a, int32_t row0) {
+    return loads_for<AK>(a.p, a.ld, a.bytes, row0);
+  }
+  __device__ static __forceinline__ Loads loads_b(const Operand& b, int32_t group, int32_t row0) {
+    return loads_for<BKM>(b.p + group * b.stride, b.ld, b.bytes, row0);
+  }
+
+  // Direct load Q (0..7) of K step ks into stage `st`: even Q A's load Q / 2, odd B's.
+  template <int Q>
+  __device__ static __forceinline__ void issue_one(const Loads& la, const Loads& lb, int32_t ks,
+                                                   uint32_t lds0, int st) {
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t at = lds0 + static_cast<uint32_t>(st * sizeof(Stage));
+    constexpr int i = Q >> 1;
+    if ((Q & 1) == 0)
+      load_lds16(la.rsrc, at + slice_at<AK>(w, i), la.voff, ks * la.step + i * la.slice);
+    else
+      load_lds16(lb.rsrc, at + B_AT + slice_at<BKM>(w, i), lb.voff, ks * lb.step + i * lb.slice);
+  }
+  template <int Q>
+  __device__ static __forceinline__ void issue_from(const Loads& la, const Loads& lb, int32_t ks,
+                                                    uint32_t lds0, int st) {
+    issue_one<Q>(la, lb, ks, lds0, st);
+    if constexpr (Q + 1 < LOADS) issue_from<Q + 1>(la, lb, ks, lds0, st);
+  }
+  __device__ static __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks,
+                                               uint32_t lds0, int st) {
+    issue_from<0>(la, lb, ks, lds0, st);
+  }
+
+  // Waits until at most `steps` steps' loads of this wave are in flight (a wave's loads
+  // complete in the order they were issued).
+  __device__ static __forceinline__ void wait_loads(int32_t steps) {
+    if (steps >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    else if (steps == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (steps == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+
+  __device__ static __forceinline__ Lanes lanes_of() {
+    const int wave = threadIdx.x >> 6;
+    Lanes ln;
+    lane_offsets<AK>(ln.a, (wave >> 1) * 128);
+    lane_offsets<BKM>(ln.b, (wave & 1) * 128);
+    return ln;
+  }
+
+  // Read item x (0..15) of a step's operands, in the order its MFMAs take them: K half
+  // x / 8, then A's block 0, B's blocks 0-3, A's blocks 1-3.
+  __device__ static __forceinline__ void read_item(Frag& f, uint32_t at, const Lanes& ln, int x) {
+    const int s = x >> 3, y = x & 7;
+    if (y == 0) f.a[0][s] = read_block<AK>(at, ln.a, 0, s);
+    else if (y <= 4) f.b[y - 1][s] = read_block<BKM>(at + B_AT, ln.b, y - 1, s);
+    else f.a[y - 4][s] = read_block<AK>(at, ln.a, y - 4, s);
+  }
+
+  // All of a step's operands from stage `st`.
+  __device__ static __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& ln, int st,
+                                                   int32_t) {
+    const uint32_t at = lds_at(&lds) + static_cast<uint32_t>(st * sizeof(Stage));
+#pragma unroll
+    for (int x = 0; x < 16; ++x) read_item(f, at, ln, x);
+  }
+
+  // Zeroes the K positions of step ks outside [lo, hi) in both operands: lane half h
+  // holds K 16 s + 8 h .. + 7 of the step in its registers of half s.
+  __device__ static __forceinline__ void mask_frag(Frag& f, int32_t ks, int32_t lo, int32_t hi) {
+    const int h = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int32_t k0 = ks * BK + 16 * s + 8 * h;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        f.a[p][s] = masked(f.a[p][s], k0, lo, hi);
+        f.b[p][s] = masked(f.b[p][s], k0, lo, hi);
+      }
+    }
+  }
+
+  // The 32 MFMAs of one step on `cur` (K half q / 16, A's block (q / 4) % 4, B's block
+  // q % 4), each followed by a slice of the memory work: with LOAD, the next loads (step
+  // ks_load into stage st_load) after MFMAs 1, 5, .. 29; with READ, the next step's
+  // operands into `nxt` after the even MFMAs, in the order its MFMAs take them.
+  template <bool LOAD, bool READ>
+  __device__ static __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la,
+                                              const Loads& lb, const Lds&, uint32_t lds0,
+                                              const Lanes& ln, int32_t ks_load, int st_load,
+                                              int32_t, int st_next, v16f acc[4][4]) {
+    const uint32_t next_at = lds0 + static_cast<uint32_t>(st_next * sizeof(Stage));
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      const int s = q >> 4, i = (q >> 2) & 3, j = q & 3;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.b[j][s], cur.a[i][s], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (LOAD && (q & 3) == 1) {
+        switch (q >> 2) {
+          case 0: issue_one<0>(la, lb, ks_load, lds0, st_load); break;
+          case 1: issue_one<1>(la, lb, ks_load, lds0, st_load); break;
+          case 2: issue_one<2>(la, lb, ks_load, lds0, st_load); break;
+          case 3: issue_one<3>(la, lb, ks_load, lds0, st_load); break;
+          case 4: issue_one<4>(la, lb, ks_load, lds0, st_load); break;
+          case 5: issue_one<5>(la, lb, ks_load, lds0, st_load); break;
+          case 6: issue_one<6>(la, lb, ks_load, lds0, st_load); break;
+          default: issue_one<7>(la, lb, ks_load, lds0, st_load); break;
         }
-        v = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
-                       e[6] | (e[7] << 16));
       }
-      *reinterpret_cast<uint4*>(lds + r * PITCH + 8 * chunk) = v;
-    } else {
-      const int kk = (t >> 4) + 16 * i, chunk = t & 15;
-      const int64_t k = k0 + kk, row = row0 + 8 * chunk;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      bool ok = k < op.ks && row < op.rows;
-      if (window && window->on_k) ok = ok && k >= window->lo && k < window->hi;
-      if (ok) v = *reinterpret_cast<const uint4*>(op.p + k * op.ld + row);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint16_t e = static_cast<uint16_t>(w[j >> 1] >> (16 * (j & 1)));
-        if (window && !window->on_k && (row + j < window->lo || row + j >= window->hi)) e = 0;
-        lds[(8 * chunk + j) * PITCH + kk] = e;
-      }
+      if (READ && (q & 1) == 0) read_item(nxt, next_at, ln, q >> 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-}
+};
 
-__device__ __forceinline__ v8bf fragment(const uint16_t* lds, int row, int k) {
-  const uint4 v = *reinterpret_cast<const uint4*>(lds + row * PITCH + k);
-  return __builtin_bit_cast(v8bf, v);
-}
+// --- the epilogue ------------------------------------------------------------------------
 
-__device__ void mainloop(const Operand& A, int64_t a_row0, const Operand& B, int64_t b_row0,
-                         int64_t k_begin, int64_t k_end, const Window* window, uint16_t* lds_a,
-                         uint16_t* lds_b, v16f acc[2][2]) {
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+// Output stores are non-temporal: the tile is written once and read by another kernel,
+// and a round of tiles' outputs passing through the XCD's L2 would evict the operands
+// the other CUs are about to reuse.
+constexpr int NT = 2;  // a buffer store's cache policy: non-temporal
+
+// The tile's rows [0, rows) and columns [0, cols) (cols a multiple of 8) at row pitch
+// ld from its corner, bfloat16 (v_cvt_pk_bf16_f32: nearest even), through the stage the
+// tile's last step left: in 4 rounds of 32 rows, each wave puts its 32 x 128 outputs in
+// a region of its own (8 KiB: 256 bytes a row, 16-byte chunk c of row r at place
+// c ^ (r % 16) and its two 8-byte halves swapped in rows 16 .. 31, so that the 64 lanes
+// of a write fill every bank twice and the 16 lanes that read a row back read it once
+// each), reads it back 16 bytes a lane, 16 lanes a row, and stores 4 runs of 256 bytes an
+// instruction. No other wave touches the region: no workgroup barrier.
+__device__ void store_tile(const v16f acc[4][4], uint16_t* tile, int32_t ld, int32_t rows,
+                           int32_t cols, Stage& stage) {
+  static_assert(4 * 32 * 256 == sizeof(Stage), "the epilogue's regions fill a stage");
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  for (int64_t k0 = k_begin; k0 < k_end; k0 += BK) {
-    load_tile(lds_a, A, a_row0, k0, window);
-    load_tile(lds_b, B, b_row0, k0, nullptr);
-    __syncthreads();
+  uint8_t* region = reinterpret_cast<uint8_t*>(&stage) + wave * 32 * 256;
+  // Lane l writes row l % 32 of the block, its 4 columns of each 8 at half l / 32.
+  const int r = lane & 31;
+  uint8_t* mine = region + r * 256 + 8 * ((lane >> 5) ^ (r >> 4));
+  const int sw = r & 15;
+  // ... and reads back chunk l % 16 (8 columns) of rows l / 16 + 4 it.
+  const int cc = lane & 15;
+  const int32_t col = wn * 128 + 8 * cc;
+  const bool whole = rows >= BM && cols >= BN;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(tile, 0, 0x7fffffff, 0x00020000);
+  const int32_t lane_off = ((wm * 128 + (lane >> 4)) * ld + col) * 2;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int k = 16 * sub + 8 * (lane >> 5);
-      v8bf a[2], b[2];
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[i] = fragment(lds_a, wm * 64 + 32 * i + (lane & 31), k);
-        b[i] = fragment(lds_b, wn * 64 + 32 * i + (lane & 31), k);
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const v16f& a = acc[i][j];
+        const bf16x2 lo = __builtin_convertvector((f32x2{a[4 * g], a[4 * g + 1]}), bf16x2);
+        const bf16x2 hi = __builtin_convertvector((f32x2{a[4 * g + 2], a[4 * g + 3]}), bf16x2);
+        *reinterpret_cast<uint2*>(mine + 16 * ((4 * j + g) ^ sw)) =
+            make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
       }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    // All 8 reads of the round go out before its first store.
+    uint4 v[8];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    for (int it = 0; it < 8; ++it) {
+      const int row = (lane >> 4) + 4 * it;
+      const uint4 t = *reinterpret_cast<const uint4*>(region + row * 256 + 16 * (cc ^ (row & 15)));
+      v[it] = it < 4 ? t : make_uint4(t.z, t.w, t.x, t.y);
     }
-    __syncthreads();
-  }
-}
-
-__device__ void store(const v16f acc[2][2], uint16_t* out, int64_t ld, int64_t row0, int64_t col0,
-                      int64_t rows, int64_t cols) {
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+    if (whole) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int it = 0; it < 8; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[it].x, v[it].y, v[it].z, v[it].w}, rsrc,
+                                               lane_off, (i * 32 + it * 4) * ld * 2, NT);
+    } else if (col < cols) {
+      uint16_t* out = tile + (wm * 128 + (lane >> 4)) * ld + col;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = col0 + wn * 64 + 32 * j + (lane & 31);
-      if (col >= cols) continue;
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int64_t row = row0 + wm * 64 + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-        if (row < rows) out[row * ld + col] = f32_to_bf16(acc[i][j][q]);
+      for (int it = 0; it < 8; ++it) {
+        const int32_t row = wm * 128 + i * 32 + it * 4 + (lane >> 4);
+        if (row < rows)
+          __builtin_nontemporal_store(u32x4{v[it].x, v[it].y, v[it].z, v[it].w},
+                                      reinterpret_cast<u32x4*>(out + (i * 32 + it * 4) * ld));
       }
     }
+    // The reads are done before the next round's writes.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+  }
 }
 
-// starts[0..groups] of the sizes, in LDS, by one workgroup.
-__device__ void group_starts(const int32_t* sizes, int32_t groups, int32_t* starts,
-                             int32_t* partial) {
-  const int t = threadIdx.x;
-  const int per = (groups + THREADS - 1) / THREADS;
-  const int lo = t * per, hi = lo + per < groups ? lo + per : groups;
-  int32_t sum = 0;
-  for (int i = lo; i < hi; ++i) sum += sizes[i];
-  partial[t] = sum;
-  __syncthreads();
-  for (int step = 1; step < THREADS; step <<= 1) {
-    const int32_t add = t >= step ? partial[t - step] : 0;
-    __syncthreads();
-    partial[t] += add;
-    __syncthreads();
+struct Out {
+  uint16_t* out;
+  int32_t ld;
+  __device__ __forceinline__ void store(const v16f acc[4][4], const Job& j, Stage& stage) const {
+    store_tile(acc, out + j.corner, ld, j.rows, j.cols, stage);
   }
-  int32_t run = t > 0 ? partial[t - 1] : 0;
-  for (int i = lo; i < hi; ++i) {
-    starts[i] = run;
-    run += sizes[i];
-  }
-  if (t == THREADS - 1) starts[groups] = partial[THREADS - 1];
-  __syncthreads();
+};
+
+// --- the kernels: one workgroup a CU -------------------------------------------------------
+
+// rows: A = x (K-major), B = w (K-major when transposed); TAIL: k is not a whole number
+// of steps.
+template <bool BKM, bool TAIL>
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_kernel(
+    Operand A, Operand B, int32_t groups, int32_t m, int32_t n, int32_t k,
+    const int32_t* __restrict__ starts, const Tile* __restrict__ tiles, int32_t col_tiles,
+    uint16_t* __restrict__ y) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  if (!list_fits(starts, groups, m, m)) return;
+  Lds& lds = *reinterpret_cast<Lds*>(smem);
+  const RowsTiles<TAIL> list{tiles, groups, n, m, col_tiles, (k + BK - 1) / BK, k};
+  const int32_t count = starts[groups + 1] * col_tiles;
+  run_tiles<Bf16<true, BKM>>(list, count, A, B, lds, Out{y, n});
 }
 
-__global__ __launch_bounds__(THREADS) void rows_kernel(const uint16_t* __restrict__ x,
-                                                       const uint16_t* __restrict__ w,
-                                                       int w_transposed,
-                                                       const int32_t* __restrict__ sizes,
-                                                       int32_t groups, int64_t m, int64_t n,
-                                                       int64_t k, int64_t col_tiles,
-                                                       uint16_t* __restrict__ y) {
-  __shared__ __align__(16) uint16_t lds_a[BM * PITCH];
-  __shared__ __align__(16) uint16_t lds_b[BN * PITCH];
-  __shared__ int32_t starts[MAX_GROUPS + 1];
-  __shared__ int32_t partial[THREADS];
-  const int64_t row0 = (blockIdx.x / col_tiles) * BM;
-  const int64_t col0 = (blockIdx.x % col_tiles) * BN;
-  group_starts(sizes, groups, starts, partial);
-  v16f acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
-  const Operand A{x, k, true, m, k};
-  for (int g = 0; g < groups; ++g) {
-    const int64_t lo = starts[g], hi = starts[g + 1];
-    if (hi <= row0 || lo >= row0 + BM || lo >= hi) continue;
-    const uint16_t* wg = w + static_cast<int64_t>(g) * k * n;
-    const Operand B = w_transposed ? Operand{wg, k, true, n, k} : Operand{wg, n, false, n, k};
-    const Window window{lo, hi, false};
-    mainloop(A, row0, B, col0, 0, k, &window, lds_a, lds_b, acc);
-  }
-  store(acc, y, n, row0, col0, m, n);
+// contract: A = x, B = dy, both MN-major over the rows (K).
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void contract_kernel(
+    Operand A, Operand B, int32_t groups, int32_t d, int32_t f, const int32_t* __restrict__ starts,
+    int32_t d_tiles, int32_t f_tiles, uint16_t* __restrict__ dw) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  if (!list_fits(starts, groups, -1, 0)) return;
+  Lds& lds = *reinterpret_cast<Lds*>(smem);
+  const ContractTiles list{starts, d, f, d_tiles, f_tiles, BK};
+  const int32_t count = groups * d_tiles * f_tiles;
+  run_tiles<Bf16<false, false>>(list, count, A, B, lds, Out{dw, f});
 }
 
-__global__ __launch_bounds__(THREADS) void contract_kernel(const uint16_t* __restrict__ x,
-                                                           const uint16_t* __restrict__ dy,
-                                                           const int32_t* __restrict__ sizes,
-                                                           int32_t groups, int64_t m, int64_t k,
-                                                           int64_t n, int64_t k_tiles,
-                                                           int64_t n_tiles,
-                                                           uint16_t* __restrict__ dw) {
-  __shared__ __align__(16) uint16_t lds_a[BM * PITCH];
-  __shared__ __align__(16) uint16_t lds_b[BN * PITCH];
-  __shared__ int32_t starts[MAX_GROUPS + 1];
-  __shared__ int32_t partial[THREADS];
-  const int64_t per_group = k_tiles * n_tiles;
-  const int64_t g = blockIdx.x / per_group, rest = blockIdx.x % per_group;
-  const int64_t row0 = (rest / n_tiles) * BM, col0 = (rest % n_tiles) * BN;
-  group_starts(sizes, groups, starts, partial);
-  v16f acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
-  const int64_t lo = starts[g], hi = starts[g + 1];
-  if (hi > lo) {
-    // A(r, i) = x[i][r] and B(c, i) = dy[i][c]: both mn-major over the rows i.
-    const Operand A{x, k, false, k, m};
-    const Operand B{dy, n, false, n, m};
-    const Window window{lo, hi, true};
-    mainloop(A, row0, B, col0, lo / BK * BK, hi, &window, lds_a, lds_b, acc);
-  }
-  store(acc, dw + g * k * n, n, row0, col0, k, n);
+// Whether every offset a kernel forms into an operand of `rows` rows of `cols` elements
+// (a tile's reads past it included) fits the 32-bit buffer offsets.
+bool fits(int64_t rows, int64_t cols) { return (rows + BM) * (cols + BM) * 2 < (1LL << 31); }
+
+template <bool BKM, bool TAIL>
+int launch_rows(const Operand& A, const Operand& B, int32_t groups, int64_t m, int64_t n,
+                int64_t k, const void* list, hipStream_t s, uint16_t* y) {
+  const int64_t col_tiles = ceil_div(n, BN), slots = row_slots(groups, m, m);
+  if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_bf16_grouped_rows: too many tiles");
+  unsigned blocks = 0;
+  if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
+  if (int rc = allow_lds(rows_kernel<BKM, TAIL>, sizeof(Lds), "bf16 rows_kernel")) return rc;
+  hipLaunchKernelGGL((rows_kernel<BKM, TAIL>), dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B,
+                     groups, static_cast<int32_t>(m), static_cast<int32_t>(n),
+                     static_cast<int32_t>(k), starts_in(list), tiles_in(list, groups),
+                     static_cast<int32_t>(col_tiles), y);
+  return launched("bf16 rows_kernel");
 }
 
 }  // namespace
 }  // namespace bux
 
+extern "C" size_t bux_bf16_grouped_rows_workspace_size(int32_t groups, int64_t m) {
+  using namespace bux;
+  return starts_bytes(groups) + static_cast<size_t>(row_slots(groups, m, m)) * sizeof(Tile);
+}
+
 extern "C" int bux_bf16_grouped_rows(const uint16_t* x, const uint16_t* w, int w_transposed,
                                      const int32_t* sizes, int32_t groups, int64_t m, int64_t n,
-                                     int64_t k, uint16_t* y, void* stream) {
+                                     int64_t k, uint16_t* y, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   using namespace bux;
   clear_error();
   BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "bux_bf16_grouped_rows: groups=%d outside [1, %d]",
@@ -239,19 +435,39 @@ extern "C" int bux_bf16_grouped_rows(const uint16_t* x, const uint16_t* w, int w
             (long long)m, (long long)n, (long long)k);
   BUX_CHECK(n % 8 == 0 && k % 8 == 0, "bux_bf16_grouped_rows: n=%lld and k=%lld must be multiples of 8",
             (long long)n, (long long)k);
+  BUX_CHECK(fits(m, k) && (w_transposed ? fits(n, k) : fits(k, n)),
+            "bux_bf16_grouped_rows: an operand of m=%lld n=%lld k=%lld exceeds 2 GiB", (long long)m,
+            (long long)n, (long long)k);
+  BUX_CHECK(sizes && w && y && (m == 0 || x), "bux_bf16_grouped_rows: NULL buffer");
+  const size_t need = bux_bf16_grouped_rows_workspace_size(groups, m);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(BUX_E_WORKSPACE, "bux_bf16_grouped_rows: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
   if (m == 0) return BUX_OK;
-  BUX_CHECK(x && w && sizes && y, "bux_bf16_grouped_rows: NULL buffer");
-  const int64_t col_tiles = ceil_div(n, BN);
-  const int64_t blocks = ceil_div(m, BM) * col_tiles;
-  BUX_CHECK(blocks < (1LL << 31), "bux_bf16_grouped_rows: too many tiles");
-  hipLaunchKernelGGL(rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0,
-                     as_stream(stream), x, w, w_transposed, sizes, groups, m, n, k, col_tiles, y);
-  return launched("bf16 rows_kernel");
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, m,
+                     row_slots(groups, m, m), 1, starts_in(workspace), tiles_in(workspace, groups),
+                     header_in(workspace), m, nullptr);
+  if (int rc = launched("prologue_kernel")) return rc;
+  const Operand A{x, static_cast<int32_t>(k), static_cast<int32_t>(m * k * 2), 0};
+  const Operand B{w, static_cast<int32_t>(w_transposed ? k : n), static_cast<int32_t>(n * k * 2), n * k};
+  const bool tail = k % BK != 0;
+  if (w_transposed)
+    return tail ? launch_rows<true, true>(A, B, groups, m, n, k, workspace, s, y)
+                : launch_rows<true, false>(A, B, groups, m, n, k, workspace, s, y);
+  return tail ? launch_rows<false, true>(A, B, groups, m, n, k, workspace, s, y)
+              : launch_rows<false, false>(A, B, groups, m, n, k, workspace, s, y);
+}
+
+extern "C" size_t bux_bf16_grouped_contract_workspace_size(int32_t groups) {
+  using namespace bux;
+  return starts_bytes(groups);  // the group starts alone: header, starts
 }
 
 extern "C" int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, const int32_t* sizes,
                                          int32_t groups, int64_t m, int64_t k, int64_t n,
-                                         uint16_t* dw, void* stream) {
+                                         uint16_t* dw, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
   using namespace bux;
   clear_error();
   BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS,
@@ -261,11 +477,29 @@ extern "C" int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, 
   BUX_CHECK(n % 8 == 0 && k % 8 == 0,
             "bux_bf16_grouped_contract: k=%lld and n=%lld must be multiples of 8", (long long)k,
             (long long)n);
-  BUX_CHECK(x && dy && sizes && dw, "bux_bf16_grouped_contract: NULL buffer");
-  const int64_t k_tiles = ceil_div(k, BM), n_tiles = ceil_div(n, BN);
-  const int64_t blocks = static_cast<int64_t>(groups) * k_tiles * n_tiles;
-  BUX_CHECK(blocks < (1LL << 31), "bux_bf16_grouped_contract: too many tiles");
-  hipLaunchKernelGGL(contract_kernel, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0,
-                     as_stream(stream), x, dy, sizes, groups, m, k, n, k_tiles, n_tiles, dw);
+  BUX_CHECK(fits(m, k) && fits(m, n),
+            "bux_bf16_grouped_contract: an operand of m=%lld k=%lld n=%lld exceeds 2 GiB",
+            (long long)m, (long long)k, (long long)n);
+  BUX_CHECK(sizes && dw && (m == 0 || (x && dy)), "bux_bf16_grouped_contract: NULL buffer");
+  const size_t need = bux_bf16_grouped_contract_workspace_size(groups);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(BUX_E_WORKSPACE, "bux_bf16_grouped_contract: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
+                     starts_in(workspace), nullptr, header_in(workspace), 0, nullptr);
+  if (int rc = launched("prologue_kernel")) return rc;
+  const int64_t d_tiles = ceil_div(k, BM), f_tiles = ceil_div(n, BN);
+  const int64_t tiles = static_cast<int64_t>(groups) * d_tiles * f_tiles;
+  BUX_CHECK(tiles < (1LL << 31), "bux_bf16_grouped_contract: too many tiles");
+  // K is the rows: A(r, i) = x[i][r] and B(c, i) = dy[i][c], both MN-major.
+  const Operand A{x, static_cast<int32_t>(k), static_cast<int32_t>(m * k * 2), 0};
+  const Operand B{dy, static_cast<int32_t>(n), static_cast<int32_t>(m * n * 2), 0};
+  unsigned blocks = 0;
+  if (int rc = grid_for(tiles, &blocks)) return rc;
+  if (int rc = allow_lds(contract_kernel, sizeof(Lds), "bf16 contract_kernel")) return rc;
+  hipLaunchKernelGGL(contract_kernel, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+                     static_cast<int32_t>(k), static_cast<int32_t>(n), starts_in(workspace),
+                     static_cast<int32_t>(d_tiles), static_cast<int32_t>(f_tiles), dw);
   return launched("bf16 contract_kernel");
 }

@@ -8,7 +8,7 @@ rows past the groups 0.
 import torch
 
 from bux_amd import _lib
-from bux_amd.kernels import lib, ptr, require, stream
+from bux_amd.kernels import lib, ptr, require, stream, workspace
 
 
 def dot(x: torch.Tensor, w: torch.Tensor, sizes: torch.Tensor, transposed: bool = False) -> torch.Tensor:
@@ -21,8 +21,10 @@ def dot(x: torch.Tensor, w: torch.Tensor, sizes: torch.Tensor, transposed: bool 
     if (w.shape[2] if transposed else w.shape[1]) != k:
         raise ValueError(f"dot: x {tuple(x.shape)}, w {tuple(w.shape)}, transposed={transposed}")
     y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+    ws = workspace(lib().bux_bf16_grouped_rows_workspace_size(groups, m), x.device)
     _lib.check(lib().bux_bf16_grouped_rows(
-        ptr(x), ptr(w), int(transposed), ptr(sizes), groups, m, n, k, ptr(y), stream()))
+        ptr(x), ptr(w), int(transposed), ptr(sizes), groups, m, n, k, ptr(y), ptr(ws),
+        ws.numel(), stream()))
     return y
 
 
@@ -33,6 +35,7 @@ def weight_grad(x: torch.Tensor, dy: torch.Tensor, sizes: torch.Tensor) -> torch
     n = dy.shape[1]
     groups = sizes.shape[0]
     dw = torch.empty(groups, k, n, dtype=torch.bfloat16, device=x.device)
+    ws = workspace(lib().bux_bf16_grouped_contract_workspace_size(groups), x.device)
     _lib.check(lib().bux_bf16_grouped_contract(
-        ptr(x), ptr(dy), ptr(sizes), groups, m, k, n, ptr(dw), stream()))
+        ptr(x), ptr(dy), ptr(sizes), groups, m, k, n, ptr(dw), ptr(ws), ws.numel(), stream()))
     return dw

@@ -192,25 +192,29 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxMxContractListed, MxContractListed,
 
 // --- a-10: the bfloat16 grouped GEMMs ----------------------------------------------------
 
-static ffi::Error Bf16Rows(hipStream_t s, In x, In w, In sizes, int64_t transposed, Out y) {
+// ws: a u8 result of bux_bf16_grouped_rows_workspace_size (_contract_) bytes.
+static ffi::Error Bf16Rows(hipStream_t s, In x, In w, In sizes, int64_t transposed, Out y,
+                           Out ws) {
   return status(bux_bf16_grouped_rows(at<const uint16_t>(x), at<const uint16_t>(w),
                                       static_cast<int>(transposed), at<const int32_t>(sizes),
                                       static_cast<int32_t>(dim(w, 0)), dim(x, 0), dim(y, 1),
-                                      dim(x, 1), at<uint16_t>(y), s));
+                                      dim(x, 1), at<uint16_t>(y), at<void>(ws), ws->size_bytes(),
+                                      s));
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxBf16Rows, Bf16Rows,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
-                                  .Attr<int64_t>("transposed").Ret<In>());
+                                  .Attr<int64_t>("transposed").Ret<In>().Ret<In>());
 
-static ffi::Error Bf16Contract(hipStream_t s, In x, In dy, In sizes, Out dw) {
+static ffi::Error Bf16Contract(hipStream_t s, In x, In dy, In sizes, Out dw, Out ws) {
   return status(bux_bf16_grouped_contract(at<const uint16_t>(x), at<const uint16_t>(dy),
                                           at<const int32_t>(sizes),
                                           static_cast<int32_t>(sizes.element_count()), dim(x, 0),
-                                          dim(x, 1), dim(dy, 1), at<uint16_t>(dw), s));
+                                          dim(x, 1), dim(dy, 1), at<uint16_t>(dw), at<void>(ws),
+                                          ws->size_bytes(), s));
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxBf16Contract, Bf16Contract,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
-                                  .Ret<In>());
+                                  .Ret<In>().Ret<In>());
 
 // --- a-2, a-3: the token path's gathers and sums ---------------------------------------
 

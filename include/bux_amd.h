@@ -223,14 +223,21 @@ int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a_scales,
  * sums, bfloat16 out, rows past sum(sizes) 0. x bfloat16 [m, k]; w bfloat16
  * [groups, k, n] (w_transposed 0) or [groups, n, k] (1: y[i] = x[i] w[g]^T, the dgrad).
  * bux_bf16_grouped_contract replaces grouped.weight_grad (grouped.py:105-146):
- * dw[g] = x[rows of g]^T dy[rows of g], x [m, k], dy [m, n] -> dw [groups, k, n].
+ * dw[g] = x[rows of g]^T dy[rows of g], x [m, k], dy [m, n] -> dw [groups, k, n]; 0 for
+ * an empty group.
+ * n and k multiples of 8; every operand (plus a tile of 256 past it each way) under
+ * 2 GiB. workspace: bux_bf16_grouped_rows_workspace_size(groups, m) /
+ * bux_bf16_grouped_contract_workspace_size(groups) bytes (the group starts and the
+ * tile list that each call builds on the device).
  */
+size_t bux_bf16_grouped_rows_workspace_size(int32_t groups, int64_t m);
 int bux_bf16_grouped_rows(const uint16_t* x, const uint16_t* w, int w_transposed,
                           const int32_t* sizes, int32_t groups, int64_t m, int64_t n, int64_t k,
-                          uint16_t* y, void* stream);
+                          uint16_t* y, void* workspace, size_t workspace_bytes, void* stream);
+size_t bux_bf16_grouped_contract_workspace_size(int32_t groups);
 int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, const int32_t* sizes,
                               int32_t groups, int64_t m, int64_t k, int64_t n, uint16_t* dw,
-                              void* stream);
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-2 / a-3. The token path's gathers and sums.

@@ -227,42 +227,79 @@ def test_contract_at_config3_down_shape(lib):
         _close_f32(got, want, f"config3 down dW group {g}")
 
 
+# bfloat16 rows GEMM cases: (sizes, m, k, n). Rows past the groups hold NaN in x (they
+# must not reach any output: those rows are 0). k = 200 is not a whole number of the
+# kernel's K steps of 32 (its last step masked); n = 264 leaves a partial column tile.
+BF16_ROWS = {
+    "five groups": ([1000, 0, 1500, 3, 1589], 4200, 256, 1024),
+    "k tail, partial tiles": ([300, 77, 0, 500], 900, 200, 264),
+    "one group, whole tiles": ([512], 512, 64, 256),
+    "64 small groups": (None, 1500, 128, 128),
+}
+
+
+def _bf16_sizes(rng, sizes, m):
+    if sizes is None:  # 64 groups of 0 .. 40 rows, some empty
+        sizes = rng.integers(0, 41, 64)
+        sizes[rng.choice(64, 8, replace=False)] = 0
+    sizes = np.asarray(sizes, np.int32)
+    assert sizes.sum() <= m
+    return sizes
+
+
 @pytest.mark.parametrize("transposed", [False, True])
-def test_bf16_rows(lib, transposed):
+@pytest.mark.parametrize("case", list(BF16_ROWS))
+def test_bf16_rows(lib, case, transposed):
     from bux_amd import grouped
     rng = np.random.default_rng(34)
-    sizes = np.array([1000, 0, 1500, 3, 1589], np.int32)
-    m, k, n = 4200, 256, 1024
+    sizes, m, k, n = BF16_ROWS[case]
+    sizes = _bf16_sizes(rng, sizes, m)
+    filled = int(sizes.sum())
     x = normal_bf16(rng, (m, k))
+    x[filled:] = 0x7FC0  # NaN
     w = normal_bf16(rng, (len(sizes), k, n), 0.02)
-    announce("bf16 rows", transposed)
+    announce("bf16 rows", case, transposed)
     wt = np.ascontiguousarray(np.swapaxes(w, 1, 2)) if transposed else w
     y = grouped.dot(to_gpu_bf16(x), to_gpu_bf16(wt), to_gpu(sizes), transposed=transposed)
     torch.cuda.synchronize()
-    want = omoe.ragged_dot_bf16(x, w, sizes, out="bf16")
+    want = omoe.ragged_dot_bf16(x[:filled], w, sizes, out="bf16")
     got = bf16.to_f32(bf16_bits(y))
-    err = rel_err(got, bf16.to_f32(want))
-    print(f"[err] bf16 rows {err:.3e}", flush=True)
+    assert (got[filled:] == 0).all()
+    err = rel_err(got[:filled], bf16.to_f32(want))
+    print(f"[err] bf16 rows {case} {err:.3e}", flush=True)
     assert err <= 1e-3  # both float32 sums rounded to bfloat16: the north star's bar
-    assert (got[sizes.sum():] == 0).all()
 
 
-def test_bf16_weight_grad(lib):
+# bfloat16 wgrad cases: (sizes, m, k, n). Group boundaries off the kernel's K step of 32
+# rows; the rows past the groups hold NaN in x and dy (a wgrad ignores them); k = 136
+# and n = 264 leave partial tiles.
+BF16_CONTRACT = {
+    "five groups": ([70, 0, 100, 3, 77], 256, 256, 512),
+    "unaligned groups, NaN past them": ([33, 0, 95, 1, 200], 400, 136, 264),
+    "64 small groups": (None, 1500, 128, 256),
+}
+
+
+@pytest.mark.parametrize("case", list(BF16_CONTRACT))
+def test_bf16_weight_grad(lib, case):
     from bux_amd import grouped
     rng = np.random.default_rng(35)
-    sizes = np.array([70, 0, 100, 3, 77], np.int32)
-    m, k, n = 256, 256, 512
+    sizes, m, k, n = BF16_CONTRACT[case]
+    sizes = _bf16_sizes(rng, sizes, m)
+    filled = int(sizes.sum())
     x = normal_bf16(rng, (m, k))
     dy = normal_bf16(rng, (m, n), 0.01)
-    announce("bf16 weight_grad")
+    x[filled:] = 0x7FC0
+    dy[filled:] = 0x7FC0
+    announce("bf16 weight_grad", case)
     dw = grouped.weight_grad(to_gpu_bf16(x), to_gpu_bf16(dy), to_gpu(sizes))
     torch.cuda.synchronize()
-    want = omoe.weight_grad_bf16(x, dy, sizes, out="bf16")
+    want = omoe.weight_grad_bf16(x[:filled], dy[:filled], sizes, out="bf16")
     got = bf16.to_f32(bf16_bits(dw))
+    assert (got[sizes == 0] == 0).all()
     err = rel_err(got, bf16.to_f32(want))
-    print(f"[err] bf16 weight_grad {err:.3e}", flush=True)
+    print(f"[err] bf16 weight_grad {case} {err:.3e}", flush=True)
     assert err <= 1e-3
-    assert (got[1] == 0).all()
 
 
 def test_a_tile_list_made_once_serves_every_gemm(lib):
