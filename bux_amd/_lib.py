@@ -99,6 +99,10 @@ SIGNATURES = {
     "bux_mx_grouped_glu": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p, _ffn, _p, _p,
                _p, _p, _p, _p, _size, _p]),
+    "bux_mx_grouped_dglu_workspace_size": (_size, [_i32, _i64, _i64, _i64]),
+    "bux_mx_grouped_dglu": (
+        _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p, _p, _ffn, _p, _p, _p, _p,
+               _p, _p, _p, _size, _p]),
     "bux_glu_backward_quantize_workspace_size": (_size, [_i64, _i64]),
     "bux_glu_backward_quantize": (
         _int, [_p, _p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p, _p,

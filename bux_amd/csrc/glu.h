@@ -33,12 +33,18 @@ struct Kind {
   static constexpr bool gated = GATED;
 };
 
+// Floating-point contraction: every function here fuses a * b + c into one FMA exactly
+// where one expression holds it (contract(on), decided by the source), never by the
+// code generator's choice, which may differ from one kernel to another: the plain, the
+// quantizing and the fused GEMM-epilogue kernels inline these functions and must agree
+// bit for bit. Their products do not fuse into a caller's sums either.
 constexpr float LOG2E = 1.44269504088896341f;
 
 // The hardware's 2^x and reciprocal (v_exp_f32, v_rcp_f32): a few float32 ulps, far
 // inside the one rounding to bfloat16 that follows. (The library's precise exp and an
 // IEEE division made the activation kernels VALU-bound, 24% slower for SwiGLU.)
 __device__ __forceinline__ float fast_sigmoid(float x) {
+#pragma clang fp contract(on)
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * LOG2E));
 }
 // tanh(x): below |x| = 1/8 its Taylor series to x^7 (the next term, 62 x^9 / 2835, is
@@ -46,6 +52,7 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
 // underflows, a float32 ulp of 1 from exact (under 1e-6 of tanh from |x| = 1/8 on).
 // Both forms are computed and one selected: no branch.
 __device__ __forceinline__ float fast_tanh(float x) {
+#pragma clang fp contract(on)
   const float x2 = x * x;
   const float series =
       x * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f - x2 * (17.0f / 315.0f))));
@@ -58,6 +65,7 @@ __device__ __forceinline__ float fast_tanh(float x) {
 // as jax takes them: relu's is 0 at 0).
 template <int KIND>
 __device__ __forceinline__ void activate(float x, float* a, float* da) {
+#pragma clang fp contract(on)
   if constexpr (KIND == BUX_RELU) {
     *a = x > 0.0f ? x : 0.0f;
     *da = x > 0.0f ? 1.0f : 0.0f;
@@ -111,6 +119,7 @@ __device__ __forceinline__ void activate(float x, float* a, float* da) {
 // clip is maximum, then minimum, and jax's gradient of each is 1/2 at a tie: 1 inside,
 // 1/2 at the limit, 0 outside; at a limit of 0 an up of 0 ties both, 1/4.
 __device__ __forceinline__ float up_branch(const Act& act, float up, float* dup) {
+#pragma clang fp contract(on)
   float d = 1.0f;
   if (act.clamped) {
     const float au = fabsf(up);
@@ -129,6 +138,7 @@ __device__ __forceinline__ float up_branch(const Act& act, float up, float* dup)
 // h of one unit from its up projection (and gate, when gated) and the row's weight.
 template <typename K>
 __device__ __forceinline__ float glu_unit(const Act& act, float up, float gate, float w) {
+#pragma clang fp contract(on)
   float dup, a, da;
   up = up_branch(act, up, &dup);
   if constexpr (!K::gated) {
@@ -146,6 +156,7 @@ __device__ __forceinline__ float glu_unit(const Act& act, float up, float gate, 
 template <typename K>
 __device__ __forceinline__ void glu_unit_grad(const Act& act, float up, float gate, float w,
                                               float g, float* d_up, float* d_gate, float* d_w) {
+#pragma clang fp contract(on)
   float dup, a, da;
   up = up_branch(act, up, &dup);
   if constexpr (!K::gated) {
@@ -166,6 +177,12 @@ __device__ __forceinline__ void glu_unit_grad(const Act& act, float up, float ga
     *d_w = g * a * uo;
   }
 }
+
+// d weight of each of m rows from its `tiles` partial sums (one a 64 columns of d
+// projected, rows past *filled 0), added in order and rounded once to bfloat16
+// (quantize.hip's glu_weights_kernel).
+int launch_glu_weights(const float* partials, int64_t m, int64_t tiles, const int32_t* filled,
+                       uint16_t* d_weights, hipStream_t s);
 
 // Calls f(Kind<act.kind, act.gated>{}) and returns what it returns.
 template <int KIND, typename F>

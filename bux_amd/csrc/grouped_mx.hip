@@ -824,6 +824,309 @@ int64_t glu_slots(int32_t groups, int64_t height) {
   return ceil_div(height + 32 * static_cast<int64_t>(groups + 1), BM) + groups + 1;
 }
 
+// --- the activation's gradient in the down dgrad's epilogue ---------------------------
+//
+// bux_mx_grouped_dglu is the rows GEMM of the down projection's dgrad (dh = dy W[g],
+// W[g] f x k) followed by bux_glu_backward_quantize, in one kernel and two small ones:
+// the epilogue rounds dh to bfloat16 as the GEMM's output would hold it, reads the
+// product's (up, gate) pairs of its units and each row's weight, computes d projected
+// (the activation's gradient) and each row's share of its weight's gradient exactly as
+// the quantizing backward kernel does, and writes both of d projected's MXFP8 copies,
+// so that dh never goes to memory. (The reference's grouped_cudnn.activation_grad,
+// grouped_cudnn.py:211-263, for groups padded to 256 rows.)
+//
+// As in the forward, tiles start at each group's first row rounded down to 32, and the
+// column copy's blocks with a group's first row strictly inside are no tile's whole:
+// the epilogue leaves d projected's rows of such a block in a slot of the workspace (32
+// rows, the slot of the block's first group that starts inside it), from which
+// dglu_edges_kernel quantizes them. A row's weight gradient: each 64 columns of d
+// projected a partial sum in the quantizing kernel's order of additions, then
+// glu_weights_kernel adds them in order. The results are the unfused kernels' bits.
+
+// The slot of 32-row block B: the first g <= groups whose first row lies strictly
+// inside the block, or -1.
+__device__ __forceinline__ int32_t edge_slot(const int32_t* starts, int32_t groups, int32_t block) {
+  const int32_t at = 32 * block;
+  int32_t lo = 0, hi = groups + 1;  // the first g with starts[g] > at
+  while (lo < hi) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (starts[mid] > at) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo <= groups && starts[lo] < at + 32 ? lo : -1;
+}
+
+// Eight bfloat16 of a uint4 as floats.
+__device__ __forceinline__ void floats8(const uint4& q, float* v) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = low_bf16(w[j]);
+    v[2 * j + 1] = high_bf16(w[j]);
+  }
+}
+
+// Two E4M3 words (8 codes) of eight bfloat16 scaled by `down`.
+__device__ __forceinline__ uint2 codes8(const uint4& q, float down) {
+  float v[8];
+  floats8(q, v);
+  return make_uint2(e4m3x4(clip448(v[0] * down), clip448(v[1] * down), clip448(v[2] * down),
+                           clip448(v[3] * down)),
+                    e4m3x4(clip448(v[4] * down), clip448(v[5] * down), clip448(v[6] * down),
+                           clip448(v[7] * down)));
+}
+
+__device__ __forceinline__ float amax8(const uint4& q) {
+  float v[8];
+  floats8(q, v);
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[j]));
+  return a;
+}
+
+// The fused dgrad's outputs. d projected's columns are (up, gate) pairs of units, as
+// the product's: unit u's at 2u and 2u + 1 (n2 = 2 f columns).
+// K: the gated activation (Kind<BUX_SWISH | BUX_QUICK_GELU | BUX_SITU, true>).
+template <typename K>
+struct DGluOut {
+  const uint16_t* projected;  // bfloat16 (rows, n2): the up GEMM's product
+  const uint16_t* weights;    // bfloat16 (rows,): each row's weight
+  uint16_t* d_projected;      // bfloat16 (rows, n2), or NULL
+  uint8_t* values;            // d projected along its columns, tiled: codes (k2/64, height, 64)
+  uint8_t* scales;            //   and scale bytes (k2/128, height, 4)
+  uint8_t* t_values;          // along the rows, tiled: codes (height/64, n2, 64)
+  uint8_t* t_scales;          //   and scale bytes (height/128, n2, 4)
+  float* partials;            // (rows, tiles): a row's weight-gradient share a 64 columns
+  uint16_t* edges;            // (groups + 1, 32, n2): rows of blocks with a first row inside
+  const int32_t* starts;
+  Act act;
+  int32_t rows, f, n2, height, tiles, groups;
+  int32_t chunks;  // 64-column chunks of the row copy (its K, 2 f padded to 128)
+  int32_t live;  // rows below it have values: min(the groups' end, rows); set on the device
+
+  // A wave's 128 rows x 128 units of the tile, 32 rows at a time: lane l holds row l % 32
+  // and, of each 32-unit accumulator block jj, units 32 jj + 8 g + 4 (l / 32) .. + 3 (run
+  // g = 0..3: registers 4 g .. 4 g + 3), i.e. d projected's columns 64 jj + 16 g +
+  // 8 (l / 32) .. + 7 of the wave's.
+  __device__ __forceinline__ void store(const v16f acc[4][4], const Job& j, Stage& stage) const {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, half = lane >> 5, r32 = lane & 31;
+    const int32_t lo = j.a_row0, first = lo + j.row_lo, end = lo + j.rows;
+    const int32_t u0 = j.b_row0 + wn * 128;  // the wave's first unit
+    // the tile's first and last blocks, where a group's first row lies inside: slots
+    const int32_t head = (first & 31) != 0 ? first >> 5 : -1;
+    const int32_t tail = (end & 31) != 0 ? end >> 5 : -1;
+    const int32_t head_slot = head >= 0 ? edge_slot(starts, groups, head) : -1;
+    const int32_t tail_slot = tail >= 0 ? edge_slot(starts, groups, tail) : -1;
+    uint32_t* region = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(&stage) +
+                                                   wave * 32 * PITCH);
+    // the product's 4 runs of (up, gate) pairs of accumulator block jj of row block i
+    auto load_runs = [&](int i, int jj, uint4 (&pr)[4]) {
+      const int32_t r = lo + wm * 128 + i * 32 + r32;
+      const bool on = r >= first && r < end && r < live;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int32_t u = u0 + 32 * jj + 8 * g + 4 * half;
+        pr[g] = on && u < f ? *reinterpret_cast<const uint4*>(projected + static_cast<int64_t>(r) * n2 + 2 * u)
+                            : make_uint4(0, 0, 0, 0);
+      }
+    };
+    uint4 pr[4];
+    load_runs(0, 0, pr);
+    // (fully unrolled: the accumulators are indexed by constants)
+#pragma clang loop unroll(full)
+    for (int i = 0; i < 4; ++i) {
+      const int32_t r0 = lo + wm * 128 + i * 32, r = r0 + r32;
+      const bool mine = r >= first && r < end;  // rows the tile holds
+      const bool on = mine && r < live;
+      const float w = on ? bf16_to_f32(weights[r]) : 0.0f;
+      const int block = r0 >> 5;
+      const int32_t slot = block == head ? head_slot : (block == tail ? tail_slot : -1);
+      const bool whole = r0 >= first && r0 + 32 <= end;  // the column copy's block
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int32_t c64 = (u0 >> 5) + jj;  // the 64 columns of d projected
+        // d projected (bfloat16 pairs, 8 columns a run) and each run's sum of weight terms
+        uint4 dp[4];
+        float sum[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int32_t u = u0 + 32 * jj + 8 * g + 4 * half;
+          float p[8], v[8];
+          floats8(pr[g], p);
+          // dh as the GEMM's bfloat16 output holds it
+          const uint2 dh = FromAcc{acc}(i, jj, g);
+          const float d[4] = {low_bf16(dh.x), high_bf16(dh.x), low_bf16(dh.y), high_bf16(dh.y)};
+          float s = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float term = 0.0f;
+            v[2 * e] = v[2 * e + 1] = 0.0f;
+            if (on && u < f) glu_unit_grad<K>(act, p[2 * e], p[2 * e + 1], w, d[e], &v[2 * e], &v[2 * e + 1], &term);
+            s += term;
+          }
+          sum[g] = s;
+          dp[g] = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                             pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+        }
+        // the next runs' product goes out while this block's copies are made
+        if (jj + 1 < 4) load_runs(i, jj + 1, pr);
+        else if (i + 1 < 4) load_runs(i + 1, 0, pr);
+        // the row's share of its weight's gradient: the quantizing kernel's 8 chunks of 4
+        // units (chunk 2 g + half) added pairwise, pairs of pairs, then the halves
+        float x[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) x[g] = sum[g] + __shfl_xor(sum[g], 32);
+        const float part = (x[0] + x[1]) + (x[2] + x[3]);
+        if (half == 0 && mine && r < rows && c64 < tiles)
+          partials[static_cast<int64_t>(r) * tiles + c64] = part;
+        // along the columns: blocks b = 0, 1 of 32 (runs 2 b, 2 b + 1 of both halves)
+        float am[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          am[b] = fmaxf(amax8(dp[2 * b]), amax8(dp[2 * b + 1]));
+          am[b] = fmaxf(am[b], __shfl_xor(am[b], 32));
+        }
+        const int e0 = scale_exponent_bf16(am[0]), e1 = scale_exponent_bf16(am[1]);
+        uint2 piece[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) piece[g] = codes8(dp[g], power_of_two_down(g < 2 ? e0 : e1));
+        // Lane half h stores block h's 32 codes: it sends the other half its pieces of the
+        // other block (runs 2 (1 - h), + 1) and receives the other half's of its own. Run
+        // 2 h + q's columns 16 q + 8 (source half) .. + 7 of the block are words
+        // 4 q + 2 (source half), + 1 of the 8.
+        // (Selects, not indices by the lane half: an array indexed by a lane's value
+        // goes to scratch memory.)
+        const uint2 own0 = half ? piece[2] : piece[0], own1 = half ? piece[3] : piece[1];
+        const uint2 oth0 = half ? piece[0] : piece[2], oth1 = half ? piece[1] : piece[3];
+        const uint32_t s0 = __shfl_xor(oth0.x, 32), s1 = __shfl_xor(oth0.y, 32);
+        const uint32_t s2 = __shfl_xor(oth1.x, 32), s3 = __shfl_xor(oth1.y, 32);
+        const uint4 run0 = half ? make_uint4(s0, s1, own0.x, own0.y) : make_uint4(own0.x, own0.y, s0, s1);
+        const uint4 run1 = half ? make_uint4(s2, s3, own1.x, own1.y) : make_uint4(own1.x, own1.y, s2, s3);
+        if (mine && c64 < chunks) {
+          uint4* at = reinterpret_cast<uint4*>(values + (static_cast<int64_t>(c64) * height + r) * 64 + 32 * half);
+          at[0] = run0;
+          at[1] = run1;
+          const int32_t bb = 2 * c64 + half;
+          scales[(static_cast<int64_t>(bb >> 2) * height + r) * 4 + (bb & 3)] =
+              static_cast<uint8_t>((half ? e1 : e0) + 127);
+        }
+        // the bfloat16 values where asked for, and the rows of an edge block
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int32_t u = u0 + 32 * jj + 8 * g + 4 * half;
+          if (mine && u < f) {
+            if (d_projected != nullptr && r < rows)
+              *reinterpret_cast<uint4*>(d_projected + static_cast<int64_t>(r) * n2 + 2 * u) = dp[g];
+            if (slot >= 0)
+              *reinterpret_cast<uint4*>(edges + (static_cast<int64_t>(slot) * 32 + r32) * n2 + 2 * u) = dp[g];
+          }
+        }
+        // Along the rows, if this tile holds all of the block from r0: through the region,
+        // 64 units (128 columns) at a time, a row 65 words apart; after the second of two
+        // accumulator blocks, lane l takes word column l (units u0 + 64 (jj / 2) + l's two
+        // columns) down the 32 rows.
+        if (whole) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint32_t* at = region + r32 * 65 + (jj & 1) * 32 + 8 * g + 4 * half;
+            at[0] = dp[g].x;
+            at[1] = dp[g].y;
+            at[2] = dp[g].z;
+            at[3] = dp[g].w;
+          }
+          if (jj & 1) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+            uint32_t v[32];
+            float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+              v[k] = region[k * 65 + lane];
+              m0 = fmaxf(m0, fabsf(low_bf16(v[k])));
+              m1 = fmaxf(m1, fabsf(high_bf16(v[k])));
+            }
+            const int t0 = scale_exponent_bf16(m0), t1 = scale_exponent_bf16(m1);
+            const float d0 = power_of_two_down(t0), d1 = power_of_two_down(t1);
+            uint32_t c0[8], c1[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              c0[q] = e4m3x4(clip448(low_bf16(v[4 * q]) * d0), clip448(low_bf16(v[4 * q + 1]) * d0),
+                             clip448(low_bf16(v[4 * q + 2]) * d0), clip448(low_bf16(v[4 * q + 3]) * d0));
+              c1[q] = e4m3x4(clip448(high_bf16(v[4 * q]) * d1), clip448(high_bf16(v[4 * q + 1]) * d1),
+                             clip448(high_bf16(v[4 * q + 2]) * d1), clip448(high_bf16(v[4 * q + 3]) * d1));
+            }
+            const int32_t u = u0 + 32 * (jj - 1) + lane;
+            if (u < f) {
+              const int64_t c = 2 * static_cast<int64_t>(u);
+              uint4* at = reinterpret_cast<uint4*>(t_values + (static_cast<int64_t>(r0 >> 6) * n2 + c) * 64 + (r0 & 63));
+              at[0] = make_uint4(c0[0], c0[1], c0[2], c0[3]);
+              at[1] = make_uint4(c0[4], c0[5], c0[6], c0[7]);
+              at[4] = make_uint4(c1[0], c1[1], c1[2], c1[3]);
+              at[5] = make_uint4(c1[4], c1[5], c1[6], c1[7]);
+              uint8_t* sc = t_scales + (static_cast<int64_t>(r0 >> 7) * n2 + c) * 4 + ((r0 >> 5) & 3);
+              sc[0] = static_cast<uint8_t>(t0 + 127);
+              sc[4] = static_cast<uint8_t>(t1 + 127);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+          }
+        }
+      }
+    }
+  }
+};
+
+template <typename K>
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void dglu_kernel(
+    Operand A, Operand B, int32_t groups, int32_t height, const int32_t* __restrict__ starts,
+    const Tile* __restrict__ tiles, int32_t col_tiles, DGluOut<K> out) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  Lds& lds = *reinterpret_cast<Lds*>(smem);
+  const GluTiles list{tiles, starts, groups, B.rows, height, col_tiles, A.k / BK};
+  out.live = smaller(starts[groups], out.rows);
+  const int32_t count = starts[groups + 1] * col_tiles;
+  run_tiles<Mx>(list, count, A, B, lds, out);
+}
+
+// d projected's column-copy blocks of 32 rows with a group's first row strictly inside,
+// from the rows the fused kernel left in the block's slot. Workgroup g takes the block of
+// group g's first row if g is its slot (no earlier group's first row strictly inside
+// it); its lane t column 256 blockIdx.y + t.
+__global__ __launch_bounds__(THREADS) void dglu_edges_kernel(
+    const int32_t* __restrict__ starts, int32_t groups, const uint16_t* __restrict__ edges,
+    int32_t n2, int32_t height, uint8_t* __restrict__ t_values, uint8_t* __restrict__ t_scales) {
+  const int g = blockIdx.x;
+  const int32_t first = starts[g];
+  if ((first & 31) == 0 || first >= height) return;
+  if (g > 0) {
+    const int32_t before = starts[g - 1];
+    if ((before & 31) != 0 && (before >> 5) == (first >> 5)) return;
+  }
+  const int32_t c = static_cast<int32_t>(blockIdx.y) * THREADS + threadIdx.x;
+  if (c >= n2) return;
+  const int32_t r0 = first & ~31;
+  float v[32], amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    v[k] = bf16_to_f32(edges[(static_cast<int64_t>(g) * 32 + k) * n2 + c]);
+    amax = fmaxf(amax, fabsf(v[k]));
+  }
+  const int e = scale_exponent_bf16(amax);
+  const float down = power_of_two_down(e);
+  uint32_t w[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    w[q] = e4m3x4(clip448(v[4 * q] * down), clip448(v[4 * q + 1] * down),
+                  clip448(v[4 * q + 2] * down), clip448(v[4 * q + 3] * down));
+  uint8_t* at = t_values + (static_cast<int64_t>(r0 >> 6) * n2 + c) * 64 + (r0 & 63);
+  *reinterpret_cast<uint4*>(at) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint4*>(at + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+  t_scales[(static_cast<int64_t>(r0 >> 7) * n2 + c) * 4 + ((r0 >> 5) & 3)] = static_cast<uint8_t>(e + 127);
+}
+
 }  // namespace
 }  // namespace bux
 
@@ -1191,4 +1494,102 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
   if (act.kind == BUX_QUICK_GELU) return run(Kind<BUX_QUICK_GELU, true>{});
   if (act.kind == BUX_SITU) return run(Kind<BUX_SITU, true>{});
   return run(Kind<BUX_SWISH, true>{});
+}
+
+// The fused dgrad's workspace: the tile list (the fused up GEMM's), then the rows'
+// weight-gradient partials (a float a row and 64 columns of d projected), then the edge
+// blocks' slots (32 rows of d projected a group and one for the groups' end).
+namespace bux {
+namespace {
+int64_t dglu_tiles(int64_t f) { return ceil_div(2 * f, 128) * 2; }
+size_t dglu_partials_at(int32_t groups, int64_t height) {
+  return align256(starts_bytes(groups) + static_cast<size_t>(glu_slots(groups, height)) * sizeof(Tile));
+}
+size_t dglu_edges_at(int32_t groups, int64_t height, int64_t rows, int64_t f) {
+  return dglu_partials_at(groups, height) +
+         align256(static_cast<size_t>(rows) * static_cast<size_t>(dglu_tiles(f)) * sizeof(float));
+}
+}  // namespace
+}  // namespace bux
+
+extern "C" size_t bux_mx_grouped_dglu_workspace_size(int32_t groups, int64_t height, int64_t rows,
+                                                     int64_t f) {
+  using namespace bux;
+  return dglu_edges_at(groups, height, rows, f) +
+         static_cast<size_t>(groups + 1) * 32 * static_cast<size_t>(2 * f) * sizeof(uint16_t);
+}
+
+extern "C" int bux_mx_grouped_dglu(const uint8_t* a_values, const uint8_t* a_scales,
+                                   const uint8_t* b_values, const uint8_t* b_scales,
+                                   const int32_t* sizes, int32_t groups, int64_t height, int64_t f,
+                                   int64_t k, int64_t rows, const uint16_t* projected,
+                                   const uint16_t* weights, const bux_ffn* ffn,
+                                   uint16_t* d_projected, uint8_t* values, uint8_t* scales,
+                                   uint8_t* t_values, uint8_t* t_scales, uint16_t* d_weights,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "bux_mx_grouped_dglu: groups=%d outside [1, %d]",
+            groups, MAX_GROUPS);
+  BUX_CHECK(height >= 0 && height % 128 == 0 && height < (1LL << 31) && f > 0 && f % 32 == 0 &&
+                k > 0 && k % 128 == 0 && rows >= 0 && rows <= height,
+            "bux_mx_grouped_dglu: bad shape height=%lld f=%lld k=%lld rows=%lld (height a "
+            "multiple of 128, f of 32, k of 128, rows at most height)",
+            (long long)height, (long long)f, (long long)k, (long long)rows);
+  BUX_CHECK(offsets_fit(height, k) && offsets_fit(f, k),
+            "bux_mx_grouped_dglu: an operand of %lld x %lld bytes exceeds 2 GiB",
+            (long long)(height > f ? height : f), (long long)k);
+  Act act;
+  if (int rc = act_of("bux_mx_grouped_dglu", ffn, &act)) return rc;
+  BUX_CHECK(act.gated && (act.kind == BUX_SWISH || act.kind == BUX_QUICK_GELU || act.kind == BUX_SITU),
+            "bux_mx_grouped_dglu: the fused epilogue is of a gated BUX_SWISH, BUX_QUICK_GELU or "
+            "BUX_SITU, not activation %d%s", act.kind, act.gated ? "" : " plain");
+  BUX_CHECK(sizes && b_values && b_scales &&
+                (height == 0 || (a_values && a_scales && values && scales && t_values && t_scales)) &&
+                (rows == 0 || (weights && projected && d_weights)),
+            "bux_mx_grouped_dglu: NULL buffer");
+  const size_t need = bux_mx_grouped_dglu_workspace_size(groups, height, rows, f);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(BUX_E_WORKSPACE, "bux_mx_grouped_dglu: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  if (height == 0) return BUX_OK;
+  hipStream_t s = as_stream(stream);
+  int32_t* starts = starts_in(workspace);
+  Tile* tiles = tiles_in(workspace, groups);
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  float* partials = reinterpret_cast<float*>(base + dglu_partials_at(groups, height));
+  uint16_t* edges = reinterpret_cast<uint16_t*>(base + dglu_edges_at(groups, height, rows, f));
+  const int64_t slots = glu_slots(groups, height);
+  const int64_t col_tiles = ceil_div(f, BN);
+  if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_dglu: too many tiles");
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, height, slots,
+                     32, starts, tiles, nullptr, 0, nullptr);
+  if (int rc = launched("prologue_kernel")) return rc;
+  const Operand A{a_values, a_scales, static_cast<int32_t>(k), static_cast<int32_t>(height)};
+  const Operand B{b_values, b_scales, static_cast<int32_t>(k), static_cast<int32_t>(f)};
+  const int32_t n2 = static_cast<int32_t>(2 * f), tiles64 = static_cast<int32_t>(dglu_tiles(f));
+  unsigned blocks = 0;
+  if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
+  auto run = [&](auto kind) {
+    using K = decltype(kind);
+    const DGluOut<K> out{projected, weights, d_projected, values, scales, t_values, t_scales,
+                         partials, edges, starts, act, static_cast<int32_t>(rows),
+                         static_cast<int32_t>(f), n2, static_cast<int32_t>(height), tiles64,
+                         groups, static_cast<int32_t>(ceil_div(n2, 128) * 2), 0};
+    if (int rc = allow_lds(dglu_kernel<K>, sizeof(Lds), "dglu_kernel")) return rc;
+    hipLaunchKernelGGL(dglu_kernel<K>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+                       static_cast<int32_t>(height), starts, tiles, static_cast<int32_t>(col_tiles),
+                       out);
+    return launched("dglu_kernel");
+  };
+  int rc = act.kind == BUX_QUICK_GELU ? run(Kind<BUX_QUICK_GELU, true>{})
+           : act.kind == BUX_SITU     ? run(Kind<BUX_SITU, true>{})
+                                      : run(Kind<BUX_SWISH, true>{});
+  if (rc != BUX_OK) return rc;
+  hipLaunchKernelGGL(dglu_edges_kernel,
+                     dim3(static_cast<unsigned>(groups + 1), static_cast<unsigned>(ceil_div(n2, THREADS))),
+                     dim3(THREADS), 0, s, starts, groups, edges, n2, static_cast<int32_t>(height),
+                     t_values, t_scales);
+  if (int rc2 = launched("dglu_edges_kernel")) return rc2;
+  return launch_glu_weights(partials, rows, tiles64, starts + groups, d_weights, s);
 }

@@ -378,6 +378,15 @@ int launch_quantize(const char* name, const Source& src, int64_t groups, int64_t
 }
 
 }  // namespace
+
+int launch_glu_weights(const float* partials, int64_t m, int64_t tiles, const int32_t* filled,
+                       uint16_t* d_weights, hipStream_t s) {
+  if (m == 0) return BUX_OK;
+  hipLaunchKernelGGL(glu_weights_kernel, dim3(static_cast<unsigned>(ceil_div(m, THREADS))),
+                     dim3(THREADS), 0, s, partials, m, tiles, filled, d_weights);
+  return launched("glu_weights_kernel");
+}
+
 }  // namespace bux
 
 extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div,
@@ -449,8 +458,6 @@ extern "C" int bux_glu_backward_quantize(const uint16_t* projected, const uint16
     return launch_quantize("bux_glu_backward_quantize", src, 1, m, cols, height, filled,
                            BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales, s);
   });
-  if (rc != BUX_OK || m == 0) return rc;
-  hipLaunchKernelGGL(glu_weights_kernel, dim3(static_cast<unsigned>(ceil_div(m, THREADS))),
-                     dim3(THREADS), 0, s, partials, m, tiles, filled, d_weights);
-  return launched("glu_weights_kernel");
+  if (rc != BUX_OK) return rc;
+  return launch_glu_weights(partials, m, tiles, filled, d_weights, s);
 }

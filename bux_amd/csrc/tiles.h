@@ -306,8 +306,10 @@ __device__ __forceinline__ void barrier_lds() {
 // then) and the next tile skips its waits for those steps; the first wait left (for
 // step 3) comes a few steps after the stores went out.
 template <typename P, typename Out, typename Tiles>
-__device__ void run_tiles(const Tiles& tiles, int32_t count, const typename P::Operand& A,
-                          const typename P::Operand& B, typename P::Lds& lds, const Out& out) {
+__device__ __forceinline__ void run_tiles(const Tiles& tiles, int32_t count,
+                                          const typename P::Operand& A,
+                                          const typename P::Operand& B, typename P::Lds& lds,
+                                          const Out& out) {
   using Loads = typename P::Loads;
   using Frag = typename P::Frag;
   const Turns mine = turns(count);

@@ -290,6 +290,60 @@ def activated(
     return projected, Tiled(vals, scales), Tiled(t_vals, t_scales)
 
 
+def activation_grad(
+    a: Tiled, b: Tiled, sizes: torch.Tensor, projected: torch.Tensor, weights: torch.Tensor,
+    ffn: _lib.FfnStruct, rows: int, keep: bool = False,
+) -> tuple[Tiled, Tiled, torch.Tensor, torch.Tensor | None]:
+    """Return the gradient of `activated`'s product (d projected) in MXFP8 along its
+    columns and, transposed, along the rows, each row's weight's gradient, and with
+    `keep` d projected in bfloat16: the down dgrad ``a @ b[g]^T`` (dh, which never goes
+    to memory) through the activation's gradient, the reference's
+    ``grouped_cudnn.activation_grad`` (grouped_cudnn.py:211-263), for groups as they lie.
+    The same bits as `rows` followed by the activation's quantizing backward
+    (``moe.weighted_units_backward_quantized``).
+
+    Args:
+        a: dy along d (height of K), group 0's first: its height is the copies'.
+        b: the groups' down kernels along d, (g, f, K).
+        sizes: int32 (g,) on the device.
+        projected: bfloat16 (rows, 2 f): the up GEMM's product, (up, gate) pairs.
+        weights: bfloat16 (rows,): each row's weight.
+        ffn: the activation as ``moe.Ffn.struct`` gives it: gated, of swish,
+            quick_gelu or situ.
+        rows: rows of the product (at most a's height).
+    """
+    require(a.values, a.scales, b.values, b.scales, sizes, projected, weights)
+    if a.values.dim() != 3 or b.values.dim() != 4:
+        raise ValueError(f"activation_grad: a {tuple(a.values.shape)} is not one matrix or "
+                         f"b {tuple(b.values.shape)} not a stack")
+    height, k = a.height, a.k
+    groups, f = b.values.shape[0], b.height
+    if b.k != k or sizes.shape != (groups,) or sizes.dtype != torch.int32:
+        raise ValueError(f"activation_grad: a {tuple(a.values.shape)}, b {tuple(b.values.shape)}, "
+                         f"sizes {tuple(sizes.shape)} {sizes.dtype}")
+    if (projected.dtype != torch.bfloat16 or projected.shape != (rows, 2 * f)
+            or not projected.is_contiguous()):
+        raise ValueError(f"activation_grad: projected {projected.dtype} {tuple(projected.shape)} "
+                         f"is not a contiguous bfloat16 ({rows}, {2 * f})")
+    if weights.dtype != torch.bfloat16 or weights.numel() < rows:
+        raise ValueError(f"activation_grad: weights {weights.dtype} of {weights.numel()} for {rows} rows")
+    dev = a.values.device
+    n2 = 2 * f
+    k2 = whole(n2, K_ALIGN)
+    vals = torch.empty(k2 // 64, height, 64, dtype=torch.uint8, device=dev)
+    scales = torch.empty(k2 // 128, height, 4, dtype=torch.uint8, device=dev)
+    t_vals = torch.empty(height // 64, n2, 64, dtype=torch.uint8, device=dev)
+    t_scales = torch.empty(height // 128, n2, 4, dtype=torch.uint8, device=dev)
+    dw = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+    dp = torch.empty(rows, n2, dtype=torch.bfloat16, device=dev) if keep else None
+    ws = workspace(lib().bux_mx_grouped_dglu_workspace_size(groups, height, rows, f), dev)
+    _lib.check(lib().bux_mx_grouped_dglu(
+        ptr(a.values), ptr(a.scales), ptr(b.values), ptr(b.scales), ptr(sizes), groups, height, f,
+        k, rows, ptr(projected), ptr(weights.contiguous()), ctypes.byref(ffn), ptr(dp), ptr(vals),
+        ptr(scales), ptr(t_vals), ptr(t_scales), ptr(dw), ptr(ws), ws.numel(), stream()))
+    return Tiled(vals, scales), Tiled(t_vals, t_scales), dw, dp
+
+
 def contract(
     a: Tiled, b: Tiled, sizes: torch.Tensor, out: torch.dtype = torch.bfloat16,
     tiles: TileList | None = None,

@@ -557,7 +557,7 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
                      ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
                      up_bias: torch.Tensor | None = None, down_bias: torch.Tensor | None = None,
                      norm: ExpertNorm | None = None, norm_scale: torch.Tensor | None = None,
-                     norm_bias: torch.Tensor | None = None,
+                     norm_bias: torch.Tensor | None = None, fused: bool = False,
                      ) -> dict[str, torch.Tensor]:
     """Return the gradients of `experts_forward`'s output, dy (t, d), to z, the
     weights (t, k), up (E, d, f, p) and down (E, f, d), all bfloat16, and with biases
@@ -565,7 +565,11 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
     "norm_scale" and "norm_bias" (d,), float32 sums; with `intermediates`,
     also the gradients between the GEMMs: "dh" (m, f) of the down GEMM's input, "dp"
     (m, p f) of the up GEMM's output, "dx" (m, d) of its input, "d_row_weights" (m,),
-    and with a norm "dv" (m, d) of the down GEMM's output. The passes are the forward's (`saved.passes`); `fmt` is checked against
+    and with a norm "dv" (m, d) of the down GEMM's output. With `fused` (and the
+    forward's conditions for its fused up GEMM: every pass in MXFP8, no bias or norm,
+    `Ffn.fusable`, no `intermediates`), the down dgrad carries the activation's gradient
+    and d projected's two copies in its epilogue (`grouped_mxfp8.activation_grad`): the
+    same bits. The passes are the forward's (`saved.passes`); `fmt` is checked against
     them."""
     s, k = saved.sorted, saved.k
     t = dy.shape[0]
@@ -603,19 +607,30 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         if not (dgrad and wgrad):
             with span("gather dy"):
                 dy_rows = token_rows(dy, s.order, k)
-    with span("down dgrad"):
-        if dgrad:
-            dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m, tiles=saved.tiles)
-        else:
-            dh = grouped.dot(dy_rows, down, s.sizes, transposed=True)
+    pv = saved.projected.view(m, f, p)
+    act_weights = saved.row_weights if norm is None else torch.ones_like(saved.row_weights)
+    # the activation's gradient in the down dgrad's epilogue: its settings as the forward's
+    twin = (fused and not intermediates and dgrad and wgrad and up_bias is None and norm is None
+            and ffn.fusable(p == 2))
+    dh = None
+    if twin:
+        with span("down dgrad + activation backward + quantize dp"):
+            dp_n, dp_m, d_rows_w, dp = grouped_mxfp8.activation_grad(
+                dy_n, saved.down_n, s.sizes, saved.projected, act_weights, ffn.struct(True), m)
+    else:
+        with span("down dgrad"):
+            if dgrad:
+                dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m, tiles=saved.tiles)
+            else:
+                dh = grouped.dot(dy_rows, down, s.sizes, transposed=True)
     with span("down wgrad"):
         if wgrad:
             d_down = grouped_mxfp8.contract(saved.h_m, dy_m, s.sizes, tiles=saved.tiles)
         else:
             d_down = grouped.weight_grad(saved.h, dy_rows, s.sizes)
-    pv = saved.projected.view(m, f, p)
-    act_weights = saved.row_weights if norm is None else torch.ones_like(saved.row_weights)
-    if dgrad or wgrad:
+    if twin:
+        pass
+    elif dgrad or wgrad:
         keep = intermediates or up_bias is not None or not (dgrad and wgrad)
         with span("activation backward + quantize dp"):
             dp_n, dp_m, d_rows_w, dp = weighted_units_backward_quantized(

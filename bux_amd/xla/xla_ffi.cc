@@ -311,6 +311,25 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxMxGroupedGlu, MxGroupedGlu,
                                   .Arg<In>().Arg<In>().Arg<In>() BUX_FFN_ATTRS.Ret<In>()
                                   .Ret<In>().Ret<In>().Ret<In>().Ret<In>().Ret<In>());
 
+// dy values [K/64, height, 64], W_down values [g, K/64, f, 64]; projected [rows, 2f]; the
+// results d projected's two copies, then d_weights [rows], then the workspace.
+static ffi::Error MxGroupedDglu(hipStream_t s, In av, In as, In bv, In bs, In sizes,
+                                In projected, In weights, BUX_FFN_PARAMS, Out values,
+                                Out scales, Out t_values, Out t_scales, Out d_weights, Out ws) {
+  const bux_ffn ffn = BUX_FFN;
+  return status(bux_mx_grouped_dglu(
+      at<const uint8_t>(av), at<const uint8_t>(as), at<const uint8_t>(bv), at<const uint8_t>(bs),
+      at<const int32_t>(sizes), static_cast<int32_t>(dim(bv, 0)), dim(av, 1), dim(bv, 2),
+      dim(av, 0) * 64, dim(projected, 0), at<const uint16_t>(projected),
+      at<const uint16_t>(weights), &ffn, nullptr, at<uint8_t>(values), at<uint8_t>(scales),
+      at<uint8_t>(t_values), at<uint8_t>(t_scales), at<uint16_t>(d_weights), at<void>(ws),
+      ws->size_bytes(), s));
+}
+XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxMxGroupedDglu, MxGroupedDglu,
+                              ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
+                                  .Arg<In>().Arg<In>().Arg<In>().Arg<In>() BUX_FFN_ATTRS
+                                  .Ret<In>().Ret<In>().Ret<In>().Ret<In>().Ret<In>().Ret<In>());
+
 // x is aliased to the result (in place): the caller passes input_output_aliases={0: 0}.
 static ffi::Error ExpertBiasAdd(hipStream_t s, In x, In bias, In offsets, Out x_out) {
   (void)x;

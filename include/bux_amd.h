@@ -436,6 +436,33 @@ int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights
                               uint16_t* d_projected, uint8_t* values, uint8_t* scales,
                               uint8_t* t_values, uint8_t* t_scales, uint16_t* d_weights,
                               void* workspace, size_t workspace_bytes, void* stream);
+/* bux_mx_grouped_dglu: the experts' down dgrad with the activation's gradient and both
+ *   MXFP8 copies of d projected in its epilogue, the reference's fused dgrad
+ *   (grouped_cudnn.activation_grad, src/bux/architecture/experts/grouped_cudnn.py:
+ *   211-263), but for groups as they lie. The same outputs, bit for bit, as
+ *   bux_mx_grouped_rows(a, b, sizes, m = height, f, k, height = rows) into dh, then
+ *   bux_glu_backward_quantize(projected, weights, dh, filled = sum(sizes), rows, f, ...,
+ *   height); dh never goes to memory:
+ *   a_values/a_scales  dy in MXFP8 along its rows, tiled, height rows of k bytes;
+ *   b_values/b_scales  each expert's (f, k) down kernel along k, tiled; f a multiple
+ *     of 32;
+ *   projected  bfloat16 [rows, 2 f]: the up GEMM's product, (up, gate) pairs;
+ *   weights    bfloat16 [rows]: each row's weight;
+ *   d_projected  NULL, or bfloat16 [rows, 2 f] to store d projected as well;
+ *   values/scales  d projected along its columns (K = 2 f rounded up to 128), height
+ *     rows; t_values/t_scales  along the rows (K = height), 2 f rows;
+ *   d_weights  bfloat16 [rows]: each row's weight's gradient (0 past sum(sizes));
+ *   workspace  bux_mx_grouped_dglu_workspace_size(groups, height, rows, f) bytes.
+ *   ffn: as bux_mx_grouped_glu's.
+ */
+size_t bux_mx_grouped_dglu_workspace_size(int32_t groups, int64_t height, int64_t rows, int64_t f);
+int bux_mx_grouped_dglu(const uint8_t* a_values, const uint8_t* a_scales, const uint8_t* b_values,
+                        const uint8_t* b_scales, const int32_t* sizes, int32_t groups,
+                        int64_t height, int64_t f, int64_t k, int64_t rows,
+                        const uint16_t* projected, const uint16_t* weights, const bux_ffn* ffn,
+                        uint16_t* d_projected, uint8_t* values, uint8_t* scales,
+                        uint8_t* t_values, uint8_t* t_scales, uint16_t* d_weights,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * The router (the path's feed: its picks are a-1's idx, its weights a-8's).

@@ -128,6 +128,28 @@ def test_fused_up_gemm_rejects_bad_arguments(lib):
     assert glu(ws_bytes=8) == 2 and "workspace" in _msg(lib)
 
 
+def test_fused_dgrad_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(16)
+    ws = lib.bux_mx_grouped_dglu_workspace_size(4, 256, 200, 64)
+    # the tile list, a float a row and 64 columns of d projected, 32 rows of d projected
+    # a group (and the groups' end)
+    assert ws >= 200 * 2 * 4 + 5 * 32 * 128 * 2
+
+    def dglu(height=256, f=64, k=128, rows=200, act=0, ws_bytes=1 << 20, groups=4, gated=1):
+        ffn = _lib.FfnStruct(act, gated, 0, 0.0, 0, 0.0, 0.0)
+        return lib.bux_mx_grouped_dglu(p, p, p, p, p, groups, height, f, k, rows, p, p,
+                                       ctypes.byref(ffn), None, p, p, p, p, p, p, ws_bytes, None)
+
+    assert dglu(height=200) == 1 and "height=200" in _msg(lib)
+    assert dglu(f=48) == 1 and "f=48" in _msg(lib)
+    assert dglu(k=64) == 1 and "k=64" in _msg(lib)
+    assert dglu(rows=300) == 1 and "rows=300" in _msg(lib)
+    assert dglu(act=5) == 1 and "activation 5" in _msg(lib)
+    assert dglu(act=0, gated=0) == 1 and "plain" in _msg(lib)
+    assert dglu(groups=0) == 1 and "groups=0" in _msg(lib)
+    assert dglu(ws_bytes=8) == 2 and "workspace" in _msg(lib)
+
+
 def test_permute_and_token_ops_reject_bad_arguments(lib):
     p = ctypes.c_void_p(16)
     rc = lib.bux_moe_permute(p, 100, 0, p, p, p, p, p, 1 << 20, None)
