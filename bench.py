@@ -265,7 +265,65 @@ def fused_up(z, idx, w, up, e, k):
             "used_in_step": "unfused"}
 
 
+def fused_down(z, idx, w, up, down, dy, e, k):
+    """Time the down dgrad with the activation's gradient and d projected's two MXFP8
+    copies in its epilogue (grouped_mxfp8.activation_grad: one GEMM kernel, a small
+    fix-up and the weights' sums) against the step's unfused pair (the rows GEMM into dh,
+    then the quantizing activation backward) on the step's own operands: the two give the
+    same bits."""
+    from bux_amd import grouped_mxfp8, moe
+
+    t, d = z.shape
+    m = t * k
+    f = up.shape[2]
+    _, saved = moe.experts_forward(z, idx, w, up, down)
+    s = saved.sorted
+    height = grouped_mxfp8.whole(m)
+    dy_n, _ = grouped_mxfp8.quantized_twice(dy, s.filled, False, s.order, k, height)
+    ffn = moe.Ffn()
+
+    def unfused():
+        dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m)
+        return moe.weighted_units_backward_quantized(ffn, saved.projected.view(m, f, 2),
+                                                     saved.row_weights, dh, s.filled, height)
+
+    def fused():
+        return grouped_mxfp8.activation_grad(dy_n, saved.down_n, s.sizes, saved.projected,
+                                             saved.row_weights, ffn.struct(True), m)
+
+    return {"fused_ms": round(timed(fused), 4), "unfused_ms": round(timed(unfused), 4),
+            "used_in_step": "unfused"}
+
+
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bfloat16 MFMA
+
+
+def compute_step(z, idx, w, up, down, dy, reps=5):
+    """The same layer step with every pass in bfloat16 (fmt "compute": the bfloat16
+    grouped GEMMs), its ops timed by spans (HIP events around each), over `reps` steps
+    after two untimed ones."""
+    from bux_amd import moe
+    from bux_amd.spans import Spans
+
+    def run():
+        _, saved = moe.experts_forward(z, idx, w, up, down, fmt="compute")
+        moe.experts_backward(saved, dy, up, down, fmt="compute")
+
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    with Spans() as spans:
+        for _ in range(reps):
+            run()
+        torch.cuda.synchronize()
+    ms = {name: float(np.mean(v)) for name, v in spans.milliseconds().items()}
+    flops = gemm_flops(z.shape[0] * idx.shape[1], z.shape[1], up.shape[2])
+    gemms = {}
+    for name, fl in flops.items():
+        tf = fl / (ms[name] * 1e-3) / 1e12
+        gemms[name] = {"ms": round(ms[name], 4), "tflops": round(tf, 1),
+                       "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    return {"ms_per_step_spans": round(sum(ms.values()), 4), "gemms": gemms}
 
 # The other configs of BASELINE.json, forward only there: (tokens, width, experts, picks,
 # units, activation (kind, limit, up offset), seed, router skew, format, the CPU
@@ -533,6 +591,8 @@ def main():
     }
     result["feed"] = feed_ops(z, idx, E, K)
     result["fused_up_gemm"] = fused_up(z, idx, w, up, E, K)
+    result["fused_down_dgrad"] = fused_down(z, idx, w, up, down, dy, E, K)
+    result["compute_step"] = compute_step(z, idx, w, up, down, dy)
     if not args.no_other_configs:
         result["other_configs"] = other_configs(device)
     if not args.no_cpu_baseline:
