@@ -162,6 +162,7 @@ struct Bf16 {
   using Operand = bux::Operand;
   using Lds = bux::Lds;
   using Loads = bux::Loads;
+  static constexpr bool HALVES = false;  // whole tiles only
   struct Lanes {
     int32_t a[4], b[4];
   };
@@ -197,7 +198,7 @@ struct Bf16 {
     if constexpr (Q + 1 < LOADS) issue_from<Q + 1>(la, lb, ks, lds0, st);
   }
   __device__ static __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks,
-                                               uint32_t lds0, int st) {
+                                               uint32_t lds0, int st, bool) {
     issue_from<0>(la, lb, ks, lds0, st);
   }
 
@@ -210,7 +211,9 @@ struct Bf16 {
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
+  template <bool H>
   __device__ static __forceinline__ Lanes lanes_of() {
+    static_assert(!H, "no half tiles");
     const int wave = threadIdx.x >> 6;
     Lanes ln;
     lane_offsets<AK>(ln.a, (wave >> 1) * 128);
@@ -228,6 +231,7 @@ struct Bf16 {
   }
 
   // All of a step's operands from stage `st`.
+  template <bool H>
   __device__ static __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& ln, int st,
                                                    int32_t) {
     const uint32_t at = lds_at(&lds) + static_cast<uint32_t>(st * sizeof(Stage));
@@ -254,7 +258,7 @@ struct Bf16 {
   // q % 4), each followed by a slice of the memory work: with LOAD, the next loads (step
   // ks_load into stage st_load) after MFMAs 1, 5, .. 29; with READ, the next step's
   // operands into `nxt` after the even MFMAs, in the order its MFMAs take them.
-  template <bool LOAD, bool READ>
+  template <bool LOAD, bool READ, bool H>
   __device__ static __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la,
                                               const Loads& lb, const Lds&, uint32_t lds0,
                                               const Lanes& ln, int32_t ks_load, int st_load,

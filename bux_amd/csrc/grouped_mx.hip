@@ -117,8 +117,12 @@ __device__ __forceinline__ Loads loads_for(const Operand& op, int32_t row0) {
 }
 
 // Direct load Q (0..9) of K step ks into stage `st`: Q < 8 a 16-row slice of A's (even
-// Q) or B's (odd Q) rows of this wave; 8 and 9 the scale words of its A and B rows.
-template <int Q>
+// Q) or B's (odd Q) rows of this wave; 8 and 9 the scale words of its A and B rows. In a
+// half tile (H) the A rows of waves 2 and 3 (128 .. 255) are not loaded: each of those
+// waves loads its A scale words again in their place (4 bytes a lane, the same bytes to
+// the same place as load 8), so that every wave issues 10 loads a step whatever the
+// tile, and the waits count them alike.
+template <int Q, bool H>
 __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int32_t ks,
                                           uint32_t lds0, int st) {
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -126,7 +130,9 @@ __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int3
   if (Q < 8) {
     constexpr int i = Q >> 1;
     const uint32_t slice = w * 4096 + i * 1024;
-    if ((Q & 1) == 0)
+    if ((Q & 1) == 0 && H && w >= 2)
+      load_lds4(la.scales, at + offsetof(Stage, as) + w * 256, la.soff, (ks >> 1) * la.word_stride);
+    else if ((Q & 1) == 0)
       load_lds16(la.values, at + offsetof(Stage, a) + slice, la.voff, ks * la.chunk_stride + i * 1024);
     else
       load_lds16(lb.values, at + offsetof(Stage, b) + slice, lb.voff, ks * lb.chunk_stride + i * 1024);
@@ -137,17 +143,18 @@ __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int3
   }
 }
 
-template <int Q>
+template <int Q, bool H>
 __device__ __forceinline__ void issue_from(const Loads& la, const Loads& lb, int32_t ks,
                                            uint32_t lds0, int st) {
-  issue_one<Q>(la, lb, ks, lds0, st);
-  if constexpr (Q + 1 < LOADS_A_STEP) issue_from<Q + 1>(la, lb, ks, lds0, st);
+  issue_one<Q, H>(la, lb, ks, lds0, st);
+  if constexpr (Q + 1 < LOADS_A_STEP) issue_from<Q + 1, H>(la, lb, ks, lds0, st);
 }
 
-// All of a wave's direct loads of K step ks into stage `st`.
+// All of a wave's direct loads of K step ks into stage `st`, of a whole or a half tile.
 __device__ __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks, uint32_t lds0,
-                                      int st) {
-  issue_from<0>(la, lb, ks, lds0, st);
+                                      int st, bool half) {
+  if (half) issue_from<0, true>(la, lb, ks, lds0, st);
+  else issue_from<0, false>(la, lb, ks, lds0, st);
 }
 
 // Waits until at most `steps` steps' loads of this wave are in flight. A wave's loads
@@ -192,13 +199,17 @@ __device__ __forceinline__ void mask_frag(Frag& f, int32_t ks, int32_t lo, int32
 // (B's) 32-row block 0 (K chunks h and 2 + h of the step for lane half h, the MFMA's two
 // blocks of 32), and its scale byte of block 0 in an even step. Block p is 2048 bytes
 // further (128 for the scale), an odd step's scale 2 bytes.
+// A whole tile's waves are 2 x 2 (each 128 rows of A, 128 of B); a half tile's 1 x 4
+// (each the tile's 128 rows of A, 64 of B).
 struct Lanes {
   int32_t a_lo, a_hi, b_lo, b_hi, sa, sb;
 };
+template <bool H>
 __device__ __forceinline__ Lanes lanes_of() {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, row = lane & 31, sw = swizzle(row);
-  const int ra = (wave >> 1) * 128 + row, rb = (wave & 1) * 128 + row;
+  const int ra = (H ? 0 : (wave >> 1) * 128) + row;
+  const int rb = (H ? wave * 64 : (wave & 1) * 128) + row;
   const int lo = (half ^ sw) << 4, hi = ((2 + half) ^ sw) << 4;
   return Lanes{ra * BK + lo, ra * BK + hi, rb * BK + lo, rb * BK + hi, ra * 4 + half, rb * 4 + half};
 }
@@ -229,12 +240,14 @@ __device__ __forceinline__ void read_b(Frag& f, const Lds& lds, const Lanes& ln,
   f.sb[p] = (reinterpret_cast<const uint8_t*>(lds.st[st].bs) + ((ks & 1) << 1) + p * 128)[ln.sb];
 }
 
+// A step's operands: A's 4 blocks and B's 4 (a half tile's wave: B's 2).
+template <bool H>
 __device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& ln, int st,
                                           int32_t ks) {
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     read_a(f, lds, ln, st, ks, p);
-    read_b(f, lds, ln, st, ks, p);
+    if (!H || p < 2) read_b(f, lds, ln, st, ks, p);
   }
 }
 
@@ -258,16 +271,16 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
     __builtin_amdgcn_sched_barrier(0);
     if (LOAD) {
       switch (q) {
-        case 0: issue_one<0>(la, lb, ks_load, lds0, st_load); break;
-        case 1: issue_one<1>(la, lb, ks_load, lds0, st_load); break;
-        case 2: issue_one<2>(la, lb, ks_load, lds0, st_load); break;
-        case 3: issue_one<3>(la, lb, ks_load, lds0, st_load); break;
-        case 4: issue_one<4>(la, lb, ks_load, lds0, st_load); break;
-        case 5: issue_one<5>(la, lb, ks_load, lds0, st_load); break;
-        case 6: issue_one<6>(la, lb, ks_load, lds0, st_load); break;
-        case 7: issue_one<7>(la, lb, ks_load, lds0, st_load); break;
-        case 8: issue_one<8>(la, lb, ks_load, lds0, st_load); break;
-        case 9: issue_one<9>(la, lb, ks_load, lds0, st_load); break;
+        case 0: issue_one<0, false>(la, lb, ks_load, lds0, st_load); break;
+        case 1: issue_one<1, false>(la, lb, ks_load, lds0, st_load); break;
+        case 2: issue_one<2, false>(la, lb, ks_load, lds0, st_load); break;
+        case 3: issue_one<3, false>(la, lb, ks_load, lds0, st_load); break;
+        case 4: issue_one<4, false>(la, lb, ks_load, lds0, st_load); break;
+        case 5: issue_one<5, false>(la, lb, ks_load, lds0, st_load); break;
+        case 6: issue_one<6, false>(la, lb, ks_load, lds0, st_load); break;
+        case 7: issue_one<7, false>(la, lb, ks_load, lds0, st_load); break;
+        case 8: issue_one<8, false>(la, lb, ks_load, lds0, st_load); break;
+        case 9: issue_one<9, false>(la, lb, ks_load, lds0, st_load); break;
         default: break;
       }
     }
@@ -275,6 +288,46 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
       if (q == 0) read_a(nxt, lds, ln, st_next, ks_next, 0);
       if (q < 4) read_b(nxt, lds, ln, st_next, ks_next, q);
       if (q == 4 || q == 8 || q == 12) read_a(nxt, lds, ln, st_next, ks_next, q >> 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// A half tile's step: each wave's 128 x 64 outputs, 8 MFMAs (MFMA q taking A's block
+// q / 2 and B's block q % 2), with the same 10 loads (one after each of the first 7
+// MFMAs, three after the last) and the next step's 6 blocks read in the order its
+// MFMAs take them (a0 b0, b1, a1, a2, a3).
+template <bool LOAD, bool READ>
+__device__ __forceinline__ void step_half(const Frag& cur, Frag& nxt, const Loads& la,
+                                          const Loads& lb, const Lds& lds, uint32_t lds0,
+                                          const Lanes& ln, int32_t ks_load, int st_load,
+                                          int32_t ks_next, int st_next, v16f acc[4][4]) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = q >> 1, j = q & 1;
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(cur.b[j], cur.a[i], acc[i][j], 0,
+                                                               0, 0, cur.sb[j], 0, cur.sa[i]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (LOAD) {
+      switch (q) {
+        case 0: issue_one<0, true>(la, lb, ks_load, lds0, st_load); break;
+        case 1: issue_one<1, true>(la, lb, ks_load, lds0, st_load); break;
+        case 2: issue_one<2, true>(la, lb, ks_load, lds0, st_load); break;
+        case 3: issue_one<3, true>(la, lb, ks_load, lds0, st_load); break;
+        case 4: issue_one<4, true>(la, lb, ks_load, lds0, st_load); break;
+        case 5: issue_one<5, true>(la, lb, ks_load, lds0, st_load); break;
+        case 6: issue_one<6, true>(la, lb, ks_load, lds0, st_load); break;
+        default:
+          issue_one<7, true>(la, lb, ks_load, lds0, st_load);
+          issue_one<8, true>(la, lb, ks_load, lds0, st_load);
+          issue_one<9, true>(la, lb, ks_load, lds0, st_load);
+          break;
+      }
+    }
+    if (READ) {
+      if (q == 0) read_a(nxt, lds, ln, st_next, ks_next, 0);
+      if (q < 2) read_b(nxt, lds, ln, st_next, ks_next, q);
+      if (q == 2 || q == 4 || q == 6) read_a(nxt, lds, ln, st_next, ks_next, q >> 1);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -408,6 +461,76 @@ __device__ __forceinline__ void store_tile(const v16f acc[4][4], float* tile, in
   store_f32(acc, tile, ld, rows, cols);
 }
 
+// A half tile's outputs, each wave's 128 rows x 64 columns (columns 64 w on; accumulator
+// blocks [i][0..1]). bfloat16 through the wave's region of the stage as store_bf16 does,
+// read back 16 bytes a lane, 8 lanes a row, in 4 rounds of 32 rows.
+__device__ void store_tile_half(const v16f acc[4][4], uint16_t* tile, int32_t ld, int32_t rows,
+                                int32_t cols, Stage& stage) {
+  const FromAcc pairs{acc};
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint8_t* region = reinterpret_cast<uint8_t*>(&stage) + wave * 32 * PITCH;
+  uint8_t* mine = region + (lane & 31) * PITCH + 8 * (lane >> 5);
+  const int cc = lane & 7;
+  const uint8_t* from = region + (lane >> 3) * PITCH + cc * 16;
+  const int32_t col = wave * 64 + 8 * cc;
+  uint16_t* out = tile + (lane >> 3) * ld + col;
+  const bool whole = rows >= BM / 2 && cols >= BN;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(tile, 0, 0x7fffffff, 0x00020000);
+  const int32_t lane_off = ((lane >> 3) * ld + col) * 2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<uint2*>(mine + (j * 4 + g) * 16) = pairs(i, j, g);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    uint4 v[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) v[it] = *reinterpret_cast<const uint4*>(from + it * 8 * PITCH);
+    if (whole) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[it].x, v[it].y, v[it].z, v[it].w}, rsrc,
+                                               lane_off, (i * 32 + it * 8) * ld * 2, NT);
+    } else if (col < cols) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int32_t row = i * 32 + it * 8 + (lane >> 3);
+        if (row < rows) {
+          uint16_t* at = out + (i * 32 + it * 8) * ld;
+          if (col + 8 <= cols) stream16(at, v[it]);
+          else stream8(at, v[it].x, v[it].y);  // cols % 4 == 0
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+// float32 (for tests), straight from the accumulators as store_f32.
+__device__ void store_tile_half(const v16f acc[4][4], float* tile, int32_t ld, int32_t rows,
+                                int32_t cols, Stage&) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int32_t row = i * 32 + (lane & 31);
+    if (row >= rows) continue;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int32_t col = wave * 64 + j * 32 + 8 * g + 4 * (lane >> 5);
+        const v16f& a = acc[i][j];
+        if (col < cols)
+          stream16(tile + row * ld + col,
+                   make_uint4(__float_as_uint(a[4 * g]), __float_as_uint(a[4 * g + 1]),
+                              __float_as_uint(a[4 * g + 2]), __float_as_uint(a[4 * g + 3])));
+      }
+  }
+}
+
 // The plain epilogue: the tile's rows [0, rows) and columns [0, cols) of a row-major
 // output of pitch ld, from its corner.
 template <typename T>
@@ -415,7 +538,8 @@ struct Plain {
   T* out;
   int32_t ld;
   __device__ __forceinline__ void store(const v16f acc[4][4], const Job& j, Stage& stage) const {
-    store_tile(acc, out + j.corner, ld, j.rows, j.cols, stage);
+    if (j.half) store_tile_half(acc, out + j.corner, ld, j.rows, j.cols, stage);
+    else store_tile(acc, out + j.corner, ld, j.rows, j.cols, stage);
   }
 };
 
@@ -433,6 +557,7 @@ struct Mx {
   using Loads = bux::Loads;
   using Lanes = bux::Lanes;
   using Frag = bux::Frag;
+  static constexpr bool HALVES = true;  // half tiles: 1 x 4 waves, 128 rows
   __device__ static __forceinline__ Loads loads_a(const Operand& a, int32_t row0) {
     return loads_for(a, row0);
   }
@@ -440,24 +565,30 @@ struct Mx {
     return loads_for(group_of(b, group), row0);
   }
   __device__ static __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks,
-                                               uint32_t lds0, int st) {
-    bux::issue(la, lb, ks, lds0, st);
+                                               uint32_t lds0, int st, bool half) {
+    bux::issue(la, lb, ks, lds0, st, half);
   }
   __device__ static __forceinline__ void wait_loads(int32_t steps) { bux::wait_loads(steps); }
-  __device__ static __forceinline__ Lanes lanes_of() { return bux::lanes_of(); }
+  template <bool H>
+  __device__ static __forceinline__ Lanes lanes_of() { return bux::lanes_of<H>(); }
+  template <bool H>
   __device__ static __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& ln, int st,
                                                    int32_t ks) {
-    bux::read_frag(f, lds, ln, st, ks);
+    bux::read_frag<H>(f, lds, ln, st, ks);
   }
   __device__ static __forceinline__ void mask_frag(Frag& f, int32_t ks, int32_t lo, int32_t hi) {
     bux::mask_frag(f, ks, lo, hi);
   }
-  template <bool LOAD, bool READ>
+  template <bool LOAD, bool READ, bool H>
   __device__ static __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la,
                                               const Loads& lb, const Lds& lds, uint32_t lds0,
                                               const Lanes& ln, int32_t ks_load, int st_load,
                                               int32_t ks_next, int st_next, v16f acc[4][4]) {
-    bux::step<LOAD, READ>(cur, nxt, la, lb, lds, lds0, ln, ks_load, st_load, ks_next, st_next, acc);
+    if constexpr (H)
+      bux::step_half<LOAD, READ>(cur, nxt, la, lb, lds, lds0, ln, ks_load, st_load, ks_next,
+                                 st_next, acc);
+    else
+      bux::step<LOAD, READ>(cur, nxt, la, lb, lds, lds0, ln, ks_load, st_load, ks_next, st_next, acc);
   }
 };
 
@@ -470,7 +601,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   extern __shared__ __align__(16) uint8_t smem[];
   if (!list_fits(starts, groups, A.rows, height)) return;
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const RowsTiles<> list{tiles, groups, n, height, col_tiles, A.k / BK, A.k};
+  const RowsTiles<false, true> list{tiles, groups, n, height, col_tiles, A.k / BK, A.k};
   const int32_t count = starts[groups + 1] * col_tiles;
   run_tiles<Mx>(list, count, A, B, lds, Plain<T>{y, n});
 }
@@ -484,7 +615,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   extern __shared__ __align__(16) uint8_t smem[];
   if (!list_fits(starts, groups, A.rows, height)) return;
   Lds& lds = *reinterpret_cast<Lds*>(smem);
-  const StartedTiles list{tiles, starts, a_starts, groups, n, height, col_tiles, A.k / BK};
+  const StartedTiles<true> list{tiles, starts, a_starts, groups, n, height, col_tiles, A.k / BK};
   const int32_t count = starts[groups + 1] * col_tiles;
   run_tiles<Mx>(list, count, A, B, lds, Plain<T>{y, n});
 }
@@ -568,6 +699,7 @@ bool offsets_fit(int64_t rows, int64_t k) { return (rows + BM) * k < (1LL << 31)
 
 // The fused GEMM's tiles: the 32-aligned tile list by 256-column tiles of the product.
 struct GluTiles {
+  static constexpr bool HALVES = false;
   const Tile* tiles;
   const int32_t* starts;
   int32_t groups, n, height, col_tiles, k_steps;
@@ -586,6 +718,7 @@ struct GluTiles {
     j.ks_begin = 0;
     j.n = t.group < groups ? k_steps : 0;  // rows past the groups: zeros
     j.mask = false;
+    j.half = false;
     j.mlo = j.mhi = 0;
     j.corner = static_cast<int64_t>(t.lo) * n + col0;
     return true;

@@ -13,6 +13,8 @@
 // the bfloat16 GEMMs' Bf16); the output, a functor with store(acc, job, stage).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace bux {
@@ -169,12 +171,13 @@ __device__ __forceinline__ int32_t smaller(int32_t a, int32_t b) { return a < b 
 // One output tile's work: C[r][c] = sum over K steps [ks_begin, ks_begin + n) of
 // A[a_row0 + r] . B[b_row0 + c] (B of `group`), the K positions outside [mlo, mhi)
 // counting 0 where `mask` (in the first and last steps); its rows [0, rows) and columns
-// [0, cols) stored at `corner`.
+// [0, cols) stored at `corner`. A `half` tile holds at most BM / 2 rows: only its first
+// BM / 2 rows of A are loaded and computed (a format that has half tiles, P::HALVES).
 struct Job {
   int32_t a_row0, b_row0, group;
   int32_t ks_begin, n;
   int32_t mlo, mhi;
-  bool mask;
+  bool mask, half;
   int64_t corner;
   int32_t rows, cols;
   int32_t row_lo;  // the first of the tile's rows it stores (the fused epilogue's)
@@ -182,9 +185,11 @@ struct Job {
 
 // The rows GEMM's tiles: the tile list's row tiles by 256-column tiles of y. K is k_end
 // positions in k_steps steps; with TAIL the last step reaches past k_end and is masked
-// there.
-template <bool TAIL = false>
+// there. With HALVES a tile of at most BM / 2 rows (a group's last, or a small group's
+// only one) is a half tile.
+template <bool TAIL = false, bool HALVES_ = false>
 struct RowsTiles {
+  static constexpr bool HALVES = HALVES_;
   const Tile* tiles;
   int32_t groups, n, height, col_tiles, k_steps, k_end;
   __device__ bool job(int32_t id, Job& j) const {
@@ -200,6 +205,7 @@ struct RowsTiles {
     j.ks_begin = 0;
     j.n = t.group < groups ? k_steps : 0;  // rows past the groups: zeros
     j.mask = TAIL;
+    j.half = HALVES && j.rows <= BM / 2;
     j.mlo = 0;
     j.mhi = k_end;
     j.corner = static_cast<int64_t>(t.lo) * n + col0;
@@ -209,8 +215,11 @@ struct RowsTiles {
 
 // The rows GEMM's tiles where each group's rows lie in a from a_starts[g] (tiles from
 // the prologue given those starts) while y's rows stay packed (starts, the prologue's):
-// a tile's rows of a map to y's by the group's shift, packed start less a's.
+// a tile's rows of a map to y's by the group's shift, packed start less a's. HALVES as
+// RowsTiles's.
+template <bool HALVES_ = false>
 struct StartedTiles {
+  static constexpr bool HALVES = HALVES_;
   const Tile* tiles;
   const int32_t* starts;    // packed: where each group's rows lie in y
   const int32_t* a_starts;  // where they lie in a
@@ -229,6 +238,7 @@ struct StartedTiles {
     j.ks_begin = 0;
     j.n = t.group < groups ? k_steps : 0;  // rows past the groups: zeros
     j.mask = false;
+    j.half = HALVES && j.rows <= BM / 2;
     j.mlo = j.mhi = 0;
     j.corner = static_cast<int64_t>(lo) * n + col0;
     return true;
@@ -239,6 +249,7 @@ struct StartedTiles {
 // rows of the operands, `step` of them a K step, and a group's sum takes its own rows
 // [starts[g], starts[g + 1]) only.
 struct ContractTiles {
+  static constexpr bool HALVES = false;
   const int32_t* starts;
   int32_t d, f, d_tiles, f_tiles, step;
   __device__ bool job(int32_t id, Job& j) const {
@@ -252,6 +263,7 @@ struct ContractTiles {
     j.ks_begin = start / step;
     j.n = end > start ? (end + step - 1) / step - j.ks_begin : 0;
     j.mask = (start % step) != 0 || (end % step) != 0;
+    j.half = false;
     j.mlo = start;
     j.mhi = end;
     j.corner = (static_cast<int64_t>(g) * d + row0) * f + col0;
@@ -305,6 +317,10 @@ __device__ __forceinline__ void barrier_lds() {
 // (the next tile's first steps, issued during this tile's last ones, have landed by
 // then) and the next tile skips its waits for those steps; the first wait left (for
 // step 3) comes a few steps after the stores went out.
+//
+// Half tiles (P::HALVES, and a tile list with them, Tiles::HALVES): the same stream and the same number of loads a step and wave
+// (P::issue stands in cheap ones for the A loads a half tile skips), so every wait
+// counts as for a whole tile; their steps run P::step's half form.
 template <typename P, typename Out, typename Tiles>
 __device__ __forceinline__ void run_tiles(const Tiles& tiles, int32_t count,
                                           const typename P::Operand& A,
@@ -317,12 +333,12 @@ __device__ __forceinline__ void run_tiles(const Tiles& tiles, int32_t count,
   Job job{}, next{};
   if (!next_job(tiles, mine, id, job)) return;
   const uint32_t lds0 = lds_at(&lds);
-  const typename P::Lanes ln = P::lanes_of();
   int32_t base = 0;   // the stage of this tile's step 0
   int32_t ready = 0;  // this tile's steps known to have landed
   {
     const Loads la = P::loads_a(A, job.a_row0), lb = P::loads_b(B, job.group, job.b_row0);
-    for (int32_t s = 0; s < STAGES && s < job.n; ++s) P::issue(la, lb, job.ks_begin + s, lds0, s);
+    for (int32_t s = 0; s < STAGES && s < job.n; ++s)
+      P::issue(la, lb, job.ks_begin + s, lds0, s, Tiles::HALVES && job.half);
   }
   for (;;) {
     const bool more = next_job(tiles, mine, id, next);
@@ -334,15 +350,18 @@ __device__ __forceinline__ void run_tiles(const Tiles& tiles, int32_t count,
     // now.
     int32_t ahead = 0;
     for (; ahead < 3 && ahead < nn && n + ahead < STAGES; ++ahead)
-      P::issue(na, nb, next.ks_begin + ahead, lds0, stage(n + ahead));
+      P::issue(na, nb, next.ks_begin + ahead, lds0, stage(n + ahead), Tiles::HALVES && next.half);
     v16f acc[4][4];
     zero_acc(acc);
-    if (n > 0) {
+    // The K loop of a whole (H false) or a half tile.
+    auto loop = [&](auto half) {
+      constexpr bool H = decltype(half)::value;
+      const typename P::Lanes ln = P::template lanes_of<H>();
       auto edge = [&](int32_t k) { return job.mask && (k == 0 || k == n - 1); };
       if (ready < 1) P::wait_loads(smaller(n, STAGES) - 1 + ahead);
       barrier_lds();
       Frag cur, nxt;
-      P::read_frag(cur, lds, ln, stage(0), job.ks_begin);
+      P::template read_frag<H>(cur, lds, ln, stage(0), job.ks_begin);
       if (edge(0)) P::mask_frag(cur, job.ks_begin, job.mlo, job.mhi);
       int32_t k = 0;
       // Steps with this tile's load 4 ahead, two a turn so that the operand sets swap
@@ -352,18 +371,18 @@ __device__ __forceinline__ void run_tiles(const Tiles& tiles, int32_t count,
         // Step k + 1's stage is whole; every wave has read step k's, which step k + 4's
         // loads take.
         barrier_lds();
-        P::template step<true, true>(cur, nxt, la, lb, lds, lds0, ln, job.ks_begin + k + 4,
-                                     stage(k), job.ks_begin + k + 1, stage(k + 1), acc);
+        P::template step<true, true, H>(cur, nxt, la, lb, lds, lds0, ln, job.ks_begin + k + 4,
+                                        stage(k), job.ks_begin + k + 1, stage(k + 1), acc);
         if (k + 2 >= ready) P::wait_loads(2);
         barrier_lds();
-        P::template step<true, true>(nxt, cur, la, lb, lds, lds0, ln, job.ks_begin + k + 5,
-                                     stage(k + 1), job.ks_begin + k + 2, stage(k + 2), acc);
+        P::template step<true, true, H>(nxt, cur, la, lb, lds, lds0, ln, job.ks_begin + k + 5,
+                                        stage(k + 1), job.ks_begin + k + 2, stage(k + 2), acc);
       }
       for (; k + 4 < n; ++k) {
         if (k + 1 >= ready) P::wait_loads(2);
         barrier_lds();
-        P::template step<true, true>(cur, nxt, la, lb, lds, lds0, ln, job.ks_begin + k + 4,
-                                     stage(k), job.ks_begin + k + 1, stage(k + 1), acc);
+        P::template step<true, true, H>(cur, nxt, la, lb, lds, lds0, ln, job.ks_begin + k + 4,
+                                        stage(k), job.ks_begin + k + 1, stage(k + 1), acc);
         cur = nxt;
       }
       // The last steps: the freed stages take the next tile's first steps.
@@ -371,16 +390,24 @@ __device__ __forceinline__ void run_tiles(const Tiles& tiles, int32_t count,
         if (k + 1 >= ready) P::wait_loads(smaller(n - 2 - k + ahead, 3));
         barrier_lds();
         if (ahead < 3 && ahead < nn && k + STAGES == n + ahead) {
-          P::issue(na, nb, next.ks_begin + ahead, lds0, stage(k));
+          P::issue(na, nb, next.ks_begin + ahead, lds0, stage(k), Tiles::HALVES && next.half);
           ++ahead;
         }
-        P::template step<false, true>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, job.ks_begin + k + 1,
-                                      stage(k + 1), acc);
+        P::template step<false, true, H>(cur, nxt, la, lb, lds, lds0, ln, 0, 0,
+                                         job.ks_begin + k + 1, stage(k + 1), acc);
         cur = nxt;
       }
       // the last step's operands (read during the step before): its edge, if it has one
       if (n > 1 && edge(n - 1)) P::mask_frag(cur, job.ks_begin + n - 1, job.mlo, job.mhi);
-      P::template step<false, false>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, 0, 0, acc);
+      P::template step<false, false, H>(cur, nxt, la, lb, lds, lds0, ln, 0, 0, 0, 0, acc);
+    };
+    if (n > 0) {
+      if constexpr (P::HALVES && Tiles::HALVES) {
+        if (job.half) loop(std::true_type{});
+        else loop(std::false_type{});
+      } else {
+        loop(std::false_type{});
+      }
     }
     // Every load in flight (the next tile's first steps) lands before the stores go out;
     // every wave is done with this tile's stages, and its last step's (stage n + 3) stages
@@ -390,7 +417,7 @@ __device__ __forceinline__ void run_tiles(const Tiles& tiles, int32_t count,
     out.store(acc, job, lds.st[stage(n + 3)]);
     barrier_lds();
     if (!more) break;
-    if (nn > 3) P::issue(na, nb, next.ks_begin + 3, lds0, stage(n + 3));
+    if (nn > 3) P::issue(na, nb, next.ks_begin + 3, lds0, stage(n + 3), Tiles::HALVES && next.half);
     base = stage(n);
     ready = ahead;
     job = next;
