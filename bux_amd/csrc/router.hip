@@ -405,22 +405,24 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // The K loop staged through LDS (at most 256 logits, d a multiple of 64). A workgroup
-// takes 64 tokens; per step of 64 columns of K, the tokens' 128-byte row pieces (8 KiB)
-// and the transposed kernel's (128 CB rows, 16 CB KiB) go straight from global memory
-// into a stage of LDS (buffer_load ... lds, 1 KiB an instruction), STAGES - 1 steps
-// ahead, one barrier a step; wave w multiplies the 64 tokens by its CB blocks of 32
-// experts from LDS. A stage's rows are 128 bytes, their 16-byte chunk c at c ^ ((row
-// / 2) % 8), so the 16 lanes that read one chunk of 16 rows hit 16 different bank
-// groups; a load's lane i takes the chunk that belongs at its place. After the loop
+// takes TOKS tokens (32 or 64); per step of 64 columns of K, the tokens' 128-byte row
+// pieces (TOKS / 8 KiB) and the transposed kernel's (128 CB rows, 16 CB KiB) go straight
+// from global memory into a stage of LDS (buffer_load ... lds, 1 KiB an instruction),
+// STAGES - 1 steps ahead, one barrier a step; wave w multiplies the tokens by its CB
+// blocks of 32 experts from LDS. A stage's rows are 128 bytes, their 16-byte chunk c at
+// c ^ ((row / 2) % 8), so the 16 lanes that read one chunk of 16 rows hit 16 different
+// bank groups; a load's lane i takes the chunk that belongs at its place. After the loop
 // the stages hold the logits tile.
-template <int CB, int CAP>
+template <int TOKS>
+constexpr int staged_stages(int cb) { return TOKS == 32 ? 3 : (cb == 1 ? 4 : 3); }
+template <int CB, int CAP, int TOKS>
 __global__ __launch_bounds__(THREADS) void route_staged_kernel(Params p) {
-  constexpr int TOKS = 64;
+  constexpr int RB = TOKS / 32;  // row blocks of 32 tokens, and a wave's loads of x a step
   constexpr int NPAD = 128 * CB;
   constexpr int X_BYTES = TOKS * 128;
   constexpr int STAGE = X_BYTES + NPAD * 128;
-  constexpr int STAGES = CB == 1 ? 4 : 3;
-  constexpr int LPS = TOKS / 32 + NPAD / 32;  // a wave's loads a step: 2 of x, 4 CB of kernel
+  constexpr int STAGES = staged_stages<TOKS>(CB);
+  constexpr int LPS = RB + NPAD / 32;  // a wave's loads a step: RB of x, 4 CB of kernel
   extern __shared__ __align__(16) float lds[];
   __shared__ uint64_t kept_groups[TOKS];
   const int pitch = pitch_of(p.npad);
@@ -436,17 +438,17 @@ __global__ __launch_bounds__(THREADS) void route_staged_kernel(Params p) {
   // This lane's place in a 1 KiB slice of 8 rows, and the chunk that belongs there.
   const int srow = lane >> 3, place = lane & 7;
   auto voff = [&](int row) { return row * static_cast<int>(row_bytes) + 16 * (place ^ ((row >> 1) & 7)); };
-  int xoff[2], koff[4 * CB];
+  int xoff[RB], koff[4 * CB];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) xoff[j] = voff((2 * wave + j) * 8 + srow);
+  for (int j = 0; j < RB; ++j) xoff[j] = voff((RB * wave + j) * 8 + srow);
 #pragma unroll
   for (int j = 0; j < 4 * CB; ++j) koff[j] = voff((wave * 4 * CB + j) * 8 + srow);
   const int steps = static_cast<int>(p.d / 64);
   auto issue = [&](int ks, int st) {
     const uint32_t at = lds0 + st * STAGE;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      load_lds16_uniform(xr, at + (2 * wave + j) * 1024, xoff[j], ks * 128);
+    for (int j = 0; j < RB; ++j)
+      load_lds16_uniform(xr, at + (RB * wave + j) * 1024, xoff[j], ks * 128);
 #pragma unroll
     for (int j = 0; j < 4 * CB; ++j)
       load_lds16_uniform(kr, at + X_BYTES + (wave * 4 * CB + j) * 1024, koff[j], ks * 128);
@@ -454,9 +456,9 @@ __global__ __launch_bounds__(THREADS) void route_staged_kernel(Params p) {
   // Lane offsets of the fragments: row block rb of x, expert block cb of the wave; the
   // chunk of K sub-step u is 2 u + h.
   auto frag_at = [&](int row, int u) { return row * 128 + 16 * ((2 * u + h) ^ ((row >> 1) & 7)); };
-  v16f acc[2][CB];
+  v16f acc[RB][CB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
   for (int s0 = 0; s0 < STAGES - 1 && s0 < steps; ++s0) issue(s0, s0);
@@ -471,16 +473,16 @@ __global__ __launch_bounds__(THREADS) void route_staged_kernel(Params p) {
     const uint8_t* st = base + (ks % STAGES) * STAGE;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      bf16x8 a[2], b[CB];
+      bf16x8 a[RB], b[CB];
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
         a[rb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(st + frag_at(rb * 32 + r, u)));
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb)
         b[cb] = __builtin_bit_cast(
             bf16x8, *reinterpret_cast<const uint4*>(st + X_BYTES + frag_at((wave * CB + cb) * 32 + r, u)));
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
           acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb], b[cb], acc[rb][cb], 0, 0, 0);
@@ -494,7 +496,7 @@ __global__ __launch_bounds__(THREADS) void route_staged_kernel(Params p) {
     if (col >= p.n) continue;
     const float bias = p.bias ? p.bias[col] : 0.0f;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int row = rb * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
@@ -512,18 +514,26 @@ __global__ __launch_bounds__(THREADS) void route_staged_kernel(Params p) {
   select<TOKS, CAP>(p, tile, pitch, t0, kept_groups);
 }
 
-template <int CB, int CAP>
-int launch_staged(const Params& p, hipStream_t s) {
-  constexpr int STAGE = (64 + 128 * CB) * 128, STAGES = CB == 1 ? 4 : 3;
-  const size_t tile = static_cast<size_t>(64) * pitch_of(p.npad) * sizeof(float);
+template <int CB, int CAP, int TOKS>
+int launch_staged_of(const Params& p, hipStream_t s) {
+  constexpr int STAGE = (TOKS + 128 * CB) * 128, STAGES = staged_stages<TOKS>(CB);
+  const size_t tile = static_cast<size_t>(TOKS) * pitch_of(p.npad) * sizeof(float);
   const size_t lds = tile > static_cast<size_t>(STAGES * STAGE) ? tile : STAGES * STAGE;
-  const void* kernel = reinterpret_cast<const void*>(route_staged_kernel<CB, CAP>);
+  const void* kernel = reinterpret_cast<const void*>(route_staged_kernel<CB, CAP, TOKS>);
   hipError_t err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(lds));
   if (err != hipSuccess) return fail(BUX_E_LAUNCH, "route_staged_kernel: %s", hipGetErrorString(err));
-  hipLaunchKernelGGL((route_staged_kernel<CB, CAP>), dim3(static_cast<unsigned>(ceil_div(p.t, 64))),
+  hipLaunchKernelGGL((route_staged_kernel<CB, CAP, TOKS>), dim3(static_cast<unsigned>(ceil_div(p.t, TOKS))),
                      dim3(THREADS), lds, s, p);
   return launched("route_staged_kernel");
+}
+
+// 32 tokens a workgroup for up to 128 logits (two workgroups a CU in LDS, one's
+// selection beside the other's K loop); 64 for more.
+template <int CB, int CAP>
+int launch_staged(const Params& p, hipStream_t s) {
+  if constexpr (CB == 1) return launch_staged_of<CB, CAP, 32>(p, s);
+  else return launch_staged_of<CB, CAP, 64>(p, s);
 }
 
 template <int SPLIT, int BLOCKS, int TOKS, int CAP>
