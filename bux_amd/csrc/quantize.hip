@@ -21,11 +21,17 @@
 //     each row's 128 bytes in one coalesced burst of 8 lanes;
 //   - the row copy: a block of 32 columns is 4 neighbouring lanes, reduced by two
 //     xor-shuffles; each lane writes its 8 codes as one 8-byte store (8 lanes a row's
-//     64 bytes of a K chunk, consecutive rows consecutive);
-//   - the column copy: the tile goes through LDS; wave w takes rows 32w..32w+31, lane
-//     l column l, reading one LDS row per step (all lanes on one row: no bank
-//     conflicts), and writes its 32 codes of x^T's row l as two 16-byte stores (half
-//     of the row's 64-byte K chunk; the other wave of the pair writes the other half).
+//     64 bytes of a K chunk, consecutive rows consecutive: a store instruction writes
+//     512 bytes in one run; pairs of lanes swapping halves for 16-byte stores measured
+//     no faster);
+//   - the column copy: the tile goes through LDS; four neighbouring lanes take a
+//     column, lane q its rows 16 q .. 16 q + 15 of each half of 64 rows (a block of 32
+//     is a pair of lanes, reduced by one xor-shuffle), and write its 16 codes of x^T's
+//     row as one 16-byte store: a wave's store is 16 of x^T's rows' 64-byte K chunks,
+//     1 KiB in one run. Lane 0 of the four writes the column's 4 scale bytes of the
+//     tile's 128 rows as one word. The tile's 16-byte chunks are swizzled by row (chunk
+//     c of row r at c ^ 2 ((r / 16) % 4)), so that the four lanes' rows, 16 apart, read
+//     different banks.
 // HBM traffic per element: 2 bytes read, 2 x (1 + 1/32) bytes written.
 //
 // With BUX_MX_TILES the scale is one per 32 x 32 tile of x instead (the mxfp8_2d
@@ -216,6 +222,10 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     int flags, uint8_t* __restrict__ values, uint8_t* __restrict__ scales,
     uint8_t* __restrict__ t_values, uint8_t* __restrict__ t_scales) {
   __shared__ uint16_t tile[TILE_ROWS][TILE_COLS];
+  // where column `col` of row `row` sits in the tile: its 16-byte chunk swizzled
+  const auto at = [&](int row, int col) -> uint16_t& {
+    return tile[row][(((col >> 3) ^ (2 * ((row >> 4) & 3))) << 3) | (col & 7)];
+  };
 
   const int t = threadIdx.x;
   // Column tiles run fastest, so that neighbouring tiles read one band of rows; and,
@@ -260,12 +270,12 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
   if (tiles) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4*>(&tile[(t >> 3) + 32 * i][8 * chunk]) = raw[i];
+      *reinterpret_cast<uint4*>(&at((t >> 3) + 32 * i, 8 * chunk)) = raw[i];
     __syncthreads();
     const int wave = t >> 6, lane = t & 63;
     float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(bf16_to_f32(tile[32 * wave + j][lane])));
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(bf16_to_f32(at(32 * wave + j, lane))));
 #pragma unroll
     for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
     if ((lane & 31) == 0) tile_e[wave][lane >> 5] = scale_exponent_bf16(amax);
@@ -309,39 +319,43 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
 
   if (!tiles) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<uint4*>(&tile[(t >> 3) + 32 * i][8 * chunk]) = raw[i];
-    }
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&at((t >> 3) + 32 * i, 8 * chunk)) = raw[i];
     __syncthreads();
   }
 
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int64_t c = col0 + lane;
-  const int64_t rb = row0 + 32 * wave;  // the block's first row (below kt: tiles cover it)
-  const int64_t kt = (height + 127) / 128 * 128;  // the column copy's K, padded
-  if (c >= cols) return;
-  float v[32];
-  float amax = 0.0f;
+  // x^T's row c (of x's column c), K (x's rows) from row0: lane q of its four holds K
+  // 64 h + 16 q .. + 15 in half h; a block of 32 is the pair q / 2.
+  const int q = t & 3, lc = t >> 2;
+  const int64_t c = col0 + lc;
+  const int64_t kt = (height + 127) / 128 * 128;  // the column copy's K, padded (tiles cover it)
+  const bool col_out = c < cols;
+  uint8_t* out = t_values + g * cols * kt + ((row0 >> 6) * cols + c) * 64 + 16 * q;
+  uint32_t word = 0;  // lane 0's scale bytes of the 4 blocks
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    v[j] = bf16_to_f32(tile[32 * wave + j][lane]);
-    amax = fmaxf(amax, fabsf(v[j]));
-  }
-  const int e = tiles ? tile_e[wave][lane >> 5] : scale_exponent_bf16(amax);
-  const float down = power_of_two_down(e);
-  uint32_t w[8];
+  for (int h = 0; h < 2; ++h) {
+    float v[16];
+    float amax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    w[j] = e4m3x4(clip448(v[4 * j] * down), clip448(v[4 * j + 1] * down),
-                  clip448(v[4 * j + 2] * down), clip448(v[4 * j + 3] * down));
+    for (int j = 0; j < 16; ++j) {
+      v[j] = bf16_to_f32(at(64 * h + 16 * q + j, lc));
+      amax = fmaxf(amax, fabsf(v[j]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    const int e = tiles ? tile_e[2 * h + (q >> 1)][lc >> 5] : scale_exponent_bf16(amax);
+    const float down = power_of_two_down(e);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = e4m3x4(clip448(v[4 * j] * down), clip448(v[4 * j + 1] * down),
+                    clip448(v[4 * j + 2] * down), clip448(v[4 * j + 3] * down));
+    if (col_out) *reinterpret_cast<uint4*>(out + h * cols * 64) = make_uint4(w[0], w[1], w[2], w[3]);
+    // block 2 h from this pair (q 0, 1), block 2 h + 1 from the other (q 2, 3)
+    const uint32_t b = static_cast<uint32_t>(e + 127);
+    const uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(b), 2));
+    word |= (b | (other << 8)) << (16 * h);
   }
-  // x^T's row c, K (x's rows) from rb: 32 bytes of its 64-byte chunk rb / 64
-  uint8_t* out = t_values + g * cols * kt + ((rb >> 6) * cols + c) * 64 + (rb & 63);
-  reinterpret_cast<uint4*>(out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-  reinterpret_cast<uint4*>(out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
-  t_scales[g * cols * (kt / 32) + ((rb >> 7) * cols + c) * 4 + ((rb >> 5) & 3)] =
-      static_cast<uint8_t>(e + 127);
+  if (col_out && q == 0)
+    *reinterpret_cast<uint32_t*>(t_scales + g * cols * (kt / 32) + ((row0 >> 7) * cols + c) * 4) = word;
 }
 
 // d weight of each row: its workgroups' partial sums, added in column order, rounded
