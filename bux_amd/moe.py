@@ -473,6 +473,11 @@ def experts_forward(
     t, k = idx.shape
     e, d, f, p = up.shape
     m = t * k
+    for name, a in (("z", z), ("weights", weights), ("up", up), ("down", down)):
+        # y, dx and dW take x's dtype, the kernels cast to it (moe.py:846,
+        # grouped_blockscaled.py:129): bfloat16 here
+        if a.dtype != torch.bfloat16:
+            raise TypeError(f"experts_forward: {name} is {a.dtype}; the layer multiplies in bfloat16")
     fprop, dgrad, wgrad = passes_of(fmt, passes)
     if quantized is not None:
         quantized.check(fmt, up, down)
@@ -573,6 +578,9 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
     them."""
     s, k = saved.sorted, saved.k
     t = dy.shape[0]
+    for name, a in (("dy", dy), ("up", up), ("down", down)):
+        if a.dtype != torch.bfloat16:
+            raise TypeError(f"experts_backward: {name} is {a.dtype}; the layer multiplies in bfloat16")
     e, d, f, p = up.shape
     m = t * k
     filled = s.filled

@@ -19,7 +19,8 @@ def test_passes_are_a_subset_of_fprop_dgrad_wgrad():
 
 
 def test_kernels_in_mxfp8_are_checked_against_the_recipe_and_the_kernels():
-    up, down = torch.empty(4, 64, 32, 2), torch.empty(4, 32, 64)
+    up = torch.empty(4, 64, 32, 2, dtype=torch.bfloat16)
+    down = torch.empty(4, 32, 64, dtype=torch.bfloat16)
     given = moe.MxWeights(None, None, None, None, "mxfp8", tuple(up.shape), tuple(down.shape))
     given.check("mxfp8", up, down)
     with pytest.raises(ValueError, match="'mxfp8' recipe, not 'mxfp8_2d'"):
@@ -30,8 +31,24 @@ def test_kernels_in_mxfp8_are_checked_against_the_recipe_and_the_kernels():
         given.check("mxfp8", torch.empty(4, 64, 48, 2), down)
     # the layer checks before it runs anything
     with pytest.raises(ValueError, match="recipe"):
-        moe.experts_forward(torch.empty(8, 64), torch.zeros(8, 2, dtype=torch.int32),
-                            torch.empty(8, 2), up, down, fmt="mxfp8_2d", quantized=given)
+        moe.experts_forward(torch.empty(8, 64, dtype=torch.bfloat16),
+                            torch.zeros(8, 2, dtype=torch.int32),
+                            torch.empty(8, 2, dtype=torch.bfloat16), up, down, fmt="mxfp8_2d",
+                            quantized=given)
+
+
+def test_the_layer_multiplies_in_bfloat16():
+    """y, dx and dW take x's dtype, the kernels cast to it (moe.py:846,
+    grouped_blockscaled.py:129): bfloat16 tokens and kernels, others refused."""
+    bf = dict(dtype=torch.bfloat16)
+    z, w = torch.empty(8, 64, **bf), torch.empty(8, 2, **bf)
+    idx = torch.zeros(8, 2, dtype=torch.int32)
+    up, down = torch.empty(4, 64, 32, 2, **bf), torch.empty(4, 32, 64, **bf)
+    for i, name in enumerate(("z", "weights", "up", "down")):
+        args = [z, idx, w, up, down]
+        args[[0, 2, 3, 4][i]] = args[[0, 2, 3, 4][i]].float()
+        with pytest.raises(TypeError, match=f"{name} is torch.float32"):
+            moe.experts_forward(*args)
 
 
 def test_an_ffn_names_one_of_the_ten_activations():
