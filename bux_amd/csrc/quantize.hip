@@ -55,6 +55,22 @@ constexpr int TILE_ROWS = 128;
 constexpr int TILE_COLS = 64;
 constexpr int THREADS = 256;
 
+// The copies' codes go out as non-temporal stores: both copies' stores write whole runs
+// (512 bytes and 1 KiB an instruction), which the GEMMs read a kernel later, and keeping
+// them out of the caches' way leaves the source rows there (rows read by index are read
+// once for each of a token's picks). The scale bytes, 2 or 4 of them a row, stay
+// ordinary stores, which L2 merges into lines. Measured at c3 in the step: W_up's copies
+// 6% faster, the step 1%.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void stream_codes(uint8_t* at, uint32_t a, uint32_t b) {
+  __builtin_nontemporal_store(u32x2{a, b}, reinterpret_cast<u32x2*>(at));
+}
+__device__ __forceinline__ void stream_codes(uint8_t* at, uint32_t a, uint32_t b, uint32_t c,
+                                             uint32_t d) {
+  __builtin_nontemporal_store(u32x4{a, b, c, d}, reinterpret_cast<u32x4*>(at));
+}
+
 // Two float32 -> two bfloat16 (nearest even) by the hardware's conversion.
 __device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
 
@@ -308,7 +324,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
       codes.y = e4m3x4(clip448(v[4] * down), clip448(v[5] * down), clip448(v[6] * down),
                        clip448(v[7] * down));
       if (r < height) {  // padding columns too: codes 0, scale byte 1
-        *reinterpret_cast<uint2*>(vg + ((col >> 6) * height + r) * 64 + (col & 63)) = codes;
+        stream_codes(vg + ((col >> 6) * height + r) * 64 + (col & 63), codes.x, codes.y);
         const int64_t b = col >> 5;
         if ((chunk & 3) == 0) sg[((b >> 2) * height + r) * 4 + (b & 3)] = static_cast<uint8_t>(e + 127);
       }
@@ -348,7 +364,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     for (int j = 0; j < 4; ++j)
       w[j] = e4m3x4(clip448(v[4 * j] * down), clip448(v[4 * j + 1] * down),
                     clip448(v[4 * j + 2] * down), clip448(v[4 * j + 3] * down));
-    if (col_out) *reinterpret_cast<uint4*>(out + h * cols * 64) = make_uint4(w[0], w[1], w[2], w[3]);
+    if (col_out) stream_codes(out + h * cols * 64, w[0], w[1], w[2], w[3]);
     // block 2 h from this pair (q 0, 1), block 2 h + 1 from the other (q 2, 3)
     const uint32_t b = static_cast<uint32_t>(e + 127);
     const uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(b), 2));
