@@ -278,25 +278,38 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     }
   }
 
-  // BUX_MX_TILES: a scale per 32 x 32 tile, both copies. The tile goes through LDS
-  // first; wave w takes the 32 rows of slab w, lane l column l, and the 32 lanes of a
-  // tile reduce its largest magnitude by xor-shuffles.
-  __shared__ int tile_e[TILE_ROWS / 32][TILE_COLS / 32];
+  // BUX_MX_TILES: a scale per 32 x 32 tile, both copies. A thread's 8 values of row
+  // (t / 8) + 32 i lie in tile (i, chunk / 4); xor-shuffles reduce each tile's largest
+  // magnitude over a wave's 8 rows of it, and the 4 waves' maxima meet in LDS (with the
+  // tile itself, which the column copy reads), so both copies take the tile's scale.
+  __shared__ float tile_max[THREADS / 64][TILE_ROWS / 32][TILE_COLS / 32];
   const bool tiles = (flags & BUX_MX_TILES) != 0;
   if (tiles) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
       *reinterpret_cast<uint4*>(&at((t >> 3) + 32 * i, 8 * chunk)) = raw[i];
-    __syncthreads();
-    const int wave = t >> 6, lane = t & 63;
-    float amax = 0.0f;
+      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+      float m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(bf16_to_f32(at(32 * wave + j, lane))));
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    if ((lane & 31) == 0) tile_e[wave][lane >> 5] = scale_exponent_bf16(amax);
+      for (int j = 0; j < 4; ++j)
+        m = fmaxf(m, fmaxf(fabsf(bf16_to_f32(static_cast<uint16_t>(w[j] & 0xffffu))),
+                           fabsf(bf16_to_f32(static_cast<uint16_t>(w[j] >> 16)))));
+      m = fmaxf(m, __shfl_xor(m, 1));
+      m = fmaxf(m, __shfl_xor(m, 2));
+      m = fmaxf(m, __shfl_xor(m, 8));
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      if ((t & 59) == 0) tile_max[t >> 6][i][(t >> 2) & 1] = m;  // lanes 0 and 4 of a wave
+    }
     __syncthreads();
   }
+  // the scale exponent of tile (i, b)
+  auto tile_e = [&](int i, int b) {
+    float m = tile_max[0][i][b];
+#pragma unroll
+    for (int w = 1; w < THREADS / 64; ++w) m = fmaxf(m, tile_max[w][i][b]);
+    return scale_exponent_bf16(m);
+  };
 
   if (flags & BUX_MX_ROWS) {
     uint8_t* vg = values + g * height * cols_pad;
@@ -316,7 +329,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
       amax = fmaxf(amax, __shfl_xor(amax, 1));
       amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const int e = tiles ? tile_e[i][chunk >> 2] : scale_exponent_bf16(amax);
+      const int e = tiles ? tile_e(i, chunk >> 2) : scale_exponent_bf16(amax);
       const float down = power_of_two_down(e);
       uint2 codes;
       codes.x = e4m3x4(clip448(v[0] * down), clip448(v[1] * down), clip448(v[2] * down),
@@ -357,7 +370,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
       amax = fmaxf(amax, fabsf(v[j]));
     }
     amax = fmaxf(amax, __shfl_xor(amax, 1));
-    const int e = tiles ? tile_e[2 * h + (q >> 1)][lc >> 5] : scale_exponent_bf16(amax);
+    const int e = tiles ? tile_e(2 * h + (q >> 1), lc >> 5) : scale_exponent_bf16(amax);
     const float down = power_of_two_down(e);
     uint32_t w[4];
 #pragma unroll
