@@ -32,12 +32,13 @@
 //     tile's 128 rows as one word. The tile's 16-byte chunks are swizzled by row (chunk
 //     c of row r at c ^ 2 ((r / 16) % 4)), so that the four lanes' rows, 16 apart, read
 //     different banks.
-// HBM traffic per element: 2 bytes read, 2 x (1 + 1/32) bytes written.
+// HBM traffic per element: 2 bytes read, 2 x (1 + 1/32) bytes written; the codes go
+// out as non-temporal stores (below).
 //
 // With BUX_MX_TILES the scale is one per 32 x 32 tile of x instead (the mxfp8_2d
-// recipe's weights, blockscaled.py:294-309): the tile is staged in LDS first and each
-// wave reduces its two tiles' largest magnitudes, so both copies take the tile's scale
-// and hold the same codes, transposed.
+// recipe's weights, blockscaled.py:294-309): xor-shuffles reduce each tile's largest
+// magnitude over a wave's rows of it and the waves' maxima meet in LDS, so both copies
+// take the tile's scale and hold the same codes, transposed.
 //
 // The values come from a source: a matrix (or a stack, or rows read by index), or the
 // experts' activation computed on the fly from its inputs (h of the forward, d projected
