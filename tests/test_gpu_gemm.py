@@ -332,6 +332,64 @@ def test_a_tile_list_made_once_serves_every_gemm(lib):
     assert torch.equal(dw0.view(torch.uint8), dw1.view(torch.uint8))
 
 
+def _c3_like_sizes():
+    rng = np.random.default_rng(33)
+    sizes = rng.integers(990, 1060, 128)
+    return sizes.tolist(), int(sizes.sum()), int((sizes.sum() + 127) // 128 * 128)
+
+
+TILE_LIST_CASES = {
+    "reference sizes": ([0, 130, 1, 3, 256, 0, 300, 100], 1024, 1024),
+    "rows past the groups": ([0, 130, 1, 3, 256, 0, 300, 100], 900, 896),
+    "every group empty": ([0, 0, 0], 256, 256),
+    "one row": ([0, 1], 1, 32),
+    "config 3 like": _c3_like_sizes(),
+}
+
+
+@pytest.mark.parametrize("case", list(TILE_LIST_CASES))
+def test_the_device_tile_list_covers_each_groups_rows_once(lib, case):
+    """The invariant of the reference's tiles_of (tests/test_grouped_mxfp8.py:31-41), on
+    the list the device prologue builds (tiles of 256 rows from each group's first row):
+    every row of group g, [starts[g], starts[g + 1]), is held by exactly one tile of g, a
+    tile (g, lo, hi) holding rows [max(lo, starts[g]), hi) inside [lo, lo + 256); the
+    rows from the groups' end to `height` are held once by tiles of group `groups`; a
+    group of s rows has ceil(s / 256) tiles, in group order; the list holds starts[groups
+    + 1] tiles and (0, 0, 0) past them; its header names the dimensions."""
+    from bux_amd import _lib, grouped_mxfp8 as gm
+    sizes, m, height = TILE_LIST_CASES[case]
+    groups = len(sizes)
+    announce("device tile list", case, groups, m, height)
+    tl = gm.tiles_of(to_gpu(np.array(sizes, np.int32)), m, height)
+    torch.cuda.synchronize()
+    buf = tl.buffer.cpu().numpy()
+    header = buf[:64].view(np.int32)
+    assert list(header[:5]) == [_lib.LIST_MAGIC, groups, m, height, 0]
+    starts = buf[64:64 + 4 * (groups + 2)].view(np.int32)
+    filled = int(np.sum(sizes))
+    assert starts[:groups + 1].tolist() == [0] + np.cumsum(sizes).tolist()
+    slots = -(-max(m, height) // 256) + groups + 1
+    first = (64 + 4 * (groups + 2) + 255) // 256 * 256
+    tiles = buf[first:first + 12 * slots].view(np.int32).reshape(slots, 3)
+    count = int(starts[groups + 1])
+    lo_of = list(starts[:groups]) + [filled]  # where each group's rows begin
+    rows_of = list(sizes) + [max(height - filled, 0)]
+    assert count == sum(-(-s // 256) for s in rows_of)
+    assert (tiles[count:] == 0).all()
+    covered = np.full(max(m, height, filled), -1)
+    last = -1
+    for g, lo, hi in tiles[:count]:
+        assert last <= g <= groups
+        last = g
+        held = max(lo, lo_of[g])
+        assert lo_of[g] <= lo and held < hi <= lo + 256 and hi <= lo_of[g] + rows_of[g]
+        assert (covered[held:hi] == -1).all()
+        covered[held:hi] = g
+    for g in range(groups + 1):
+        assert (covered[lo_of[g]:lo_of[g] + rows_of[g]] == g).all()
+    assert (covered >= 0).sum() == filled + max(height - filled, 0)
+
+
 def test_a_tile_list_made_for_other_dimensions_is_refused_on_the_device(lib):
     """A list whose header names other dimensions than the call's (but long enough for
     them, so the host lets it by) is refused by the GEMM kernel as it starts: its status
