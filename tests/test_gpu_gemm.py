@@ -85,7 +85,7 @@ ROW_CASES = [
     ([700, 0, 1, 300, 513, 2000], 512, 640, 3712),  # tiles of 256 from each group's start
     ([0, 300, 1, 0, 250, 49], 7168, 256, None),  # config 5's d as K: a 112-step K loop
     ([100, 0, 37], 256, 7168, 160),  # config 5's d as N: 28 column tiles
-    # n a whole number of 384s: tiles of 256 x 384 (4 x 6 blocks a wave)
+    # n a whole number of 384s: the last column tile of 256 half full
     ([0, 130, 1, 3, 256, 0, 300, 100], 256, 768, None),
     ([700, 0, 1, 300, 513, 2000], 512, 1152, 3712),
     ([0, 300, 1, 0, 250, 49], 2048, 1536, None),  # config 3's up fprop shape, ragged
@@ -126,7 +126,7 @@ CONTRACT_CASES = [
     ([0, 0], 64, 64, 64),  # nothing: dW 0
     ([700, 0, 1, 300, 513, 2000], 640, 384, 3584),  # 256-wide tiles, a partial one
     ([300, 0, 212, 0], 7168, 256, 512),  # config 5's d as the wgrad's rows
-    # tiles of 256 x 384 (d whole 256s, f whole 384s) and 384 x 256 (d 384s, f 256s)
+    # d or f a whole number of 384s: the last row or column tile of 256 half full
     ([70, 0, 100, 3, 77], 256, 768, 256),
     ([0, 130, 1, 3, 256, 0, 300, 100], 2048, 1536, 896),  # config 3's up wgrad shape
     ([70, 0, 100, 3, 77], 768, 256, 256),
