@@ -11,6 +11,7 @@ dominant kernel (per-op HIP events over the timed steps) and `cpu_baseline` (the
 oracle on a bounded sample of the same layer, on this host's cores).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py --config-forward N   # config N's forward alone (1, 2, 4 or 5)
 """
 
 import argparse
@@ -495,6 +496,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the forward timings of configs 2, 4 and 5")
+    ap.add_argument("--config-forward", type=int, default=0, metavar="N",
+                    help="run only config N's forward timing (1, 2, 4 or 5; as other_configs "
+                         "reports it) and print its JSON: the command a per-config kernel "
+                         "trace profiles")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run only a plain device-to-device copy of MIB MiB, 10 times: the "
                          "kernel of known traffic that scales rocprofv3's FETCH_SIZE and "
@@ -520,6 +525,14 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": n, "copies": 10}), flush=True)
+        return
+    if args.config_forward:
+        names = [n for n in OTHER_CONFIGS if n.startswith(f"config {args.config_forward}:")]
+        if not names:
+            raise SystemExit(f"no config {args.config_forward} among {list(OTHER_CONFIGS)}")
+        name = names[0]
+        out = other_config(*OTHER_CONFIGS[name], device)
+        print(json.dumps({"config": name, **out}), flush=True)
         return
     log(f"inputs: config 3, T={T} d={D} E={E} k={K} f={F}")
     z, idx, w, up, down, dy = inputs(T, D, E, K, F, device)
