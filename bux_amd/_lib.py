@@ -59,7 +59,8 @@ SIGNATURES = {
     "bux_version": (_int, []),
     "bux_moe_permute_workspace_size": (_size, [_i64, _i32]),
     "bux_moe_permute": (_int, [_p, _i64, _i32, _p, _p, _p, _p, _p, _size, _p]),
-    "bux_mx_quantize": (_int, [_p, _p, _i32, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p, _p, _p]),
+    "bux_mx_quantize": (
+        _int, [_p, _p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p, _p, _p]),
     "bux_mx_grouped_rows_workspace_size": (_size, [_i32, _i64, _i64]),
     "bux_mx_grouped_rows": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
@@ -80,17 +81,17 @@ SIGNATURES = {
         _int, [_p, _p, _int, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
     "bux_bf16_grouped_contract_workspace_size": (_size, [_i32]),
     "bux_bf16_grouped_contract": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
-    "bux_token_rows": (_int, [_p, _p, _i64, _i32, _i64, _p, _p]),
+    "bux_token_rows": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums_biased": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p, _i32, _p, _p, _p]),
     "bux_expert_bias_add": (_int, [_p, _i64, _i64, _p, _p, _i32, _p]),
-    "bux_expert_sums": (_int, [_p, _p, _i32, _p, _i64, _i64, _p, _i32, _p, _p]),
-    "bux_expert_bias_weight_grad": (_int, [_p, _p, _i32, _i64, _i64, _p, _p, _i32, _p, _p]),
+    "bux_expert_sums": (_int, [_p, _p, _i32, _i64, _p, _i64, _i64, _p, _i32, _p, _p]),
+    "bux_expert_bias_weight_grad": (_int, [_p, _p, _i32, _i64, _i64, _i64, _p, _p, _i32, _p, _p]),
     "bux_expert_norm_forward": (_int, [_p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p]),
     "bux_expert_norm_backward_workspace_size": (_size, [_i64, _i64]),
     "bux_expert_norm_backward": (
-        _int, [_p, _p, _i32, _p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p, _p, _p, _p,
-               _size, _p]),
+        _int, [_p, _p, _i32, _i64, _p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p, _p, _p,
+               _p, _size, _p]),
     "bux_glu_forward": (_int, [_p, _p, _p, _i64, _i64, _ffn, _p, _p]),
     "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _ffn, _p, _p, _p]),
     "bux_glu_quantize": (

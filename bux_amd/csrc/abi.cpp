@@ -31,4 +31,4 @@ int launched(const char* kernel) {
 
 extern "C" const char* bux_last_error(void) { return bux::last_error; }
 
-extern "C" int bux_version(void) { return 100; }
+extern "C" int bux_version(void) { return 200; }

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(THREADS) void norm_forward_kernel(
 // and its columns' gain and bias gradients summed over its rows into partials[2][block][d].
 __global__ __launch_bounds__(THREADS) void norm_backward_kernel(
     const uint16_t* __restrict__ dy, const int32_t* __restrict__ index, int32_t index_div,
-    const uint16_t* __restrict__ y, int64_t m, int64_t d, NormArgs a,
+    int64_t sources, const uint16_t* __restrict__ y, int64_t m, int64_t d, NormArgs a,
     const uint16_t* __restrict__ weights, uint16_t* __restrict__ dv,
     uint16_t* __restrict__ d_weights, float* __restrict__ partials) {
   __shared__ float red[4];
@@ -210,7 +210,11 @@ __global__ __launch_bounds__(THREADS) void norm_backward_kernel(
     float mean, rs;
     norm_stats(a, x, d, chunks, red, &mean, &rs);
     const float w = bf16_to_f32(weights[r]);
-    const uint16_t* g_row = dy + (index ? static_cast<int64_t>(index[r] / index_div) : r) * d;
+    // dy's row: r, or by index (a row of 0 where that lies outside dy's sources rows)
+    const int64_t src =
+        index ? (index[r] < 0 ? -1 : static_cast<int64_t>(index[r] / index_div)) : r;
+    const bool g_live = src >= 0 && (index == nullptr || src < sources);
+    const uint16_t* g_row = dy + (g_live ? src : 0) * d;
     // dn = g w; the weight's gradient sum_c g n (products rounded, as bfloat16 ops);
     // dxn = dn (times the gain); and the two sums the normalization's VJP takes
     Row dxn;
@@ -221,7 +225,7 @@ __global__ __launch_bounds__(THREADS) void norm_backward_kernel(
       const int64_t c = (static_cast<int64_t>(i) * THREADS + threadIdx.x) * VEC;
       float g[VEC] = {0, 0, 0, 0, 0, 0, 0, 0}, b[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
       if (c < d) {
-        load8(g_row + c, g);
+        if (g_live) load8(g_row + c, g);
         if (a.biased) load8(a.bias + c, b);
       }
 #pragma unroll
@@ -351,7 +355,7 @@ extern "C" size_t bux_expert_norm_backward_workspace_size(int64_t m, int64_t d) 
 }
 
 extern "C" int bux_expert_norm_backward(const uint16_t* dy, const int32_t* index, int32_t index_div,
-                                        const uint16_t* y, int64_t m, int64_t d,
+                                        int64_t sources, const uint16_t* y, int64_t m, int64_t d,
                                         const uint16_t* down_bias, const int32_t* offsets,
                                         int32_t experts, const bux_norm* norm,
                                         const uint16_t* scale, const uint16_t* bias,
@@ -362,6 +366,8 @@ extern "C" int bux_expert_norm_backward(const uint16_t* dy, const int32_t* index
   clear_error();
   if (int rc = norm_shape("bux_expert_norm_backward", m, d)) return rc;
   BUX_CHECK(index == nullptr || index_div >= 1, "bux_expert_norm_backward: index_div=%d", index_div);
+  BUX_CHECK(index == nullptr || sources >= 0, "bux_expert_norm_backward: sources=%lld",
+            (long long)sources);
   NormArgs a;
   if (int rc = norm_args("bux_expert_norm_backward", norm, scale, bias, down_bias, offsets, experts, &a))
     return rc;
@@ -376,7 +382,7 @@ extern "C" int bux_expert_norm_backward(const uint16_t* dy, const int32_t* index
   if (m > 0) {
     BUX_CHECK(dy && y && weights && dv && d_weights, "bux_expert_norm_backward: NULL buffer");
     hipLaunchKernelGGL(norm_backward_kernel, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0,
-                       s, dy, index, index_div, y, m, d, a, weights, dv, d_weights,
+                       s, dy, index, index_div, sources, y, m, d, a, weights, dv, d_weights,
                        static_cast<float*>(workspace));
     if (int rc = launched("norm_backward_kernel")) return rc;
   }

@@ -84,6 +84,7 @@ struct Matrix {
   const uint16_t* x;
   const int32_t* index;
   int32_t index_div;
+  int64_t sources;  // with an index, x's rows: a source row outside [0, sources) reads 0
   int64_t rows, cols;
   bool halves;
   // Whether the tiles go in XCD runs (quantize_kernel): not for rows read by index,
@@ -102,6 +103,7 @@ struct Matrix {
       // a power-of-two divisor (every top-k bux's configs use) by a shift
       src = (index_div & (index_div - 1)) == 0 ? (at >> (31 - __builtin_clz(index_div)))
                                                : at / index_div;
+      if (src >= sources) return make_uint4(0, 0, 0, 0);
     }
     const uint16_t* row = (index ? x : x + g * rows * cols) + src * cols;
     if (!halves) return *reinterpret_cast<const uint4*>(row + col);
@@ -452,21 +454,24 @@ int launch_glu_weights(const float* partials, int64_t m, int64_t tiles, const in
 }  // namespace bux
 
 extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div,
-                               int64_t groups, int64_t rows, int64_t cols, int64_t height,
-                               const int32_t* filled, int flags, uint8_t* values, uint8_t* scales,
-                               uint8_t* t_values, uint8_t* t_scales, void* stream) {
+                               int64_t sources, int64_t groups, int64_t rows, int64_t cols,
+                               int64_t height, const int32_t* filled, int flags, uint8_t* values,
+                               uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
+                               void* stream) {
   using namespace bux;
   clear_error();
   BUX_CHECK(x != nullptr, "bux_mx_quantize: x is NULL");
   BUX_CHECK(index == nullptr || index_div >= 1, "bux_mx_quantize: index_div=%d", index_div);
   BUX_CHECK(index == nullptr || groups == 1, "bux_mx_quantize: index takes one matrix, not %lld",
             (long long)groups);
+  BUX_CHECK(index == nullptr || sources >= 0, "bux_mx_quantize: sources=%lld", (long long)sources);
   const bool halves = (flags & BUX_MX_HALVES) != 0;
   BUX_CHECK(!halves || cols % 64 == 0, "bux_mx_quantize: BUX_MX_HALVES needs cols=%lld a multiple of 64",
             (long long)cols);
-  return launch_quantize("bux_mx_quantize", Matrix{x, index, index_div, rows, cols, halves}, groups,
-                         rows, cols, height, filled, flags & ~BUX_MX_HALVES, values, scales, t_values,
-                         t_scales, as_stream(stream));
+  const Matrix source{x, index, index_div, sources, rows, cols, halves};
+  return launch_quantize("bux_mx_quantize", source, groups, rows, cols, height, filled,
+                         flags & ~BUX_MX_HALVES, values, scales, t_values, t_scales,
+                         as_stream(stream));
 }
 
 extern "C" int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights,

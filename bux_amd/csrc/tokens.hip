@@ -1,6 +1,8 @@
 // The token path's gathers and sums, and the experts' activation between the GEMMs.
 //
 //   token_rows  rows[i] = z[order[i] / k]           moe.py:991-1016, 1027-1032
+//               (a row of 0 where that row lies outside z, a negative index too: the
+//               reference's orders never do, and no read leaves z)
 //   token_sums  out[t] = sum_j y[inverse[t k + j]]  grouped_blockscaled.py:141-148,
 //               in float32, picks in order, one rounding to bfloat16; an index outside
 //               y's rows adds 0 (jnp.take's mode="fill").
@@ -46,7 +48,16 @@ __device__ __forceinline__ uint4 spread4(const uint2& r) {
   return make_uint4(r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16);
 }
 
+// The row of z that pick `at` (an index entry) reads: at / k, or -1 (a row of 0) when
+// that lies outside z's `tokens` rows, a negative entry included.
+__device__ __forceinline__ int64_t source_row(int32_t at, int32_t k, int64_t tokens) {
+  if (at < 0) return -1;
+  const int64_t src = at / k;
+  return src < tokens ? src : -1;
+}
+
 __global__ __launch_bounds__(THREADS) void token_rows_kernel(const uint16_t* __restrict__ z,
+                                                             int64_t tokens,
                                                              const int32_t* __restrict__ order,
                                                              int32_t k, int64_t width,
                                                              uint16_t* __restrict__ rows) {
@@ -54,19 +65,20 @@ __global__ __launch_bounds__(THREADS) void token_rows_kernel(const uint16_t* __r
   const int64_t i = blockIdx.x / chunks;
   const int64_t c = ((blockIdx.x % chunks) * THREADS + threadIdx.x) * VEC;
   if (c >= width) return;
-  const int64_t token = order[i] / k;
+  const int64_t token = source_row(order[i], k, tokens);
   *reinterpret_cast<uint4*>(rows + i * width + c) =
-      *reinterpret_cast<const uint4*>(z + token * width + c);
+      token < 0 ? make_uint4(0, 0, 0, 0) : *reinterpret_cast<const uint4*>(z + token * width + c);
 }
 
 // Rows narrower than a vector (a pick's weight, width 1): an element a lane.
 __global__ __launch_bounds__(THREADS) void token_rows_narrow_kernel(
-    const uint16_t* __restrict__ z, const int32_t* __restrict__ order, int64_t m, int32_t k,
-    int64_t width, uint16_t* __restrict__ rows) {
+    const uint16_t* __restrict__ z, int64_t tokens, const int32_t* __restrict__ order, int64_t m,
+    int32_t k, int64_t width, uint16_t* __restrict__ rows) {
   const int64_t e = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
   if (e >= m * width) return;
   const int64_t i = e / width, c = e % width;
-  rows[e] = z[(order[i] / k) * width + c];
+  const int64_t token = source_row(order[i], k, tokens);
+  rows[e] = token < 0 ? uint16_t{0} : z[token * width + c];
 }
 
 // KMAX > 0: the token's k <= KMAX picks' rows are all requested before the first is
@@ -249,19 +261,20 @@ __global__ __launch_bounds__(THREADS) void expert_bias_add_kernel(
 constexpr int SUM_COLS = 64 * VEC;  // a workgroup's columns
 __global__ __launch_bounds__(THREADS) void expert_sums_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ index, int32_t index_div,
-    const uint16_t* __restrict__ weights, int64_t width, const int32_t* __restrict__ offsets,
-    int32_t experts, float* __restrict__ out) {
+    int64_t sources, const uint16_t* __restrict__ weights, int64_t m, int64_t width,
+    const int32_t* __restrict__ offsets, int32_t experts, float* __restrict__ out) {
   __shared__ float part[THREADS / 64][SUM_COLS];
   const int64_t chunks = (width + SUM_COLS - 1) / SUM_COLS;
   const int64_t e = blockIdx.x / chunks;
   const int64_t c0 = (blockIdx.x % chunks) * SUM_COLS;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t c = c0 + lane * VEC;
-  const int64_t lo = offsets[e], hi = offsets[e + 1];
+  const int64_t lo = offsets[e], hi = offsets[e + 1] < m ? offsets[e + 1] : m;
   float acc[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (c < width) {
     for (int64_t r = lo + wave; r < hi; r += THREADS / 64) {
-      const int64_t src = index ? index[r] / index_div : r;
+      const int64_t src = index ? source_row(index[r], index_div, sources) : r;
+      if (src < 0) continue;  // a row of 0
       float v[VEC];
       unpack8(*reinterpret_cast<const uint4*>(x + src * width + c), v);
       if (weights) {
@@ -292,15 +305,15 @@ __global__ __launch_bounds__(THREADS) void expert_sums_kernel(
 // xor-shuffles.
 __global__ __launch_bounds__(THREADS) void expert_bias_weight_grad_kernel(
     const uint16_t* __restrict__ dy, const int32_t* __restrict__ index, int32_t index_div,
-    int64_t m, int64_t width, const uint16_t* __restrict__ bias,
+    int64_t sources, int64_t m, int64_t width, const uint16_t* __restrict__ bias,
     const int32_t* __restrict__ offsets, int32_t experts, uint16_t* __restrict__ d_weights) {
   const int lane = threadIdx.x & 63;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * (THREADS / 64) + (threadIdx.x >> 6);
   if (r >= m) return;
   const int32_t e = expert_of(offsets, experts, r);
   float sum = 0.0f;
-  if (e >= 0) {
-    const int64_t src = index ? index[r] / index_div : r;
+  const int64_t src = e < 0 ? -1 : index ? source_row(index[r], index_div, sources) : r;
+  if (src >= 0) {
     for (int64_t c = lane * VEC; c < width; c += 64 * VEC) {
       float g[VEC], b[VEC];
       unpack8(*reinterpret_cast<const uint4*>(dy + src * width + c), g);
@@ -318,24 +331,25 @@ __global__ __launch_bounds__(THREADS) void expert_bias_weight_grad_kernel(
 }  // namespace
 }  // namespace bux
 
-extern "C" int bux_token_rows(const uint16_t* z, const int32_t* order, int64_t m, int32_t k,
-                              int64_t width, uint16_t* rows, void* stream) {
+extern "C" int bux_token_rows(const uint16_t* z, int64_t tokens, const int32_t* order, int64_t m,
+                              int32_t k, int64_t width, uint16_t* rows, void* stream) {
   using namespace bux;
   clear_error();
-  BUX_CHECK(m >= 0 && m <= 2147483647LL && k >= 1 && width > 0,
-            "bux_token_rows: bad shape m=%lld k=%d width=%lld", (long long)m, k, (long long)width);
+  BUX_CHECK(m >= 0 && m <= 2147483647LL && k >= 1 && width > 0 && tokens >= 0,
+            "bux_token_rows: bad shape tokens=%lld m=%lld k=%d width=%lld", (long long)tokens,
+            (long long)m, k, (long long)width);
   if (m == 0) return BUX_OK;
   BUX_CHECK(z && order && rows, "bux_token_rows: NULL buffer");
   if (width % VEC != 0) {
     BUX_CHECK(ceil_div(m * width, THREADS) < (1LL << 31), "bux_token_rows: too large");
     hipLaunchKernelGGL(token_rows_narrow_kernel, dim3(static_cast<unsigned>(ceil_div(m * width, THREADS))),
-                       dim3(THREADS), 0, as_stream(stream), z, order, m, k, width, rows);
+                       dim3(THREADS), 0, as_stream(stream), z, tokens, order, m, k, width, rows);
     return launched("token_rows_narrow_kernel");
   }
   BUX_CHECK(m * ceil_div(width, THREADS * VEC) < (1LL << 31), "bux_token_rows: too large");
   dim3 grid(static_cast<unsigned>(m * ceil_div(width, THREADS * VEC)));
-  hipLaunchKernelGGL(token_rows_kernel, grid, dim3(THREADS), 0, as_stream(stream), z, order, k,
-                     width, rows);
+  hipLaunchKernelGGL(token_rows_kernel, grid, dim3(THREADS), 0, as_stream(stream), z, tokens,
+                     order, k, width, rows);
   return launched("token_rows_kernel");
 }
 
@@ -415,30 +429,32 @@ extern "C" int bux_expert_bias_add(uint16_t* x, int64_t m, int64_t width, const 
 }
 
 extern "C" int bux_expert_sums(const uint16_t* x, const int32_t* index, int32_t index_div,
-                               const uint16_t* weights, int64_t m, int64_t width,
-                               const int32_t* offsets, int32_t experts, float* out,
-                               void* stream) {
+                               int64_t sources, const uint16_t* weights, int64_t m,
+                               int64_t width, const int32_t* offsets, int32_t experts,
+                               float* out, void* stream) {
   using namespace bux;
   clear_error();
   BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
             "bux_expert_sums: bad shape m=%lld width=%lld (a multiple of %d)", (long long)m,
             (long long)width, VEC);
   BUX_CHECK(index == nullptr || index_div >= 1, "bux_expert_sums: index_div=%d", index_div);
+  BUX_CHECK(index == nullptr || sources >= 0, "bux_expert_sums: sources=%lld", (long long)sources);
   if (int rc = experts_ok("bux_expert_sums", offsets, experts)) return rc;
   BUX_CHECK(out != nullptr && (m == 0 || x != nullptr), "bux_expert_sums: NULL buffer");
-  // every expert's sum is written (0 for none): offsets[experts] <= m is the caller's
+  // every expert's sum is written (0 for none); rows at or past m add nothing
   const int64_t chunks = ceil_div(width, SUM_COLS);
   BUX_CHECK(experts * chunks < (1LL << 31), "bux_expert_sums: too large");
   hipLaunchKernelGGL(expert_sums_kernel, dim3(static_cast<unsigned>(experts * chunks)),
-                     dim3(THREADS), 0, as_stream(stream), x, index, index_div, weights, width,
-                     offsets, experts, out);
+                     dim3(THREADS), 0, as_stream(stream), x, index, index_div, sources, weights,
+                     m, width, offsets, experts, out);
   return launched("expert_sums_kernel");
 }
 
 extern "C" int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index,
-                                           int32_t index_div, int64_t m, int64_t width,
-                                           const uint16_t* bias, const int32_t* offsets,
-                                           int32_t experts, uint16_t* d_weights, void* stream) {
+                                           int32_t index_div, int64_t sources, int64_t m,
+                                           int64_t width, const uint16_t* bias,
+                                           const int32_t* offsets, int32_t experts,
+                                           uint16_t* d_weights, void* stream) {
   using namespace bux;
   clear_error();
   BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
@@ -446,13 +462,15 @@ extern "C" int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* in
             (long long)m, (long long)width, VEC);
   BUX_CHECK(index == nullptr || index_div >= 1, "bux_expert_bias_weight_grad: index_div=%d",
             index_div);
+  BUX_CHECK(index == nullptr || sources >= 0, "bux_expert_bias_weight_grad: sources=%lld",
+            (long long)sources);
   if (int rc = experts_ok("bux_expert_bias_weight_grad", offsets, experts)) return rc;
   if (m == 0) return BUX_OK;
   BUX_CHECK(dy && bias && d_weights, "bux_expert_bias_weight_grad: NULL buffer");
   hipLaunchKernelGGL(expert_bias_weight_grad_kernel,
                      dim3(static_cast<unsigned>(ceil_div(m, THREADS / 64))), dim3(THREADS), 0,
-                     as_stream(stream), dy, index, index_div, m, width, bias, offsets, experts,
-                     d_weights);
+                     as_stream(stream), dy, index, index_div, sources, m, width, bias, offsets,
+                     experts, d_weights);
   return launched("expert_bias_weight_grad_kernel");
 }
 

@@ -156,7 +156,8 @@ def quantized_twice(
     if halves:
         flags |= _lib.MX_HALVES
     _lib.check(lib().bux_mx_quantize(
-        ptr(x), ptr(index), index_div, groups, r, c, h, ptr(filled), flags,
+        ptr(x), ptr(index), index_div, x.shape[0] if index is not None else 0, groups, r, c, h,
+        ptr(filled), flags,
         ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))
     along_rows = Tiled(vals, scales) if rows else None
     along_columns = Tiled(t_vals, t_scales) if columns else None

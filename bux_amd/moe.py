@@ -68,7 +68,8 @@ def token_rows(z: torch.Tensor, order: torch.Tensor, k: int) -> torch.Tensor:
     require(z, order)
     m, width = order.shape[0], z.shape[-1]
     rows = torch.empty(m, width, dtype=z.dtype, device=z.device)
-    _lib.check(lib().bux_token_rows(ptr(z), ptr(order), m, k, width, ptr(rows), stream()))
+    _lib.check(lib().bux_token_rows(ptr(z), z.shape[0], ptr(order), m, k, width, ptr(rows),
+                                    stream()))
     return rows
 
 
@@ -237,8 +238,8 @@ def expert_sums(x: torch.Tensor, offsets: torch.Tensor, index: torch.Tensor | No
     if weights is not None and weights.numel() != m:
         raise ValueError(f"expert_sums: {weights.numel()} weights for {m} rows")
     out = torch.empty(e, width, dtype=torch.float32, device=x.device)
-    _lib.check(lib().bux_expert_sums(ptr(x), ptr(index), index_div, ptr(weights), m, width,
-                                     ptr(offsets), e, ptr(out), stream()))
+    _lib.check(lib().bux_expert_sums(ptr(x), ptr(index), index_div, x.shape[0], ptr(weights), m,
+                                     width, ptr(offsets), e, ptr(out), stream()))
     return out
 
 
@@ -268,7 +269,7 @@ def add_bias_weight_grad(d_weights: torch.Tensor, dy: torch.Tensor, order: torch
     require(d_weights, dy, order, bias, offsets)
     e = _experts(offsets)
     m, width = order.numel(), dy.shape[-1]
-    _lib.check(lib().bux_expert_bias_weight_grad(ptr(dy), ptr(order), k, m, width,
+    _lib.check(lib().bux_expert_bias_weight_grad(ptr(dy), ptr(order), k, dy.shape[0], m, width,
                                                  ptr(bias.contiguous()), ptr(offsets), e,
                                                  ptr(d_weights), stream()))
     return d_weights
@@ -336,7 +337,8 @@ def expert_norm_backward(dy: torch.Tensor, order: torch.Tensor, k: int, y: torch
     ws = workspace(lib().bux_expert_norm_backward_workspace_size(m, d), dev)
     st = norm.struct()
     _lib.check(lib().bux_expert_norm_backward(
-        ptr(dy), ptr(order), k, ptr(y), m, d, ptr(down_bias), ptr(offsets), e, ctypes.byref(st),
+        ptr(dy), ptr(order), k, dy.shape[0], ptr(y), m, d, ptr(down_bias), ptr(offsets), e,
+        ctypes.byref(st),
         ptr(scale), ptr(bias), ptr(row_weights), ptr(dv), ptr(dw), ptr(d_scale), ptr(d_bias),
         ptr(ws), ws.numel(), stream()))
     return dv, dw, d_scale, d_bias

@@ -109,7 +109,8 @@ static ffi::Error MxQuantize(hipStream_t s, In x, In index, In filled, int64_t i
                              int64_t groups, int64_t rows, int64_t height, int64_t flags,
                              Out values, Out scales, Out t_values, Out t_scales) {
   return status(bux_mx_quantize(at<const uint16_t>(x), at<const int32_t>(index),
-                                static_cast<int32_t>(index_div), groups, rows, dim(x, -1), height,
+                                static_cast<int32_t>(index_div), dim(x, 0), groups, rows,
+                                dim(x, -1), height,
                                 at<const int32_t>(filled), static_cast<int>(flags),
                                 at<uint8_t>(values), at<uint8_t>(scales), at<uint8_t>(t_values),
                                 at<uint8_t>(t_scales), s));
@@ -219,8 +220,9 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxBf16Contract, Bf16Contract,
 // --- a-2, a-3: the token path's gathers and sums ---------------------------------------
 
 static ffi::Error TokenRows(hipStream_t s, In z, In order, int64_t k, Out rows) {
-  return status(bux_token_rows(at<const uint16_t>(z), at<const int32_t>(order), dim(rows, 0),
-                               static_cast<int32_t>(k), dim(z, -1), at<uint16_t>(rows), s));
+  return status(bux_token_rows(at<const uint16_t>(z), dim(z, 0), at<const int32_t>(order),
+                               dim(rows, 0), static_cast<int32_t>(k), dim(z, -1),
+                               at<uint16_t>(rows), s));
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxTokenRows, TokenRows,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>()
@@ -347,7 +349,8 @@ static ffi::Error ExpertSums(hipStream_t s, In x, In index, In weights, In offse
                              int64_t index_div, Out out) {
   const int64_t m = index.size_bytes() ? static_cast<int64_t>(index.element_count()) : dim(x, 0);
   return status(bux_expert_sums(at<const uint16_t>(x), at<const int32_t>(index),
-                                static_cast<int32_t>(index_div), at<const uint16_t>(weights), m,
+                                static_cast<int32_t>(index_div), dim(x, 0),
+                                at<const uint16_t>(weights), m,
                                 dim(out, 1), at<const int32_t>(offsets),
                                 static_cast<int32_t>(offsets.element_count() - 1),
                                 at<float>(out), s));
@@ -375,7 +378,8 @@ static ffi::Error ExpertBiasWeightGrad(hipStream_t s, In dy, In index, In bias, 
   (void)d_weights;
   return status(bux_expert_bias_weight_grad(
       at<const uint16_t>(dy), at<const int32_t>(index), static_cast<int32_t>(index_div),
-      static_cast<int64_t>(d_weights_out->element_count()), dim(dy, 1), at<const uint16_t>(bias),
+      dim(dy, 0), static_cast<int64_t>(d_weights_out->element_count()), dim(dy, 1),
+      at<const uint16_t>(bias),
       at<const int32_t>(offsets), static_cast<int32_t>(offsets.element_count() - 1),
       at<uint16_t>(d_weights_out), s));
 }
@@ -404,7 +408,7 @@ static ffi::Error ExpertNormBackward(hipStream_t s, In dy, In index, In y, In do
   const bux_norm norm = BUX_NORM;
   return status(bux_expert_norm_backward(
       at<const uint16_t>(dy), at<const int32_t>(index), static_cast<int32_t>(index_div),
-      at<const uint16_t>(y), dim(y, 0), dim(y, 1), at<const uint16_t>(down_bias),
+      dim(dy, 0), at<const uint16_t>(y), dim(y, 0), dim(y, 1), at<const uint16_t>(down_bias),
       at<const int32_t>(offsets), static_cast<int32_t>(offsets.element_count() - 1), &norm,
       at<const uint16_t>(scale), at<const uint16_t>(bias), at<const uint16_t>(weights),
       at<uint16_t>(dv), at<uint16_t>(d_weights), at<float>(d_scale), at<float>(d_bias),

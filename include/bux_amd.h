@@ -12,6 +12,11 @@
  * `bux_last_error` returns on the same thread. Shapes are checked on the host before
  * any kernel is launched.
  *
+ * Rows read through an index (a pick's token, index / index_div) come from a matrix
+ * whose rows the call also takes (`sources`, `tokens`, `n`): a row that lies outside
+ * it, or a negative index, reads as a row of 0. The reference's indices (the sort's
+ * order) are always inside; the bound keeps every read inside the caller's buffer.
+ *
  * Layouts (row-major throughout):
  *   bfloat16   uint16_t bit patterns;
  *   MXFP8      an (r, c) matrix in blocks of 32 along its rows -- the reference's
@@ -81,10 +86,12 @@ int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_experts, in
  * zeros), each value times 2^-e clipped to +-448 and rounded to nearest even E4M3.
  *
  * x         bfloat16 [groups, rows, cols] (a stack of `groups` matrices), or, with an
- *           index, the matrix the rows are read from.
+ *           index, the matrix the rows are read from, [sources, cols].
  * index     NULL, or int32 [rows]: row i is x[index[i] / index_div] (groups must be 1),
- *           a row whose index is negative reading 0 -- the reference's `Picked` rows,
- *           tokens[order // k] (grouped_blockscaled.py:53-62, grouped_triton.py:208-214).
+ *           a row whose index is negative, or whose source row is not below `sources`,
+ *           reading 0 -- the reference's `Picked` rows, tokens[order // k]
+ *           (grouped_blockscaled.py:53-62, grouped_triton.py:208-214).
+ * sources   with an index, x's rows (ignored without one).
  * rows      rows of the matrix (x's, or the index's entries).
  * height    rows of the copies, a multiple of 32, >= rows; rows from `rows` on are 0
  *           (the reference pads to whole tiles, grouped_blockscaled.py:122-128).
@@ -106,10 +113,10 @@ int bux_moe_permute(const int32_t* idx, int64_t n_picks, int32_t num_experts, in
  *           cols must be a multiple of 32.
  */
 enum { BUX_MX_ROWS = 1, BUX_MX_COLUMNS = 2, BUX_MX_TILES = 4, BUX_MX_HALVES = 8 };
-int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t groups,
-                    int64_t rows, int64_t cols, int64_t height, const int32_t* filled, int flags,
-                    uint8_t* values, uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
-                    void* stream);
+int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t sources,
+                    int64_t groups, int64_t rows, int64_t cols, int64_t height,
+                    const int32_t* filled, int flags, uint8_t* values, uint8_t* scales,
+                    uint8_t* t_values, uint8_t* t_scales, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-6. Grouped MXFP8 GEMM over rows: y[i] = a[i] b[g(i)]^T.
@@ -243,15 +250,16 @@ int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, const int32
  * a-2 / a-3. The token path's gathers and sums.
  *
  * bux_token_rows replaces moe.token_rows (moe.py:991-1016) and picked_weights
- * (:1027-1032): rows[i] = z[order[i] / k] for i < m (width columns, bfloat16).
+ * (:1027-1032): rows[i] = z[order[i] / k] for i < m (width columns, bfloat16), z
+ * [tokens, width]; a row of 0 where order[i] / k lies outside [0, tokens).
  * Any width; a multiple of 8 moves 16 bytes a lane.
  * bux_token_sums replaces grouped_blockscaled.sum_by_token (grouped_blockscaled.py:
  * 141-148) and moe.token_sums (moe.py:1035-1066): out[t] = sum_j y[inverse[t k + j]]
  * added in float32 in pick order, rounded once to bfloat16; an inverse outside
  * [0, y_rows) adds 0.
  */
-int bux_token_rows(const uint16_t* z, const int32_t* order, int64_t m, int32_t k, int64_t width,
-                   uint16_t* rows, void* stream);
+int bux_token_rows(const uint16_t* z, int64_t tokens, const int32_t* order, int64_t m, int32_t k,
+                   int64_t width, uint16_t* rows, void* stream);
 int bux_token_sums(const uint16_t* y, int64_t y_rows, const int32_t* inverse, int64_t tokens,
                    int32_t k, int64_t width, uint16_t* out, void* stream);
 
@@ -312,17 +320,20 @@ int bux_glu_backward(const uint16_t* projected, const uint16_t* weights, const u
  *   moe.py:876-885, and weighted's, :922-925, for the down bias):
  *   out[e] = sum over rows r of e of v_r, in float32, out float32 [experts, width];
  *   v_r = x[src(r)], or with weights (bfloat16 [m]) x[src(r)] * weights[r] rounded
- *   to bfloat16; src(r) = r, or with index index[r] / index_div (a pick's token).
+ *   to bfloat16; src(r) = r, or with index index[r] / index_div (a pick's token: x
+ *   then [sources, width], a source row outside it reading 0). Rows at or past m (an
+ *   expert's offsets reaching beyond them) add nothing.
  * bux_token_sums_biased replaces the down bias's forward (moe.py:866-870):
  *   out[t] = sum_by_token(y) + sum_by_token(bias[e(r)] * weights[r]), each sum as
  *   bux_token_sums adds it (the products rounded to bfloat16 first), their sum rounded.
  * bux_expert_bias_weight_grad adds the down bias's share of the weights' gradient
  *   (weighted's VJP, moe.py:922-925): d_weights[r] += sum_c dy[src(r)][c] bias[e(r)][c]
- *   (products rounded to bfloat16, summed in float32, rounded, then added in bfloat16).
+ *   (products rounded to bfloat16, summed in float32, rounded, then added in bfloat16);
+ *   src(r) as bux_expert_sums's, dy [sources, width] with an index.
  */
 int bux_expert_bias_add(uint16_t* x, int64_t m, int64_t width, const uint16_t* bias,
                         const int32_t* offsets, int32_t experts, void* stream);
-int bux_expert_sums(const uint16_t* x, const int32_t* index, int32_t index_div,
+int bux_expert_sums(const uint16_t* x, const int32_t* index, int32_t index_div, int64_t sources,
                     const uint16_t* weights, int64_t m, int64_t width, const int32_t* offsets,
                     int32_t experts, float* out, void* stream);
 int bux_token_sums_biased(const uint16_t* y, int64_t y_rows, const int32_t* inverse,
@@ -330,7 +341,7 @@ int bux_token_sums_biased(const uint16_t* y, int64_t y_rows, const int32_t* inve
                           const int32_t* offsets, int32_t experts, const uint16_t* weights,
                           uint16_t* out, void* stream);
 int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index, int32_t index_div,
-                                int64_t m, int64_t width, const uint16_t* bias,
+                                int64_t sources, int64_t m, int64_t width, const uint16_t* bias,
                                 const int32_t* offsets, int32_t experts, uint16_t* d_weights,
                                 void* stream);
 
@@ -349,8 +360,9 @@ int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index, int32_
  * eps; rmsnorm: the latter alone); the result rounded to bfloat16, each later product
  * and sum rounded as the reference's bfloat16 ops round. scale [d] (affine) and bias
  * [d] (bias) bfloat16, else NULL. d a multiple of 8, at most 8192.
- * bux_expert_norm_backward: its VJP, given the tokens' gradient dy read through
- * index / index_div (the sort's order and k): dv [m, d], the gradient to y (and, by
+ * bux_expert_norm_backward: its VJP, given the tokens' gradient dy [sources, d] read
+ * through index / index_div (the sort's order and k; dy [m, d] read row for row with
+ * index NULL, sources then ignored): dv [m, d], the gradient to y (and, by
  * expert, to the down bias: bux_expert_sums of it); d_weights [m] (written: the norm
  * path's only use of the weights); d_scale and d_bias [d] float32 sums over the rows
  * (NULL where the norm has none). workspace:
@@ -371,8 +383,9 @@ int bux_expert_norm_forward(const uint16_t* y, int64_t m, int64_t d, const uint1
                             uint16_t* out, void* stream);
 size_t bux_expert_norm_backward_workspace_size(int64_t m, int64_t d);
 int bux_expert_norm_backward(const uint16_t* dy, const int32_t* index, int32_t index_div,
-                             const uint16_t* y, int64_t m, int64_t d, const uint16_t* down_bias,
-                             const int32_t* offsets, int32_t experts, const bux_norm* norm,
+                             int64_t sources, const uint16_t* y, int64_t m, int64_t d,
+                             const uint16_t* down_bias, const int32_t* offsets, int32_t experts,
+                             const bux_norm* norm,
                              const uint16_t* scale, const uint16_t* bias,
                              const uint16_t* weights, uint16_t* dv, uint16_t* d_weights,
                              float* d_scale, float* d_bias, void* workspace,

@@ -56,24 +56,26 @@ def _msg(lib) -> str:
 
 def test_quantize_rejects_bad_shapes_and_flags(lib):
     p = ctypes.c_void_p(16)  # never dereferenced: the checks fail first
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 48, 64, None, 3, p, p, p, p, None)
+    rc = lib.bux_mx_quantize(p, None, 1, 64, 1, 64, 48, 64, None, 3, p, p, p, p, None)
     assert rc == 1 and "cols=48" in _msg(lib)
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 40, None, 3, p, p, p, p, None)
+    rc = lib.bux_mx_quantize(p, None, 1, 64, 1, 64, 64, 40, None, 3, p, p, p, p, None)
     assert rc == 1 and "height=40" in _msg(lib)
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 0, p, p, p, p, None)
+    rc = lib.bux_mx_quantize(p, None, 1, 64, 1, 64, 64, 64, None, 0, p, p, p, p, None)
     assert rc == 1 and "flags" in _msg(lib)
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 4, p, p, p, p, None)
+    rc = lib.bux_mx_quantize(p, None, 1, 64, 1, 64, 64, 64, None, 4, p, p, p, p, None)
     assert rc == 1 and "flags=4" in _msg(lib)  # tiles alone: no copy asked for
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 16 | 1, p, p, p, p, None)
+    rc = lib.bux_mx_quantize(p, None, 1, 64, 1, 64, 64, 64, None, 16 | 1, p, p, p, p, None)
     assert rc == 1 and "flags=17" in _msg(lib)
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 96, 64, None, 8 | 1, p, p, p, p, None)
+    rc = lib.bux_mx_quantize(p, None, 1, 64, 1, 64, 96, 64, None, 8 | 1, p, p, p, p, None)
     assert rc == 1 and "BUX_MX_HALVES" in _msg(lib)  # halves: whole 64s of columns
-    rc = lib.bux_mx_quantize(p, None, 1, 1, 64, 64, 64, None, 2, p, p, None, None, None)
+    rc = lib.bux_mx_quantize(p, None, 1, 64, 1, 64, 64, 64, None, 2, p, p, None, None, None)
     assert rc == 1 and "t_values" in _msg(lib)
-    rc = lib.bux_mx_quantize(p, p, 1, 2, 64, 64, 64, None, 1, p, p, None, None, None)
+    rc = lib.bux_mx_quantize(p, p, 1, 64, 2, 64, 64, 64, None, 1, p, p, None, None, None)
     assert rc == 1 and "index" in _msg(lib)
-    rc = lib.bux_mx_quantize(p, p, 0, 1, 64, 64, 64, None, 1, p, p, None, None, None)
+    rc = lib.bux_mx_quantize(p, p, 0, 64, 1, 64, 64, 64, None, 1, p, p, None, None, None)
     assert rc == 1 and "index_div" in _msg(lib)
+    rc = lib.bux_mx_quantize(p, p, 1, -1, 1, 64, 64, 64, None, 1, p, p, None, None, None)
+    assert rc == 1 and "sources=-1" in _msg(lib)
 
 
 def test_gemms_reject_bad_shapes_and_small_workspaces(lib):
@@ -189,17 +191,21 @@ def test_bias_ops_reject_bad_arguments(lib):
     rc = lib.bux_expert_bias_add(p, 10, 16, p, p, 0, None)
     assert rc == 1 and "0 experts" in _msg(lib)
     assert lib.bux_expert_bias_add(None, 0, 16, None, p, 4, None) == 0  # no rows
-    rc = lib.bux_expert_sums(p, p, 0, None, 10, 16, p, 4, p, None)
+    rc = lib.bux_expert_sums(p, p, 0, 10, None, 10, 16, p, 4, p, None)
     assert rc == 1 and "index_div=0" in _msg(lib)
-    rc = lib.bux_expert_sums(p, None, 1, None, 10, 16, p, 4, None, None)
+    rc = lib.bux_expert_sums(p, p, 1, -1, None, 10, 16, p, 4, p, None)
+    assert rc == 1 and "sources=-1" in _msg(lib)
+    rc = lib.bux_expert_sums(p, None, 1, 0, None, 10, 16, p, 4, None, None)
     assert rc == 1 and "NULL" in _msg(lib)
     rc = lib.bux_token_sums_biased(p, 10, p, 5, 2, 16, None, p, 4, p, p, None)
     assert rc == 1 and "NULL bias" in _msg(lib)
     rc = lib.bux_token_sums_biased(p, 10, p, 5, 2, 12, p, p, 4, p, p, None)
     assert rc == 1 and "width=12" in _msg(lib)
-    rc = lib.bux_expert_bias_weight_grad(p, p, 0, 10, 16, p, p, 4, p, None)
+    rc = lib.bux_expert_bias_weight_grad(p, p, 0, 10, 10, 16, p, p, 4, p, None)
     assert rc == 1 and "index_div=0" in _msg(lib)
-    rc = lib.bux_expert_bias_weight_grad(p, None, 1, 10, 16, p, p, 0, p, None)
+    rc = lib.bux_expert_bias_weight_grad(p, p, 1, -1, 10, 16, p, p, 4, p, None)
+    assert rc == 1 and "sources=-1" in _msg(lib)
+    rc = lib.bux_expert_bias_weight_grad(p, None, 1, 0, 10, 16, p, p, 0, p, None)
     assert rc == 1 and "0 experts" in _msg(lib)
 
 

@@ -183,6 +183,49 @@ def test_expert_bias_ops(lib):
     np.testing.assert_array_equal(got_dw[filled:], bf16.to_f32(dwg[filled:]) + 0.0)
 
 
+def test_index_readers_read_zeros_outside_the_tokens(lib):
+    """The ops that read dy through the picks' tokens (the down bias's sums and weight
+    gradient, the norm's backward): an order entry whose token lies outside dy, past its
+    rows or negative, reads a row of 0 and no read leaves dy. Checked bit for bit
+    against the same ops pointed at an explicit row of zeros appended to dy. (The
+    reference's orders, the sort's, always lie inside.)"""
+    from bux_amd import moe
+    rng = np.random.default_rng(64)
+    t, k, e, d = 300, 4, 12, 256
+    m = t * k
+    idx, s = _sorted_case(rng, t, k, e)
+    filled = int(s.sizes.sum())
+    go = to_gpu(np.concatenate([s.offsets, [filled]]).astype(np.int32))
+    dy = normal_bf16(rng, (t, d))
+    dy_zero = np.concatenate([dy, np.zeros((1, d), np.uint16)])  # token t: zeros
+    rw = bf16.to_bf16(rng.random(m).astype(np.float32))
+    down_bias = normal_bf16(rng, (e, d))
+    y = normal_bf16(rng, (m, d), 2.0)
+    y[filled:] = 0
+    outside = rng.choice(filled, 9, replace=False)
+    order = s.order.astype(np.int32).copy()
+    order[outside] = [-1, -k, t * k, t * k + k - 1, t * k + k, 2**31 - 1, -(2**31), 5 * t * k, -7]
+    order_zero = s.order.astype(np.int32).copy()
+    order_zero[outside] = t * k  # the appended row
+    g = moe.ExpertNorm("rmsnorm", 1e-6, True, False, False, False)
+    scale = to_gpu_bf16(bf16.to_bf16((1 + 0.3 * rng.standard_normal(d)).astype(np.float32)))
+    announce("index readers outside the tokens")
+    got, want = [], []
+    for rows, idx_ in ((dy, order), (dy_zero, order_zero)):
+        gdy, gorder = to_gpu_bf16(rows), to_gpu(idx_)
+        sums = moe.expert_sums(gdy, go, gorder, k, to_gpu_bf16(rw))
+        gdw = to_gpu_bf16(normal_bf16(np.random.default_rng(1), (m,), 0.1))
+        moe.add_bias_weight_grad(gdw, gdy, gorder, k, to_gpu_bf16(down_bias), go)
+        dv, dw, dscale, _ = moe.expert_norm_backward(gdy, gorder, k, to_gpu_bf16(y), go, g, scale,
+                                                     None, to_gpu_bf16(rw))
+        torch.cuda.synchronize()
+        (got if rows is dy else want).append(
+            [sums.cpu().numpy().view(np.uint32), bf16_bits(gdw), bf16_bits(dv), bf16_bits(dw),
+             dscale.cpu().numpy().view(np.uint32)])
+    for name, a, b in zip(("sums", "weight grad", "dv", "dw", "d_scale"), got[0], want[0]):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+
+
 NORMS = [
     # (kind, eps, affine, bias, zero_centered, scale_input)
     ("rmsnorm", 1e-6, True, False, False, False),

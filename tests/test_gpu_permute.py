@@ -91,6 +91,25 @@ def test_token_rows_and_picked_weights(lib):
     np.testing.assert_array_equal(bf16_bits(pw), omoe.picked_weights(w, s.order))
 
 
+@pytest.mark.parametrize("d", [264, 1])
+def test_token_rows_read_zeros_where_an_order_entry_leaves_the_tokens(lib, d):
+    """An order entry whose token lies outside z (past its rows, or negative) gives a row
+    of 0 rather than a read outside z; the others are z[order // k]. (The reference's
+    orders, the sort's, always lie inside.) Width 1 is picked_weights' kernel."""
+    from bux_amd import moe
+    rng = np.random.default_rng(26)
+    t, k, m = 200, 4, 700
+    z = normal_bf16(rng, (t, d))
+    order = rng.permutation(t * k)[:m].astype(np.int32)
+    order[:6] = [-1, -k, t * k, t * k + k - 1, 2**31 - 1, -(2**31)]
+    announce("token_rows out of range", d)
+    rows = moe.token_rows(to_gpu_bf16(z), to_gpu(order), k)
+    torch.cuda.synchronize()
+    inside = (order >= 0) & (order // k < t)
+    want = np.where(inside[:, None], z[np.where(inside, order // k, 0)], 0).astype(np.uint16)
+    np.testing.assert_array_equal(bf16_bits(rows), want)
+
+
 @pytest.mark.parametrize("t,k,d", [(300, 8, 2048), (64, 2, 256), (50, 4, 2880)])
 def test_sum_by_token_adds_in_float32_in_pick_order(lib, t, k, d):
     """Bit-exact: each token's k rows added in float32, in order, rounded once; an index

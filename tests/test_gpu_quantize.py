@@ -92,20 +92,23 @@ def test_every_bf16_pattern_shuffled(lib):
 
 @pytest.mark.parametrize("cols", [32, 96, 2048])
 def test_gathered_rows_past_filled_and_padding(lib, cols):
-    """Picked rows ``tokens[order // k]`` (a -1 reads 0), rows from `filled` on and the
+    """Picked rows ``tokens[order // k]`` (a -1 reads 0, and so does an entry whose
+    token lies past the tokens: no read leaves them), rows from `filled` on and the
     padding up to whole tiles of 128 as 0 (grouped_blockscaled.py:122-128, 314)."""
     rng = np.random.default_rng(12)
     tokens, k, m = 300, 4, 1000
     z = with_outliers(rng, normal_bf16(rng, (tokens, cols)), 0.01)
     order = rng.permutation(tokens * k)[:m].astype(np.int32)
     order[rng.choice(m, 7, replace=False)] = -1
+    past = rng.choice(m, 5, replace=False)
+    order[past] = tokens * k + np.array([0, 1, k, 1000, 2**31 - 1 - tokens * k])[:5]
     filled = 937
     height = 1024
     announce("quantize gathered", tokens, cols, m, filled, height)
     got_rows, got_cols = _quantize(
         to_gpu_bf16(z), filled=to_gpu(np.array([filled], np.int32)), columns=True,
         index=to_gpu(order), index_div=k, height=height)
-    index = np.where(order >= 0, order // k, -1)
+    index = np.where((order >= 0) & (order // k < tokens), order // k, -1)
     want_rows, want_cols = mxfp8.quantized_twice(z, filled, True, index=index, height=height)
     _equal(got_rows, want_rows, "rows")
     _equal(got_cols, want_cols, "columns")
