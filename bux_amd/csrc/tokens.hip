@@ -269,7 +269,9 @@ __global__ __launch_bounds__(THREADS) void expert_sums_kernel(
   const int64_t c0 = (blockIdx.x % chunks) * SUM_COLS;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t c = c0 + lane * VEC;
-  const int64_t lo = offsets[e], hi = offsets[e + 1] < m ? offsets[e + 1] : m;
+  // rows inside [0, m) only, whatever the offsets say
+  const int64_t lo = offsets[e] > 0 ? offsets[e] : 0;
+  const int64_t hi = offsets[e + 1] < m ? offsets[e + 1] : m;
   float acc[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (c < width) {
     for (int64_t r = lo + wave; r < hi; r += THREADS / 64) {
