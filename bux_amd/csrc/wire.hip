@@ -60,7 +60,9 @@ __global__ __launch_bounds__(THREADS) void pack_kernel(const uint16_t* __restric
                                                        int64_t d, uint8_t* __restrict__ packed) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * (THREADS / 64) + (threadIdx.x >> 6);
   if (i >= m) return;
-  const int64_t src = index ? index[i] / div : i;
+  // a negative index reads zeros, as one past x does (C's division would take -1 / k
+  // to row 0)
+  const int64_t src = index ? (index[i] < 0 ? -1 : index[i] / div) : i;
   const bool live = src >= 0 && src < n;
   const int64_t blocks = d / 32, row_bytes = d + blocks;
   uint8_t* out = packed + i * row_bytes;

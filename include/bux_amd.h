@@ -518,7 +518,7 @@ int bux_route(const uint16_t* x, const uint16_t* kernel, const float* bias, int6
  * // k] (experts.py:624): packed[i] (d + d/32 bytes: the E4M3 codes of the row
  * quantized in blocks of 32 along d, then its d/32 E8M0 scale bytes) of x[index[i] /
  * index_div] (x[i] with index NULL), i < m; x bfloat16 [n, d]. A source row outside
- * [0, n) packs as zeros.
+ * [0, n), or a negative index, packs as zeros.
  * bux_mx_unpack_rows replaces parallel/experts._from_mxfp8 (experts.py:666-672) =
  * dequantized(mx_unpacked(packed, d)).astype(bfloat16) (blockscaled.py:223-229,
  * 378-380): out[i][j] = code * 2^(scale byte - 127) in float32, rounded to bfloat16

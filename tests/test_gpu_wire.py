@@ -47,14 +47,15 @@ def test_a_pick_outside_the_tokens_packs_zeros(lib):
     from bux_amd import dispatch
     rng = np.random.default_rng(52)
     z = normal_bf16(rng, (4, 64))
-    order = np.array([0, 7, 40, -3], np.int32)  # // 2: 0, 3, 20 (past), -2 (before)
+    # // 2: 0, 3, then 20 (past), -2 and -1 (before; C's division would take -1 to 0)
+    order = np.array([0, 7, 40, -3, -1, 2**31 - 1], np.int32)
     announce("pack out of range")
     got = dispatch.picked_in_mxfp8(to_gpu_bf16(z), to_gpu(order), 2).cpu().numpy()
     want = mxfp8.in_mxfp8(z)
     np.testing.assert_array_equal(got[:2], want[[0, 3]])
     zeros = mxfp8.in_mxfp8(np.zeros((1, 64), np.uint16))[0]
-    np.testing.assert_array_equal(got[2], zeros)
-    np.testing.assert_array_equal(got[3], zeros)
+    for row in got[2:]:
+        np.testing.assert_array_equal(row, zeros)
 
 
 @pytest.mark.parametrize("d", [2048, 2880, 96, 128])
