@@ -34,31 +34,32 @@ struct Tile {
 
 // --- the device-side prologue: group starts and the ragged tile list ----------------
 
-// Exclusive scan of data[0, n) in LDS by one workgroup of THREADS lanes; returns the
-// total. `partial` is THREADS ints of LDS.
-__device__ int32_t block_scan(int32_t* data, int n, int32_t* partial) {
+// Exclusive scan of data[0, n) (each >= 0) in LDS by one workgroup of THREADS lanes,
+// in 64 bits, each prefix sum capped at `cap`; returns the capped total. `partial` is
+// THREADS int64s of LDS.
+__device__ int32_t block_scan(int32_t* data, int n, int64_t* partial, int32_t cap) {
   const int t = threadIdx.x;
   const int per = (n + THREADS - 1) / THREADS;
   const int lo = t * per, hi = lo + per < n ? lo + per : n;
-  int32_t sum = 0;
+  int64_t sum = 0;
   for (int i = lo; i < hi; ++i) sum += data[i];
   partial[t] = sum;
   __syncthreads();
   for (int step = 1; step < THREADS; step <<= 1) {
-    const int32_t add = t >= step ? partial[t - step] : 0;
+    const int64_t add = t >= step ? partial[t - step] : 0;
     __syncthreads();
     partial[t] += add;
     __syncthreads();
   }
-  int32_t run = t > 0 ? partial[t - 1] : 0;
+  int64_t run = t > 0 ? partial[t - 1] : 0;
   for (int i = lo; i < hi; ++i) {
     const int32_t c = data[i];
-    data[i] = run;
+    data[i] = static_cast<int32_t>(run < cap ? run : cap);
     run += c;
   }
-  const int32_t total = partial[THREADS - 1];
+  const int64_t total = partial[THREADS - 1];
   __syncthreads();
-  return total;
+  return static_cast<int32_t>(total < cap ? total : cap);
 }
 
 // A tile list opens with a header of LIST_HEADER bytes: LIST_MAGIC, the groups, m and
@@ -68,7 +69,8 @@ constexpr int LIST_HEADER = 64;
 constexpr int32_t LIST_MAGIC = BUX_LIST_MAGIC;  // "BUXT"
 constexpr int32_t LIST_REFUSED = BUX_LIST_REFUSED;
 
-// starts[g] for g <= groups (starts[groups] = sum of sizes), then, if `tiles`, the
+// starts[g] for g <= groups (starts[groups] = sum of sizes; a negative size counts as
+// 0, and with `tiles` the sums stop at max(m, height)), then, if `tiles`, the
 // tile list of `slots` entries: each group's rows in tiles of BM from its first row
 // rounded down to a multiple of `align` (a power of two; the last tile partial), then
 // the rows from the sum of sizes to `height` as group `groups`, then empty tiles
@@ -94,18 +96,25 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
   }
   __shared__ int32_t starts[MAX_GROUPS + 2];
   __shared__ int32_t before[MAX_GROUPS + 2];
-  __shared__ int32_t partial[THREADS];
+  __shared__ int64_t partial[THREADS];
   const int t = threadIdx.x;
-  for (int g = t; g < groups; g += THREADS) starts[g] = sizes[g];
+  // The sizes as the tiles take them: a negative one as 0, and the starts capped at the
+  // rows there are (m or height, whichever is more; unbounded for a list of starts
+  // alone), so that sizes past them give the last groups fewer rows, never a tile
+  // outside the rows or a count that overflows.
+  const int64_t rows = m > height ? m : height;
+  const int32_t cap = tiles != nullptr && rows > 0 && rows < INT32_MAX ? static_cast<int32_t>(rows)
+                                                                        : INT32_MAX;
+  for (int g = t; g < groups; g += THREADS) starts[g] = sizes[g] > 0 ? sizes[g] : 0;
   __syncthreads();
-  const int32_t filled = block_scan(starts, groups, partial);
+  const int32_t filled = block_scan(starts, groups, partial, cap);
   if (t == 0) starts[groups] = filled;
   __syncthreads();
   for (int g = t; g <= groups; g += THREADS) starts_out[g] = starts[g];
   if (tiles == nullptr) return;
   const int all = groups + 1;
   auto size_of = [&](int g) -> int64_t {
-    if (g < groups) return sizes[g];
+    if (g < groups) return starts[g + 1] - starts[g];
     return height > filled ? height - filled : 0;
   };
   // where group g's rows lie in a: `a_starts` (given), else packed; the rows past the
@@ -122,12 +131,12 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
   };
   for (int g = t; g < all; g += THREADS) before[g] = static_cast<int32_t>(count_of(g));
   __syncthreads();
-  const int32_t used = block_scan(before, all, partial);
+  const int32_t used = block_scan(before, all, partial, INT32_MAX);
   for (int g = t; g < all; g += THREADS) {
     const int64_t s = size_of(g), start = first(g), end = start + s;
     const int64_t base = start & ~static_cast<int64_t>(align - 1), count = count_of(g);
-    // Sizes summing past the rows there are would list more tiles than there are
-    // slots: those are dropped, never written past the list.
+    // The capped starts keep the counts within the slots; a tile past them would be
+    // dropped, never written past the list.
     for (int64_t j = 0; j < count && before[g] + j < slots; ++j) {
       const int64_t lo = base + j * BM;
       tiles[before[g] + j] = Tile{g, static_cast<int32_t>(lo),

@@ -127,7 +127,8 @@ int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, 
  *
  * a_values/a_scales  MXFP8 tiled, m rows of k bytes: the rows, group 0's first.
  * b_values/b_scales  MXFP8 tiled, a stack of groups matrices of n rows of k bytes.
- * sizes     device int32 [groups], summing to at most m.
+ * sizes     device int32 [groups], summing to at most m (a negative size counts as 0,
+ *           and sizes summing past max(m, height) give the last groups fewer rows).
  * k         the tiled K: the contracted length rounded up to a multiple of 128.
  * y         [height, n], bfloat16 (out_dtype BUX_BF16) or float32 (BUX_F32); rows
  *           from sum(sizes) to height are 0. Any height: a's quantized copy may be

@@ -119,6 +119,34 @@ def test_rows(lib, sizes, k, n, height):
     assert (got16[filled:] == 0).all()
 
 
+@pytest.mark.parametrize("sizes", [[100, -7, 150, 400, 90], [100, 2**31 - 1, 5], [-(2**31), 64]])
+def test_rows_take_a_negative_size_as_none_and_stop_at_the_rows(lib, sizes):
+    """Sizes are device data the host cannot check: a negative one counts as 0, and sizes
+    summing past the rows there are (512) give the last groups fewer rows, so that no
+    tile starts before row 0 or stores past y. The result is the oracle's on the sizes
+    so taken ([100, 0, 150, 262, 0], [100, 412, 0], [0, 64])."""
+    from bux_amd import grouped_mxfp8
+    rng = np.random.default_rng(36)
+    m = h = 512
+    k, n = 256, 384
+    sizes = np.array(sizes, np.int64)
+    taken, start = [], 0
+    for size in np.maximum(sizes, 0).tolist():
+        taken.append(min(size, m - start))
+        start += taken[-1]
+    taken = np.array(taken, np.int32)
+    a = _codes(rng, (m, k))
+    b = _codes(rng, (len(sizes), n, k), 0.02)
+    announce("rows with sizes outside the rows", sizes.tolist())
+    y32 = grouped_mxfp8.rows(_gpu(a), _gpu(b), to_gpu(sizes.astype(np.int32)), torch.float32,
+                             height=h)
+    torch.cuda.synchronize()
+    got = y32.cpu().numpy()
+    want = _rows64(a, b, taken, h)
+    _close_f32(got, want, f"rows {sizes.tolist()} taken as {taken.tolist()}")
+    assert (got[int(taken.sum()):] == 0).all()
+
+
 CONTRACT_CASES = [
     ([70, 0, 100, 3, 77], 256, 192, 256),
     ([0, 130, 1, 3, 256, 0, 300, 100], 2880, 160, 800),  # d not whole tiles, blocks across groups
