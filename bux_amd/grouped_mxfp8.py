@@ -108,7 +108,8 @@ def quantized_twice(
             for every row.
         columns: whether to return x^T too.
         index: int32 (m,): row i is ``x[index[i] // index_div]``, 0 where the index
-            is negative (the reference's ``Picked`` rows, ``tokens[order // k]``).
+            is negative or that row lies past x's (the reference's ``Picked`` rows,
+            ``tokens[order // k]``).
         index_div: the divisor of `index` (k, the picks a token).
         height: rows of the copies, a multiple of 32 (rows past x's are 0); None for
             x's (the index's) rows rounded up to 32.

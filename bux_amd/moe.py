@@ -64,7 +64,8 @@ def sort_by_expert(idx: torch.Tensor, num_experts: int) -> Sorted:
 
 
 def token_rows(z: torch.Tensor, order: torch.Tensor, k: int) -> torch.Tensor:
-    """Return ``z[order // k]`` (bfloat16 rows)."""
+    """Return ``z[order // k]`` (bfloat16 rows), a row of 0 where ``order // k`` lies
+    outside z's rows (a negative entry too; the sort's orders never do)."""
     require(z, order)
     m, width = order.shape[0], z.shape[-1]
     rows = torch.empty(m, width, dtype=z.dtype, device=z.device)
