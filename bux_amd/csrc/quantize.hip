@@ -87,10 +87,14 @@ struct Matrix {
   int64_t sources;  // with an index, x's rows: a source row outside [0, sources) reads 0
   int64_t rows, cols;
   bool halves;
-  // Whether the tiles go in XCD runs (quantize_kernel): not for rows read by index,
-  // which measured 3% slower so (a token's rows lie in 8 places of the index, and no
-  // order of the tiles keeps them in one L2).
-  __device__ __forceinline__ bool xcd_runs() const { return index == nullptr; }
+  // The tiles go in XCD runs (quantize_kernel); rows read by index take them a column
+  // tile at a time, its row tiles one after another: an XCD then works on one or two
+  // column tiles at once, and those columns of every token (c3: 16384 tokens x 128
+  // bytes, 2 MiB) stay in its L2 for all k of a token's picks, which lie in k places
+  // of the index. (Column tiles fastest, an XCD held four at once, 8 MiB, and the
+  // tokens came from beyond L2 5.2 times over.)
+  __device__ __forceinline__ bool xcd_runs() const { return true; }
+  __device__ __forceinline__ bool by_columns() const { return index != nullptr; }
   // Columns [col, col + 8) of row r of matrix g; `live`: r holds values and the
   // columns are the matrix's (`inside`: the columns are; padding past them is not).
   __device__ __forceinline__ uint4 load(int64_t g, int64_t r, int64_t col, bool live, bool,
@@ -139,6 +143,7 @@ template <typename K>
 struct GluForward {
   static constexpr bool kPartials = false;
   __device__ __forceinline__ bool xcd_runs() const { return true; }
+  __device__ __forceinline__ bool by_columns() const { return false; }
   const uint16_t* projected;
   const uint16_t* weights;
   uint16_t* h;
@@ -180,6 +185,7 @@ template <typename K>
 struct GluBackward {
   static constexpr bool kPartials = true;
   __device__ __forceinline__ bool xcd_runs() const { return true; }
+  __device__ __forceinline__ bool by_columns() const { return false; }
   static constexpr int P = K::gated ? 2 : 1;
   const uint16_t* projected;
   const uint16_t* weights;
@@ -247,18 +253,20 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
   };
 
   const int t = threadIdx.x;
-  // Column tiles run fastest, so that neighbouring tiles read one band of rows; and,
-  // where the source asks, the tiles are renumbered so that each XCD (workgroup id % 8)
-  // takes a contiguous run of them, neighbouring tiles then sharing its L2 (two 64-column
-  // tiles of d projected read the two halves of one 128-byte line of dh a row; measured
-  // at c3: W_up's copies 10% faster, the activations' 4%). They cover the K padding of
-  // the row copy too (columns read as 0 there).
+  // The tiles are renumbered so that each XCD (workgroup id % 8) takes a contiguous run
+  // of them, neighbouring tiles then sharing its L2. Column tiles run fastest, so that
+  // neighbouring tiles read one band of rows (two 64-column tiles of d projected read the
+  // two halves of one 128-byte line of dh a row; measured at c3: W_up's copies 10% faster,
+  // the activations' 4%); rows read by index take row tiles fastest (Matrix::by_columns:
+  // quantize x and dy by index 8% and 4% faster in the c3 step). They cover the K
+  // padding of the row copy too (columns read as 0 there).
   const int64_t cols_pad = (cols + 127) / 128 * 128;
   const int64_t col_tiles = cols_pad / TILE_COLS;
   const int64_t tile_id = src.xcd_runs() ? xcd_run(blockIdx.x, gridDim.x) : blockIdx.x;
-  const int64_t col_tile = tile_id % col_tiles;
+  const int64_t row_tiles = gridDim.x / col_tiles;
+  const int64_t col_tile = src.by_columns() ? tile_id / row_tiles : tile_id % col_tiles;
   const int64_t col0 = col_tile * TILE_COLS;
-  const int64_t row0 = (tile_id / col_tiles) * TILE_ROWS;
+  const int64_t row0 = (src.by_columns() ? tile_id % row_tiles : tile_id / col_tiles) * TILE_ROWS;
   const int64_t g = blockIdx.y;
   const int64_t filled = filled_ptr ? static_cast<int64_t>(*filled_ptr) : height;
 
