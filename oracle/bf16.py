@@ -5,7 +5,9 @@ their bits in uint16 and widens to float32 exactly.
 
 Pins (``tests/test_oracle.py``): `to_bf16` against torch's float32 -> bfloat16 cast on
 random and edge values (ties, subnormals, overflow to inf); `to_f32` is exact by
-construction (a shift), checked on all 65536 patterns against torch.
+construction (a shift), checked on all 65536 patterns against torch; `from_f64` (one
+rounding from float64) against exact rational rounding (``fractions.Fraction``) on
+values just off bfloat16 ties, where rounding through float32 would round twice.
 """
 
 import numpy as np
@@ -30,3 +32,20 @@ def to_bf16(x: np.ndarray) -> np.ndarray:
 def round_f32(x: np.ndarray) -> np.ndarray:
     """Return float32 values rounded to bfloat16 and widened back: x.astype(bf16)."""
     return to_f32(to_bf16(x))
+
+
+def from_f64(x: np.ndarray) -> np.ndarray:
+    """Return float64 values rounded once to nearest even bfloat16, as uint16 bits
+    (finite, normal-range values): float64 -> float32 rounded to odd (truncated, its
+    last bit set when inexact), then float32 -> bfloat16 to nearest even. Rounding to
+    odd keeps the information a second rounding needs, since float32 carries 16 more
+    bits than bfloat16."""
+    x = np.asarray(x, np.float64)
+    r = x.astype(np.float32)
+    # truncate toward zero: step back where rounding went away from 0
+    away = np.abs(r.astype(np.float64)) > np.abs(x)
+    r = np.where(away, np.nextafter(r, np.float32(0)), r)
+    u = r.view(np.uint32).copy()
+    inexact = r.astype(np.float64) != x
+    u[inexact] |= np.uint32(1)
+    return to_bf16(u.view(np.float32))

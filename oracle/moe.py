@@ -81,20 +81,24 @@ def picked_weights(weights: np.ndarray, order: np.ndarray) -> np.ndarray:
     return np.asarray(weights).reshape(-1)[np.asarray(order)]
 
 
-def sum_by_token(y: np.ndarray, inverse: np.ndarray, out_bf16: bool = True) -> np.ndarray:
+def sum_by_token(y: np.ndarray, inverse: np.ndarray, out_bf16: bool = True,
+                 exact: bool = False) -> np.ndarray:
     """Return each token's sum of its k rows of y at ``inverse`` (t, k), added in
     float32 in pick order; an index outside y's rows adds 0
     (grouped_blockscaled.py:141-148). y is bfloat16 bits or float32; the result is
-    bfloat16 bits if `out_bf16`, else float32."""
-    values = bf16.to_f32(y) if y.dtype == np.uint16 else np.asarray(y, np.float32)
+    bfloat16 bits if `out_bf16`, else float32. `exact`: float64 sums, one rounding."""
+    t_ = _sums(exact)
+    values = (bf16.to_f32(y) if y.dtype == np.uint16 else np.asarray(y, np.float32)).astype(t_)
     inverse = np.asarray(inverse)
     m = values.shape[0]
     inside = (inverse >= 0) & (inverse < m)
-    total = np.zeros((inverse.shape[0], values.shape[1]), np.float32)
+    total = np.zeros((inverse.shape[0], values.shape[1]), t_)
     for j in range(inverse.shape[1]):
         rows = values[np.where(inside[:, j], inverse[:, j], 0)]
-        total += np.where(inside[:, j, None], rows, np.float32(0))
-    return bf16.to_bf16(total) if out_bf16 else total
+        total += np.where(inside[:, j, None], rows, t_(0))
+    if not out_bf16:
+        return total.astype(np.float32)
+    return bf16.from_f64(total) if exact else bf16.to_bf16(total)
 
 
 def tiles_of(sizes: np.ndarray, m: int, tile: int, starts: np.ndarray | None = None) -> np.ndarray:
@@ -125,19 +129,35 @@ def whole(rows: int, tile: int = 128) -> int:
 
 
 def _cast(y: np.ndarray, out: str) -> np.ndarray:
+    """The GEMMs' output: "bf16" bits (rounded once), "f32", or "f64" (exact sums
+    unrounded, for tests that model another summation's error before the rounding)."""
+    if out == "f64":
+        return y.astype(np.float64)
+    if y.dtype == np.float64:  # exact sums: one rounding
+        return bf16.from_f64(y) if out == "bf16" else y.astype(np.float32)
     return bf16.to_bf16(y) if out == "bf16" else y.astype(np.float32)
 
 
+def _sums(exact: bool):
+    """The dtype the GEMMs multiply and add in: float32 (XLA:CPU's, the oracle's), or
+    float64 with `exact` (products of dequantized E4M3 or bfloat16 values are exact
+    there, and sums of up to 2^20 of them lose at most a few float64 ulps): the exact
+    restatement that tells how far from the exact result a float32 order lands."""
+    return np.float64 if exact else np.float32
+
+
 def rows_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16", height: int | None = None,
-            starts: np.ndarray | None = None) -> np.ndarray:
+            starts: np.ndarray | None = None, exact: bool = False) -> np.ndarray:
     """Return each group's rows of a times its matrix b[g]^T: a (m, k) and b
     (g, n, k) in MXFP8 along k, dequantized and multiplied in float32; rows past the
     groups are 0 (grouped_blockscaled.py:220-233, grouped_mxfp8.py:116-154). With
-    `starts`, group g's rows of a start at starts[g], y's stay packed."""
-    x = mxfp8.dequantized(a)
-    w = mxfp8.dequantized(b)
+    `starts`, group g's rows of a start at starts[g], y's stay packed. `exact`: sums in
+    float64, one rounding (`_sums`)."""
+    t = _sums(exact)
+    x = mxfp8.dequantized(a).astype(t)
+    w = mxfp8.dequantized(b).astype(t)
     m = x.shape[0] if height is None else height
-    y = np.zeros((m, w.shape[1]), np.float32)
+    y = np.zeros((m, w.shape[1]), t)
     start = 0
     for g, size in enumerate(np.asarray(sizes).tolist()):
         at = start if starts is None else int(starts[g])
@@ -147,14 +167,16 @@ def rows_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16", height: 
     return _cast(y, out)
 
 
-def contract_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
+def contract_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16",
+                exact: bool = False) -> np.ndarray:
     """Return dW[g] = a[:, rows of g] b[:, rows of g]^T: a (d, m) and b (f, m) in
     MXFP8 along m, dequantized and multiplied in float32 (grouped_blockscaled.py:
-    236-250)."""
-    x = mxfp8.dequantized(a)
-    y = mxfp8.dequantized(b)
+    236-250). `exact`: sums in float64, one rounding (`_sums`)."""
+    t = _sums(exact)
+    x = mxfp8.dequantized(a).astype(t)
+    y = mxfp8.dequantized(b).astype(t)
     sizes = np.asarray(sizes).tolist()
-    dw = np.zeros((len(sizes), x.shape[0], y.shape[0]), np.float32)
+    dw = np.zeros((len(sizes), x.shape[0], y.shape[0]), t)
     start = 0
     for g, size in enumerate(sizes):
         if size:
@@ -163,11 +185,14 @@ def contract_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16") -> n
     return _cast(dw, out)
 
 
-def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
+def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = "bf16",
+                    exact: bool = False) -> np.ndarray:
     """Return ``jax.lax.ragged_dot`` of bfloat16 x (m, k) and w (g, k, n): float32
-    sums rounded to bfloat16, rows past the groups 0 (grouped.py:42-62,90-102)."""
-    xf, wf = bf16.to_f32(x), bf16.to_f32(w)
-    y = np.zeros((xf.shape[0], wf.shape[2]), np.float32)
+    sums rounded to bfloat16, rows past the groups 0 (grouped.py:42-62,90-102).
+    `exact`: sums in float64, one rounding (`_sums`)."""
+    t = _sums(exact)
+    xf, wf = bf16.to_f32(x).astype(t), bf16.to_f32(w).astype(t)
+    y = np.zeros((xf.shape[0], wf.shape[2]), t)
     start = 0
     for g, size in enumerate(np.asarray(sizes).tolist()):
         if size:
@@ -176,11 +201,14 @@ def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = 
     return _cast(y, out)
 
 
-def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str = "bf16") -> np.ndarray:
-    """Return x^T dy per group (grouped.py:105-146), float32 sums."""
-    xf, gf = bf16.to_f32(x), bf16.to_f32(dy)
+def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str = "bf16",
+                     exact: bool = False) -> np.ndarray:
+    """Return x^T dy per group (grouped.py:105-146), float32 sums (`exact`: float64,
+    one rounding)."""
+    t = _sums(exact)
+    xf, gf = bf16.to_f32(x).astype(t), bf16.to_f32(dy).astype(t)
     sizes = np.asarray(sizes).tolist()
-    dw = np.zeros((len(sizes), xf.shape[1], gf.shape[1]), np.float32)
+    dw = np.zeros((len(sizes), xf.shape[1], gf.shape[1]), t)
     start = 0
     for g, size in enumerate(sizes):
         if size:
@@ -487,6 +515,7 @@ def layer_forward(
     norm: Norm | None = None,
     norm_scale: np.ndarray | None = None,
     norm_bias: np.ndarray | None = None,
+    exact: bool = False,
 ) -> tuple[np.ndarray, Saved]:
     """Return the MoE's routed experts' output (t, d) as bfloat16 bits, and what the
     backward takes: ``routed`` (moe.py:733-773) on one device with picked rows in and
@@ -507,6 +536,9 @@ def layer_forward(
         up_bias: bfloat16 bits (E, f, p) or None; down_bias: (E, d) or None.
         norm: the experts' output norm (moe.py:871-872), with its scale and bias
             (bfloat16 bits (d,)); the activation is then unweighted.
+        exact: every GEMM and token sum in float64, rounded once (the quantization and
+            rounding points unchanged): the exact restatement float32 orders are
+            measured against.
     """
     t, k = idx.shape
     e, d, f, p = up.shape
@@ -528,24 +560,27 @@ def layer_forward(
         up_n, up_k = mxfp8.quantized_twice(up2, d, tiles=tiles)
         down_n, down_k = mxfp8.quantized_twice(down, f, tiles=tiles)
     if fprop:
-        projected = rows_mx(x_k, up_k, s.sizes, height=m)
+        projected = rows_mx(x_k, up_k, s.sizes, height=m, exact=exact)
     else:
-        projected = ragged_dot_bf16(z[tokens], up2, s.sizes)
+        projected = ragged_dot_bf16(z[tokens], up2, s.sizes, exact=exact)
     if up_bias is not None:
         projected = add_expert_bias(projected, up_bias, s.sizes)
     act_weights = row_weights if norm is None else bf16.to_bf16(np.ones(m, np.float32))
     h = weighted_units(ffn, projected.reshape(m, f, p), act_weights)
     if fprop or wgrad:
         h_k, h_m = mxfp8.quantized_twice(h, filled, True, height=whole(m))
-    y = rows_mx(h_k, down_k, s.sizes, height=m) if fprop else ragged_dot_bf16(h, down, s.sizes)
+    if fprop:
+        y = rows_mx(h_k, down_k, s.sizes, height=m, exact=exact)
+    else:
+        y = ragged_dot_bf16(h, down, s.sizes, exact=exact)
     y_rows = None
     if norm is not None:
         y_rows = y
         y = expert_norm_forward(norm, y_rows, s.sizes, row_weights, norm_scale, norm_bias, down_bias)
-    out = sum_by_token(y, s.inverse.reshape(t, k))
+    out = sum_by_token(y, s.inverse.reshape(t, k), exact=exact)
     if down_bias is not None and norm is None:
         b = weighted_bias_rows(down_bias, s.sizes, row_weights, m)
-        bsum = sum_by_token(b, s.inverse.reshape(t, k))
+        bsum = sum_by_token(b, s.inverse.reshape(t, k), exact=exact)
         out = bf16.to_bf16(bf16.to_f32(out) + bf16.to_f32(bsum))
     return out, Saved(s, row_weights, projected, h, x_m, up_n, h_m, down_n, (fprop, dgrad, wgrad),
                       y_rows)
@@ -556,14 +591,14 @@ def layer_backward(
     k: int, ffn: Ffn = Ffn(), fmt: str = "mxfp8",
     up_bias: np.ndarray | None = None, down_bias: np.ndarray | None = None,
     norm: Norm | None = None, norm_scale: np.ndarray | None = None,
-    norm_bias: np.ndarray | None = None,
+    norm_bias: np.ndarray | None = None, exact: bool = False,
 ) -> dict[str, np.ndarray]:
     """Return the gradients of `layer_forward`'s output, dy (t, d) bfloat16 bits, to
     z, the weights, up and down (bfloat16 bits), to the biases (float64 sums), and
     between the GEMMs "dh" (m, f) and "dp" (m, p f) (bfloat16 bits):
     grouped_blockscaled._backward (:191-211) for each GEMM, weighted_units' VJP between
     them, and the gathers' and biases' VJPs (moe.py:857-870,1018-1021,1060-1063). The
-    passes are the forward's."""
+    passes are the forward's; `exact` as `layer_forward`'s."""
     s = saved.sorted
     t = dy.shape[0]
     e, d, f, p = up.shape
@@ -587,13 +622,14 @@ def layer_backward(
             dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens, height=whole(m))
         dy_rows = dy[tokens]
     if dgrad:
-        dh = rows_mx(dy_n, saved.down_n, s.sizes, height=m)
+        dh = rows_mx(dy_n, saved.down_n, s.sizes, height=m, exact=exact)
     else:
-        dh = ragged_dot_bf16(dy_rows, np.ascontiguousarray(np.swapaxes(down, 1, 2)), s.sizes)
+        dh = ragged_dot_bf16(dy_rows, np.ascontiguousarray(np.swapaxes(down, 1, 2)), s.sizes,
+                             exact=exact)
     if wgrad:
-        d_down = contract_mx(saved.h_m, dy_m, s.sizes)
+        d_down = contract_mx(saved.h_m, dy_m, s.sizes, exact=exact)
     else:
-        d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes)
+        d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes, exact=exact)
     act_weights = saved.row_weights if norm is None else bf16.to_bf16(np.ones(m, np.float32))
     dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), act_weights, dh)
     if norm is not None:
@@ -602,13 +638,14 @@ def layer_backward(
     if dgrad or wgrad:
         dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True, height=whole(m))
     if dgrad:
-        dx = rows_mx(dp_n, saved.up_n, s.sizes, height=m)
+        dx = rows_mx(dp_n, saved.up_n, s.sizes, height=m, exact=exact)
     else:
-        dx = ragged_dot_bf16(dp, np.ascontiguousarray(np.swapaxes(up2, 1, 2)), s.sizes)
+        dx = ragged_dot_bf16(dp, np.ascontiguousarray(np.swapaxes(up2, 1, 2)), s.sizes,
+                             exact=exact)
     if wgrad:
-        d_up = contract_mx(saved.x_m, dp_m, s.sizes)
+        d_up = contract_mx(saved.x_m, dp_m, s.sizes, exact=exact)
     else:
-        d_up = weight_grad_bf16(z[tokens], dp, s.sizes)
+        d_up = weight_grad_bf16(z[tokens], dp, s.sizes, exact=exact)
     if up_bias is not None:
         grads["up_bias"] = expert_sums(bf16.to_f32(dp), s.sizes).reshape(e, f, p)
     if down_bias is not None and norm is None:
@@ -621,7 +658,7 @@ def layer_backward(
         grads["down_bias"] = expert_sums(np.where(live, bf16.round_f32(g * w), 0), s.sizes)
         extra = bf16.round_f32(bf16.round_f32(g * b_rows).sum(-1, dtype=np.float32))
         d_rows_w = bf16.to_bf16(bf16.to_f32(d_rows_w) + extra)
-    dz = sum_by_token(dx, s.inverse.reshape(t, k))
+    dz = sum_by_token(dx, s.inverse.reshape(t, k), exact=exact)
     d_weights = d_rows_w[s.inverse].reshape(t, k)
     grads.update(z=dz, weights=d_weights, up=d_up.reshape(e, d, f, p), down=d_down, dh=dh, dp=dp)
     return grads

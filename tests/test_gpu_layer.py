@@ -396,3 +396,61 @@ without this account of its cause)."""
         assert c["codes"] <= CODE_SHARE * c["of"], (what, c)
     for key, err in errs.items():
         assert err <= END_TO_END_ATTRIBUTED, (key, err)
+
+
+# The GPU layer's distance from the exact layer (oracle.moe with exact sums: float64,
+# rounded once), against the two float implementations it is measured beside: the
+# oracle's float32 order lands far inside 1e-3 of the exact layer, and the exact layer
+# with each GEMM perturbed by noise of the size of the GPU GEMM's own error (measured
+# here, float32 out on the same operands, against float64 sums: ~1.5e-5 relative, left
+# inside each block-scaled MFMA instruction) lands where the GPU does. The 1e-3 bar of
+# the north star holds for a GEMM on identical inputs and for an IEEE float32 order end
+# to end; no layer built on this instruction can hold it end to end (tests/test_exact.py
+# shows the same on the CPU).
+@pytest.mark.parametrize("name,t,k,e,d,f,act", [
+    ("small", 1024, 4, 16, 256, 256, "swiglu"), ("gptoss_like", 256, 4, 8, 1440, 1440, "clamped")])
+def test_the_gpu_layers_drift_from_the_exact_layer_is_the_mfmas(lib, monkeypatch, name, t, k, e, d,
+                                                               f, act):
+    from bux_amd import grouped_mxfp8 as gm
+    from bux_amd import moe
+    from oracle import mxfp8 as omx
+    from tests.test_exact import rel as rel_bits, run_layer, with_gemm_noise
+    o, g = _ffn(act)
+    rng = np.random.default_rng(47)
+    z, idx, w, up, down, dy = _inputs(rng, t, k, e, d, f, None)
+    announce("layer vs exact", name)
+    gz, gidx, gw, gup, gdown, gdy = (to_gpu_bf16(z), to_gpu(idx), to_gpu_bf16(w), to_gpu_bf16(up),
+                                      to_gpu_bf16(down), to_gpu_bf16(dy))
+    out, saved = moe.experts_forward(gz, gidx, gw, gup, gdown, g)
+    grads = moe.experts_backward(saved, gdy, gup, gdown, g)
+    # the up GEMM's own error: float32 out on the layer's operands, against float64 sums
+    m, hp = t * k, -(-(t * k) // 128) * 128
+    x_k, _ = gm.quantized_twice(gz, saved.sorted.filled, False, saved.sorted.order, k, hp)
+    _, up_k = gm.quantized_twice(gup.reshape(e, d, 2 * f))
+    y32 = gm.rows(x_k, up_k, saved.sorted.sizes, torch.float32, height=m)
+    torch.cuda.synchronize()
+    gpu = {"y": bf16_bits(out), **{key: bf16_bits(grads[key]) for key in ("z", "weights", "up", "down")}}
+    args = (z, idx, w, up, down, dy)
+    exact = run_layer(*args, exact=True, ffn=o)
+    f32 = run_layer(*args, exact=False, ffn=o)
+    s = omoe.sort_by_expert(idx, e)
+    filled = int(s.sizes.sum())
+    ox_k, _ = omx.quantized_twice(z, filled, True, index=s.order // k, height=hp)
+    _, oup_k = omx.quantized_twice(up.reshape(e, d, 2 * f), d)
+    y64 = omoe.rows_mx(ox_k, oup_k, s.sizes, out="f64", height=m, exact=True)
+    sigma = float(np.linalg.norm(y32.cpu().numpy().astype(np.float64) - y64) / np.linalg.norm(y64))
+    with_gemm_noise(monkeypatch, sigma, seed=7)
+    model = run_layer(*args, exact=True, ffn=o)
+    monkeypatch.undo()
+    errs = {key: (rel_bits(gpu[key], exact[key]), rel_bits(f32[key], exact[key]),
+                  rel_bits(model[key], exact[key])) for key in exact}
+    print(f"[exact] {name} gemm error {sigma:.2e}; vs exact (gpu, float32 order, exact + gemm-sized "
+          "noise): " + " ".join(f"{key}=({a:.2e}, {b:.2e}, {c:.2e})" for key, (a, b, c) in errs.items()),
+          flush=True)
+    # measured on the MI355X: the GEMM's error 1.45e-5 at both shapes; the GPU layer
+    # 1.1e-3 to 2.2e-3 from the exact one, the noise model 1.0e-3 to 2.2e-3 (the GPU at
+    # most 1.14x the model), the float32 order at most 3.8e-4 (y at gptoss_like)
+    assert sigma <= 5e-5
+    for key, (a, b, c) in errs.items():
+        assert b <= 5e-4, (key, b)
+        assert a <= 1.5 * c, (key, a, c)
