@@ -61,8 +61,8 @@ constexpr int LOADS_A_STEP = 10;  // direct loads a wave issues a step
 
 // An operand in the tiled layout: row r's byte k at values[((k / 64) rows + r) 64 +
 // k % 64], the scale byte of its block b (of 32) at scales[((b / 4) rows + r) 4 + b % 4].
-// Sizes are 32-bit: the host checks that an operand's bytes fit (and the kernels'
-// buffer offsets with them).
+// Its bytes may pass 4 GiB: the loads address one K chunk at a time (chunk_at), so only
+// a chunk's rows x 64 bytes must fit 32 bits (the host checks the rows).
 struct Operand {
   const uint8_t* values;
   const uint8_t* scales;
@@ -95,19 +95,42 @@ __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 // the 16-byte chunk that belongs in its swizzled place) and the scale words of those
 // rows. Slices are 1 KiB apart in memory and in LDS alike (rows 16 apart share a
 // swizzle), so one lane offset serves them all, the scalar offset adding 1 KiB a slice.
-// Rows past the operand read whatever follows (0 past its end); their outputs are never
-// stored.
+// Rows past the operand read 0 (or, in a narrow operand's chunk, the next chunk's rows);
+// their outputs are never stored.
 struct Loads {
-  i32x4 values, scales;
+  const uint8_t* values;              // the operand's codes and scale words
+  const uint8_t* scales;
+  i32x4 rv, rs;                       // resources over the whole operand (narrow)
   int32_t voff, soff;                 // this lane's
-  int32_t chunk_stride, word_stride;  // bytes from a K chunk (64 / 128 bytes) to the next
+  int32_t chunk_stride, word_stride;  // a K chunk's bytes (64 / 128 bytes of K): rows x 64, rows x 4
 };
+
+// The buffer resource of K chunk c of an operand and the scalar offset into it: a wide
+// operand's (W) base moves a chunk at a time in 64 bits and the resource holds that
+// chunk's rows alone, so that no offset passes 32 bits whatever the operand's size (a
+// resource over the whole operand holds at most 4 GiB, and a scalar offset of c x
+// stride 2 GiB); a narrow one (under 2 GiB with a tile's reads past its rows) takes
+// its one resource and the offset c x stride, which costs the K loop no scalar
+// arithmetic (wide: 3% slower at c3).
+template <bool W>
+__device__ __forceinline__ i32x4 chunk_at(const uint8_t* base, const i32x4& whole, int32_t c,
+                                          int32_t stride, int32_t& soff) {
+  if constexpr (W) {
+    soff = 0;
+    return resource(base + static_cast<int64_t>(c) * stride, stride);
+  } else {
+    soff = c * stride;
+    return whole;
+  }
+}
 
 __device__ __forceinline__ Loads loads_for(const Operand& op, int32_t row0) {
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   Loads ld;
-  ld.values = resource(op.values, static_cast<int64_t>(op.k) * op.rows);
-  ld.scales = resource(op.scales, static_cast<int64_t>(op.k / 32) * op.rows);
+  ld.values = op.values;
+  ld.scales = op.scales;
+  ld.rv = resource(op.values, static_cast<int64_t>(op.k) * op.rows);
+  ld.rs = resource(op.scales, static_cast<int64_t>(op.k / 32) * op.rows);
   const int r = w * 64 + (l >> 2);
   ld.voff = (row0 + r) * 64 + 16 * ((l & 3) ^ swizzle(r));
   ld.soff = (row0 + w * 64 + l) * 4;
@@ -122,7 +145,7 @@ __device__ __forceinline__ Loads loads_for(const Operand& op, int32_t row0) {
 // waves loads its A scale words again in their place (4 bytes a lane, the same bytes to
 // the same place as load 8), so that every wave issues 10 loads a step whatever the
 // tile, and the waits count them alike.
-template <int Q, bool H>
+template <int Q, bool H, bool W>
 __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int32_t ks,
                                           uint32_t lds0, int st) {
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -130,31 +153,41 @@ __device__ __forceinline__ void issue_one(const Loads& la, const Loads& lb, int3
   if (Q < 8) {
     constexpr int i = Q >> 1;
     const uint32_t slice = w * 4096 + i * 1024;
-    if ((Q & 1) == 0 && H && w >= 2)
-      load_lds4(la.scales, at + offsetof(Stage, as) + w * 256, la.soff, (ks >> 1) * la.word_stride);
-    else if ((Q & 1) == 0)
-      load_lds16(la.values, at + offsetof(Stage, a) + slice, la.voff, ks * la.chunk_stride + i * 1024);
-    else
-      load_lds16(lb.values, at + offsetof(Stage, b) + slice, lb.voff, ks * lb.chunk_stride + i * 1024);
+    int32_t so;
+    if ((Q & 1) == 0 && H && w >= 2) {
+      const i32x4 r = chunk_at<W>(la.scales, la.rs, ks >> 1, la.word_stride, so);
+      load_lds4(r, at + offsetof(Stage, as) + w * 256, la.soff, so);
+    } else if ((Q & 1) == 0) {
+      const i32x4 r = chunk_at<W>(la.values, la.rv, ks, la.chunk_stride, so);
+      load_lds16(r, at + offsetof(Stage, a) + slice, la.voff, so + i * 1024);
+    } else {
+      const i32x4 r = chunk_at<W>(lb.values, lb.rv, ks, lb.chunk_stride, so);
+      load_lds16(r, at + offsetof(Stage, b) + slice, lb.voff, so + i * 1024);
+    }
   } else if (Q == 8) {
-    load_lds4(la.scales, at + offsetof(Stage, as) + w * 256, la.soff, (ks >> 1) * la.word_stride);
+    int32_t so;
+    const i32x4 r = chunk_at<W>(la.scales, la.rs, ks >> 1, la.word_stride, so);
+    load_lds4(r, at + offsetof(Stage, as) + w * 256, la.soff, so);
   } else {
-    load_lds4(lb.scales, at + offsetof(Stage, bs) + w * 256, lb.soff, (ks >> 1) * lb.word_stride);
+    int32_t so;
+    const i32x4 r = chunk_at<W>(lb.scales, lb.rs, ks >> 1, lb.word_stride, so);
+    load_lds4(r, at + offsetof(Stage, bs) + w * 256, lb.soff, so);
   }
 }
 
-template <int Q, bool H>
+template <int Q, bool H, bool W>
 __device__ __forceinline__ void issue_from(const Loads& la, const Loads& lb, int32_t ks,
                                            uint32_t lds0, int st) {
-  issue_one<Q, H>(la, lb, ks, lds0, st);
-  if constexpr (Q + 1 < LOADS_A_STEP) issue_from<Q + 1, H>(la, lb, ks, lds0, st);
+  issue_one<Q, H, W>(la, lb, ks, lds0, st);
+  if constexpr (Q + 1 < LOADS_A_STEP) issue_from<Q + 1, H, W>(la, lb, ks, lds0, st);
 }
 
 // All of a wave's direct loads of K step ks into stage `st`, of a whole or a half tile.
+template <bool W>
 __device__ __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks, uint32_t lds0,
                                       int st, bool half) {
-  if (half) issue_from<0, true>(la, lb, ks, lds0, st);
-  else issue_from<0, false>(la, lb, ks, lds0, st);
+  if (half) issue_from<0, true, W>(la, lb, ks, lds0, st);
+  else issue_from<0, false, W>(la, lb, ks, lds0, st);
 }
 
 // Waits until at most `steps` steps' loads of this wave are in flight. A wave's loads
@@ -258,7 +291,7 @@ __device__ __forceinline__ void read_frag(Frag& f, const Lds& lds, const Lanes& 
 // MFMAs apart), so that each lands a dozen MFMAs before its first use. The MFMA goes
 // first: a load that waits to issue (the memory pipe full) then waits while the MFMA
 // runs, rather than holding the MFMA back.
-template <bool LOAD, bool READ>
+template <bool LOAD, bool READ, bool W>
 __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la, const Loads& lb,
                                      const Lds& lds, uint32_t lds0, const Lanes& ln,
                                      int32_t ks_load, int st_load, int32_t ks_next, int st_next,
@@ -271,16 +304,16 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
     __builtin_amdgcn_sched_barrier(0);
     if (LOAD) {
       switch (q) {
-        case 0: issue_one<0, false>(la, lb, ks_load, lds0, st_load); break;
-        case 1: issue_one<1, false>(la, lb, ks_load, lds0, st_load); break;
-        case 2: issue_one<2, false>(la, lb, ks_load, lds0, st_load); break;
-        case 3: issue_one<3, false>(la, lb, ks_load, lds0, st_load); break;
-        case 4: issue_one<4, false>(la, lb, ks_load, lds0, st_load); break;
-        case 5: issue_one<5, false>(la, lb, ks_load, lds0, st_load); break;
-        case 6: issue_one<6, false>(la, lb, ks_load, lds0, st_load); break;
-        case 7: issue_one<7, false>(la, lb, ks_load, lds0, st_load); break;
-        case 8: issue_one<8, false>(la, lb, ks_load, lds0, st_load); break;
-        case 9: issue_one<9, false>(la, lb, ks_load, lds0, st_load); break;
+        case 0: issue_one<0, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 1: issue_one<1, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 2: issue_one<2, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 3: issue_one<3, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 4: issue_one<4, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 5: issue_one<5, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 6: issue_one<6, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 7: issue_one<7, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 8: issue_one<8, false, W>(la, lb, ks_load, lds0, st_load); break;
+        case 9: issue_one<9, false, W>(la, lb, ks_load, lds0, st_load); break;
         default: break;
       }
     }
@@ -297,7 +330,7 @@ __device__ __forceinline__ void step(const Frag& cur, Frag& nxt, const Loads& la
 // q / 2 and B's block q % 2), with the same 10 loads (one after each of the first 7
 // MFMAs, three after the last) and the next step's 6 blocks read in the order its
 // MFMAs take them (a0 b0, b1, a1, a2, a3).
-template <bool LOAD, bool READ>
+template <bool LOAD, bool READ, bool W>
 __device__ __forceinline__ void step_half(const Frag& cur, Frag& nxt, const Loads& la,
                                           const Loads& lb, const Lds& lds, uint32_t lds0,
                                           const Lanes& ln, int32_t ks_load, int st_load,
@@ -310,17 +343,17 @@ __device__ __forceinline__ void step_half(const Frag& cur, Frag& nxt, const Load
     __builtin_amdgcn_sched_barrier(0);
     if (LOAD) {
       switch (q) {
-        case 0: issue_one<0, true>(la, lb, ks_load, lds0, st_load); break;
-        case 1: issue_one<1, true>(la, lb, ks_load, lds0, st_load); break;
-        case 2: issue_one<2, true>(la, lb, ks_load, lds0, st_load); break;
-        case 3: issue_one<3, true>(la, lb, ks_load, lds0, st_load); break;
-        case 4: issue_one<4, true>(la, lb, ks_load, lds0, st_load); break;
-        case 5: issue_one<5, true>(la, lb, ks_load, lds0, st_load); break;
-        case 6: issue_one<6, true>(la, lb, ks_load, lds0, st_load); break;
+        case 0: issue_one<0, true, W>(la, lb, ks_load, lds0, st_load); break;
+        case 1: issue_one<1, true, W>(la, lb, ks_load, lds0, st_load); break;
+        case 2: issue_one<2, true, W>(la, lb, ks_load, lds0, st_load); break;
+        case 3: issue_one<3, true, W>(la, lb, ks_load, lds0, st_load); break;
+        case 4: issue_one<4, true, W>(la, lb, ks_load, lds0, st_load); break;
+        case 5: issue_one<5, true, W>(la, lb, ks_load, lds0, st_load); break;
+        case 6: issue_one<6, true, W>(la, lb, ks_load, lds0, st_load); break;
         default:
-          issue_one<7, true>(la, lb, ks_load, lds0, st_load);
-          issue_one<8, true>(la, lb, ks_load, lds0, st_load);
-          issue_one<9, true>(la, lb, ks_load, lds0, st_load);
+          issue_one<7, true, W>(la, lb, ks_load, lds0, st_load);
+          issue_one<8, true, W>(la, lb, ks_load, lds0, st_load);
+          issue_one<9, true, W>(la, lb, ks_load, lds0, st_load);
           break;
       }
     }
@@ -550,8 +583,10 @@ __device__ __forceinline__ Operand group_of(const Operand& B, int32_t group) {
   return b;
 }
 
-// The MXFP8 format's part of the shared pipeline (run_tiles).
-struct Mx {
+// The MXFP8 format's part of the shared pipeline (run_tiles); W: operands wide enough
+// that the loads address them a K chunk at a time (chunk_at).
+template <bool W>
+struct MxOf {
   using Operand = bux::Operand;
   using Lds = bux::Lds;
   using Loads = bux::Loads;
@@ -566,7 +601,7 @@ struct Mx {
   }
   __device__ static __forceinline__ void issue(const Loads& la, const Loads& lb, int32_t ks,
                                                uint32_t lds0, int st, bool half) {
-    bux::issue(la, lb, ks, lds0, st, half);
+    bux::issue<W>(la, lb, ks, lds0, st, half);
   }
   __device__ static __forceinline__ void wait_loads(int32_t steps) { bux::wait_loads(steps); }
   template <bool H>
@@ -585,15 +620,16 @@ struct Mx {
                                               const Lanes& ln, int32_t ks_load, int st_load,
                                               int32_t ks_next, int st_next, v16f acc[4][4]) {
     if constexpr (H)
-      bux::step_half<LOAD, READ>(cur, nxt, la, lb, lds, lds0, ln, ks_load, st_load, ks_next,
+      bux::step_half<LOAD, READ, W>(cur, nxt, la, lb, lds, lds0, ln, ks_load, st_load, ks_next,
                                  st_next, acc);
     else
-      bux::step<LOAD, READ>(cur, nxt, la, lb, lds, lds0, ln, ks_load, st_load, ks_next, st_next, acc);
+      bux::step<LOAD, READ, W>(cur, nxt, la, lb, lds, lds0, ln, ks_load, st_load, ks_next, st_next, acc);
   }
 };
+using Mx = MxOf<false>;
 
 // The kernels: one workgroup a CU.
-template <typename T>
+template <typename T, bool W>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_kernel(
     Operand A, Operand B, int32_t groups, int32_t n, int32_t height,
     const int32_t* __restrict__ starts, const Tile* __restrict__ tiles, int32_t col_tiles,
@@ -603,11 +639,11 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const RowsTiles<false, true> list{tiles, groups, n, height, col_tiles, A.k / BK, A.k};
   const int32_t count = starts[groups + 1] * col_tiles;
-  run_tiles<Mx>(list, count, A, B, lds, Plain<T>{y, n});
+  run_tiles<MxOf<W>>(list, count, A, B, lds, Plain<T>{y, n});
 }
 
 // rows_kernel with each group's rows of a from a_starts[g] (the reference's `starts`).
-template <typename T>
+template <typename T, bool W>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void rows_started_kernel(
     Operand A, Operand B, int32_t groups, int32_t n, int32_t height,
     const int32_t* __restrict__ starts, const int32_t* __restrict__ a_starts,
@@ -617,10 +653,10 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const StartedTiles<true> list{tiles, starts, a_starts, groups, n, height, col_tiles, A.k / BK};
   const int32_t count = starts[groups + 1] * col_tiles;
-  run_tiles<Mx>(list, count, A, B, lds, Plain<T>{y, n});
+  run_tiles<MxOf<W>>(list, count, A, B, lds, Plain<T>{y, n});
 }
 
-template <typename T>
+template <typename T, bool W>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1))) void contract_kernel(
     Operand A, Operand B, int32_t groups, const int32_t* __restrict__ starts, int32_t d_tiles,
     int32_t f_tiles, T* __restrict__ dw) {
@@ -629,56 +665,69 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   Lds& lds = *reinterpret_cast<Lds*>(smem);
   const ContractTiles list{starts, A.rows, B.rows, d_tiles, f_tiles, BK};
   const int32_t count = groups * d_tiles * f_tiles;
-  run_tiles<Mx>(list, count, A, B, lds, Plain<T>{dw, B.rows});
+  run_tiles<MxOf<W>>(list, count, A, B, lds, Plain<T>{dw, B.rows});
 }
 
-template <typename T>
+// Whether an operand of `rows` rows fits the loads' 32-bit offsets within a K chunk
+// (a tile's reads past its rows included): rows x 64 bytes, whatever its K.
+constexpr int64_t MAX_ROWS = (1LL << 31) / BK - BM;  // 33,554,176
+bool rows_fit(int64_t rows) { return rows <= MAX_ROWS; }
+// Whether an operand of `rows` rows of `k` bytes of K (and a tile's reads past its rows)
+// fits one buffer resource and 32-bit offsets (MxOf<false>); wider ones go a K chunk at
+// a time (MxOf<true>).
+bool narrow(int64_t rows, int64_t k) { return (rows + BM) * k < (1LL << 31); }
+
+template <typename T, bool W = false>
 int launch_rows(const Operand& A, const Operand& B, int32_t groups, int64_t n, int64_t height,
                 const int32_t* starts, const Tile* tiles, int64_t slots, void* y, hipStream_t s) {
+  if (!W && !(narrow(A.rows, A.k) && narrow(B.rows, B.k)))
+    return launch_rows<T, true>(A, B, groups, n, height, starts, tiles, slots, y, s);
   const int64_t col_tiles = ceil_div(n, BN);
   if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_rows: too many tiles");
   unsigned blocks = 0;
   if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
-  if (int rc = allow_lds(rows_kernel<T>, sizeof(Lds), "rows_kernel")) return rc;
-  hipLaunchKernelGGL(rows_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+  if (int rc = allow_lds(rows_kernel<T, W>, sizeof(Lds), "rows_kernel")) return rc;
+  hipLaunchKernelGGL((rows_kernel<T, W>), dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
                      static_cast<int32_t>(n), static_cast<int32_t>(height), starts, tiles,
                      static_cast<int32_t>(col_tiles), static_cast<T*>(y));
   return launched("rows_kernel");
 }
 
-template <typename T>
+template <typename T, bool W = false>
 int launch_rows_started(const Operand& A, const Operand& B, int32_t groups, int64_t n,
                         int64_t height, const int32_t* starts, const int32_t* a_starts,
                         const Tile* tiles, int64_t slots, void* y, hipStream_t s) {
+  if (!W && !(narrow(A.rows, A.k) && narrow(B.rows, B.k)))
+    return launch_rows_started<T, true>(A, B, groups, n, height, starts, a_starts, tiles, slots,
+                                        y, s);
   const int64_t col_tiles = ceil_div(n, BN);
   if (slots * col_tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_rows_started: too many tiles");
   unsigned blocks = 0;
   if (int rc = grid_for(slots * col_tiles, &blocks)) return rc;
-  if (int rc = allow_lds(rows_started_kernel<T>, sizeof(Lds), "rows_started_kernel")) return rc;
-  hipLaunchKernelGGL(rows_started_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B,
+  if (int rc = allow_lds(rows_started_kernel<T, W>, sizeof(Lds), "rows_started_kernel")) return rc;
+  hipLaunchKernelGGL((rows_started_kernel<T, W>), dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B,
                      groups, static_cast<int32_t>(n), static_cast<int32_t>(height), starts,
                      a_starts, tiles, static_cast<int32_t>(col_tiles), static_cast<T*>(y));
   return launched("rows_started_kernel");
 }
 
-template <typename T>
+template <typename T, bool W = false>
 int launch_contract(const Operand& A, const Operand& B, int32_t groups, const int32_t* starts,
                     void* dw, hipStream_t s) {
+  if (!W && !(narrow(A.rows, A.k) && narrow(B.rows, B.k)))
+    return launch_contract<T, true>(A, B, groups, starts, dw, s);
   const int64_t d_tiles = ceil_div(A.rows, BM), f_tiles = ceil_div(B.rows, BN);
   const int64_t tiles = static_cast<int64_t>(groups) * d_tiles * f_tiles;
   if (tiles >= (1LL << 31)) return fail(BUX_E_ARGUMENT, "bux_mx_grouped_contract: too many tiles");
   unsigned blocks = 0;
   if (int rc = grid_for(tiles, &blocks)) return rc;
-  if (int rc = allow_lds(contract_kernel<T>, sizeof(Lds), "contract_kernel")) return rc;
-  hipLaunchKernelGGL(contract_kernel<T>, dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
+  if (int rc = allow_lds(contract_kernel<T, W>, sizeof(Lds), "contract_kernel")) return rc;
+  hipLaunchKernelGGL((contract_kernel<T, W>), dim3(blocks), dim3(THREADS), sizeof(Lds), s, A, B, groups,
                      starts, static_cast<int32_t>(d_tiles), static_cast<int32_t>(f_tiles),
                      static_cast<T*>(dw));
   return launched("contract_kernel");
 }
 
-// Whether an operand of `rows` rows of `k` bytes (and a tile's reads past it) fits the
-// kernels' 32-bit buffer offsets.
-bool offsets_fit(int64_t rows, int64_t k) { return (rows + BM) * k < (1LL << 31); }
 
 // --- the fused activation: the up GEMM's tiles straight to h in MXFP8 ---------------
 //
@@ -1278,8 +1327,8 @@ int check_rows(const char* name, const uint8_t* a_values, const uint8_t* a_scale
   BUX_CHECK(k % 128 == 0, "%s: k=%lld is not a multiple of 128 (the tiled layout's padded K)",
             name, (long long)k);
   BUX_CHECK(n % 4 == 0, "%s: n=%lld is not a multiple of 4", name, (long long)n);
-  BUX_CHECK(offsets_fit(m, k) && offsets_fit(n, k), "%s: an operand of %lld x %lld bytes exceeds 2 GiB",
-            name, (long long)(m > n ? m : n), (long long)k);
+  BUX_CHECK(rows_fit(m) && rows_fit(n), "%s: an operand of %lld rows exceeds %lld", name,
+            (long long)(m > n ? m : n), (long long)MAX_ROWS);
   BUX_CHECK(out_dtype == BUX_BF16 || out_dtype == BUX_F32, "%s: out_dtype=%d", name, out_dtype);
   BUX_CHECK(b_values && b_scales && y && (m == 0 || (a_values && a_scales)), "%s: NULL buffer",
             name);
@@ -1291,12 +1340,12 @@ int check_contract(const char* name, const uint8_t* a_values, const uint8_t* a_s
                    int64_t f, int64_t m, int out_dtype, const void* dw) {
   BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS, "%s: groups=%d outside [1, %d]", name, groups,
             MAX_GROUPS);
-  BUX_CHECK(d > 0 && f > 0 && m >= 0, "%s: bad shape d=%lld f=%lld m=%lld", name, (long long)d,
-            (long long)f, (long long)m);
+  BUX_CHECK(d > 0 && f > 0 && m >= 0 && m < (1LL << 31), "%s: bad shape d=%lld f=%lld m=%lld",
+            name, (long long)d, (long long)f, (long long)m);
   BUX_CHECK(m % 128 == 0, "%s: m=%lld is not a multiple of 128", name, (long long)m);
   BUX_CHECK(f % 4 == 0, "%s: f=%lld is not a multiple of 4", name, (long long)f);
-  BUX_CHECK(offsets_fit(d, m) && offsets_fit(f, m), "%s: an operand of %lld x %lld bytes exceeds 2 GiB",
-            name, (long long)(d > f ? d : f), (long long)m);
+  BUX_CHECK(rows_fit(d) && rows_fit(f), "%s: an operand of %lld rows exceeds %lld", name,
+            (long long)(d > f ? d : f), (long long)MAX_ROWS);
   BUX_CHECK(out_dtype == BUX_BF16 || out_dtype == BUX_F32, "%s: out_dtype=%d", name, out_dtype);
   BUX_CHECK(dw && (m == 0 || (a_values && a_scales && b_values && b_scales)), "%s: NULL buffer",
             name);
@@ -1576,7 +1625,7 @@ extern "C" int bux_mx_grouped_glu(const uint8_t* a_values, const uint8_t* a_scal
             "bux_mx_grouped_glu: bad shape height=%lld n=%lld k=%lld rows=%lld (height a "
             "multiple of 128, n of 64, k of 128, rows at most height)",
             (long long)height, (long long)n, (long long)k, (long long)rows);
-  BUX_CHECK(offsets_fit(height, k) && offsets_fit(n, k),
+  BUX_CHECK(narrow(height, k) && narrow(n, k),
             "bux_mx_grouped_glu: an operand of %lld x %lld bytes exceeds 2 GiB",
             (long long)(height > n ? height : n), (long long)k);
   Act act;
@@ -1669,7 +1718,7 @@ extern "C" int bux_mx_grouped_dglu(const uint8_t* a_values, const uint8_t* a_sca
             "bux_mx_grouped_dglu: bad shape height=%lld f=%lld k=%lld rows=%lld (height a "
             "multiple of 128, f of 32, k of 128, rows at most height)",
             (long long)height, (long long)f, (long long)k, (long long)rows);
-  BUX_CHECK(offsets_fit(height, k) && offsets_fit(f, k),
+  BUX_CHECK(narrow(height, k) && narrow(f, k),
             "bux_mx_grouped_dglu: an operand of %lld x %lld bytes exceeds 2 GiB",
             (long long)(height > f ? height : f), (long long)k);
   Act act;

@@ -134,6 +134,9 @@ int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, 
  *           from sum(sizes) to height are 0. Any height: a's quantized copy may be
  *           padded past the height of y (e.g. to whole tiles) and rows of the groups
  *           past height are not stored. n must be a multiple of 4.
+ * Sizes: m, n and height up to 33,554,176 rows (a K chunk's rows x 64 bytes within 2 GiB);
+ * an operand's bytes have no cap (past 2 GiB the kernel loads it one K chunk at a time
+ * from a 64-bit base).
  */
 enum { BUX_BF16 = 0, BUX_F32 = 1 };
 size_t bux_mx_grouped_rows_workspace_size(int32_t groups, int64_t m, int64_t height);
@@ -215,6 +218,8 @@ int bux_mx_grouped_rows_noalloc(const uint8_t* a_values, const uint8_t* a_scales
  * sizes     device int32 [groups]; sum(sizes) <= m; m a multiple of 128.
  * dw        [groups, d, f], bfloat16 or float32 (out_dtype); 0 for an empty group.
  *           f must be a multiple of 4.
+ * Sizes: d and f up to 33,554,176 rows, m below 2^31; an operand's bytes have no cap, as
+ * for bux_mx_grouped_rows.
  */
 size_t bux_mx_grouped_contract_workspace_size(int32_t groups);
 int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a_scales,

@@ -93,6 +93,12 @@ def test_gemms_reject_bad_shapes_and_small_workspaces(lib):
     assert rc == 1 and "out_dtype" in _msg(lib)
     rc = lib.bux_mx_grouped_contract(p, p, p, p, p, 4, 64, 64, 100, 0, p, p, 1 << 10, None)
     assert rc == 1 and "m=100" in _msg(lib)
+    # an operand's bytes have no cap, its rows do (a K chunk's rows x 64 bytes in 2 GiB)
+    rows = 33_554_177
+    rc = lib.bux_mx_grouped_rows(p, p, p, p, p, 4, rows, 128, 128, rows, 0, p, p, 1 << 40, None)
+    assert rc == 1 and "rows exceeds 33554176" in _msg(lib)
+    rc = lib.bux_mx_grouped_contract(p, p, p, p, p, 4, rows, 64, 128, 0, p, p, 1 << 10, None)
+    assert rc == 1 and "rows exceeds 33554176" in _msg(lib)
     rc = lib.bux_mx_grouped_contract(p, p, p, p, p, 4, 64, 64, 128, 0, p, p, 4, None)
     assert rc == 2 and "workspace" in _msg(lib)
     rc = lib.bux_bf16_grouped_rows(p, p, 0, p, 4, 64, 100, 64, p, p, 1 << 20, None)

@@ -106,3 +106,86 @@ def test_a_permutation_of_the_tokens_permutes_y_and_dz(lib, name):
     assert torch.equal(_bits(out1[perm]), _bits(out2))
     assert torch.equal(_bits(dz1[perm]), _bits(g2["z"]))
     assert torch.equal(_bits(dw1[perm]), _bits(g2["weights"]))
+
+
+# Operands past 4 GiB: the GEMMs load one K chunk at a time from a 64-bit base, so an
+# operand's size is bounded by its rows alone (bux_amd.h). Each group's outputs depend on
+# its own rows and matrix only, so the GEMM over all groups equals, bit for bit, the
+# GEMMs over two runs of whole groups taken apart (each of them under 4 GiB); a sample
+# of rows from the operand's last K chunks is checked against float64 sums.
+def _tiled_codes(lead, chunks, rows, gen):
+    from bux_amd.grouped_mxfp8 import Tiled
+    v = torch.randint(0, 0x70, (*lead, chunks, rows, 64), dtype=torch.uint8, device="cuda",
+                      generator=gen)
+    v |= torch.randint(0, 2, v.shape, dtype=torch.uint8, device="cuda", generator=gen) << 7
+    s = torch.randint(118, 124, (*lead, chunks // 2, rows, 4), dtype=torch.uint8, device="cuda",
+                      generator=gen)
+    return Tiled(v, s)
+
+
+def _rows_of(t, lo, hi):
+    from bux_amd.grouped_mxfp8 import Tiled
+    return Tiled(t.values[..., lo:hi, :].contiguous(), t.scales[..., lo:hi, :].contiguous())
+
+
+def _f64(t):
+    """A Tiled operand's values as float64 (rows, K), on the CPU."""
+    from oracle import mxfp8
+    v = t.values.cpu().numpy()
+    s = t.scales.cpu().numpy()
+    codes = v.transpose(1, 0, 2).reshape(v.shape[1], -1)
+    scales = s.transpose(1, 0, 2).reshape(s.shape[1], -1)
+    return mxfp8.dequantized(mxfp8.Blocks(codes, scales)).astype("float64")
+
+
+def test_a_rows_gemm_over_an_operand_past_4_gib(lib):
+    import numpy as np
+    from bux_amd import grouped_mxfp8 as gm
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    k, n, m = 7168, 256, 1_000_064  # a: 7.2 GB of codes, K chunks 64 MB apart
+    sizes = torch.tensor([200_000, 0, 300_064, 123_456, 376_544], dtype=torch.int32, device="cuda")
+    announce("rows gemm past 4 GiB", m, k)
+    a = _tiled_codes((), k // 64, m, gen)
+    b = _tiled_codes((5,), k // 64, n, gen)
+    y = gm.rows(a, b, sizes, height=m)
+    first = 500_064  # groups 0-2 | 3-4
+    lo = gm.rows(_rows_of(a, 0, first), gm.Tiled(b.values[:3], b.scales[:3]), sizes[:3])
+    hi = gm.rows(_rows_of(a, first, m), gm.Tiled(b.values[3:], b.scales[3:]), sizes[3:])
+    torch.cuda.synchronize()
+    assert torch.equal(y[:first].view(torch.int16), lo.view(torch.int16))
+    assert torch.equal(y[first:].view(torch.int16), hi.view(torch.int16))
+    # the last group's last rows against float64 sums (the bars of the GEMM tests)
+    sample = _rows_of(a, m - 64, m)
+    x = _f64(sample)
+    w = _f64(gm.Tiled(b.values[4].contiguous(), b.scales[4].contiguous()))
+    y32 = gm.rows(a, b, sizes, torch.float32, height=m)[m - 64:].cpu().numpy().astype(np.float64)
+    want = x @ w.T
+    assert np.abs(y32 - want).max() <= 5e-4 * np.abs(want).max()
+
+
+def test_a_contract_gemm_over_an_operand_past_4_gib(lib):
+    import numpy as np
+    from bux_amd import grouped_mxfp8 as gm
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    d, f, m = 256, 256, 20_000_000  # a: x^T, 5.1 GB of codes
+    sizes = torch.tensor([5_000_000, 0, 7_000_000, 7_999_936], dtype=torch.int32, device="cuda")
+    announce("contract gemm past 4 GiB", m)
+    a = _tiled_codes((), m // 64, d, gen)
+    b = _tiled_codes((), m // 64, f, gen)
+    dw = gm.contract(a, b, sizes)
+    first = 12_000_000  # groups 0-2 | 3, a multiple of 128 rows (the K chunks align)
+
+    def part(t, lo, hi):
+        return gm.Tiled(t.values[lo // 64:hi // 64].contiguous(), t.scales[lo // 128:hi // 128].contiguous())
+    lo = gm.contract(part(a, 0, first), part(b, 0, first), sizes[:3])
+    hi = gm.contract(part(a, first, m), part(b, first, m), sizes[3:])
+    torch.cuda.synchronize()
+    assert torch.equal(dw[:3].view(torch.int16), lo.view(torch.int16))
+    assert torch.equal(dw[3:].view(torch.int16), hi.view(torch.int16))
+    # the last group's sum over its last 1024 rows alone, against float64 sums
+    tail = torch.tensor([0, 0, 0, 1024], dtype=torch.int32, device="cuda")
+    start = m - 128 - 1024  # a whole 128 rows (the scale chunks align); past the groups none
+    sub = gm.contract(part(a, start, m), part(b, start, m), tail, torch.float32)[3].cpu().numpy()
+    xa, ya = _f64(part(a, start, start + 1024)), _f64(part(b, start, start + 1024))
+    want = xa @ ya.T
+    assert np.abs(sub.astype(np.float64) - want).max() <= 5e-4 * np.abs(want).max()
