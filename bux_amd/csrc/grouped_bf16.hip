@@ -490,8 +490,9 @@ extern "C" int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, 
     return fail(BUX_E_WORKSPACE, "bux_bf16_grouped_contract: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
   hipStream_t s = as_stream(stream);
+  // the starts capped at the contract's K (m rows), as the rows GEMM caps them at its rows
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
-                     starts_in(workspace), nullptr, header_in(workspace), 0, nullptr);
+                     starts_in(workspace), nullptr, header_in(workspace), m, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   const int64_t d_tiles = ceil_div(k, BM), f_tiles = ceil_div(n, BN);
   const int64_t tiles = static_cast<int64_t>(groups) * d_tiles * f_tiles;

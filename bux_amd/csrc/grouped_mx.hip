@@ -1576,8 +1576,9 @@ extern "C" int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a
     return fail(BUX_E_WORKSPACE, "bux_mx_grouped_contract: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
   hipStream_t s = as_stream(stream);
+  // the starts capped at the contract's K (m rows), as the rows GEMM caps them at its rows
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
-                     starts_in(workspace), nullptr, header_in(workspace), 0, nullptr);
+                     starts_in(workspace), nullptr, header_in(workspace), m, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
   return launch_contract_of(a_values, a_scales, b_values, b_scales, starts_in(workspace), groups,
                             d, f, m,

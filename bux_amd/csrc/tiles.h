@@ -70,7 +70,7 @@ constexpr int32_t LIST_MAGIC = BUX_LIST_MAGIC;  // "BUXT"
 constexpr int32_t LIST_REFUSED = BUX_LIST_REFUSED;
 
 // starts[g] for g <= groups (starts[groups] = sum of sizes; a negative size counts as
-// 0, and with `tiles` the sums stop at max(m, height)), then, if `tiles`, the
+// 0, and the sums stop at max(m, height) where that is positive), then, if `tiles`, the
 // tile list of `slots` entries: each group's rows in tiles of BM from its first row
 // rounded down to a multiple of `align` (a power of two; the last tile partial), then
 // the rows from the sum of sizes to `height` as group `groups`, then empty tiles
@@ -99,12 +99,12 @@ __global__ __launch_bounds__(THREADS) void prologue_kernel(const int32_t* __rest
   __shared__ int64_t partial[THREADS];
   const int t = threadIdx.x;
   // The sizes as the tiles take them: a negative one as 0, and the starts capped at the
-  // rows there are (m or height, whichever is more; unbounded for a list of starts
-  // alone), so that sizes past them give the last groups fewer rows, never a tile
-  // outside the rows or a count that overflows.
+  // rows there are (m or height, whichever is more: the rows GEMM's rows, the contract's
+  // K; unbounded where neither is given), so that sizes past them give the last groups
+  // fewer rows, the same in the rows GEMM and the contract, never a tile outside the
+  // rows or a count that overflows.
   const int64_t rows = m > height ? m : height;
-  const int32_t cap = tiles != nullptr && rows > 0 && rows < INT32_MAX ? static_cast<int32_t>(rows)
-                                                                        : INT32_MAX;
+  const int32_t cap = rows > 0 && rows < INT32_MAX ? static_cast<int32_t>(rows) : INT32_MAX;
   for (int g = t; g < groups; g += THREADS) starts[g] = sizes[g] > 0 ? sizes[g] : 0;
   __syncthreads();
   const int32_t filled = block_scan(starts, groups, partial, cap);

@@ -196,7 +196,10 @@ int bux_mx_grouped_contract_listed(const uint8_t* a_values, const uint8_t* a_sca
  * fails with BUX_E_WORKSPACE (256 KiB: e.g. 1024 groups and 3.5 M rows). Nothing in the
  * array needs clearing (each call's prologue writes all it reads), but every call on a
  * GPU shares that GPU's array: calls that overlap on one GPU (two streams, two host
- * threads) race. Same outputs as bux_mx_grouped_rows, bit for bit.
+ * threads) race. Same outputs as bux_mx_grouped_rows, bit for bit. The array's address
+ * is looked up once per device, on the first call there, and kept for the process:
+ * after a hipDeviceReset (or a reload of the library's code object) that address is
+ * stale, so the entry point must not be used across a device reset.
  */
 enum { BUX_NOALLOC_SCRATCH_BYTES = 262144 };
 int bux_mx_grouped_rows_noalloc(const uint8_t* a_values, const uint8_t* a_scales,

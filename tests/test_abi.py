@@ -291,3 +291,40 @@ def test_every_entry_point_has_an_xla_ffi_handler():
               and n not in ("bux_last_error", "bux_version", "bux_mx_grouped_rows_noalloc")}
     assert wanted <= called, wanted - called
     assert len(re.findall(r"XLA_FFI_DEFINE_HANDLER_SYMBOL\(", src)) == len(wanted)
+
+
+def _calls(text: str, name_re: str) -> dict[str, list[int]]:
+    """Each `name(` in text: the number of its top-level arguments (commas outside
+    nested parentheses, brackets and angle-bracketed template arguments)."""
+    found: dict[str, list[int]] = {}
+    for m in re.finditer(name_re, text):
+        i, depth, args, saw = m.end(), 1, 0, False
+        while depth:
+            c = text[i]
+            if c in "([{<":
+                depth += 1
+            elif c in ")]}>":
+                depth -= 1
+            elif c == "," and depth == 1:
+                args += 1
+            elif not c.isspace():
+                saw = True
+            i += 1
+        found.setdefault(m.group(1), []).append(args + 1 if saw else 0)
+    return found
+
+
+def test_each_xla_ffi_handler_passes_every_argument_the_header_declares():
+    """xla_ffi.cc compiles only where the XLA FFI headers are: the argument count of each
+    of its calls into the library must match the declaration in include/bux_amd.h."""
+    header = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    declared = {n: counts[0] for n, counts in
+                _calls(header, r"\b(?:int|size_t|const char\*)\s+(bux_\w+)\s*\(").items()}
+    src = open(os.path.join(ROOT, "bux_amd", "xla", "xla_ffi.cc")).read()
+    src = re.sub(r"//[^\n]*", "", src).replace("->", ".")
+    calls = _calls(src, r"\b(bux_\w+)\(")
+    calls.pop("bux_last_error", None)
+    assert calls
+    for name, counts in calls.items():
+        assert name in declared, name
+        assert set(counts) == {declared[name]}, (name, counts, declared[name])

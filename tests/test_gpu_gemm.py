@@ -145,6 +145,14 @@ def test_rows_take_a_negative_size_as_none_and_stop_at_the_rows(lib, sizes):
     want = _rows64(a, b, taken, h)
     _close_f32(got, want, f"rows {sizes.tolist()} taken as {taken.tolist()}")
     assert (got[int(taken.sum()):] == 0).all()
+    # the contract takes the same sizes the same way, its K (m) as the rows: the wgrad of
+    # a group agrees with its forward
+    at, bt = _codes(rng, (k, m)), _codes(rng, (128, m))
+    announce("contract with sizes outside the rows", sizes.tolist())
+    dw = grouped_mxfp8.contract(_gpu(at), _gpu(bt), to_gpu(sizes.astype(np.int32)), torch.float32)
+    torch.cuda.synchronize()
+    _close_f32(dw.cpu().numpy(), _contract64(at, bt, taken),
+               f"contract {sizes.tolist()} taken as {taken.tolist()}")
 
 
 CONTRACT_CASES = [
