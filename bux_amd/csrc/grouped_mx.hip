@@ -564,6 +564,63 @@ __device__ void store_tile_half(const v16f acc[4][4], float* tile, int32_t ld, i
   }
 }
 
+// bfloat16 of a tile that stores every row and column (PH: a half tile's 128 rows),
+// through the wave's region of the stage as pairs of 32 x 32 accumulator blocks: a whole
+// tile's wave holds 8 pairs (block row p / 2, its 64 columns from 64 (p % 2)), a half
+// tile's 4 (block row p, the wave's 64 columns). Two buffers of 32 rows 136 bytes apart
+// (128 bytes of a pair's row and 8 of pad: the 32 rows of a lane half start on distinct
+// banks) fill the region; each lane writes its row's 4 runs of 4 columns of both blocks
+// (8 bytes each), reads back 16 bytes of a row, 8 lanes a row (as two 8-byte reads: the
+// rows are 8-byte aligned), and a store writes 8 whole rows of 128 bytes. Pair p + 1 is
+// converted and written while pair p's reads are in flight, and pair p's stores go out
+// after them: the wave's LDS operations run in order, so a read after a write sees it and
+// a write after a read (into the buffer the pair before last used) leaves it alone.
+constexpr int PAIR_PITCH = 136;
+constexpr int PAIR_BUF = 32 * PAIR_PITCH;
+static_assert(2 * PAIR_BUF == 32 * PITCH, "a wave's two pair buffers fill its region of the stage");
+
+template <bool PH>
+__device__ void store_pairs(const v16f acc[4][4], uint16_t* tile, int32_t ld, Stage& stage) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* region = reinterpret_cast<uint8_t*>(&stage) + wave * 2 * PAIR_BUF;
+  uint8_t* mine = region + (lane & 31) * PAIR_PITCH + 8 * (lane >> 5);
+  const uint8_t* from = region + (lane >> 3) * PAIR_PITCH + (lane & 7) * 16;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(tile, 0, 0x7fffffff, 0x00020000);
+  const int32_t lane_off = ((lane >> 3) * ld + 8 * (lane & 7)) * 2;
+  const FromAcc pairs{acc};
+  constexpr int M = PH ? 4 : 8;
+  auto write = [&](int p) {
+    const int i = PH ? p : p >> 1, j0 = PH ? 0 : (p & 1) * 2;
+    uint8_t* at = mine + (p & 1) * PAIR_BUF;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<uint2*>(at + jb * 64 + g * 16) = pairs(i, j0 + jb, g);
+  };
+  write(0);
+#pragma unroll
+  for (int p = 0; p < M; ++p) {
+    const uint8_t* at = from + (p & 1) * PAIR_BUF;
+    uint2 v[8];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      v[2 * it] = *reinterpret_cast<const uint2*>(at + it * 8 * PAIR_PITCH);
+      v[2 * it + 1] = *reinterpret_cast<const uint2*>(at + it * 8 * PAIR_PITCH + 8);
+    }
+    if (p + 1 < M) write(p + 1);
+    const int32_t row0 = PH ? p * 32 : (wave >> 1) * 128 + (p >> 1) * 32;
+    const int32_t col0 = PH ? wave * 64 : (wave & 1) * 128 + (p & 1) * 64;
+    const int32_t corner = (row0 * ld + col0) * 2;
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{v[2 * it].x, v[2 * it].y, v[2 * it + 1].x, v[2 * it + 1].y}, rsrc, lane_off,
+          corner + it * 8 * ld * 2, NT);
+  }
+}
+
 // The plain epilogue: the tile's rows [0, rows) and columns [0, cols) of a row-major
 // output of pitch ld, from its corner.
 template <typename T>
@@ -571,6 +628,13 @@ struct Plain {
   T* out;
   int32_t ld;
   __device__ __forceinline__ void store(const v16f acc[4][4], const Job& j, Stage& stage) const {
+    if constexpr (std::is_same<T, uint16_t>::value) {
+      if (j.cols >= BN && j.rows >= (j.half ? BM / 2 : BM)) {
+        if (j.half) store_pairs<true>(acc, out + j.corner, ld, stage);
+        else store_pairs<false>(acc, out + j.corner, ld, stage);
+        return;
+      }
+    }
     if (j.half) store_tile_half(acc, out + j.corner, ld, j.rows, j.cols, stage);
     else store_tile(acc, out + j.corner, ld, j.rows, j.cols, stage);
   }
