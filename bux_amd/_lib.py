@@ -61,6 +61,8 @@ SIGNATURES = {
     "bux_moe_permute": (_int, [_p, _i64, _i32, _p, _p, _p, _p, _p, _size, _p]),
     "bux_mx_quantize": (
         _int, [_p, _p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p, _p, _p]),
+    "bux_mx_quantize_f32": (
+        _int, [_p, _p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p, _p, _p]),
     "bux_mx_grouped_rows_workspace_size": (_size, [_i32, _i64, _i64]),
     "bux_mx_grouped_rows": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _int, _p, _p, _size, _p]),
@@ -83,6 +85,7 @@ SIGNATURES = {
     "bux_bf16_grouped_contract": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
     "bux_token_rows": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
+    "bux_token_sums_f32": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums_biased": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p, _i32, _p, _p, _p]),
     "bux_expert_bias_add": (_int, [_p, _i64, _i64, _p, _p, _i32, _p]),
     "bux_expert_sums": (_int, [_p, _p, _i32, _i64, _p, _i64, _i64, _p, _i32, _p, _p]),
@@ -96,6 +99,8 @@ SIGNATURES = {
     "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _ffn, _p, _p, _p]),
     "bux_glu_quantize": (
         _int, [_p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p]),
+    "bux_glu_quantize_f32": (
+        _int, [_p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p]),
     "bux_mx_grouped_glu_workspace_size": (_size, [_i32, _i64]),
     "bux_mx_grouped_glu": (
         _int, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p, _ffn, _p, _p,
@@ -106,6 +111,9 @@ SIGNATURES = {
                _p, _p, _p, _size, _p]),
     "bux_glu_backward_quantize_workspace_size": (_size, [_i64, _i64]),
     "bux_glu_backward_quantize": (
+        _int, [_p, _p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p, _p,
+               _size, _p]),
+    "bux_glu_backward_quantize_f32": (
         _int, [_p, _p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p, _p,
                _size, _p]),
     "bux_mx_pack_rows": (_int, [_p, _p, _i32, _i64, _i64, _i64, _p, _p]),

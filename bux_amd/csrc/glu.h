@@ -62,8 +62,9 @@ __device__ __forceinline__ float fast_tanh(float x) {
 }
 
 // The activation a(x) and its derivative a'(x) (functional.py:12-40, their gradients
-// as jax takes them: relu's is 0 at 0).
-template <int KIND>
+// as jax takes them: relu's is 0 at 0). F32: a layer in float32, whose weakly typed
+// constants jax takes in float32.
+template <int KIND, bool F32 = false>
 __device__ __forceinline__ void activate(float x, float* a, float* da) {
 #pragma clang fp contract(on)
   if constexpr (KIND == BUX_RELU) {
@@ -107,8 +108,9 @@ __device__ __forceinline__ void activate(float x, float* a, float* da) {
   } else {
     static_assert(KIND == BUX_SWISH || KIND == BUX_QUICK_GELU, "no such activation");
     // swish: x sigmoid(x); quick_gelu: x sigmoid(1.702 x), jax multiplying the
-    // bfloat16 gate by 1.702 as a bfloat16 constant, 1.703125
-    constexpr float alpha = KIND == BUX_QUICK_GELU ? 1.703125f : 1.0f;
+    // bfloat16 gate by 1.702 as a bfloat16 constant, 1.703125 (a float32 gate by
+    // 1.702's float32)
+    constexpr float alpha = KIND == BUX_QUICK_GELU ? (F32 ? 1.702f : 1.703125f) : 1.0f;
     const float s = fast_sigmoid(alpha * x);
     *a = x * s;
     *da = s + alpha * x * s * (1.0f - s);
@@ -136,31 +138,31 @@ __device__ __forceinline__ float up_branch(const Act& act, float up, float* dup)
 }
 
 // h of one unit from its up projection (and gate, when gated) and the row's weight.
-template <typename K>
+template <typename K, bool F32 = false>
 __device__ __forceinline__ float glu_unit(const Act& act, float up, float gate, float w) {
 #pragma clang fp contract(on)
   float dup, a, da;
   up = up_branch(act, up, &dup);
   if constexpr (!K::gated) {
-    activate<K::kind>(up, &a, &da);
+    activate<K::kind, F32>(up, &a, &da);
     return a * w;
   } else {
     if (act.clamped) gate = fminf(gate, act.limit);
-    activate<K::kind>(gate, &a, &da);
+    activate<K::kind, F32>(gate, &a, &da);
     return a * (up + act.offset) * w;
   }
 }
 
 // The gradients of one unit's h, given dh = g: to up and (gated) gate, and the unit's
 // term of the row weight's gradient.
-template <typename K>
+template <typename K, bool F32 = false>
 __device__ __forceinline__ void glu_unit_grad(const Act& act, float up, float gate, float w,
                                               float g, float* d_up, float* d_gate, float* d_w) {
 #pragma clang fp contract(on)
   float dup, a, da;
   up = up_branch(act, up, &dup);
   if constexpr (!K::gated) {
-    activate<K::kind>(up, &a, &da);
+    activate<K::kind, F32>(up, &a, &da);
     *d_up = g * w * da * dup;
     *d_gate = 0.0f;
     *d_w = g * a;
@@ -170,7 +172,7 @@ __device__ __forceinline__ void glu_unit_grad(const Act& act, float up, float ga
       gate_pass = gate < act.limit ? 1.0f : (gate == act.limit ? 0.5f : 0.0f);
       gate = fminf(gate, act.limit);
     }
-    activate<K::kind>(gate, &a, &da);
+    activate<K::kind, F32>(gate, &a, &da);
     const float uo = up + act.offset;
     *d_up = g * w * a * dup;
     *d_gate = g * w * uo * da * gate_pass;

@@ -46,6 +46,8 @@
 // round trip through HBM; those values are the ones the activation kernels would store
 // (float32 arithmetic, one rounding to bfloat16), and can be stored too.
 
+#include <type_traits>
+
 #include "common.h"
 #include "glu.h"
 
@@ -72,16 +74,77 @@ __device__ __forceinline__ void stream_codes(uint8_t* at, uint32_t a, uint32_t b
   __builtin_nontemporal_store(u32x4{a, b, c, d}, reinterpret_cast<u32x4*>(at));
 }
 
-// Two float32 -> two bfloat16 (nearest even) by the hardware's conversion.
-__device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+// Eight bfloat16 of a uint4 as floats.
+__device__ __forceinline__ void floats8(const uint4& r, float* v) {
+  const uint32_t q[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = bf16_to_f32(static_cast<uint16_t>(q[j] & 0xffffu));
+    v[2 * j + 1] = bf16_to_f32(static_cast<uint16_t>(q[j] >> 16));
+  }
+}
+
+// Eight values of a source's type V: bfloat16 (V = uint16_t, 16 bytes) or float32 (V =
+// float, 32 bytes), as a thread loads, stores and widens them.
+template <typename V>
+struct Pack8;
+template <>
+struct Pack8<uint16_t> {
+  typedef uint4 type;
+  __device__ static __forceinline__ type zero() { return make_uint4(0, 0, 0, 0); }
+  __device__ static __forceinline__ type load(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ static __forceinline__ void store(uint16_t* p, const type& x) { *reinterpret_cast<uint4*>(p) = x; }
+  __device__ static __forceinline__ void floats(const type& x, float* v) { floats8(x, v); }
+  // the 8 values of v as the type holds them (rounded to bfloat16, nearest even)
+  __device__ static __forceinline__ type of(const float* v) {
+    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                      pack_bf16x2(v[6], v[7]));
+  }
+  __device__ static __forceinline__ float widen(uint16_t x) { return bf16_to_f32(x); }
+  __device__ static __forceinline__ uint16_t narrow(float x) { return f32_to_bf16(x); }
+  // the scale exponent of a block whose largest magnitude (a value of the type) is amax
+  __device__ static __forceinline__ int exponent(float amax) { return scale_exponent_bf16(amax); }
+};
+template <>
+struct Pack8<float> {
+  struct type {
+    uint4 lo, hi;
+  };
+  __device__ static __forceinline__ type zero() { return type{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)}; }
+  __device__ static __forceinline__ type load(const float* p) {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+    return type{q[0], q[1]};
+  }
+  __device__ static __forceinline__ void store(float* p, const type& x) {
+    uint4* q = reinterpret_cast<uint4*>(p);
+    q[0] = x.lo;
+    q[1] = x.hi;
+  }
+  __device__ static __forceinline__ void floats(const type& x, float* v) {
+    const uint32_t w[8] = {x.lo.x, x.lo.y, x.lo.z, x.lo.w, x.hi.x, x.hi.y, x.hi.z, x.hi.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(w[j]);
+  }
+  __device__ static __forceinline__ type of(const float* v) {
+    return type{make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                           __float_as_uint(v[3])),
+                make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                           __float_as_uint(v[7]))};
+  }
+  __device__ static __forceinline__ float widen(float x) { return x; }
+  __device__ static __forceinline__ float narrow(float x) { return x; }
+  __device__ static __forceinline__ int exponent(float amax) { return scale_exponent(amax); }
+};
 
 // A matrix of bfloat16 (matrix g of a stack), or its rows read by index. With
 // `halves`, its columns are read as a GLU's halves (grouped_cudnn.halves_of,
 // grouped_cudnn.py:150-155): column c of the copies is, in each 64, the gate (odd column)
 // of pair c % 32 for c % 64 < 32, else that pair's up (even column).
-struct Matrix {
+template <typename V>
+struct MatrixOf {
+  typedef V Value;
   static constexpr bool kPartials = false;
-  const uint16_t* x;
+  const V* x;
   const int32_t* index;
   int32_t index_div;
   int64_t sources;  // with an index, x's rows: a source row outside [0, sources) reads 0
@@ -97,80 +160,82 @@ struct Matrix {
   __device__ __forceinline__ bool by_columns() const { return index != nullptr; }
   // Columns [col, col + 8) of row r of matrix g; `live`: r holds values and the
   // columns are the matrix's (`inside`: the columns are; padding past them is not).
-  __device__ __forceinline__ uint4 load(int64_t g, int64_t r, int64_t col, bool live, bool,
-                                        float*) const {
-    if (!live) return make_uint4(0, 0, 0, 0);
+  __device__ __forceinline__ typename Pack8<V>::type load(int64_t g, int64_t r, int64_t col,
+                                                          bool live, bool, float*) const {
+    if (!live) return Pack8<V>::zero();
     int64_t src = r;
     if (index) {
       const int32_t at = index[r];
-      if (at < 0) return make_uint4(0, 0, 0, 0);
+      if (at < 0) return Pack8<V>::zero();
       // a power-of-two divisor (every top-k bux's configs use) by a shift
       src = (index_div & (index_div - 1)) == 0 ? (at >> (31 - __builtin_clz(index_div)))
                                                : at / index_div;
-      if (src >= sources) return make_uint4(0, 0, 0, 0);
+      if (src >= sources) return Pack8<V>::zero();
     }
-    const uint16_t* row = (index ? x : x + g * rows * cols) + src * cols;
-    if (!halves) return *reinterpret_cast<const uint4*>(row + col);
-    // 8 columns of one half: 16 consecutive columns of pairs, every other one
+    const V* row = (index ? x : x + g * rows * cols) + src * cols;
+    if (!halves) return Pack8<V>::load(row + col);
+    // 8 columns of one half: 16 consecutive columns of pairs, every other one (a gate
+    // is a pair's second, an up its first)
     const int64_t q = col & 63;
-    const uint4* p = reinterpret_cast<const uint4*>(row + (col - q) + 2 * (q & 31));
-    const uint4 lo = p[0], hi = p[1];
-    const int shift = q < 32 ? 16 : 0;  // a gate is a pair's high half, an up its low
-    const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    uint32_t o[4];
+    const typename Pack8<V>::type lo = Pack8<V>::load(row + (col - q) + 2 * (q & 31));
+    const typename Pack8<V>::type hi = Pack8<V>::load(row + (col - q) + 2 * (q & 31) + 8);
+    if constexpr (std::is_same<V, uint16_t>::value) {
+      const int shift = q < 32 ? 16 : 0;  // bits: a gate is a pair's high half, an up its low
+      const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      uint32_t o[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o[j] = ((w[2 * j] >> shift) & 0xffffu) | (((w[2 * j + 1] >> shift) & 0xffffu) << 16);
-    return make_uint4(o[0], o[1], o[2], o[3]);
+      for (int j = 0; j < 4; ++j)
+        o[j] = ((w[2 * j] >> shift) & 0xffffu) | (((w[2 * j + 1] >> shift) & 0xffffu) << 16);
+      return make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+      const uint32_t w[16] = {lo.lo.x, lo.lo.y, lo.lo.z, lo.lo.w, lo.hi.x, lo.hi.y, lo.hi.z, lo.hi.w,
+                              hi.lo.x, hi.lo.y, hi.lo.z, hi.lo.w, hi.hi.x, hi.hi.y, hi.hi.z, hi.hi.w};
+      const int pick = q < 32 ? 1 : 0;
+      return typename Pack8<V>::type{
+          make_uint4(w[pick], w[2 + pick], w[4 + pick], w[6 + pick]),
+          make_uint4(w[8 + pick], w[10 + pick], w[12 + pick], w[14 + pick])};
+    }
   }
   __device__ __forceinline__ void partial(int64_t, int64_t, float) const {}
 };
-
-// Eight bfloat16 of a uint4 as floats.
-__device__ __forceinline__ void floats8(const uint4& r, float* v) {
-  const uint32_t q[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[2 * j] = bf16_to_f32(static_cast<uint16_t>(q[j] & 0xffffu));
-    v[2 * j + 1] = bf16_to_f32(static_cast<uint16_t>(q[j] >> 16));
-  }
-}
+typedef MatrixOf<uint16_t> Matrix;
 
 // h = act(gate) (up + offset) w, or act(up) w, from projected ((m, f, 2) gated, (m, f)
 // plain) and the rows' weights; columns are units. Rows past `filled` give 0. With `h`,
 // the values are stored there too.
-template <typename K>
+template <typename K, typename V = uint16_t>
 struct GluForward {
+  typedef V Value;
   static constexpr bool kPartials = false;
   __device__ __forceinline__ bool xcd_runs() const { return true; }
   __device__ __forceinline__ bool by_columns() const { return false; }
-  const uint16_t* projected;
-  const uint16_t* weights;
-  uint16_t* h;
+  const V* projected;
+  const V* weights;
+  V* h;
   Act act;
   int64_t m, f;
-  __device__ __forceinline__ uint4 load(int64_t, int64_t r, int64_t col, bool live, bool inside,
-                                        float*) const {
-    uint4 out = make_uint4(0, 0, 0, 0);
+  __device__ __forceinline__ typename Pack8<V>::type load(int64_t, int64_t r, int64_t col,
+                                                          bool live, bool inside, float*) const {
+    typename Pack8<V>::type out = Pack8<V>::zero();
     if (live) {
-      const float w = bf16_to_f32(weights[r]);
+      const float w = Pack8<V>::widen(weights[r]);
       float v[8];
       if constexpr (K::gated) {
-        const uint4* p = reinterpret_cast<const uint4*>(projected + (r * f + col) * 2);
+        const V* p = projected + (r * f + col) * 2;
         float pair[16];
-        floats8(p[0], pair);
-        floats8(p[1], pair + 8);
+        Pack8<V>::floats(Pack8<V>::load(p), pair);
+        Pack8<V>::floats(Pack8<V>::load(p + 8), pair + 8);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = glu_unit<K>(act, pair[2 * j], pair[2 * j + 1], w);
+        for (int j = 0; j < 8; ++j) v[j] = glu_unit<K, std::is_same<V, float>::value>(act, pair[2 * j], pair[2 * j + 1], w);
       } else {
         float up[8];
-        floats8(*reinterpret_cast<const uint4*>(projected + r * f + col), up);
+        Pack8<V>::floats(Pack8<V>::load(projected + r * f + col), up);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = glu_unit<K>(act, up[j], 0.0f, w);
+        for (int j = 0; j < 8; ++j) v[j] = glu_unit<K, std::is_same<V, float>::value>(act, up[j], 0.0f, w);
       }
-      out = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+      out = Pack8<V>::of(v);
     }
-    if (h && r < m && inside) *reinterpret_cast<uint4*>(h + r * f + col) = out;
+    if (h && r < m && inside) Pack8<V>::store(h + r * f + col, out);
     return out;
   }
   __device__ __forceinline__ void partial(int64_t, int64_t, float) const {}
@@ -181,52 +246,68 @@ struct GluForward {
 // its 64 columns' share of each row's d weight (the sum of its units' terms) in
 // `partials` (m rows of `tiles`), which glu_weights_kernel sums in order. With
 // `d_projected`, the values are stored there too.
-template <typename K>
+template <typename K, typename V = uint16_t>
 struct GluBackward {
+  typedef V Value;
   static constexpr bool kPartials = true;
   __device__ __forceinline__ bool xcd_runs() const { return true; }
   __device__ __forceinline__ bool by_columns() const { return false; }
   static constexpr int P = K::gated ? 2 : 1;
-  const uint16_t* projected;
-  const uint16_t* weights;
-  const uint16_t* dh;
-  uint16_t* d_projected;
+  const V* projected;
+  const V* weights;
+  const V* dh;
+  V* d_projected;
   float* partials;
   Act act;
   int64_t m, f, tiles;
-  __device__ __forceinline__ uint4 load(int64_t, int64_t r, int64_t col, bool live, bool inside,
-                                        float* dw) const {
-    uint4 out = make_uint4(0, 0, 0, 0);
+  // dh's 4 values from p (bfloat16: 8 bytes; float32: 16)
+  __device__ static __forceinline__ void four(const V* p, float* g) {
+    if constexpr (std::is_same<V, uint16_t>::value) {
+      const uint2 d = *reinterpret_cast<const uint2*>(p);
+      g[0] = bf16_to_f32(d.x & 0xffffu);
+      g[1] = bf16_to_f32(d.x >> 16);
+      g[2] = bf16_to_f32(d.y & 0xffffu);
+      g[3] = bf16_to_f32(d.y >> 16);
+    } else {
+      const float4 d = *reinterpret_cast<const float4*>(p);
+      g[0] = d.x;
+      g[1] = d.y;
+      g[2] = d.z;
+      g[3] = d.w;
+    }
+  }
+  __device__ __forceinline__ typename Pack8<V>::type load(int64_t, int64_t r, int64_t col,
+                                                          bool live, bool inside,
+                                                          float* dw) const {
+    typename Pack8<V>::type out = Pack8<V>::zero();
     *dw = 0.0f;
     if (live) {
       float p[8], v[8], sum = 0.0f;
-      floats8(*reinterpret_cast<const uint4*>(projected + r * f * P + col), p);
-      const float w = bf16_to_f32(weights[r]);
+      Pack8<V>::floats(Pack8<V>::load(projected + r * f * P + col), p);
+      const float w = Pack8<V>::widen(weights[r]);
       if constexpr (K::gated) {
-        const uint2 d = *reinterpret_cast<const uint2*>(dh + r * f + col / 2);
-        const float g[4] = {bf16_to_f32(d.x & 0xffffu), bf16_to_f32(d.x >> 16),
-                            bf16_to_f32(d.y & 0xffffu), bf16_to_f32(d.y >> 16)};
+        float g[4];
+        four(dh + r * f + col / 2, g);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float term;
-          glu_unit_grad<K>(act, p[2 * j], p[2 * j + 1], w, g[j], &v[2 * j], &v[2 * j + 1], &term);
+          glu_unit_grad<K, std::is_same<V, float>::value>(act, p[2 * j], p[2 * j + 1], w, g[j], &v[2 * j], &v[2 * j + 1], &term);
           sum += term;
         }
       } else {
         float g[8];
-        floats8(*reinterpret_cast<const uint4*>(dh + r * f + col), g);
+        Pack8<V>::floats(Pack8<V>::load(dh + r * f + col), g);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           float term, none;
-          glu_unit_grad<K>(act, p[j], 0.0f, w, g[j], &v[j], &none, &term);
+          glu_unit_grad<K, std::is_same<V, float>::value>(act, p[j], 0.0f, w, g[j], &v[j], &none, &term);
           sum += term;
         }
       }
       *dw = sum;
-      out = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+      out = Pack8<V>::of(v);
     }
-    if (d_projected && r < m && inside)
-      *reinterpret_cast<uint4*>(d_projected + r * f * P + col) = out;
+    if (d_projected && r < m && inside) Pack8<V>::store(d_projected + r * f * P + col, out);
     return out;
   }
   __device__ __forceinline__ void partial(int64_t r, int64_t tile, float v) const {
@@ -246,9 +327,12 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     Source src, int64_t rows, int64_t cols, int64_t height, const int32_t* __restrict__ filled_ptr,
     int flags, uint8_t* __restrict__ values, uint8_t* __restrict__ scales,
     uint8_t* __restrict__ t_values, uint8_t* __restrict__ t_scales) {
-  __shared__ uint16_t tile[TILE_ROWS][TILE_COLS];
-  // where column `col` of row `row` sits in the tile: its 16-byte chunk swizzled
-  const auto at = [&](int row, int col) -> uint16_t& {
+  typedef typename Source::Value V;
+  typedef Pack8<V> P8;
+  __shared__ V tile[TILE_ROWS][TILE_COLS];
+  // where column `col` of row `row` sits in the tile: its group of 8 values (16 bytes of
+  // bfloat16, 32 of float32) swizzled
+  const auto at = [&](int row, int col) -> V& {
     return tile[row][(((col >> 3) ^ (2 * ((row >> 4) & 3))) << 3) | (col & 7)];
   };
 
@@ -274,7 +358,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
   const int64_t col = col0 + 8 * chunk;
   const bool col_in = col < cols;  // cols is a multiple of 32: a chunk is all in or out
 
-  uint4 raw[4];
+  typename P8::type raw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t r = row0 + (t >> 3) + 32 * i;
@@ -298,13 +382,12 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
   if (tiles) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<uint4*>(&at((t >> 3) + 32 * i, 8 * chunk)) = raw[i];
-      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+      P8::store(&at((t >> 3) + 32 * i, 8 * chunk), raw[i]);
+      float w[8];
+      P8::floats(raw[i], w);
       float m = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        m = fmaxf(m, fmaxf(fabsf(bf16_to_f32(static_cast<uint16_t>(w[j] & 0xffffu))),
-                           fabsf(bf16_to_f32(static_cast<uint16_t>(w[j] >> 16)))));
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(w[j]));
       m = fmaxf(m, __shfl_xor(m, 1));
       m = fmaxf(m, __shfl_xor(m, 2));
       m = fmaxf(m, __shfl_xor(m, 8));
@@ -319,7 +402,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     float m = tile_max[0][i][b];
 #pragma unroll
     for (int w = 1; w < THREADS / 64; ++w) m = fmaxf(m, tile_max[w][i][b]);
-    return scale_exponent_bf16(m);
+    return P8::exponent(m);
   };
 
   if (flags & BUX_MX_ROWS) {
@@ -328,19 +411,14 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t r = row0 + (t >> 3) + 32 * i;
-      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
       float v[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = bf16_to_f32(static_cast<uint16_t>(w[j] & 0xffffu));
-        v[2 * j + 1] = bf16_to_f32(static_cast<uint16_t>(w[j] >> 16));
-      }
+      P8::floats(raw[i], v);
       float amax = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
       amax = fmaxf(amax, __shfl_xor(amax, 1));
       amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const int e = tiles ? tile_e(i, chunk >> 2) : scale_exponent_bf16(amax);
+      const int e = tiles ? tile_e(i, chunk >> 2) : P8::exponent(amax);
       const float down = power_of_two_down(e);
       uint2 codes;
       codes.x = e4m3x4(clip448(v[0] * down), clip448(v[1] * down), clip448(v[2] * down),
@@ -359,7 +437,7 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
 
   if (!tiles) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&at((t >> 3) + 32 * i, 8 * chunk)) = raw[i];
+    for (int i = 0; i < 4; ++i) P8::store(&at((t >> 3) + 32 * i, 8 * chunk), raw[i]);
     __syncthreads();
   }
 
@@ -377,11 +455,11 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      v[j] = bf16_to_f32(at(64 * h + 16 * q + j, lc));
+      v[j] = P8::widen(at(64 * h + 16 * q + j, lc));
       amax = fmaxf(amax, fabsf(v[j]));
     }
     amax = fmaxf(amax, __shfl_xor(amax, 1));
-    const int e = tiles ? tile_e(2 * h + (q >> 1), lc >> 5) : scale_exponent_bf16(amax);
+    const int e = tiles ? tile_e(2 * h + (q >> 1), lc >> 5) : P8::exponent(amax);
     const float down = power_of_two_down(e);
     uint32_t w[4];
 #pragma unroll
@@ -399,11 +477,12 @@ __global__ __launch_bounds__(THREADS) void quantize_kernel(
 }
 
 // d weight of each row: its workgroups' partial sums, added in column order, rounded
-// once to bfloat16; rows past `filled` give 0.
+// once to V (bfloat16; float32 keeps the sum); rows past `filled` give 0.
+template <typename V>
 __global__ __launch_bounds__(THREADS) void glu_weights_kernel(const float* __restrict__ partials,
                                                               int64_t m, int64_t tiles,
                                                               const int32_t* __restrict__ filled_ptr,
-                                                              uint16_t* __restrict__ d_weights) {
+                                                              V* __restrict__ d_weights) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
   if (r >= m) return;
   const int64_t filled = filled_ptr ? static_cast<int64_t>(*filled_ptr) : m;
@@ -417,7 +496,7 @@ __global__ __launch_bounds__(THREADS) void glu_weights_kernel(const float* __res
       sum += v.y;
     }
   }
-  d_weights[r] = f32_to_bf16(sum);
+  d_weights[r] = Pack8<V>::narrow(sum);
 }
 
 // Checks shared by the entry points, then the launch over `groups` matrices.
@@ -451,14 +530,42 @@ int launch_quantize(const char* name, const Source& src, int64_t groups, int64_t
 
 }  // namespace
 
+template <typename V>
 int launch_glu_weights(const float* partials, int64_t m, int64_t tiles, const int32_t* filled,
-                       uint16_t* d_weights, hipStream_t s) {
+                       V* d_weights, hipStream_t s) {
   if (m == 0) return BUX_OK;
-  hipLaunchKernelGGL(glu_weights_kernel, dim3(static_cast<unsigned>(ceil_div(m, THREADS))),
+  hipLaunchKernelGGL(glu_weights_kernel<V>, dim3(static_cast<unsigned>(ceil_div(m, THREADS))),
                      dim3(THREADS), 0, s, partials, m, tiles, filled, d_weights);
   return launched("glu_weights_kernel");
 }
+int launch_glu_weights(const float* partials, int64_t m, int64_t tiles, const int32_t* filled,
+                       uint16_t* d_weights, hipStream_t s) {
+  return launch_glu_weights<uint16_t>(partials, m, tiles, filled, d_weights, s);
+}
 
+}  // namespace bux
+
+namespace bux {
+namespace {
+template <typename V>
+int mx_quantize(const char* name, const V* x, const int32_t* index, int32_t index_div,
+                int64_t sources, int64_t groups, int64_t rows, int64_t cols, int64_t height,
+                const int32_t* filled, int flags, uint8_t* values, uint8_t* scales,
+                uint8_t* t_values, uint8_t* t_scales, void* stream) {
+  clear_error();
+  BUX_CHECK(x != nullptr, "%s: x is NULL", name);
+  BUX_CHECK(index == nullptr || index_div >= 1, "%s: index_div=%d", name, index_div);
+  BUX_CHECK(index == nullptr || groups == 1, "%s: index takes one matrix, not %lld", name,
+            (long long)groups);
+  BUX_CHECK(index == nullptr || sources >= 0, "%s: sources=%lld", name, (long long)sources);
+  const bool halves = (flags & BUX_MX_HALVES) != 0;
+  BUX_CHECK(!halves || cols % 64 == 0, "%s: BUX_MX_HALVES needs cols=%lld a multiple of 64", name,
+            (long long)cols);
+  const MatrixOf<V> source{x, index, index_div, sources, rows, cols, halves};
+  return launch_quantize(name, source, groups, rows, cols, height, filled, flags & ~BUX_MX_HALVES,
+                         values, scales, t_values, t_scales, as_stream(stream));
+}
+}  // namespace
 }  // namespace bux
 
 extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div,
@@ -466,38 +573,54 @@ extern "C" int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t 
                                int64_t height, const int32_t* filled, int flags, uint8_t* values,
                                uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
                                void* stream) {
-  using namespace bux;
-  clear_error();
-  BUX_CHECK(x != nullptr, "bux_mx_quantize: x is NULL");
-  BUX_CHECK(index == nullptr || index_div >= 1, "bux_mx_quantize: index_div=%d", index_div);
-  BUX_CHECK(index == nullptr || groups == 1, "bux_mx_quantize: index takes one matrix, not %lld",
-            (long long)groups);
-  BUX_CHECK(index == nullptr || sources >= 0, "bux_mx_quantize: sources=%lld", (long long)sources);
-  const bool halves = (flags & BUX_MX_HALVES) != 0;
-  BUX_CHECK(!halves || cols % 64 == 0, "bux_mx_quantize: BUX_MX_HALVES needs cols=%lld a multiple of 64",
-            (long long)cols);
-  const Matrix source{x, index, index_div, sources, rows, cols, halves};
-  return launch_quantize("bux_mx_quantize", source, groups, rows, cols, height, filled,
-                         flags & ~BUX_MX_HALVES, values, scales, t_values, t_scales,
-                         as_stream(stream));
+  return bux::mx_quantize("bux_mx_quantize", x, index, index_div, sources, groups, rows, cols,
+                          height, filled, flags, values, scales, t_values, t_scales, stream);
 }
+
+extern "C" int bux_mx_quantize_f32(const float* x, const int32_t* index, int32_t index_div,
+                                   int64_t sources, int64_t groups, int64_t rows, int64_t cols,
+                                   int64_t height, const int32_t* filled, int flags,
+                                   uint8_t* values, uint8_t* scales, uint8_t* t_values,
+                                   uint8_t* t_scales, void* stream) {
+  return bux::mx_quantize("bux_mx_quantize_f32", x, index, index_div, sources, groups, rows, cols,
+                          height, filled, flags, values, scales, t_values, t_scales, stream);
+}
+
+namespace bux {
+namespace {
+template <typename V>
+int glu_quantize(const char* name, const V* projected, const V* weights, const int32_t* filled,
+                 int64_t m, int64_t f, const bux_ffn* ffn, int64_t height, V* h, uint8_t* values,
+                 uint8_t* scales, uint8_t* t_values, uint8_t* t_scales, void* stream) {
+  clear_error();
+  Act act;
+  if (int rc = act_of(name, ffn, &act)) return rc;
+  BUX_CHECK(m == 0 || (projected && weights), "%s: NULL input", name);
+  return with_kind(act, [&](auto kind) {
+    using K = decltype(kind);
+    const GluForward<K, V> src{projected, weights, h, act, m, f};
+    return launch_quantize(name, src, 1, m, f, height, filled, BUX_MX_ROWS | BUX_MX_COLUMNS,
+                           values, scales, t_values, t_scales, as_stream(stream));
+  });
+}
+}  // namespace
+}  // namespace bux
 
 extern "C" int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights,
                                 const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
                                 int64_t height, uint16_t* h, uint8_t* values, uint8_t* scales,
                                 uint8_t* t_values, uint8_t* t_scales, void* stream) {
-  using namespace bux;
-  clear_error();
-  Act act;
-  if (int rc = act_of("bux_glu_quantize", ffn, &act)) return rc;
-  BUX_CHECK(m == 0 || (projected && weights), "bux_glu_quantize: NULL input");
-  return with_kind(act, [&](auto kind) {
-    using K = decltype(kind);
-    const GluForward<K> src{projected, weights, h, act, m, f};
-    return launch_quantize("bux_glu_quantize", src, 1, m, f, height, filled,
-                           BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales,
-                           as_stream(stream));
-  });
+  return bux::glu_quantize("bux_glu_quantize", projected, weights, filled, m, f, ffn, height, h,
+                           values, scales, t_values, t_scales, stream);
+}
+
+extern "C" int bux_glu_quantize_f32(const float* projected, const float* weights,
+                                    const int32_t* filled, int64_t m, int64_t f,
+                                    const bux_ffn* ffn, int64_t height, float* h, uint8_t* values,
+                                    uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
+                                    void* stream) {
+  return bux::glu_quantize("bux_glu_quantize_f32", projected, weights, filled, m, f, ffn, height,
+                           h, values, scales, t_values, t_scales, stream);
 }
 
 extern "C" size_t bux_glu_backward_quantize_workspace_size(int64_t m, int64_t f) {
@@ -506,6 +629,39 @@ extern "C" size_t bux_glu_backward_quantize_workspace_size(int64_t m, int64_t f)
   return static_cast<size_t>(m) * static_cast<size_t>(ceil_div(2 * f, 128) * 2) * sizeof(float);
 }
 
+namespace bux {
+namespace {
+template <typename V>
+int glu_backward_quantize(const char* name, const V* projected, const V* weights, const V* dh,
+                          const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
+                          int64_t height, V* d_projected, uint8_t* values, uint8_t* scales,
+                          uint8_t* t_values, uint8_t* t_scales, V* d_weights, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  clear_error();
+  Act act;
+  if (int rc = act_of(name, ffn, &act)) return rc;
+  BUX_CHECK(m == 0 || (projected && weights && dh && d_weights), "%s: NULL input or d_weights",
+            name);
+  const size_t need = bux_glu_backward_quantize_workspace_size(m, f);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(BUX_E_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", name, workspace_bytes,
+                need);
+  const int64_t cols = (act.gated ? 2 : 1) * f;
+  const int64_t tiles = ceil_div(cols, 128) * 2;
+  float* partials = static_cast<float*>(workspace);
+  hipStream_t s = as_stream(stream);
+  const int rc = with_kind(act, [&](auto kind) {
+    using K = decltype(kind);
+    const GluBackward<K, V> src{projected, weights, dh, d_projected, partials, act, m, f, tiles};
+    return launch_quantize(name, src, 1, m, cols, height, filled, BUX_MX_ROWS | BUX_MX_COLUMNS,
+                           values, scales, t_values, t_scales, s);
+  });
+  if (rc != BUX_OK) return rc;
+  return launch_glu_weights<V>(partials, m, tiles, filled, d_weights, s);
+}
+}  // namespace
+}  // namespace bux
+
 extern "C" int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights,
                                          const uint16_t* dh, const int32_t* filled, int64_t m,
                                          int64_t f, const bux_ffn* ffn, int64_t height,
@@ -513,26 +669,21 @@ extern "C" int bux_glu_backward_quantize(const uint16_t* projected, const uint16
                                          uint8_t* t_values, uint8_t* t_scales,
                                          uint16_t* d_weights, void* workspace,
                                          size_t workspace_bytes, void* stream) {
-  using namespace bux;
-  clear_error();
-  Act act;
-  if (int rc = act_of("bux_glu_backward_quantize", ffn, &act)) return rc;
-  BUX_CHECK(m == 0 || (projected && weights && dh && d_weights),
-            "bux_glu_backward_quantize: NULL input or d_weights");
-  const size_t need = bux_glu_backward_quantize_workspace_size(m, f);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-    return fail(BUX_E_WORKSPACE, "bux_glu_backward_quantize: workspace of %zu bytes, %zu needed",
-                workspace_bytes, need);
-  const int64_t cols = (act.gated ? 2 : 1) * f;
-  const int64_t tiles = ceil_div(cols, 128) * 2;
-  float* partials = static_cast<float*>(workspace);
-  hipStream_t s = as_stream(stream);
-  const int rc = with_kind(act, [&](auto kind) {
-    using K = decltype(kind);
-    const GluBackward<K> src{projected, weights, dh, d_projected, partials, act, m, f, tiles};
-    return launch_quantize("bux_glu_backward_quantize", src, 1, m, cols, height, filled,
-                           BUX_MX_ROWS | BUX_MX_COLUMNS, values, scales, t_values, t_scales, s);
-  });
-  if (rc != BUX_OK) return rc;
-  return launch_glu_weights(partials, m, tiles, filled, d_weights, s);
+  return bux::glu_backward_quantize("bux_glu_backward_quantize", projected, weights, dh, filled,
+                                    m, f, ffn, height, d_projected, values, scales, t_values,
+                                    t_scales, d_weights, workspace, workspace_bytes, stream);
+}
+
+extern "C" int bux_glu_backward_quantize_f32(const float* projected, const float* weights,
+                                             const float* dh, const int32_t* filled, int64_t m,
+                                             int64_t f, const bux_ffn* ffn, int64_t height,
+                                             float* d_projected, uint8_t* values,
+                                             uint8_t* scales, uint8_t* t_values,
+                                             uint8_t* t_scales, float* d_weights,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  return bux::glu_backward_quantize("bux_glu_backward_quantize_f32", projected, weights, dh,
+                                    filled, m, f, ffn, height, d_projected, values, scales,
+                                    t_values, t_scales, d_weights, workspace, workspace_bytes,
+                                    stream);
 }

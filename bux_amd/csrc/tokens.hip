@@ -155,6 +155,44 @@ __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __r
   *reinterpret_cast<uint4*>(out + t * width + c) = pack8(acc);
 }
 
+// token_sums_kernel<KMAX, false> for a layer in float32: float32 rows, the picks added
+// in the same order, the float32 sum stored as it is (the reference's sum_by_token casts
+// its float32 sum back to y's dtype, grouped_blockscaled.py:148). A lane moves 8 floats
+// (32 bytes) a pick.
+template <int KMAX>
+__global__ __launch_bounds__(THREADS) void token_sums_f32_kernel(const float* __restrict__ y,
+                                                                 int64_t y_rows,
+                                                                 const int32_t* __restrict__ inverse,
+                                                                 int32_t k, int64_t width,
+                                                                 float* __restrict__ out) {
+  const int64_t chunks = (width + THREADS * VEC - 1) / (THREADS * VEC);
+  const int64_t t = blockIdx.x / chunks;
+  const int64_t c = ((blockIdx.x % chunks) * THREADS + threadIdx.x) * VEC;
+  if (c >= width) return;
+  float4 acc[2] = {make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0)};
+  auto add = [&](const float4* row) {
+    const float4 a = row[0], b = row[1];
+    acc[0].x += a.x; acc[0].y += a.y; acc[0].z += a.z; acc[0].w += a.w;
+    acc[1].x += b.x; acc[1].y += b.y; acc[1].z += b.z; acc[1].w += b.w;
+  };
+  if constexpr (KMAX > 0) {
+    int64_t r[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) r[j] = j < k ? inverse[t * k + j] : -1;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      if (r[j] >= 0 && r[j] < y_rows) add(reinterpret_cast<const float4*>(y + r[j] * width + c));
+  } else {
+    for (int j = 0; j < k; ++j) {
+      const int64_t r = inverse[t * k + j];
+      if (r >= 0 && r < y_rows) add(reinterpret_cast<const float4*>(y + r * width + c));
+    }
+  }
+  float4* o = reinterpret_cast<float4*>(out + t * width + c);
+  o[0] = acc[0];
+  o[1] = acc[1];
+}
+
 // A lane takes 4 units of a row: 16 bytes of projected gated (4 up-gate pairs), 8 plain.
 template <typename K>
 __global__ __launch_bounds__(THREADS) void glu_forward_kernel(
@@ -383,6 +421,27 @@ int token_sums(const char* name, const uint16_t* y, int64_t y_rows, const int32_
   return launched("token_sums_kernel");
 }
 
+int token_sums_f32(const char* name, const float* y, int64_t y_rows, const int32_t* inverse,
+                   int64_t tokens, int32_t k, int64_t width, float* out, void* stream) {
+  BUX_CHECK(tokens >= 0 && tokens <= 2147483647LL && k >= 1 && width > 0 && y_rows >= 0,
+            "%s: bad shape tokens=%lld k=%d width=%lld", name, (long long)tokens, k,
+            (long long)width);
+  BUX_CHECK(width % VEC == 0, "%s: width=%lld is not a multiple of %d", name, (long long)width,
+            VEC);
+  if (tokens == 0) return BUX_OK;
+  BUX_CHECK(y && inverse && out, "%s: NULL buffer", name);
+  BUX_CHECK(tokens * ceil_div(width, THREADS * VEC) < (1LL << 31), "%s: too large", name);
+  dim3 grid(static_cast<unsigned>(tokens * ceil_div(width, THREADS * VEC)));
+  hipStream_t s = as_stream(stream);
+  if (k <= 8)
+    hipLaunchKernelGGL((token_sums_f32_kernel<8>), grid, dim3(THREADS), 0, s, y, y_rows, inverse,
+                       k, width, out);
+  else
+    hipLaunchKernelGGL((token_sums_f32_kernel<0>), grid, dim3(THREADS), 0, s, y, y_rows, inverse,
+                       k, width, out);
+  return launched("token_sums_f32_kernel");
+}
+
 int experts_ok(const char* name, const int32_t* offsets, int32_t experts) {
   BUX_CHECK(offsets != nullptr && experts >= 1 && experts <= (1 << 20),
             "%s: offsets of %d experts (1 .. 2^20, not NULL)", name, experts);
@@ -397,6 +456,14 @@ extern "C" int bux_token_sums(const uint16_t* y, int64_t y_rows, const int32_t* 
   using namespace bux;
   clear_error();
   return token_sums("bux_token_sums", y, y_rows, inverse, tokens, k, width, nullptr, out, stream);
+}
+
+extern "C" int bux_token_sums_f32(const float* y, int64_t y_rows, const int32_t* inverse,
+                                  int64_t tokens, int32_t k, int64_t width, float* out,
+                                  void* stream) {
+  using namespace bux;
+  clear_error();
+  return token_sums_f32("bux_token_sums_f32", y, y_rows, inverse, tokens, k, width, out, stream);
 }
 
 extern "C" int bux_token_sums_biased(const uint16_t* y, int64_t y_rows, const int32_t* inverse,

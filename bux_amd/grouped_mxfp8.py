@@ -102,8 +102,9 @@ def quantized_twice(
     (``blockscaled.mx_tiles_twice``, blockscaled.py:294-309: the mxfp8_2d recipe's W).
 
     Args:
-        x: bfloat16, a matrix (r, c) or a stack (g, r, c); with `index`, the matrix
-            the rows are read from. c is a multiple of 32.
+        x: bfloat16 or float32, a matrix (r, c) or a stack (g, r, c); with `index`, the
+            matrix the rows are read from. c is a multiple of 32. (float32: the
+            reference quantizes any float dtype alike, in float32, blockscaled.py:323-343.)
         filled: a device int32 (one element): rows from it on quantize as 0; None
             for every row.
         columns: whether to return x^T too.
@@ -123,8 +124,8 @@ def quantized_twice(
         rows of K = height padded to 128 (a stack of g of each for a stack).
     """
     require(x, filled, index)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"quantized_twice takes bfloat16, got {x.dtype}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"quantized_twice takes bfloat16 or float32, got {x.dtype}")
     if not isinstance(tiles, bool):
         raise TypeError(f"quantized_twice: tiles is a bool (the mxfp8_2d recipe's scales), "
                         f"not {type(tiles).__name__}")
@@ -156,7 +157,8 @@ def quantized_twice(
         flags |= _lib.MX_TILES
     if halves:
         flags |= _lib.MX_HALVES
-    _lib.check(lib().bux_mx_quantize(
+    quantize = lib().bux_mx_quantize if x.dtype == torch.bfloat16 else lib().bux_mx_quantize_f32
+    _lib.check(quantize(
         ptr(x), ptr(index), index_div, x.shape[0] if index is not None else 0, groups, r, c, h,
         ptr(filled), flags,
         ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))

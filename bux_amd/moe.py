@@ -64,9 +64,11 @@ def sort_by_expert(idx: torch.Tensor, num_experts: int) -> Sorted:
 
 
 def token_rows(z: torch.Tensor, order: torch.Tensor, k: int) -> torch.Tensor:
-    """Return ``z[order // k]`` (bfloat16 rows), a row of 0 where ``order // k`` lies
-    outside z's rows (a negative entry too; the sort's orders never do)."""
+    """Return ``z[order // k]`` (bfloat16 or float32 rows), a row of 0 where ``order //
+    k`` lies outside z's rows (a negative entry too; the sort's orders never do)."""
     require(z, order)
+    if z.dtype == torch.float32:  # a float32 row moves as twice the 16-bit words
+        return token_rows(z.view(torch.int16), order, k).view(torch.float32)
     m, width = order.shape[0], z.shape[-1]
     rows = torch.empty(m, width, dtype=z.dtype, device=z.device)
     _lib.check(lib().bux_token_rows(ptr(z), z.shape[0], ptr(order), m, k, width, ptr(rows),
@@ -80,14 +82,14 @@ def picked_weights(weights: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
 
 
 def sum_by_token(y: torch.Tensor, inverse: torch.Tensor) -> torch.Tensor:
-    """Return each token's sum of its k rows of y at `inverse` (t, k), added in float32;
-    a row outside y adds 0."""
+    """Return each token's sum of its k rows of y at `inverse` (t, k), added in float32
+    and given y's dtype (bfloat16 or float32); a row outside y adds 0."""
     require(y, inverse)
     tokens, k = inverse.shape
     width = y.shape[-1]
     out = torch.empty(tokens, width, dtype=y.dtype, device=y.device)
-    _lib.check(lib().bux_token_sums(ptr(y), y.shape[0], ptr(inverse), tokens, k, width,
-                                    ptr(out), stream()))
+    sums = lib().bux_token_sums_f32 if y.dtype == torch.float32 else lib().bux_token_sums
+    _lib.check(sums(ptr(y), y.shape[0], ptr(inverse), tokens, k, width, ptr(out), stream()))
     return out
 
 
@@ -119,6 +121,16 @@ class Ffn(NamedTuple):
         return gated and self.activation in ("swish", "quick_gelu", "situ")
 
 
+def _f32(*tensors: torch.Tensor) -> bool:
+    """Whether the activation's inputs are float32 (all of them), not bfloat16 (all)."""
+    kinds = {t.dtype for t in tensors}
+    if kinds == {torch.float32}:
+        return True
+    if kinds == {torch.bfloat16}:
+        return False
+    raise TypeError(f"the activation's inputs are all bfloat16 or all float32, not {kinds}")
+
+
 def _gating(projected: torch.Tensor) -> tuple[int, int, bool]:
     """(m, f, gated) of projected (m, f, 2) or (m, f, 1)."""
     if projected.dim() != 3 or projected.shape[2] not in (1, 2):
@@ -145,7 +157,8 @@ def weighted_units_quantized(ffn: Ffn, projected: torch.Tensor, weights: torch.T
                              ) -> tuple[Tiled, Tiled, torch.Tensor | None]:
     """Return `weighted_units` in MXFP8 along its rows and, as h^T, along m (both tiled,
     `height` rows of the copies), computed and quantized in one pass; with `keep`, h
-    itself (bfloat16 (m, f)) too, else None."""
+    itself (projected's dtype (m, f)) too, else None. In float32 (projected and weights
+    float32) h is the float32 result, quantized as it is."""
     require(projected, weights, filled)
     m, f, gated = _gating(projected)
     dev = projected.device
@@ -154,9 +167,10 @@ def weighted_units_quantized(ffn: Ffn, projected: torch.Tensor, weights: torch.T
     scales = torch.empty(kf // 128, height, 4, dtype=torch.uint8, device=dev)
     t_vals = torch.empty(kh // 64, f, 64, dtype=torch.uint8, device=dev)
     t_scales = torch.empty(kh // 128, f, 4, dtype=torch.uint8, device=dev)
-    h = torch.empty(m, f, dtype=torch.bfloat16, device=dev) if keep else None
+    h = torch.empty(m, f, dtype=projected.dtype, device=dev) if keep else None
     st = ffn.struct(gated)
-    _lib.check(lib().bux_glu_quantize(
+    quantize = lib().bux_glu_quantize_f32 if _f32(projected, weights) else lib().bux_glu_quantize
+    _lib.check(quantize(
         ptr(projected), ptr(weights), ptr(filled), m, f, ctypes.byref(st), height, ptr(h),
         ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))
     return Tiled(vals, scales), Tiled(t_vals, t_scales), h
@@ -168,8 +182,10 @@ def weighted_units_backward_quantized(
 ) -> tuple[Tiled, Tiled, torch.Tensor, torch.Tensor | None]:
     """Return the gradient of `weighted_units` to projected in MXFP8 along its rows (p f)
     and, transposed, along m (both tiled, `height` rows of the copies), the gradient to
-    the weights (m,), and with `keep` the bfloat16 gradient to projected (m, f, p)."""
+    the weights (m,), and with `keep` the gradient to projected (m, f, p), in projected's
+    dtype (bfloat16, or float32 with weights and dh float32 too)."""
     require(projected, weights, dh, filled)
+    f32 = _f32(projected, weights, dh)
     m, f, gated = _gating(projected)
     p = projected.shape[2]
     dev = projected.device
@@ -178,11 +194,13 @@ def weighted_units_backward_quantized(
     scales = torch.empty(kp // 128, height, 4, dtype=torch.uint8, device=dev)
     t_vals = torch.empty(kh // 64, p * f, 64, dtype=torch.uint8, device=dev)
     t_scales = torch.empty(kh // 128, p * f, 4, dtype=torch.uint8, device=dev)
-    dw = torch.empty(m, dtype=torch.bfloat16, device=dev)
-    dp = torch.empty(m, f, p, dtype=torch.bfloat16, device=dev) if keep else None
+    dtype = torch.float32 if f32 else torch.bfloat16
+    dw = torch.empty(m, dtype=dtype, device=dev)
+    dp = torch.empty(m, f, p, dtype=dtype, device=dev) if keep else None
     ws = workspace(lib().bux_glu_backward_quantize_workspace_size(m, f), dev)
     st = ffn.struct(gated)
-    _lib.check(lib().bux_glu_backward_quantize(
+    backward = lib().bux_glu_backward_quantize_f32 if f32 else lib().bux_glu_backward_quantize
+    _lib.check(backward(
         ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f, ctypes.byref(st), height,
         ptr(dp), ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), ptr(dw), ptr(ws), ws.numel(),
         stream()))
@@ -432,6 +450,24 @@ class Saved(NamedTuple):
     y: torch.Tensor | None = None  # with an expert norm: the down GEMM's rows (m, d)
 
 
+def _layer_dtype(name: str, x: torch.Tensor) -> torch.dtype:
+    """The layer's dtype, x's: bfloat16 or float32."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{name}: the tokens are bfloat16 or float32, not {x.dtype}")
+    return x.dtype
+
+
+def _float32_built(name: str, fmt: str, passes: tuple[bool, bool, bool], up_bias, down_bias,
+                   norm) -> None:
+    """Raise for what a float32 layer does not run here: every GEMM in MXFP8 (the
+    bfloat16 "compute" GEMMs take bfloat16 operands), no biases, no expert norm."""
+    if fmt not in MX_FORMATS or not all(passes):
+        raise NotImplementedError(f"{name}: float32 tokens take every GEMM in MXFP8 "
+                                  f"(fmt {fmt!r}, passes {passes})")
+    if up_bias is not None or down_bias is not None or norm is not None:
+        raise NotImplementedError(f"{name}: float32 tokens with biases or an expert norm")
+
+
 def experts_forward(
     z: torch.Tensor, idx: torch.Tensor, weights: torch.Tensor, up: torch.Tensor,
     down: torch.Tensor, ffn: Ffn = Ffn(), fmt: str = "mxfp8", intermediates: bool = False,
@@ -440,17 +476,24 @@ def experts_forward(
     norm: ExpertNorm | None = None, norm_scale: torch.Tensor | None = None,
     norm_bias: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, Saved]:
-    """Return the routed experts' output (t, d), bfloat16, and what the backward takes.
-    In MXFP8 the activation goes straight to its quantized copies; with `intermediates`
-    it is kept in bfloat16 too (Saved.h).
+    """Return the routed experts' output (t, d), in z's dtype, and what the backward
+    takes. In MXFP8 the activation goes straight to its quantized copies; with
+    `intermediates` it is kept too (Saved.h).
+
+    The layer computes in z's dtype, bfloat16 or float32, as the reference's does in x's
+    (the kernels and weights cast to it, experts/moe.py:846; the GEMMs' outputs in it,
+    grouped_blockscaled.Dtypes, grouped_blockscaled.py:129): in float32 no value is
+    rounded to bfloat16 between the steps (the MXFP8 operands are quantized from the
+    float32 values), and every GEMM multiplies in MXFP8 with no biases or expert norm
+    (others raise NotImplementedError).
 
     Args:
-        z: the tokens, bfloat16 (t, d).
+        z: the tokens, bfloat16 or float32 (t, d).
         idx: each token's k experts, int32 (t, k).
-        weights: their weights, bfloat16 (t, k).
-        up: the experts' up kernels, bfloat16 (E, d, f, p): p = 2 for a gated FFN (up
-            and gate), 1 for a plain one.
-        down: the experts' down kernels, bfloat16 (E, f, d).
+        weights: their weights (t, k), cast to z's dtype.
+        up: the experts' up kernels (E, d, f, p), cast to z's dtype: p = 2 for a gated
+            FFN (up and gate), 1 for a plain one.
+        down: the experts' down kernels (E, f, d), cast to z's dtype.
         ffn: the activation.
         fmt: "mxfp8" (Transformer Engine's recipe: every operand in blocks of 32 along
             what its GEMM contracts), "mxfp8_2d" (the same, but each W with a scale per
@@ -476,12 +519,14 @@ def experts_forward(
     t, k = idx.shape
     e, d, f, p = up.shape
     m = t * k
-    for name, a in (("z", z), ("weights", weights), ("up", up), ("down", down)):
-        # y, dx and dW take x's dtype, the kernels cast to it (moe.py:846,
-        # grouped_blockscaled.py:129): bfloat16 here
-        if a.dtype != torch.bfloat16:
-            raise TypeError(f"experts_forward: {name} is {a.dtype}; the layer multiplies in bfloat16")
+    dt = _layer_dtype("experts_forward", z)
+    # the kernels and the weights take x's dtype (moe.py:846); y, dx and dW then come in
+    # it (grouped_blockscaled.py:129)
+    up, down, weights = up.to(dt), down.to(dt), weights.to(dt)
     fprop, dgrad, wgrad = passes_of(fmt, passes)
+    if dt == torch.float32:
+        _float32_built("experts_forward", fmt, (fprop, dgrad, wgrad), up_bias, down_bias, norm)
+        fused = False  # the fused up GEMM's epilogue is bfloat16's
     if quantized is not None:
         quantized.check(fmt, up, down)
     with span("permute"):
@@ -519,7 +564,7 @@ def experts_forward(
     else:
         with span("up fprop"):
             if fprop:
-                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, height=m, tiles=listed)
+                projected = grouped_mxfp8.rows(x_k, up_k, s.sizes, dt, height=m, tiles=listed)
             else:
                 projected = grouped.dot(rows, up2, s.sizes)
         if up_bias is not None:
@@ -541,7 +586,7 @@ def experts_forward(
                 down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
     with span("down fprop"):
         if fprop:
-            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, height=m, tiles=listed)
+            y = grouped_mxfp8.rows(h_k, down_k, s.sizes, dt, height=m, tiles=listed)
         else:
             y = grouped.dot(h, down, s.sizes)
     y_rows = None
@@ -567,8 +612,9 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
                      norm: ExpertNorm | None = None, norm_scale: torch.Tensor | None = None,
                      norm_bias: torch.Tensor | None = None, fused: bool = False,
                      ) -> dict[str, torch.Tensor]:
-    """Return the gradients of `experts_forward`'s output, dy (t, d), to z, the
-    weights (t, k), up (E, d, f, p) and down (E, f, d), all bfloat16, and with biases
+    """Return the gradients of `experts_forward`'s output, dy (t, d, in the forward's
+    dtype), to z and the weights (t, k) in that dtype, to up (E, d, f, p) and down
+    (E, f, d) in theirs (computed in the forward's, then cast), and with biases
     to "up_bias" (E, f, p) and "down_bias" (E, d), float32 sums, and with a norm to
     "norm_scale" and "norm_bias" (d,), float32 sums; with `intermediates`,
     also the gradients between the GEMMs: "dh" (m, f) of the down GEMM's input, "dp"
@@ -581,9 +627,13 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
     them."""
     s, k = saved.sorted, saved.k
     t = dy.shape[0]
-    for name, a in (("dy", dy), ("up", up), ("down", down)):
-        if a.dtype != torch.bfloat16:
-            raise TypeError(f"experts_backward: {name} is {a.dtype}; the layer multiplies in bfloat16")
+    dt = saved.projected.dtype  # the forward's x's
+    if _layer_dtype("experts_backward", dy) != dt:
+        raise TypeError(f"experts_backward: dy is {dy.dtype}, the forward's tokens {dt}")
+    up_dtype, down_dtype = up.dtype, down.dtype
+    up, down = up.to(dt), down.to(dt)
+    if dt == torch.float32:
+        fused = False
     e, d, f, p = up.shape
     m = t * k
     filled = s.filled
@@ -631,12 +681,12 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
     else:
         with span("down dgrad"):
             if dgrad:
-                dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, height=m, tiles=saved.tiles)
+                dh = grouped_mxfp8.rows(dy_n, saved.down_n, s.sizes, dt, height=m, tiles=saved.tiles)
             else:
                 dh = grouped.dot(dy_rows, down, s.sizes, transposed=True)
     with span("down wgrad"):
         if wgrad:
-            d_down = grouped_mxfp8.contract(saved.h_m, dy_m, s.sizes, tiles=saved.tiles)
+            d_down = grouped_mxfp8.contract(saved.h_m, dy_m, s.sizes, dt, tiles=saved.tiles)
         else:
             d_down = grouped.weight_grad(saved.h, dy_rows, s.sizes)
     if twin:
@@ -655,12 +705,12 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         dp = dp.view(m, f * p)
     with span("up dgrad"):
         if dgrad:
-            dx = grouped_mxfp8.rows(dp_n, saved.up_n, s.sizes, height=m, tiles=saved.tiles)
+            dx = grouped_mxfp8.rows(dp_n, saved.up_n, s.sizes, dt, height=m, tiles=saved.tiles)
         else:
             dx = grouped.dot(dp, up2, s.sizes, transposed=True)
     with span("up wgrad"):
         if wgrad:
-            d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes, tiles=saved.tiles)
+            d_up = grouped_mxfp8.contract(saved.x_m, dp_m, s.sizes, dt, tiles=saved.tiles)
         else:
             d_up = grouped.weight_grad(saved.rows, dp, s.sizes)
     if up_bias is not None:
@@ -674,7 +724,9 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
     with span("combine dx"):
         dz = sum_by_token(dx, s.inverse.view(t, k))
         d_weights = token_rows(d_rows_w.view(m, 1), s.inverse, 1).view(t, k)
-    grads.update(z=dz, weights=d_weights, up=d_up.view(e, d, f, p), down=d_down)
+    # the kernels' gradients back in their own dtypes (the cast's transpose)
+    grads.update(z=dz, weights=d_weights, up=d_up.view(e, d, f, p).to(up_dtype),
+                 down=d_down.to(down_dtype))
     if intermediates:
         grads.update(dh=dh, dp=dp, dx=dx, d_row_weights=d_rows_w)
         if norm is not None:

@@ -54,6 +54,7 @@ ffi::Error status(int rc) {
   return ffi::Error(ffi::ErrorCode::kInternal, std::string(bux_last_error()));
 }
 int dtype_of(Out& y) { return y->element_type() == ffi::DataType::F32 ? BUX_F32 : BUX_BF16; }
+bool f32(const In& b) { return b.element_type() == ffi::DataType::F32; }
 
 bux_ffn ffn_of(int64_t activation, int64_t gated, int64_t clamped, float limit, int64_t capped,
                float up_softcap, float up_offset) {
@@ -103,11 +104,18 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxMoePermute, MoePermute,
 
 // --- a-4: MXFP8 quantization -----------------------------------------------------------
 
-// x [groups, rows, cols] (or with an index the matrix read from); index and filled may be
-// empty; a copy's results empty when not asked for.
+// x [groups, rows, cols] (or with an index the matrix read from), bfloat16 or float32;
+// index and filled may be empty; a copy's results empty when not asked for.
 static ffi::Error MxQuantize(hipStream_t s, In x, In index, In filled, int64_t index_div,
                              int64_t groups, int64_t rows, int64_t height, int64_t flags,
                              Out values, Out scales, Out t_values, Out t_scales) {
+  if (f32(x))
+    return status(bux_mx_quantize_f32(at<const float>(x), at<const int32_t>(index),
+                                      static_cast<int32_t>(index_div), dim(x, 0), groups, rows,
+                                      dim(x, -1), height, at<const int32_t>(filled),
+                                      static_cast<int>(flags), at<uint8_t>(values),
+                                      at<uint8_t>(scales), at<uint8_t>(t_values),
+                                      at<uint8_t>(t_scales), s));
   return status(bux_mx_quantize(at<const uint16_t>(x), at<const int32_t>(index),
                                 static_cast<int32_t>(index_div), dim(x, 0), groups, rows,
                                 dim(x, -1), height,
@@ -228,8 +236,12 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxTokenRows, TokenRows,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>()
                                   .Attr<int64_t>("k").Ret<In>());
 
-// inverse [t, k]
+// inverse [t, k]; y and out bfloat16 or float32
 static ffi::Error TokenSums(hipStream_t s, In y, In inverse, Out out) {
+  if (f32(y))
+    return status(bux_token_sums_f32(at<const float>(y), dim(y, 0), at<const int32_t>(inverse),
+                                     dim(inverse, 0), static_cast<int32_t>(dim(inverse, 1)),
+                                     dim(y, 1), at<float>(out), s));
   return status(bux_token_sums(at<const uint16_t>(y), dim(y, 0), at<const int32_t>(inverse),
                                dim(inverse, 0), static_cast<int32_t>(dim(inverse, 1)), dim(y, 1),
                                at<uint16_t>(out), s));
@@ -269,6 +281,11 @@ static ffi::Error GluQuantize(hipStream_t s, In projected, In weights, In filled
                               int64_t m, int64_t f, int64_t height, Out h, Out values, Out scales,
                               Out t_values, Out t_scales) {
   const bux_ffn ffn = BUX_FFN;
+  if (f32(projected))  // a layer in float32: projected, weights and h float32
+    return status(bux_glu_quantize_f32(at<const float>(projected), at<const float>(weights),
+                                       at<const int32_t>(filled), m, f, &ffn, height,
+                                       at<float>(h), at<uint8_t>(values), at<uint8_t>(scales),
+                                       at<uint8_t>(t_values), at<uint8_t>(t_scales), s));
   return status(bux_glu_quantize(at<const uint16_t>(projected), at<const uint16_t>(weights),
                                  at<const int32_t>(filled), m, f, &ffn, height, at<uint16_t>(h),
                                  at<uint8_t>(values), at<uint8_t>(scales), at<uint8_t>(t_values),
@@ -285,6 +302,12 @@ static ffi::Error GluBackwardQuantize(hipStream_t s, In projected, In weights, I
                                       Out values, Out scales, Out t_values, Out t_scales,
                                       Out d_weights, Out ws) {
   const bux_ffn ffn = BUX_FFN;
+  if (f32(projected))  // a layer in float32
+    return status(bux_glu_backward_quantize_f32(
+        at<const float>(projected), at<const float>(weights), at<const float>(dh),
+        at<const int32_t>(filled), dim(dh, 0), dim(dh, 1), &ffn, height, at<float>(d_projected),
+        at<uint8_t>(values), at<uint8_t>(scales), at<uint8_t>(t_values), at<uint8_t>(t_scales),
+        at<float>(d_weights), at<void>(ws), ws->size_bytes(), s));
   return status(bux_glu_backward_quantize(
       at<const uint16_t>(projected), at<const uint16_t>(weights), at<const uint16_t>(dh),
       at<const int32_t>(filled), dim(dh, 0), dim(dh, 1), &ffn, height, at<uint16_t>(d_projected),

@@ -117,6 +117,15 @@ int bux_mx_quantize(const uint16_t* x, const int32_t* index, int32_t index_div, 
                     int64_t groups, int64_t rows, int64_t cols, int64_t height,
                     const int32_t* filled, int flags, uint8_t* values, uint8_t* scales,
                     uint8_t* t_values, uint8_t* t_scales, void* stream);
+/* bux_mx_quantize_f32: the same of a float32 x (the reference quantizes any float dtype
+ * the same way, in float32: blockscaled._in_e4m3, precision/blockscaled.py:323-343; its
+ * layer's tokens and kernels in float32, experts/moe.py:846 and
+ * grouped_blockscaled.py:129): a block's scale from its largest magnitude's float32
+ * quotient by 448, the codes of x times 2^-e. */
+int bux_mx_quantize_f32(const float* x, const int32_t* index, int32_t index_div,
+                        int64_t sources, int64_t groups, int64_t rows, int64_t cols,
+                        int64_t height, const int32_t* filled, int flags, uint8_t* values,
+                        uint8_t* scales, uint8_t* t_values, uint8_t* t_scales, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-6. Grouped MXFP8 GEMM over rows: y[i] = a[i] b[g(i)]^T.
@@ -271,6 +280,10 @@ int bux_token_rows(const uint16_t* z, int64_t tokens, const int32_t* order, int6
                    int64_t width, uint16_t* rows, void* stream);
 int bux_token_sums(const uint16_t* y, int64_t y_rows, const int32_t* inverse, int64_t tokens,
                    int32_t k, int64_t width, uint16_t* out, void* stream);
+/* bux_token_sums_f32: the same for float32 y (a layer in float32): float32 sums in the
+ * same order, stored as they are (no rounding). */
+int bux_token_sums_f32(const float* y, int64_t y_rows, const int32_t* inverse, int64_t tokens,
+                       int32_t k, int64_t width, float* out, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-8. The experts' activation between the two GEMMs, times each row's weight.
@@ -427,6 +440,15 @@ int bux_expert_norm_backward(const uint16_t* dy, const int32_t* index, int32_t i
 int bux_glu_quantize(const uint16_t* projected, const uint16_t* weights, const int32_t* filled,
                      int64_t m, int64_t f, const bux_ffn* ffn, int64_t height, uint16_t* h, uint8_t* values, uint8_t* scales,
                      uint8_t* t_values, uint8_t* t_scales, void* stream);
+/* bux_glu_quantize_f32 / bux_glu_backward_quantize_f32: the same for a layer in float32
+ *   (tokens and kernels float32: the reference computes the activation and its gradient
+ *   in x's dtype, experts/moe.py:846-885): projected, weights, dh, h, d_projected and
+ *   d_weights float32, each value the float32 result of the same arithmetic (no
+ *   rounding to bfloat16), quantized as bux_mx_quantize_f32 quantizes. */
+int bux_glu_quantize_f32(const float* projected, const float* weights, const int32_t* filled,
+                         int64_t m, int64_t f, const bux_ffn* ffn, int64_t height, float* h,
+                         uint8_t* values, uint8_t* scales, uint8_t* t_values, uint8_t* t_scales,
+                         void* stream);
 /* bux_mx_grouped_glu: the experts' up GEMM with the activation and both MXFP8 copies
  *   of h in its epilogue, the reference's fused up GEMM (grouped_cudnn.activated,
  *   src/bux/architecture/experts/grouped_cudnn.py:161-205), but for groups as they lie
@@ -458,6 +480,12 @@ int bux_glu_backward_quantize(const uint16_t* projected, const uint16_t* weights
                               uint16_t* d_projected, uint8_t* values, uint8_t* scales,
                               uint8_t* t_values, uint8_t* t_scales, uint16_t* d_weights,
                               void* workspace, size_t workspace_bytes, void* stream);
+int bux_glu_backward_quantize_f32(const float* projected, const float* weights, const float* dh,
+                                  const int32_t* filled, int64_t m, int64_t f,
+                                  const bux_ffn* ffn, int64_t height, float* d_projected,
+                                  uint8_t* values, uint8_t* scales, uint8_t* t_values,
+                                  uint8_t* t_scales, float* d_weights, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 /* bux_mx_grouped_dglu: the experts' down dgrad with the activation's gradient and both
  *   MXFP8 copies of d projected in its epilogue, the reference's fused dgrad
  *   (grouped_cudnn.activation_grad, src/bux/architecture/experts/grouped_cudnn.py:

@@ -30,7 +30,11 @@ Pins, run by ``tests/test_oracle.py``:
 - `rows_mx`, `contract_mx`: brute-force float64 triple loops on small shapes; empty
   groups and rows past the groups are 0; garbage past ``filled`` changes no dW
   (tests/test_grouped.py:89-95);
-- `weighted_units_backward`: against torch.autograd of the same forward in float64.
+- `weighted_units_backward`: against torch.autograd of the same forward in float64,
+  for bfloat16 inputs and (to 1e-6) for a float32 layer's;
+- `_act`: each activation and its derivative against torch in float64 over [-30, 30],
+  and to 1e-12 relative of the textbook functions in 400-digit arithmetic (mpmath)
+  from x = -700 to 300, where e^x-sized values must not cancel to 0.
 
 Bit-level parity of float sums is unpinned: XLA:CPU's summation order inside
 ``ragged_dot`` and its bfloat16 excess-precision choices are not observable without
@@ -238,41 +242,50 @@ class Ffn(NamedTuple):
 
 
 def _sigmoid(x: np.ndarray) -> np.ndarray:
-    return 0.5 * (1.0 + np.tanh(0.5 * x))
+    """1 / (1 + e^-x), to a few float64 ulps of itself everywhere (``(1 + tanh(x/2)) / 2``
+    is 0 from x = -37 on, where the true value is e^x, still a float32 down to -87)."""
+    return special.expit(x)
 
 
-def _act(name: str, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def _act(name: str, x: np.ndarray, f32: bool = False) -> tuple[np.ndarray, np.ndarray]:
     """Return act(x) and act'(x) in float64 (functional.py:12-40; relu's gradient 0 at
-    0, as jax.nn.relu's)."""
+    0, as jax.nn.relu's); `f32`: of a layer in float32."""
     if name in ("swish", "quick_gelu"):
         # functional.py:29 writes ``x * jax.nn.sigmoid(1.702 * x)``: jax casts the weakly
-        # typed 1.702 to x's dtype, bfloat16, whose nearest value is 1.703125.
-        alpha = 1.0 if name == "swish" else QUICK_GELU_ALPHA
-        s = _sigmoid(alpha * x)
-        return x * s, s + alpha * x * s * (1.0 - s)
+        # typed 1.702 to x's dtype, bfloat16, whose nearest value is 1.703125 (in
+        # float32, 1.702's nearest float32).
+        alpha = 1.0 if name == "swish" else (
+            float(np.float32(1.702)) if f32 else QUICK_GELU_ALPHA)
+        s, sc = _sigmoid(alpha * x), _sigmoid(-alpha * x)  # sc = 1 - s, without cancelling
+        return x * s, s + alpha * x * s * sc
     if name == "relu":
         return np.maximum(x, 0.0), (x > 0).astype(np.float64)
     if name == "relu2":
         r = np.maximum(x, 0.0)
         return r * r, 2.0 * r
+    # below, 1 + tanh(z) = 2 sigmoid(2 z), 1 - tanh(z)^2 = 1 / cosh(z)^2 and
+    # 1 + erf(z) = erfc(-z): the same values, with no cancellation where tanh(z) nears -1
     if name == "gelu":
-        phi = 0.5 * (1.0 + special.erf(x / np.sqrt(2.0)))
+        phi = 0.5 * special.erfc(-x / np.sqrt(2.0))
         return x * phi, phi + x * np.exp(-0.5 * x * x) / np.sqrt(2.0 * np.pi)
     if name == "gelu_tanh":
         c = np.sqrt(2.0 / np.pi)
-        t = np.tanh(c * (x + 0.044715 * x ** 3))
-        return 0.5 * x * (1.0 + t), 0.5 * (1.0 + t) + 0.5 * x * (1.0 - t * t) * c * (1.0 + 3 * 0.044715 * x * x)
+        z = c * (x + 0.044715 * x ** 3)
+        s, sc = _sigmoid(2.0 * z), _sigmoid(-2.0 * z)
+        return x * s, s + 2.0 * x * s * sc * c * (1.0 + 3 * 0.044715 * x * x)
     if name == "sigmoid":
         s = _sigmoid(x)
-        return s, s * (1.0 - s)
+        return s, s * _sigmoid(-x)
     if name == "tanh":
-        t = np.tanh(x)
-        return t, 1.0 - t * t
+        with np.errstate(over="ignore"):
+            return np.tanh(x), 1.0 / np.cosh(x) ** 2
     if name == "softplus":
         return np.logaddexp(x, 0.0), _sigmoid(x)
     if name == "situ":
-        t, s = np.tanh(x / 4.0), _sigmoid(x)
-        return 4.0 * t * s, (1.0 - t * t) * s + 4.0 * t * s * (1.0 - s)
+        t, s, sc = np.tanh(x / 4.0), _sigmoid(x), _sigmoid(-x)
+        with np.errstate(over="ignore"):
+            sech2 = 1.0 / np.cosh(x / 4.0) ** 2
+        return 4.0 * t * s, sech2 * s + 4.0 * t * s * sc
     raise ValueError(name)
 
 
@@ -292,41 +305,56 @@ def _up_branch(ffn: Ffn, up: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return up, d
 
 
+def _wide(x: np.ndarray) -> np.ndarray:
+    """bfloat16 bits (uint16) or float32 values as float64, exactly."""
+    x = np.asarray(x)
+    return (bf16.to_f32(x) if x.dtype == np.uint16 else x.astype(np.float32)).astype(np.float64)
+
+
+def _narrow(v: np.ndarray, f32: bool) -> np.ndarray:
+    """float64 values rounded once: to float32 (`f32`), else to bfloat16 bits (through
+    float32, as the activation's float32 result is rounded)."""
+    return v.astype(np.float32) if f32 else bf16.to_bf16(v.astype(np.float32))
+
+
 def weighted_units(ffn: Ffn, projected: np.ndarray, weights: np.ndarray) -> np.ndarray:
     """Return ``act(gate) * (up + offset) * w`` for projected (m, f, 2) [up, gate], or
-    ``act(up) * w`` for (m, f, 1) or (m, f), and row weights (m,), as bfloat16 bits,
-    computed in float64 and rounded once (mlp.py:20-35, moe.py:898-926)."""
-    p = bf16.to_f32(projected).astype(np.float64)
+    ``act(up) * w`` for (m, f, 1) or (m, f), and row weights (m,), computed in float64
+    and rounded once (mlp.py:20-35, moe.py:898-926): bfloat16 bits of bfloat16 bits, or
+    float32 of float32 (a layer in float32)."""
+    f32 = np.asarray(projected).dtype == np.float32
+    p = _wide(projected)
     if p.ndim == 2:
         p = p[..., None]
-    w = bf16.to_f32(weights).astype(np.float64)[:, None]
+    w = _wide(weights)[:, None]
     up, _ = _up_branch(ffn, p[..., 0])
     if p.shape[-1] == 1:
-        a, _ = _act(ffn.activation, up)
-        return bf16.to_bf16((a * w).astype(np.float32))
+        a, _ = _act(ffn.activation, up, f32)
+        return _narrow(a * w, f32)
     gate = p[..., 1]
     if ffn.limit is not None:
         gate = np.minimum(gate, ffn.limit)
-    a, _ = _act(ffn.activation, gate)
-    return bf16.to_bf16((a * (up + ffn.up_offset) * w).astype(np.float32))
+    a, _ = _act(ffn.activation, gate, f32)
+    return _narrow(a * (up + ffn.up_offset) * w, f32)
 
 
 def weighted_units_backward(
     ffn: Ffn, projected: np.ndarray, weights: np.ndarray, dh: np.ndarray
 ) -> tuple[np.ndarray, np.ndarray]:
     """Return the gradients of `weighted_units` to projected (its shape) and to the row
-    weights (m,), as bfloat16 bits (the VJP jax takes of it, moe.py:898-910, with
-    jax's gradients of clip and minimum: 1 strictly inside, 0.5 at the limit, 0
-    outside)."""
-    p = bf16.to_f32(projected).astype(np.float64)
+    weights (m,), as bfloat16 bits (float32 for float32 inputs) (the VJP jax takes of it,
+    moe.py:898-910, with jax's gradients of clip and minimum: 1 strictly inside, 0.5 at
+    the limit, 0 outside)."""
+    f32 = np.asarray(projected).dtype == np.float32
+    p = _wide(projected)
     plain2d = p.ndim == 2
     if plain2d:
         p = p[..., None]
-    w = bf16.to_f32(weights).astype(np.float64)[:, None]
-    g_ = bf16.to_f32(dh).astype(np.float64)
+    w = _wide(weights)[:, None]
+    g_ = _wide(dh)
     up, up_pass = _up_branch(ffn, p[..., 0])
     if p.shape[-1] == 1:
-        a, da = _act(ffn.activation, up)
+        a, da = _act(ffn.activation, up, f32)
         dp = (g_ * w * da * up_pass)[..., None]
         d_w = (g_ * a).sum(-1)
     else:
@@ -335,13 +363,13 @@ def weighted_units_backward(
         if ffn.limit is not None:
             gate_pass = np.where(gate < ffn.limit, 1.0, np.where(gate == ffn.limit, 0.5, 0.0))
             gate = np.minimum(gate, ffn.limit)
-        a, da = _act(ffn.activation, gate)
+        a, da = _act(ffn.activation, gate, f32)
         u = up + ffn.up_offset
         dp = np.stack([g_ * w * a * up_pass, g_ * w * u * da * gate_pass], -1)
         d_w = (g_ * a * u).sum(-1)
     if plain2d:
         dp = dp[..., 0]
-    return bf16.to_bf16(dp.astype(np.float32)), bf16.to_bf16(d_w.astype(np.float32))
+    return _narrow(dp, f32), _narrow(d_w, f32)
 
 
 # --- The experts' biases ----------------------------------------------------------------
@@ -494,6 +522,15 @@ class Saved(NamedTuple):
     y: np.ndarray | None = None  # with a norm: the down GEMM's rows, bf16 bits (m, d)
 
 
+def _float32_built(fmt: str, passes, up_bias, down_bias, norm) -> None:
+    """The float32 layer this build runs (bux_amd.moe._float32_built): every GEMM in
+    MXFP8, no biases, no norm."""
+    if _passes(fmt, passes) != (True, True, True):
+        raise NotImplementedError("float32 tokens take every GEMM in MXFP8")
+    if up_bias is not None or down_bias is not None or norm is not None:
+        raise NotImplementedError("float32 tokens with biases or an expert norm")
+
+
 def _passes(fmt: str, passes) -> tuple[bool, bool, bool]:
     if fmt not in ("mxfp8", "mxfp8_2d"):
         return False, False, False
@@ -542,12 +579,17 @@ def layer_forward(
     """
     t, k = idx.shape
     e, d, f, p = up.shape
+    f32 = np.asarray(z).dtype == np.float32
+    if f32:
+        _float32_built(fmt, passes, up_bias, down_bias, norm)
+    gemm_out = "f32" if f32 else "bf16"
     s = sort_by_expert(idx, e)
     m = t * k
     filled = int(s.sizes.sum())
     tokens = s.order // k
     inside = (idx.reshape(-1) >= 0) & (idx.reshape(-1) < e)
-    kept = np.where(inside, np.asarray(weights).reshape(-1), np.uint16(0)).astype(np.uint16)
+    w_flat = np.asarray(weights).reshape(-1)
+    kept = np.where(inside, w_flat, w_flat.dtype.type(0)).astype(w_flat.dtype)
     row_weights = kept[s.order]
     up2 = np.asarray(up).reshape(e, d, f * p)
     x_m = up_n = h_m = down_n = None
@@ -560,7 +602,7 @@ def layer_forward(
         up_n, up_k = mxfp8.quantized_twice(up2, d, tiles=tiles)
         down_n, down_k = mxfp8.quantized_twice(down, f, tiles=tiles)
     if fprop:
-        projected = rows_mx(x_k, up_k, s.sizes, height=m, exact=exact)
+        projected = rows_mx(x_k, up_k, s.sizes, out=gemm_out, height=m, exact=exact)
     else:
         projected = ragged_dot_bf16(z[tokens], up2, s.sizes, exact=exact)
     if up_bias is not None:
@@ -570,14 +612,14 @@ def layer_forward(
     if fprop or wgrad:
         h_k, h_m = mxfp8.quantized_twice(h, filled, True, height=whole(m))
     if fprop:
-        y = rows_mx(h_k, down_k, s.sizes, height=m, exact=exact)
+        y = rows_mx(h_k, down_k, s.sizes, out=gemm_out, height=m, exact=exact)
     else:
         y = ragged_dot_bf16(h, down, s.sizes, exact=exact)
     y_rows = None
     if norm is not None:
         y_rows = y
         y = expert_norm_forward(norm, y_rows, s.sizes, row_weights, norm_scale, norm_bias, down_bias)
-    out = sum_by_token(y, s.inverse.reshape(t, k), exact=exact)
+    out = sum_by_token(y, s.inverse.reshape(t, k), out_bf16=not f32, exact=exact)
     if down_bias is not None and norm is None:
         b = weighted_bias_rows(down_bias, s.sizes, row_weights, m)
         bsum = sum_by_token(b, s.inverse.reshape(t, k), exact=exact)
@@ -603,6 +645,8 @@ def layer_backward(
     t = dy.shape[0]
     e, d, f, p = up.shape
     m = t * k
+    f32 = np.asarray(dy).dtype == np.float32
+    gemm_out = "f32" if f32 else "bf16"
     filled = int(s.sizes.sum())
     tokens = s.order // k
     up2 = np.asarray(up).reshape(e, d, f * p)
@@ -622,12 +666,12 @@ def layer_backward(
             dy_n, dy_m = mxfp8.quantized_twice(dy, filled, True, index=tokens, height=whole(m))
         dy_rows = dy[tokens]
     if dgrad:
-        dh = rows_mx(dy_n, saved.down_n, s.sizes, height=m, exact=exact)
+        dh = rows_mx(dy_n, saved.down_n, s.sizes, out=gemm_out, height=m, exact=exact)
     else:
         dh = ragged_dot_bf16(dy_rows, np.ascontiguousarray(np.swapaxes(down, 1, 2)), s.sizes,
                              exact=exact)
     if wgrad:
-        d_down = contract_mx(saved.h_m, dy_m, s.sizes, exact=exact)
+        d_down = contract_mx(saved.h_m, dy_m, s.sizes, out=gemm_out, exact=exact)
     else:
         d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes, exact=exact)
     act_weights = saved.row_weights if norm is None else bf16.to_bf16(np.ones(m, np.float32))
@@ -638,12 +682,12 @@ def layer_backward(
     if dgrad or wgrad:
         dp_n, dp_m = mxfp8.quantized_twice(dp, filled, True, height=whole(m))
     if dgrad:
-        dx = rows_mx(dp_n, saved.up_n, s.sizes, height=m, exact=exact)
+        dx = rows_mx(dp_n, saved.up_n, s.sizes, out=gemm_out, height=m, exact=exact)
     else:
         dx = ragged_dot_bf16(dp, np.ascontiguousarray(np.swapaxes(up2, 1, 2)), s.sizes,
                              exact=exact)
     if wgrad:
-        d_up = contract_mx(saved.x_m, dp_m, s.sizes, exact=exact)
+        d_up = contract_mx(saved.x_m, dp_m, s.sizes, out=gemm_out, exact=exact)
     else:
         d_up = weight_grad_bf16(z[tokens], dp, s.sizes, exact=exact)
     if up_bias is not None:
@@ -658,7 +702,7 @@ def layer_backward(
         grads["down_bias"] = expert_sums(np.where(live, bf16.round_f32(g * w), 0), s.sizes)
         extra = bf16.round_f32(bf16.round_f32(g * b_rows).sum(-1, dtype=np.float32))
         d_rows_w = bf16.to_bf16(bf16.to_f32(d_rows_w) + extra)
-    dz = sum_by_token(dx, s.inverse.reshape(t, k), exact=exact)
+    dz = sum_by_token(dx, s.inverse.reshape(t, k), out_bf16=not f32, exact=exact)
     d_weights = d_rows_w[s.inverse].reshape(t, k)
     grads.update(z=dz, weights=d_weights, up=d_up.reshape(e, d, f, p), down=d_down, dh=dh, dp=dp)
     return grads

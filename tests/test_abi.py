@@ -283,14 +283,18 @@ def test_tile_lists_reject_bad_arguments(lib):
 def test_every_entry_point_has_an_xla_ffi_handler():
     """bux_amd/xla/xla_ffi.cc binds every compute entry point for jax.ffi (the workspace
     sizes are trace-time queries through ctypes; the entry point that allocates nothing
-    is for callers outside XLA, which owns every buffer)."""
+    is for callers outside XLA, which owns every buffer). A float32 twin is called from
+    its bfloat16 twin's handler, which picks by the buffer's element type."""
     src = open(os.path.join(ROOT, "bux_amd", "xla", "xla_ffi.cc")).read()
     called = set(re.findall(r"\b(bux_\w+)\(", src)) - {"bux_last_error"}
     wanted = {n for n in _declared()
               if not n.endswith("_workspace_size")
               and n not in ("bux_last_error", "bux_version", "bux_mx_grouped_rows_noalloc")}
     assert wanted <= called, wanted - called
-    assert len(re.findall(r"XLA_FFI_DEFINE_HANDLER_SYMBOL\(", src)) == len(wanted)
+    twins = {n for n in wanted if n.endswith("_f32")}
+    assert {n[:-4] for n in twins} <= wanted
+    handlers = len(re.findall(r"XLA_FFI_DEFINE_HANDLER_SYMBOL\(", src))
+    assert handlers == len(wanted - twins)
 
 
 def _calls(text: str, name_re: str) -> dict[str, list[int]]:

@@ -355,6 +355,46 @@ def test_each_activation_and_its_derivative_are_torchs(name):
     np.testing.assert_allclose(da, xt.grad.numpy(), rtol=1e-8, atol=1e-14)
 
 
+def _textbook(name, alpha):
+    """functional.py:12-40's activations as written there, in mpmath."""
+    import mpmath as mp
+    sig = lambda v: 1 / (1 + mp.exp(-v))  # noqa: E731
+    return {
+        "swish": lambda v: v * sig(v),
+        "quick_gelu": lambda v: v * sig(alpha * v),
+        "relu": lambda v: mp.mpf(max(v, 0)),
+        "relu2": lambda v: mp.mpf(max(v, 0)) ** 2,
+        "gelu": lambda v: v * (1 + mp.erf(v / mp.sqrt(2))) / 2,
+        "gelu_tanh": lambda v: v * (1 + mp.tanh(mp.sqrt(2 / mp.pi) * (v + mp.mpf("0.044715") * v ** 3))) / 2,
+        "sigmoid": sig,
+        "tanh": mp.tanh,
+        "softplus": lambda v: mp.log(1 + mp.exp(v)),
+        "situ": lambda v: 4 * mp.tanh(v / 4) * sig(v),
+    }[name]
+
+
+@pytest.mark.parametrize("f32", [False, True])
+@pytest.mark.parametrize("name", moe.ACTIVATIONS)
+def test_each_activation_holds_its_relative_precision_in_the_tails(name, f32):
+    """The oracle's values and derivatives to 1e-12 relative of the textbook functions
+    evaluated in 400-digit arithmetic (derivatives by mpmath's numerical differentiation),
+    from x = -700 to 300: e^x-sized values far in the negative tail, where a
+    (1 + tanh) / 2 or 1 + erf form cancels to 0 (values below float64's range, 1e-300,
+    are taken as 0)."""
+    import mpmath as mp
+    alpha = float(np.float32(1.702)) if f32 else moe.QUICK_GELU_ALPHA
+    lo = {"gelu_tanh": -12.0, "gelu": -30.0}.get(name, -700.0)
+    x = np.array([v for v in (-700, -300, -120, -87, -60, -40, -30, -20, -12, -9, -6, -3, -0.5,
+                              0.3, 2.5, 7, 15, 40, 90, 300) if v >= lo], np.float64)
+    a, da = moe._act(name, x, f32)
+    f = _textbook(name, mp.mpf(alpha))
+    with mp.workdps(400):
+        want = np.array([float(f(mp.mpf(v))) for v in x])
+        dwant = np.array([float(mp.diff(f, mp.mpf(v))) for v in x])
+    np.testing.assert_allclose(a, want, rtol=1e-12, atol=1e-300)
+    np.testing.assert_allclose(da, dwant, rtol=1e-12, atol=1e-300)
+
+
 FFNS = [
     # (ffn, p): p = 2 gated (gated_mlp), 1 plain (mlp)
     (moe.Ffn(), 2),
@@ -370,9 +410,10 @@ FFNS = [
 ]
 
 
-def _torch_units(ffn, pt, wt):
+def _torch_units(ffn, pt, wt, alpha=None):
     """weighted_units in torch float64: mlp.activate (layers/mlp.py:20-35), with
-    maximum/minimum for the clip (their gradients 0.5 at a tie, as jax's)."""
+    maximum/minimum for the clip (their gradients 0.5 at a tie, as jax's); `alpha`
+    replaces quick_gelu's."""
     up = pt[..., 0]
     if ffn.limit is not None:
         lim = torch.tensor(ffn.limit, dtype=torch.float64)
@@ -380,6 +421,8 @@ def _torch_units(ffn, pt, wt):
     if ffn.up_softcap is not None:
         up = ffn.up_softcap * torch.tanh(up / ffn.up_softcap)
     act = TORCH_ACTS[ffn.activation]
+    if alpha is not None and ffn.activation == "quick_gelu":
+        act = lambda x: x * torch.sigmoid(alpha * x)  # noqa: E731
     if pt.shape[-1] == 1:
         return act(up) * wt[:, None]
     gate = pt[..., 1]
@@ -406,6 +449,30 @@ def test_the_activations_gradient_is_autograds(ffn, p):
     h.backward(torch.tensor(bf16.to_f32(dh), dtype=torch.float64))
     np.testing.assert_allclose(bf16.to_f32(dp), pt.grad.numpy(), rtol=8e-3, atol=1e-5)
     np.testing.assert_allclose(bf16.to_f32(dw), wt.grad.numpy(), rtol=8e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("ffn,p", FFNS)
+def test_a_float32_layers_activation_rounds_once_to_float32(ffn, p):
+    """In float32 the activation and its gradients come from float32 inputs, each
+    rounded once to float32 (quick_gelu's 1.702 its float32 value, functional.py:29):
+    within float32's rounding of torch's float64 autograd, far inside bfloat16's."""
+    rng = np.random.default_rng(19)
+    m, f = 64, 48
+    pr = (rng.standard_normal((m, f, p)) * 4).astype(np.float32)
+    if ffn.limit is not None:  # ties with the clamp, both signs
+        pr.reshape(-1)[:8] = np.array([1, -1, 1, -1, 2, -2, 0.5, 0], np.float32) * ffn.limit
+    w = rng.random(m).astype(np.float32)
+    dh = rng.standard_normal((m, f)).astype(np.float32)
+    h = moe.weighted_units(ffn, pr, w)
+    dp, dw = moe.weighted_units_backward(ffn, pr, w, dh)
+    assert h.dtype == dp.dtype == dw.dtype == np.float32
+    pt = torch.tensor(pr, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    ht = _torch_units(ffn, pt, wt, alpha=float(np.float32(1.702)))
+    np.testing.assert_allclose(h, ht.detach().numpy(), rtol=1e-6, atol=1e-12)
+    ht.backward(torch.tensor(dh, dtype=torch.float64))
+    np.testing.assert_allclose(dp, pt.grad.numpy(), rtol=1e-6, atol=1e-12)
+    np.testing.assert_allclose(dw, wt.grad.numpy(), rtol=1e-6, atol=1e-9)
 
 
 def test_a_plain_ffn_takes_its_projection_with_or_without_the_last_axis():
