@@ -400,6 +400,179 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
   run_tiles<Bf16<false, false>>(list, count, A, B, lds, Out{dw, f});
 }
 
+// --- any shape ----------------------------------------------------------------------------
+//
+// A matrix whose rows are not a whole number of 16-byte chunks (n or k not a multiple
+// of 8) has rows that start off the chunks, which the direct loads above cannot take;
+// one past 2 GiB has offsets past the buffer loads' 32 bits. These kernels read their
+// operands an element at a time (2-byte loads at 64-bit addresses, each checked against
+// the matrix and the group) into LDS and otherwise multiply as the kernels above do:
+// the same tile list, v_mfma_f32_32x32x16_bf16, float32 sums, one rounding to
+// bfloat16. A workgroup of 4 waves takes 256 rows by 64 columns of the output, wave w
+// its rows 64 w .. 64 w + 63 as 2 x 2 MFMA blocks of 32 x 32; K goes 16 a step. Both
+// operands sit in LDS K-contiguous, 16 elements (32 bytes) a row, so that a lane's
+// MFMA operand (row l % 32, K 8 (l / 32) .. + 7) is one 16-byte read.
+
+constexpr int ANY_BN = 64;
+constexpr int ANY_BK = 16;
+
+struct AnyStage {
+  uint16_t a[BM][ANY_BK];
+  uint16_t b[ANY_BN][ANY_BK];
+};
+
+// The 4 MFMAs of a step: wave w's A blocks 2 w, 2 w + 1 (rows 64 w + 32 p) by B's 2.
+__device__ __forceinline__ void any_step(const AnyStage& st, v16f acc[2][2]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  v8bf a[2], b[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    a[p] = *reinterpret_cast<const v8bf*>(&st.a[wave * 64 + p * 32 + r][8 * h]);
+    b[p] = *reinterpret_cast<const v8bf*>(&st.b[p * 32 + r][8 * h]);
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      acc[p][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p], b[q], acc[p][q], 0, 0, 0);
+}
+
+// The block's outputs: lane l holds column 32 q + l % 32 of rows 64 w + 32 p + 8 (j / 4)
+// + 4 (l / 32) + j % 4, stored where row < rows and column < cols (2-byte stores).
+__device__ __forceinline__ void any_store(const v16f acc[2][2], uint16_t* tile, int64_t ld,
+                                          int32_t rows, int32_t cols) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int32_t col = q * 32 + (lane & 31);
+      if (col >= cols) continue;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int32_t row = wave * 64 + p * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        if (row < rows) tile[row * ld + col] = f32_to_bf16(acc[p][q][j]);
+      }
+    }
+}
+
+__device__ __forceinline__ uint16_t any_at(const uint16_t* p, bool inside) { return inside ? *p : 0; }
+
+// rows, any shape: y[i] = x[i] w[g(i)] (w [g, k, n]; BKM: w [g, n, k] and x[i] w[g(i)]^T).
+// Block b: tile b / col_tiles of the list, columns 64 (b % col_tiles) on.
+template <bool BKM>
+__global__ __launch_bounds__(THREADS) void rows_any_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int32_t groups, int64_t m,
+    int64_t n, int64_t k, const int32_t* __restrict__ starts, const Tile* __restrict__ tiles,
+    int64_t col_tiles, uint16_t* __restrict__ y) {
+  __shared__ __align__(16) AnyStage st;
+  if (!list_fits(starts, groups, static_cast<int32_t>(m), static_cast<int32_t>(m))) return;
+  const int64_t id = blockIdx.x / col_tiles;
+  if (id >= starts[groups + 1]) return;
+  const Tile t = tiles[id];
+  const int64_t col0 = (blockIdx.x % col_tiles) * ANY_BN;
+  const int64_t hi = t.hi < m ? t.hi : m;
+  const int32_t rows = static_cast<int32_t>(hi - t.lo);
+  if (rows <= 0) return;
+  const int32_t cols = static_cast<int32_t>(n - col0 < ANY_BN ? n - col0 : ANY_BN);
+  v16f acc[2][2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[p][q][j] = 0.0f;
+  if (t.group < groups) {  // the rows past the groups: zeros
+    const uint16_t* wg = w + static_cast<int64_t>(t.group) * n * k;
+    const int tid = threadIdx.x, kk = tid & 15;
+    for (int64_t k0 = 0; k0 < k; k0 += ANY_BK) {
+      const bool kin = k0 + kk < k;
+      uint16_t av[16], bv[4];
+      // A: 16 rows an instruction, 16 consecutive K of each
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int32_t r = (tid >> 4) + 16 * i;
+        av[i] = any_at(x + (t.lo + r) * k + k0 + kk, kin && r < rows);
+      }
+      if constexpr (BKM) {  // w [g, n, k]: 16 columns an instruction, 16 consecutive K
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int32_t c = (tid >> 4) + 16 * i;
+          bv[i] = any_at(wg + (col0 + c) * k + k0 + kk, kin && c < cols);
+        }
+      } else {  // w [g, k, n]: K row tid / 16, 4 consecutive columns
+        const int64_t kr = k0 + (tid >> 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int32_t c = 4 * (tid & 15) + i;
+          bv[i] = any_at(wg + kr * n + col0 + c, kr < k && c < cols);
+        }
+      }
+      __syncthreads();  // the last step's reads are done
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st.a[(tid >> 4) + 16 * i][kk] = av[i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (BKM) st.b[(tid >> 4) + 16 * i][kk] = bv[i];
+        else st.b[4 * (tid & 15) + i][tid >> 4] = bv[i];
+      }
+      __syncthreads();
+      any_step(st, acc);
+    }
+  }
+  any_store(acc, y + t.lo * n + col0, n, rows, cols);
+}
+
+// contract, any shape: dw[g] = x[rows of g]^T dy[rows of g], x [m, k], dy [m, n], dw
+// [g, k, n]; K is the group's rows. Block b: group b / (k_tiles col_tiles), its rows of
+// dw 256 (b / col_tiles % k_tiles) on, columns 64 (b % col_tiles) on.
+__global__ __launch_bounds__(THREADS) void contract_any_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy, int32_t groups, int64_t m,
+    int64_t k, int64_t n, const int32_t* __restrict__ starts, int64_t k_tiles, int64_t col_tiles,
+    uint16_t* __restrict__ dw) {
+  __shared__ __align__(16) AnyStage st;
+  if (!list_fits(starts, groups, -1, 0)) return;
+  const int64_t per = k_tiles * col_tiles;
+  const int32_t g = static_cast<int32_t>(blockIdx.x / per);
+  const int64_t row0 = (blockIdx.x / col_tiles % k_tiles) * BM, col0 = (blockIdx.x % col_tiles) * ANY_BN;
+  const int32_t rows = static_cast<int32_t>(k - row0 < BM ? k - row0 : BM);
+  const int32_t cols = static_cast<int32_t>(n - col0 < ANY_BN ? n - col0 : ANY_BN);
+  v16f acc[2][2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[p][q][j] = 0.0f;
+  const int64_t start = starts[g], end = starts[g + 1] < m ? starts[g + 1] : m;
+  const int tid = threadIdx.x;
+  for (int64_t i0 = start; i0 < end; i0 += ANY_BK) {
+    uint16_t av[16], bv[4];
+    // A(r, i) = x[i][r]: thread tid takes r = tid of the 16 rows i
+#pragma unroll
+    for (int i = 0; i < 16; ++i) av[i] = any_at(x + (i0 + i) * k + row0 + tid, i0 + i < end && tid < rows);
+    // B(c, i) = dy[i][c]: row i0 + tid / 16, 4 consecutive columns
+    const int64_t ir = i0 + (tid >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int32_t c = 4 * (tid & 15) + i;
+      bv[i] = any_at(dy + ir * n + col0 + c, ir < end && c < cols);
+    }
+    __syncthreads();
+    uint32_t packed[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) packed[i] = av[2 * i] | (static_cast<uint32_t>(av[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4*>(&st.a[tid][0]) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    *reinterpret_cast<uint4*>(&st.a[tid][8]) = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.b[4 * (tid & 15) + i][tid >> 4] = bv[i];
+    __syncthreads();
+    any_step(st, acc);
+  }
+  any_store(acc, dw + (static_cast<int64_t>(g) * k + row0) * n + col0, n, rows, cols);
+}
+
 // Whether every offset a kernel forms into an operand of `rows` rows of `cols` elements
 // (a tile's reads past it included) fits the 32-bit buffer offsets.
 bool fits(int64_t rows, int64_t cols) { return (rows + BM) * (cols + BM) * 2 < (1LL << 31); }
@@ -437,11 +610,7 @@ extern "C" int bux_bf16_grouped_rows(const uint16_t* x, const uint16_t* w, int w
             groups, MAX_GROUPS);
   BUX_CHECK(m >= 0 && n > 0 && k > 0, "bux_bf16_grouped_rows: bad shape m=%lld n=%lld k=%lld",
             (long long)m, (long long)n, (long long)k);
-  BUX_CHECK(n % 8 == 0 && k % 8 == 0, "bux_bf16_grouped_rows: n=%lld and k=%lld must be multiples of 8",
-            (long long)n, (long long)k);
-  BUX_CHECK(fits(m, k) && (w_transposed ? fits(n, k) : fits(k, n)),
-            "bux_bf16_grouped_rows: an operand of m=%lld n=%lld k=%lld exceeds 2 GiB", (long long)m,
-            (long long)n, (long long)k);
+  BUX_CHECK(m < INT32_MAX, "bux_bf16_grouped_rows: m=%lld rows", (long long)m);
   BUX_CHECK(sizes && w && y && (m == 0 || x), "bux_bf16_grouped_rows: NULL buffer");
   const size_t need = bux_bf16_grouped_rows_workspace_size(groups, m);
   if (workspace == nullptr || workspace_bytes < need)
@@ -453,6 +622,21 @@ extern "C" int bux_bf16_grouped_rows(const uint16_t* x, const uint16_t* w, int w
                      row_slots(groups, m, m), 1, starts_in(workspace), tiles_in(workspace, groups),
                      header_in(workspace), m, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
+  // n or k off 16-byte rows, or an operand past 32-bit offsets: the any-shape kernel
+  if (n % 8 != 0 || k % 8 != 0 || !fits(m, k) || !(w_transposed ? fits(n, k) : fits(k, n))) {
+    const int64_t col_tiles = ceil_div(n, ANY_BN), slots = row_slots(groups, m, m);
+    const int64_t blocks = slots * col_tiles;
+    BUX_CHECK(blocks < (1LL << 31), "bux_bf16_grouped_rows: too many tiles");
+    if (w_transposed)
+      hipLaunchKernelGGL(rows_any_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0, s,
+                         x, w, groups, m, n, k, starts_in(workspace), tiles_in(workspace, groups),
+                         col_tiles, y);
+    else
+      hipLaunchKernelGGL(rows_any_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0, s,
+                         x, w, groups, m, n, k, starts_in(workspace), tiles_in(workspace, groups),
+                         col_tiles, y);
+    return launched("bf16 rows_any_kernel");
+  }
   const Operand A{x, static_cast<int32_t>(k), static_cast<int32_t>(m * k * 2), 0};
   const Operand B{w, static_cast<int32_t>(w_transposed ? k : n), static_cast<int32_t>(n * k * 2), n * k};
   const bool tail = k % BK != 0;
@@ -478,12 +662,7 @@ extern "C" int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, 
             "bux_bf16_grouped_contract: groups=%d outside [1, %d]", groups, MAX_GROUPS);
   BUX_CHECK(m >= 0 && n > 0 && k > 0, "bux_bf16_grouped_contract: bad shape m=%lld k=%lld n=%lld",
             (long long)m, (long long)k, (long long)n);
-  BUX_CHECK(n % 8 == 0 && k % 8 == 0,
-            "bux_bf16_grouped_contract: k=%lld and n=%lld must be multiples of 8", (long long)k,
-            (long long)n);
-  BUX_CHECK(fits(m, k) && fits(m, n),
-            "bux_bf16_grouped_contract: an operand of m=%lld k=%lld n=%lld exceeds 2 GiB",
-            (long long)m, (long long)k, (long long)n);
+  BUX_CHECK(m < INT32_MAX, "bux_bf16_grouped_contract: m=%lld rows", (long long)m);
   BUX_CHECK(sizes && dw && (m == 0 || (x && dy)), "bux_bf16_grouped_contract: NULL buffer");
   const size_t need = bux_bf16_grouped_contract_workspace_size(groups);
   if (workspace == nullptr || workspace_bytes < need)
@@ -494,6 +673,14 @@ extern "C" int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, 
   hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
                      starts_in(workspace), nullptr, header_in(workspace), m, nullptr);
   if (int rc = launched("prologue_kernel")) return rc;
+  if (n % 8 != 0 || k % 8 != 0 || !fits(m, k) || !fits(m, n)) {  // the any-shape kernel
+    const int64_t k_tiles = ceil_div(k, BM), col_tiles = ceil_div(n, ANY_BN);
+    const int64_t blocks = static_cast<int64_t>(groups) * k_tiles * col_tiles;
+    BUX_CHECK(blocks < (1LL << 31), "bux_bf16_grouped_contract: too many tiles");
+    hipLaunchKernelGGL(contract_any_kernel, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0, s, x,
+                       dy, groups, m, k, n, starts_in(workspace), k_tiles, col_tiles, dw);
+    return launched("bf16 contract_any_kernel");
+  }
   const int64_t d_tiles = ceil_div(k, BM), f_tiles = ceil_div(n, BN);
   const int64_t tiles = static_cast<int64_t>(groups) * d_tiles * f_tiles;
   BUX_CHECK(tiles < (1LL << 31), "bux_bf16_grouped_contract: too many tiles");

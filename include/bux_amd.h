@@ -250,8 +250,11 @@ int bux_mx_grouped_contract(const uint8_t* a_values, const uint8_t* a_scales,
  * bux_bf16_grouped_contract replaces grouped.weight_grad (grouped.py:105-146):
  * dw[g] = x[rows of g]^T dy[rows of g], x [m, k], dy [m, n] -> dw [groups, k, n]; 0 for
  * an empty group.
- * n and k multiples of 8; every operand (plus a tile of 256 past it each way) under
- * 2 GiB. workspace: bux_bf16_grouped_rows_workspace_size(groups, m) /
+ * Any n and k. With n and k multiples of 8 and every operand (plus a tile of 256 past
+ * it each way) under 2 GiB, the operands' rows go to LDS by 16-byte direct loads; other
+ * shapes (the reference's ragged_dot takes any) are read an element at a time by
+ * slower kernels with the same sums and rounding. m under 2^31. workspace:
+ * bux_bf16_grouped_rows_workspace_size(groups, m) /
  * bux_bf16_grouped_contract_workspace_size(groups) bytes (the group starts and the
  * tile list that each call builds on the device).
  */

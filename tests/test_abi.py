@@ -101,17 +101,18 @@ def test_gemms_reject_bad_shapes_and_small_workspaces(lib):
     assert rc == 1 and "rows exceeds 33554176" in _msg(lib)
     rc = lib.bux_mx_grouped_contract(p, p, p, p, p, 4, 64, 64, 128, 0, p, p, 4, None)
     assert rc == 2 and "workspace" in _msg(lib)
-    rc = lib.bux_bf16_grouped_rows(p, p, 0, p, 4, 64, 100, 64, p, p, 1 << 20, None)
-    assert rc == 1 and "multiples of 8" in _msg(lib)
+    # any n and k (off multiples of 8 and past 2 GiB: the any-shape kernels); rows in int32
+    rc = lib.bux_bf16_grouped_rows(p, p, 0, p, 4, 64, 100, 37, p, p, 8, None)
+    assert rc == 2 and "workspace" in _msg(lib)
     rc = lib.bux_bf16_grouped_rows(p, p, 0, p, 4, 64, 128, 64, p, p, 8, None)
     assert rc == 2 and "workspace" in _msg(lib)
     assert lib.bux_bf16_grouped_rows_workspace_size(4, 64) >= 64 + 6 * 4 + 6 * 12
-    rc = lib.bux_bf16_grouped_rows(p, p, 1, p, 4, 1 << 20, 128, 2048, p, p, 1 << 30, None)
-    assert rc == 1 and "exceeds 2 GiB" in _msg(lib)
-    rc = lib.bux_bf16_grouped_contract(p, p, p, 4, 64, 64, 100, p, p, 1 << 10, None)
-    assert rc == 1 and "multiples of 8" in _msg(lib)
-    rc = lib.bux_bf16_grouped_contract(p, p, p, 4, 64, 64, 128, p, p, 4, None)
+    rc = lib.bux_bf16_grouped_rows(p, p, 1, p, 4, 1 << 31, 128, 2048, p, p, 1 << 30, None)
+    assert rc == 1 and "m=2147483648 rows" in _msg(lib)
+    rc = lib.bux_bf16_grouped_contract(p, p, p, 4, 64, 45, 100, p, p, 4, None)
     assert rc == 2 and "workspace" in _msg(lib)
+    rc = lib.bux_bf16_grouped_contract(p, p, p, 4, 1 << 31, 64, 128, p, p, 1 << 10, None)
+    assert rc == 1 and "m=2147483648 rows" in _msg(lib)
 
 
 def test_fused_up_gemm_rejects_bad_arguments(lib):

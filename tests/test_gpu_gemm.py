@@ -274,6 +274,11 @@ BF16_ROWS = {
     "k under one step, n of 8": ([5, 0, 7], 20, 8, 8),
     "one row": ([1], 1, 64, 64),
     "all groups empty": ([0, 0, 0], 300, 64, 64),
+    # rows off 16-byte chunks: the any-shape kernels (element loads)
+    "n and k off multiples of 8": ([300, 0, 41, 500], 900, 45, 37),
+    "k off 8, n whole tiles": ([700, 3, 297], 1000, 100, 264),
+    "k and n of 1": ([5, 0, 3], 10, 1, 1),
+    "n off 8, 64 small groups": (None, 1500, 64, 70),
 }
 
 
@@ -318,6 +323,10 @@ BF16_CONTRACT = {
     "64 small groups": (None, 1500, 128, 256),
     "k and n of 8, rows under one step": ([3, 0, 9], 16, 8, 8),
     "all groups empty": ([0, 0], 100, 64, 64),
+    # rows off 16-byte chunks: the any-shape kernel
+    "k and n off multiples of 8": ([33, 0, 95, 1, 200], 400, 45, 37),
+    "k of 300, n of 3": ([70, 0, 100, 3, 77], 256, 300, 3),
+    "all groups empty, n off 8": ([0, 0], 100, 5, 9),
 }
 
 
