@@ -31,4 +31,6 @@ int launched(const char* kernel) {
 
 extern "C" const char* bux_last_error(void) { return bux::last_error; }
 
-extern "C" int bux_version(void) { return 200; }
+// 0.3.0: the float32 twins (bux_mx_quantize_f32, bux_glu_quantize_f32,
+// bux_glu_backward_quantize_f32, bux_token_sums_f32) and bfloat16 GEMMs of any shape.
+extern "C" int bux_version(void) { return 300; }
