@@ -89,6 +89,31 @@ def test_gradients_double_with_dy_and_the_forward_repeats(lib, name):
         assert torch.equal(_bits(g1[key] * 2), _bits(g2[key])), f"d{key} is not doubled exactly"
 
 
+@pytest.mark.parametrize("name", ["config3", "config4"])
+def test_a_float32_layers_gradients_double_with_dy_and_its_forward_repeats(lib, name):
+    """The same properties for tokens and kernels in float32 (the kernels cast to the
+    tokens' dtype, y and every gradient float32): doubling dy doubles each float32
+    product and sum exactly, and the activation's gradient is linear in dh."""
+    from bux_amd import moe
+    cfg = CONFIGS[name]
+    z, idx, w, up, down, dy = (x.float() if x.dtype == torch.bfloat16 else x
+                               for x in _inputs(cfg, 4))
+    ffn = moe.Ffn(*cfg["act"])
+    announce("full size float32", name, "dy and 2 dy")
+    out1, g1 = _layer(z, idx, w, up, down, dy, ffn)
+    out2, g2 = _layer(z, idx, w, up, down, dy * 2, ffn)
+    torch.cuda.synchronize()
+    assert out1.dtype == torch.float32
+    assert torch.equal(out1.view(torch.int32), out2.view(torch.int32)), "the forward differs"
+    assert torch.isfinite(out1).all()
+    for key in g1:
+        assert g1[key].dtype == torch.float32, key
+        assert torch.isfinite(g1[key]).all(), key
+        assert g1[key].abs().max() > 0, key
+        assert torch.equal((g1[key] * 2).view(torch.int32), g2[key].view(torch.int32)), \
+            f"d{key} is not doubled exactly"
+
+
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_a_permutation_of_the_tokens_permutes_y_and_dz(lib, name):
     from bux_amd import moe
