@@ -4,12 +4,14 @@
 // Semantics: src/bux/architecture/precision/blockscaled.py:282-356 (mx_twice,
 // mx_quantize, _in_e4m3, _ceil_log2, _power_of_two) as grouped_blockscaled._quantized
 // (grouped_blockscaled.py:296-317) applies them, and grouped_triton.quantized_twice
-// (grouped_triton.py:44-101) for rows read by index. Per block of 32 values v (bfloat16,
-// widened exactly to float32):
+// (grouped_triton.py:44-101) for rows read by index. Per block of 32 values v (bfloat16
+// widened exactly to float32, or float32 for a layer in float32):
 //   e      = ceil_log2(max|v| / 448) clipped to [-126, 126]   scale byte e + 127
 //   code_i = RNE_E4M3(clip(v_i * 2^-e, -448, 448))
 // v_i * 2^-e is exact in float32 as in bfloat16 (a power of two, no overflow), so the
-// float32 product gives the reference's bfloat16 product's code.
+// float32 product gives the reference's bfloat16 product's code. The exponent of a
+// bfloat16 block comes from its maximum's bits; of a float32 block, from the float32
+// quotient max / 448 (a float32 maximum has mantissa bits the shortcut would drop).
 //
 // The copies are written in the grouped GEMMs' tiled layout (include/bux_amd.h): codes
 // [K/64][rows][64] and scale bytes [K/128][rows][4], K padded to whole 128s by codes of
@@ -32,8 +34,8 @@
 //     tile's 128 rows as one word. The tile's 16-byte chunks are swizzled by row (chunk
 //     c of row r at c ^ 2 ((r / 16) % 4)), so that the four lanes' rows, 16 apart, read
 //     different banks.
-// HBM traffic per element: 2 bytes read, 2 x (1 + 1/32) bytes written; the codes go
-// out as non-temporal stores (below).
+// HBM traffic per element: 2 bytes read (4 of float32), 2 x (1 + 1/32) bytes written; the
+// codes go out as non-temporal stores (below).
 //
 // With BUX_MX_TILES the scale is one per 32 x 32 tile of x instead (the mxfp8_2d
 // recipe's weights, blockscaled.py:294-309): xor-shuffles reduce each tile's largest
