@@ -95,6 +95,14 @@ SIGNATURES = {
     "bux_expert_norm_backward": (
         _int, [_p, _p, _i32, _i64, _p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p, _p, _p,
                _p, _size, _p]),
+    "bux_token_sums_biased_f32": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p, _i32, _p, _p, _p]),
+    "bux_expert_bias_add_f32": (_int, [_p, _i64, _i64, _p, _p, _i32, _p]),
+    "bux_expert_sums_f32": (_int, [_p, _p, _i32, _i64, _p, _i64, _i64, _p, _i32, _p, _p]),
+    "bux_expert_bias_weight_grad_f32": (_int, [_p, _p, _i32, _i64, _i64, _i64, _p, _p, _i32, _p, _p]),
+    "bux_expert_norm_forward_f32": (_int, [_p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p]),
+    "bux_expert_norm_backward_f32": (
+        _int, [_p, _p, _i32, _i64, _p, _i64, _i64, _p, _p, _i32, _norm, _p, _p, _p, _p, _p, _p, _p,
+               _p, _size, _p]),
     "bux_glu_forward": (_int, [_p, _p, _p, _i64, _i64, _ffn, _p, _p]),
     "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _ffn, _p, _p, _p]),
     "bux_glu_quantize": (

@@ -33,4 +33,7 @@ extern "C" const char* bux_last_error(void) { return bux::last_error; }
 
 // 0.3.0: the float32 twins (bux_mx_quantize_f32, bux_glu_quantize_f32,
 // bux_glu_backward_quantize_f32, bux_token_sums_f32) and bfloat16 GEMMs of any shape.
-extern "C" int bux_version(void) { return 300; }
+// 0.3.1: float32 twins of the bias ops (bux_expert_bias_add_f32, bux_expert_sums_f32,
+// bux_token_sums_biased_f32, bux_expert_bias_weight_grad_f32) and of the expert norm
+// (bux_expert_norm_forward_f32, bux_expert_norm_backward_f32).
+extern "C" int bux_version(void) { return 301; }

@@ -91,6 +91,55 @@ __device__ __forceinline__ float power_of_two_down(int e) {
 
 __device__ __forceinline__ float clip448(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
 
+// --- the layer's element types ----------------------------------------------------
+
+// A layer computes in its tokens' dtype (the reference's x.dtype, experts/moe.py:846):
+// bfloat16, each op's float32 result rounded to it, or float32. Elem<T> moves 8
+// elements at once (16 or 32 bytes, aligned) as float32 values and rounds a float32
+// result as one op in T does.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<uint16_t> {
+  static __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bf16_to_f32(static_cast<uint16_t>(w[j] & 0xffffu));
+      v[2 * j + 1] = bf16_to_f32(static_cast<uint16_t>(w[j] >> 16));
+    }
+  }
+  static __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = static_cast<uint32_t>(f32_to_bf16(v[2 * j])) |
+             (static_cast<uint32_t>(f32_to_bf16(v[2 * j + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  static __device__ __forceinline__ float value(uint16_t x) { return bf16_to_f32(x); }
+  static __device__ __forceinline__ uint16_t make(float x) { return f32_to_bf16(x); }
+  static __device__ __forceinline__ float round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+};
+
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ void load8(const float* p, float* v) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store8(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  static __device__ __forceinline__ float value(float x) { return x; }
+  static __device__ __forceinline__ float make(float x) { return x; }
+  static __device__ __forceinline__ float round(float x) { return x; }
+};
+
 // --- direct loads into LDS ---------------------------------------------------------
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));

@@ -101,12 +101,13 @@ __global__ __launch_bounds__(THREADS) void token_rows_narrow_kernel(
 // The additions are the same either way: picks in order, a row outside y skipped.
 // With BIAS, a second sum beside: each pick's bias[e(r)] * weights[r] (rounded to
 // bfloat16), the picks of rows in no expert adding 0; out = the two sums, each rounded
-// to bfloat16, added and rounded.
+// to bfloat16, added and rounded. T: the layer's element type.
+template <typename T>
 struct PickBias {
-  const uint16_t* bias;
+  const T* bias;
   const int32_t* offsets;
   int32_t experts;
-  const uint16_t* weights;
+  const T* weights;
 };
 
 template <int KMAX, bool BIAS>
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __r
                                                              int64_t y_rows,
                                                              const int32_t* __restrict__ inverse,
                                                              int32_t k, int64_t width,
-                                                             PickBias pb,
+                                                             PickBias<uint16_t> pb,
                                                              uint16_t* __restrict__ out) {
   const int64_t chunks = (width + THREADS * VEC - 1) / (THREADS * VEC);
   const int64_t t = blockIdx.x / chunks;
@@ -169,16 +170,20 @@ __global__ __launch_bounds__(THREADS) void token_sums_kernel(const uint16_t* __r
   *reinterpret_cast<uint4*>(out + t * width + c) = pack8(acc);
 }
 
-// token_sums_kernel<KMAX, false> for a layer in float32: float32 rows, the picks added
-// in the same order, the float32 sum stored as it is (the reference's sum_by_token casts
-// its float32 sum back to y's dtype, grouped_blockscaled.py:148). A lane moves 8 floats
-// (32 bytes) a pick.
-template <int KMAX>
+// token_sums_kernel for a layer in float32: float32 rows, the picks added in the same
+// order, the float32 sum stored as it is (the reference's sum_by_token casts its float32
+// sum back to y's dtype, grouped_blockscaled.py:148); with BIAS the picks' float32
+// products bias[e(r)] * weights[r] summed beside and added. A lane moves 8 floats (32
+// bytes) a pick.
+template <int KMAX, bool BIAS>
 __global__ __launch_bounds__(THREADS) void token_sums_f32_kernel(const float* __restrict__ y,
                                                                  int64_t y_rows,
                                                                  const int32_t* __restrict__ inverse,
                                                                  int32_t k, int64_t width,
+                                                                 PickBias<float> pb,
                                                                  float* __restrict__ out) {
+  // Each product rounds before it is added, as the reference's ops do (no FMA contraction).
+#pragma clang fp contract(off)
   const int64_t chunks = (width + THREADS * VEC - 1) / (THREADS * VEC);
   const int64_t t = blockIdx.x / chunks;
   const int64_t c = ((blockIdx.x % chunks) * THREADS + threadIdx.x) * VEC;
@@ -201,6 +206,22 @@ __global__ __launch_bounds__(THREADS) void token_sums_f32_kernel(const float* __
       const int64_t r = inverse[t * k + j];
       if (r >= 0 && r < y_rows) add(reinterpret_cast<const float4*>(y + r * width + c));
     }
+  }
+  if constexpr (BIAS) {
+    float bsum[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < k; ++j) {
+      const int64_t r = inverse[t * k + j];
+      if (r < 0 || r >= y_rows) continue;
+      const int32_t e = expert_of(pb.offsets, pb.experts, r);
+      if (e < 0) continue;
+      const float w = pb.weights[r];
+      float b[VEC];
+      Elem<float>::load8(pb.bias + e * width + c, b);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) bsum[q] += b[q] * w;
+    }
+    acc[0].x += bsum[0]; acc[0].y += bsum[1]; acc[0].z += bsum[2]; acc[0].w += bsum[3];
+    acc[1].x += bsum[4]; acc[1].y += bsum[5]; acc[1].z += bsum[6]; acc[1].w += bsum[7];
   }
   float4* o = reinterpret_cast<float4*>(out + t * width + c);
   o[0] = acc[0];
@@ -289,32 +310,41 @@ __global__ __launch_bounds__(THREADS) void glu_backward_kernel(
 
 // --- The experts' biases --------------------------------------------------------------
 
+// The bias kernels take the layer's element type T (uint16_t: bfloat16 bits, each op
+// rounded to bfloat16; float: float32 ops).
+
 // x[i] += bias[e(i)] in place, 8 columns a lane; rows in no expert add 0.
+template <typename T>
 __global__ __launch_bounds__(THREADS) void expert_bias_add_kernel(
-    uint16_t* __restrict__ x, int64_t width, const uint16_t* __restrict__ bias,
+    T* __restrict__ x, int64_t width, const T* __restrict__ bias,
     const int32_t* __restrict__ offsets, int32_t experts) {
+  using E = Elem<T>;
   const int64_t chunks = (width + THREADS * VEC - 1) / (THREADS * VEC);
   const int64_t i = blockIdx.x / chunks;
   const int64_t c = ((blockIdx.x % chunks) * THREADS + threadIdx.x) * VEC;
   if (c >= width) return;
   const int32_t e = expert_of(offsets, experts, i);
   float v[VEC], b[VEC] = {0, 0, 0, 0, 0, 0, 0, 0};
-  uint4* at = reinterpret_cast<uint4*>(x + i * width + c);
-  unpack8(*at, v);
-  if (e >= 0) unpack8(*reinterpret_cast<const uint4*>(bias + e * width + c), b);
+  T* at = x + i * width + c;
+  E::load8(at, v);
+  if (e >= 0) E::load8(bias + e * width + c, b);
 #pragma unroll
   for (int q = 0; q < VEC; ++q) v[q] += b[q];
-  *at = pack8(v);
+  E::store8(at, v);
 }
 
-// out[e] = sum over e's rows of v_r (x[src(r)], times weights[r] rounded to bfloat16 if
+// out[e] = sum over e's rows of v_r (x[src(r)], times weights[r] rounded to T if
 // weights). Workgroup (e, column chunk): wave w adds rows w, w + 4, ... of e in order,
 // lanes 8 columns each; the four waves' sums are added in wave order. Deterministic.
 constexpr int SUM_COLS = 64 * VEC;  // a workgroup's columns
+template <typename T>
 __global__ __launch_bounds__(THREADS) void expert_sums_kernel(
-    const uint16_t* __restrict__ x, const int32_t* __restrict__ index, int32_t index_div,
-    int64_t sources, const uint16_t* __restrict__ weights, int64_t m, int64_t width,
+    const T* __restrict__ x, const int32_t* __restrict__ index, int32_t index_div,
+    int64_t sources, const T* __restrict__ weights, int64_t m, int64_t width,
     const int32_t* __restrict__ offsets, int32_t experts, float* __restrict__ out) {
+  // Each product rounds before it is added, as the reference's ops do (no FMA contraction).
+#pragma clang fp contract(off)
+  using E = Elem<T>;
   __shared__ float part[THREADS / 64][SUM_COLS];
   const int64_t chunks = (width + SUM_COLS - 1) / SUM_COLS;
   const int64_t e = blockIdx.x / chunks;
@@ -330,11 +360,11 @@ __global__ __launch_bounds__(THREADS) void expert_sums_kernel(
       const int64_t src = index ? source_row(index[r], index_div, sources) : r;
       if (src < 0) continue;  // a row of 0
       float v[VEC];
-      unpack8(*reinterpret_cast<const uint4*>(x + src * width + c), v);
+      E::load8(x + src * width + c, v);
       if (weights) {
-        const float w = bf16_to_f32(weights[r]);
+        const float w = E::value(weights[r]);
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) v[q] = bf16_to_f32(f32_to_bf16(v[q] * w));
+        for (int q = 0; q < VEC; ++q) v[q] = E::round(v[q] * w);
       }
 #pragma unroll
       for (int q = 0; q < VEC; ++q) acc[q] += v[q];
@@ -355,12 +385,16 @@ __global__ __launch_bounds__(THREADS) void expert_sums_kernel(
 }
 
 // d_weights[r] += sum_c dy[src(r)][c] bias[e(r)][c]: one wave a row, lanes 8 columns a
-// step, each lane's products (rounded to bfloat16) in column order, then the lanes by
-// xor-shuffles.
+// step, each lane's products (rounded to T) in column order, then the lanes by
+// xor-shuffles; the sum rounded to T, added and rounded.
+template <typename T>
 __global__ __launch_bounds__(THREADS) void expert_bias_weight_grad_kernel(
-    const uint16_t* __restrict__ dy, const int32_t* __restrict__ index, int32_t index_div,
-    int64_t sources, int64_t m, int64_t width, const uint16_t* __restrict__ bias,
-    const int32_t* __restrict__ offsets, int32_t experts, uint16_t* __restrict__ d_weights) {
+    const T* __restrict__ dy, const int32_t* __restrict__ index, int32_t index_div,
+    int64_t sources, int64_t m, int64_t width, const T* __restrict__ bias,
+    const int32_t* __restrict__ offsets, int32_t experts, T* __restrict__ d_weights) {
+  // Each product rounds before it is added, as the reference's ops do (no FMA contraction).
+#pragma clang fp contract(off)
+  using E = Elem<T>;
   const int lane = threadIdx.x & 63;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * (THREADS / 64) + (threadIdx.x >> 6);
   if (r >= m) return;
@@ -370,16 +404,15 @@ __global__ __launch_bounds__(THREADS) void expert_bias_weight_grad_kernel(
   if (src >= 0) {
     for (int64_t c = lane * VEC; c < width; c += 64 * VEC) {
       float g[VEC], b[VEC];
-      unpack8(*reinterpret_cast<const uint4*>(dy + src * width + c), g);
-      unpack8(*reinterpret_cast<const uint4*>(bias + e * width + c), b);
+      E::load8(dy + src * width + c, g);
+      E::load8(bias + e * width + c, b);
 #pragma unroll
-      for (int q = 0; q < VEC; ++q) sum += bf16_to_f32(f32_to_bf16(g[q] * b[q]));
+      for (int q = 0; q < VEC; ++q) sum += E::round(g[q] * b[q]);
     }
   }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) sum += __shfl_xor(sum, s);
-  if (lane == 0)
-    d_weights[r] = f32_to_bf16(bf16_to_f32(d_weights[r]) + bf16_to_f32(f32_to_bf16(sum)));
+  if (lane == 0) d_weights[r] = E::make(E::value(d_weights[r]) + E::round(sum));
 }
 
 }  // namespace
@@ -410,8 +443,8 @@ extern "C" int bux_token_rows(const uint16_t* z, int64_t tokens, const int32_t* 
 namespace bux {
 namespace {
 int token_sums(const char* name, const uint16_t* y, int64_t y_rows, const int32_t* inverse,
-               int64_t tokens, int32_t k, int64_t width, const PickBias* pb, uint16_t* out,
-               void* stream) {
+               int64_t tokens, int32_t k, int64_t width, const PickBias<uint16_t>* pb,
+               uint16_t* out, void* stream) {
   BUX_CHECK(tokens >= 0 && tokens <= 2147483647LL && k >= 1 && width > 0 && y_rows >= 0,
             "%s: bad shape tokens=%lld k=%d width=%lld", name, (long long)tokens, k,
             (long long)width);
@@ -421,7 +454,7 @@ int token_sums(const char* name, const uint16_t* y, int64_t y_rows, const int32_
   BUX_CHECK(y && inverse && out, "%s: NULL buffer", name);
   BUX_CHECK(tokens * ceil_div(width, THREADS * VEC) < (1LL << 31), "%s: too large", name);
   dim3 grid(static_cast<unsigned>(tokens * ceil_div(width, THREADS * VEC)));
-  const PickBias none{nullptr, nullptr, 0, nullptr};
+  const PickBias<uint16_t> none{nullptr, nullptr, 0, nullptr};
   hipStream_t s = as_stream(stream);
   if (pb)
     hipLaunchKernelGGL((token_sums_kernel<0, true>), grid, dim3(THREADS), 0, s, y, y_rows,
@@ -436,7 +469,8 @@ int token_sums(const char* name, const uint16_t* y, int64_t y_rows, const int32_
 }
 
 int token_sums_f32(const char* name, const float* y, int64_t y_rows, const int32_t* inverse,
-                   int64_t tokens, int32_t k, int64_t width, float* out, void* stream) {
+                   int64_t tokens, int32_t k, int64_t width, const PickBias<float>* pb,
+                   float* out, void* stream) {
   BUX_CHECK(tokens >= 0 && tokens <= 2147483647LL && k >= 1 && width > 0 && y_rows >= 0,
             "%s: bad shape tokens=%lld k=%d width=%lld", name, (long long)tokens, k,
             (long long)width);
@@ -447,12 +481,16 @@ int token_sums_f32(const char* name, const float* y, int64_t y_rows, const int32
   BUX_CHECK(tokens * ceil_div(width, THREADS * VEC) < (1LL << 31), "%s: too large", name);
   dim3 grid(static_cast<unsigned>(tokens * ceil_div(width, THREADS * VEC)));
   hipStream_t s = as_stream(stream);
-  if (k <= 8)
-    hipLaunchKernelGGL((token_sums_f32_kernel<8>), grid, dim3(THREADS), 0, s, y, y_rows, inverse,
-                       k, width, out);
+  const PickBias<float> none{nullptr, nullptr, 0, nullptr};
+  if (pb)
+    hipLaunchKernelGGL((token_sums_f32_kernel<0, true>), grid, dim3(THREADS), 0, s, y, y_rows,
+                       inverse, k, width, *pb, out);
+  else if (k <= 8)
+    hipLaunchKernelGGL((token_sums_f32_kernel<8, false>), grid, dim3(THREADS), 0, s, y, y_rows,
+                       inverse, k, width, none, out);
   else
-    hipLaunchKernelGGL((token_sums_f32_kernel<0>), grid, dim3(THREADS), 0, s, y, y_rows, inverse,
-                       k, width, out);
+    hipLaunchKernelGGL((token_sums_f32_kernel<0, false>), grid, dim3(THREADS), 0, s, y, y_rows,
+                       inverse, k, width, none, out);
   return launched("token_sums_f32_kernel");
 }
 
@@ -460,6 +498,61 @@ int experts_ok(const char* name, const int32_t* offsets, int32_t experts) {
   BUX_CHECK(offsets != nullptr && experts >= 1 && experts <= (1 << 20),
             "%s: offsets of %d experts (1 .. 2^20, not NULL)", name, experts);
   return BUX_OK;
+}
+
+template <typename T>
+int bias_add(const char* name, T* x, int64_t m, int64_t width, const T* bias,
+             const int32_t* offsets, int32_t experts, void* stream) {
+  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
+            "%s: bad shape m=%lld width=%lld (a multiple of %d)", name, (long long)m,
+            (long long)width, VEC);
+  if (int rc = experts_ok(name, offsets, experts)) return rc;
+  if (m == 0) return BUX_OK;
+  BUX_CHECK(x && bias, "%s: NULL buffer", name);
+  BUX_CHECK(m * ceil_div(width, THREADS * VEC) < (1LL << 31), "%s: too large", name);
+  dim3 grid(static_cast<unsigned>(m * ceil_div(width, THREADS * VEC)));
+  hipLaunchKernelGGL(expert_bias_add_kernel<T>, grid, dim3(THREADS), 0, as_stream(stream), x,
+                     width, bias, offsets, experts);
+  return launched("expert_bias_add_kernel");
+}
+
+template <typename T>
+int expert_sums(const char* name, const T* x, const int32_t* index, int32_t index_div,
+                int64_t sources, const T* weights, int64_t m, int64_t width,
+                const int32_t* offsets, int32_t experts, float* out, void* stream) {
+  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
+            "%s: bad shape m=%lld width=%lld (a multiple of %d)", name, (long long)m,
+            (long long)width, VEC);
+  BUX_CHECK(index == nullptr || index_div >= 1, "%s: index_div=%d", name, index_div);
+  BUX_CHECK(index == nullptr || sources >= 0, "%s: sources=%lld", name, (long long)sources);
+  if (int rc = experts_ok(name, offsets, experts)) return rc;
+  BUX_CHECK(out != nullptr && (m == 0 || x != nullptr), "%s: NULL buffer", name);
+  // every expert's sum is written (0 for none); rows at or past m add nothing
+  const int64_t chunks = ceil_div(width, SUM_COLS);
+  BUX_CHECK(experts * chunks < (1LL << 31), "%s: too large", name);
+  hipLaunchKernelGGL(expert_sums_kernel<T>, dim3(static_cast<unsigned>(experts * chunks)),
+                     dim3(THREADS), 0, as_stream(stream), x, index, index_div, sources, weights,
+                     m, width, offsets, experts, out);
+  return launched("expert_sums_kernel");
+}
+
+template <typename T>
+int bias_weight_grad(const char* name, const T* dy, const int32_t* index, int32_t index_div,
+                     int64_t sources, int64_t m, int64_t width, const T* bias,
+                     const int32_t* offsets, int32_t experts, T* d_weights, void* stream) {
+  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
+            "%s: bad shape m=%lld width=%lld (a multiple of %d)", name, (long long)m,
+            (long long)width, VEC);
+  BUX_CHECK(index == nullptr || index_div >= 1, "%s: index_div=%d", name, index_div);
+  BUX_CHECK(index == nullptr || sources >= 0, "%s: sources=%lld", name, (long long)sources);
+  if (int rc = experts_ok(name, offsets, experts)) return rc;
+  if (m == 0) return BUX_OK;
+  BUX_CHECK(dy && bias && d_weights, "%s: NULL buffer", name);
+  hipLaunchKernelGGL(expert_bias_weight_grad_kernel<T>,
+                     dim3(static_cast<unsigned>(ceil_div(m, THREADS / 64))), dim3(THREADS), 0,
+                     as_stream(stream), dy, index, index_div, sources, m, width, bias, offsets,
+                     experts, d_weights);
+  return launched("expert_bias_weight_grad_kernel");
 }
 }  // namespace
 }  // namespace bux
@@ -477,7 +570,8 @@ extern "C" int bux_token_sums_f32(const float* y, int64_t y_rows, const int32_t*
                                   void* stream) {
   using namespace bux;
   clear_error();
-  return token_sums_f32("bux_token_sums_f32", y, y_rows, inverse, tokens, k, width, out, stream);
+  return token_sums_f32("bux_token_sums_f32", y, y_rows, inverse, tokens, k, width, nullptr, out,
+                        stream);
 }
 
 extern "C" int bux_token_sums_biased(const uint16_t* y, int64_t y_rows, const int32_t* inverse,
@@ -489,48 +583,53 @@ extern "C" int bux_token_sums_biased(const uint16_t* y, int64_t y_rows, const in
   clear_error();
   if (int rc = experts_ok("bux_token_sums_biased", offsets, experts)) return rc;
   BUX_CHECK(tokens == 0 || (bias && weights), "bux_token_sums_biased: NULL bias or weights");
-  const PickBias pb{bias, offsets, experts, weights};
+  const PickBias<uint16_t> pb{bias, offsets, experts, weights};
   return token_sums("bux_token_sums_biased", y, y_rows, inverse, tokens, k, width, &pb, out,
                     stream);
 }
 
-extern "C" int bux_expert_bias_add(uint16_t* x, int64_t m, int64_t width, const uint16_t* bias,
-                                   const int32_t* offsets, int32_t experts, void* stream) {
+extern "C" int bux_token_sums_biased_f32(const float* y, int64_t y_rows, const int32_t* inverse,
+                                         int64_t tokens, int32_t k, int64_t width,
+                                         const float* bias, const int32_t* offsets,
+                                         int32_t experts, const float* weights, float* out,
+                                         void* stream) {
   using namespace bux;
   clear_error();
-  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
-            "bux_expert_bias_add: bad shape m=%lld width=%lld (a multiple of %d)", (long long)m,
-            (long long)width, VEC);
-  if (int rc = experts_ok("bux_expert_bias_add", offsets, experts)) return rc;
-  if (m == 0) return BUX_OK;
-  BUX_CHECK(x && bias, "bux_expert_bias_add: NULL buffer");
-  BUX_CHECK(m * ceil_div(width, THREADS * VEC) < (1LL << 31), "bux_expert_bias_add: too large");
-  dim3 grid(static_cast<unsigned>(m * ceil_div(width, THREADS * VEC)));
-  hipLaunchKernelGGL(expert_bias_add_kernel, grid, dim3(THREADS), 0, as_stream(stream), x, width,
-                     bias, offsets, experts);
-  return launched("expert_bias_add_kernel");
+  if (int rc = experts_ok("bux_token_sums_biased_f32", offsets, experts)) return rc;
+  BUX_CHECK(tokens == 0 || (bias && weights), "bux_token_sums_biased_f32: NULL bias or weights");
+  const PickBias<float> pb{bias, offsets, experts, weights};
+  return token_sums_f32("bux_token_sums_biased_f32", y, y_rows, inverse, tokens, k, width, &pb,
+                        out, stream);
+}
+
+extern "C" int bux_expert_bias_add(uint16_t* x, int64_t m, int64_t width, const uint16_t* bias,
+                                   const int32_t* offsets, int32_t experts, void* stream) {
+  bux::clear_error();
+  return bux::bias_add("bux_expert_bias_add", x, m, width, bias, offsets, experts, stream);
+}
+
+extern "C" int bux_expert_bias_add_f32(float* x, int64_t m, int64_t width, const float* bias,
+                                       const int32_t* offsets, int32_t experts, void* stream) {
+  bux::clear_error();
+  return bux::bias_add("bux_expert_bias_add_f32", x, m, width, bias, offsets, experts, stream);
 }
 
 extern "C" int bux_expert_sums(const uint16_t* x, const int32_t* index, int32_t index_div,
                                int64_t sources, const uint16_t* weights, int64_t m,
                                int64_t width, const int32_t* offsets, int32_t experts,
                                float* out, void* stream) {
-  using namespace bux;
-  clear_error();
-  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
-            "bux_expert_sums: bad shape m=%lld width=%lld (a multiple of %d)", (long long)m,
-            (long long)width, VEC);
-  BUX_CHECK(index == nullptr || index_div >= 1, "bux_expert_sums: index_div=%d", index_div);
-  BUX_CHECK(index == nullptr || sources >= 0, "bux_expert_sums: sources=%lld", (long long)sources);
-  if (int rc = experts_ok("bux_expert_sums", offsets, experts)) return rc;
-  BUX_CHECK(out != nullptr && (m == 0 || x != nullptr), "bux_expert_sums: NULL buffer");
-  // every expert's sum is written (0 for none); rows at or past m add nothing
-  const int64_t chunks = ceil_div(width, SUM_COLS);
-  BUX_CHECK(experts * chunks < (1LL << 31), "bux_expert_sums: too large");
-  hipLaunchKernelGGL(expert_sums_kernel, dim3(static_cast<unsigned>(experts * chunks)),
-                     dim3(THREADS), 0, as_stream(stream), x, index, index_div, sources, weights,
-                     m, width, offsets, experts, out);
-  return launched("expert_sums_kernel");
+  bux::clear_error();
+  return bux::expert_sums("bux_expert_sums", x, index, index_div, sources, weights, m, width,
+                          offsets, experts, out, stream);
+}
+
+extern "C" int bux_expert_sums_f32(const float* x, const int32_t* index, int32_t index_div,
+                                   int64_t sources, const float* weights, int64_t m,
+                                   int64_t width, const int32_t* offsets, int32_t experts,
+                                   float* out, void* stream) {
+  bux::clear_error();
+  return bux::expert_sums("bux_expert_sums_f32", x, index, index_div, sources, weights, m, width,
+                          offsets, experts, out, stream);
 }
 
 extern "C" int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index,
@@ -538,23 +637,19 @@ extern "C" int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* in
                                            int64_t width, const uint16_t* bias,
                                            const int32_t* offsets, int32_t experts,
                                            uint16_t* d_weights, void* stream) {
-  using namespace bux;
-  clear_error();
-  BUX_CHECK(m >= 0 && width > 0 && width % VEC == 0,
-            "bux_expert_bias_weight_grad: bad shape m=%lld width=%lld (a multiple of %d)",
-            (long long)m, (long long)width, VEC);
-  BUX_CHECK(index == nullptr || index_div >= 1, "bux_expert_bias_weight_grad: index_div=%d",
-            index_div);
-  BUX_CHECK(index == nullptr || sources >= 0, "bux_expert_bias_weight_grad: sources=%lld",
-            (long long)sources);
-  if (int rc = experts_ok("bux_expert_bias_weight_grad", offsets, experts)) return rc;
-  if (m == 0) return BUX_OK;
-  BUX_CHECK(dy && bias && d_weights, "bux_expert_bias_weight_grad: NULL buffer");
-  hipLaunchKernelGGL(expert_bias_weight_grad_kernel,
-                     dim3(static_cast<unsigned>(ceil_div(m, THREADS / 64))), dim3(THREADS), 0,
-                     as_stream(stream), dy, index, index_div, sources, m, width, bias, offsets,
-                     experts, d_weights);
-  return launched("expert_bias_weight_grad_kernel");
+  bux::clear_error();
+  return bux::bias_weight_grad("bux_expert_bias_weight_grad", dy, index, index_div, sources, m,
+                               width, bias, offsets, experts, d_weights, stream);
+}
+
+extern "C" int bux_expert_bias_weight_grad_f32(const float* dy, const int32_t* index,
+                                               int32_t index_div, int64_t sources, int64_t m,
+                                               int64_t width, const float* bias,
+                                               const int32_t* offsets, int32_t experts,
+                                               float* d_weights, void* stream) {
+  bux::clear_error();
+  return bux::bias_weight_grad("bux_expert_bias_weight_grad_f32", dy, index, index_div, sources,
+                               m, width, bias, offsets, experts, d_weights, stream);
 }
 
 extern "C" int bux_glu_forward(const uint16_t* projected, const uint16_t* weights,

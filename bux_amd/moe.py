@@ -231,34 +231,50 @@ def _experts(offsets: torch.Tensor) -> int:
     return offsets.numel() - 1
 
 
+def _runs_f32(name: str, x: torch.Tensor, *others: torch.Tensor | None) -> bool:
+    """Whether the op runs in float32: x is bfloat16 or float32, and every other tensor
+    given (the biases, weights and norm parameters beside it) has x's dtype."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{name}: bfloat16 or float32 rows, not {x.dtype}")
+    for t in others:
+        if t is not None and t.dtype != x.dtype:
+            raise TypeError(f"{name}: a {t.dtype} tensor beside {x.dtype} rows")
+    return x.dtype == torch.float32
+
+
 def add_expert_bias(x: torch.Tensor, bias: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
     """Add each row's expert's row of `bias` (E, width) to x (m, width) in place and
-    return x: ``x + by_expert(bias, sizes)`` in bfloat16 (moe.py:857-861,876-885)."""
+    return x: ``x + by_expert(bias, sizes)`` in x's dtype, bfloat16 or float32 (bias
+    the same) (moe.py:848-849,857-861,876-885)."""
     require(x, bias, offsets)
     e = _experts(offsets)
     m, width = x.shape[0], x.numel() // max(x.shape[0], 1)
-    if bias.dtype != torch.bfloat16 or bias.numel() != e * width:
-        raise ValueError(f"bias {bias.dtype} {tuple(bias.shape)} for {e} experts of {width}")
-    _lib.check(lib().bux_expert_bias_add(ptr(x), m, width, ptr(bias.contiguous()), ptr(offsets), e,
-                                         stream()))
+    f32 = _runs_f32("add_expert_bias", x, bias)
+    if bias.numel() != e * width:
+        raise ValueError(f"bias {tuple(bias.shape)} for {e} experts of {width}")
+    add = lib().bux_expert_bias_add_f32 if f32 else lib().bux_expert_bias_add
+    _lib.check(add(ptr(x), m, width, ptr(bias.contiguous()), ptr(offsets), e, stream()))
     return x
 
 
 def expert_sums(x: torch.Tensor, offsets: torch.Tensor, index: torch.Tensor | None = None,
                 index_div: int = 1, weights: torch.Tensor | None = None) -> torch.Tensor:
     """Return each expert's sum of its rows, float32 (E, width): rows ``x[index[r] //
-    index_div]`` (or ``x[r]``), each times ``weights[r]`` (rounded to bfloat16) if
+    index_div]`` (or ``x[r]``), each times ``weights[r]`` (rounded to x's dtype) if
     given. The gradient of `add_expert_bias`'s bias, and with the picks' tokens and
-    weights of the down bias (moe.py:866-870)."""
+    weights of the down bias (moe.py:866-870). x bfloat16 or float32, weights x's
+    dtype."""
     require(x, offsets, index, weights)
     e = _experts(offsets)
     m = index.numel() if index is not None else x.shape[0]
     width = x.numel() // x.shape[0] if x.shape[0] else x.shape[-1]
+    f32 = _runs_f32("expert_sums", x, weights)
     if weights is not None and weights.numel() != m:
         raise ValueError(f"expert_sums: {weights.numel()} weights for {m} rows")
     out = torch.empty(e, width, dtype=torch.float32, device=x.device)
-    _lib.check(lib().bux_expert_sums(ptr(x), ptr(index), index_div, x.shape[0], ptr(weights), m,
-                                     width, ptr(offsets), e, ptr(out), stream()))
+    sums = lib().bux_expert_sums_f32 if f32 else lib().bux_expert_sums
+    _lib.check(sums(ptr(x), ptr(index), index_div, x.shape[0], ptr(weights), m, width,
+                    ptr(offsets), e, ptr(out), stream()))
     return out
 
 
@@ -266,17 +282,18 @@ def sum_by_token_biased(y: torch.Tensor, inverse: torch.Tensor, bias: torch.Tens
                         offsets: torch.Tensor, row_weights: torch.Tensor) -> torch.Tensor:
     """Return `sum_by_token` (y) plus each token's sum of its picks' ``bias[e] * w``:
     the down bias's forward, ``y + sums_of_tokens(weighted(by_expert(down_bias),
-    weights))`` (moe.py:866-870)."""
+    weights))`` (moe.py:866-870), in y's dtype (bias and row_weights the same)."""
     require(y, inverse, bias, offsets, row_weights)
     e = _experts(offsets)
     tokens, k = inverse.shape
     width = y.shape[-1]
-    if bias.dtype != torch.bfloat16 or bias.numel() != e * width:
-        raise ValueError(f"bias {bias.dtype} {tuple(bias.shape)} for {e} experts of {width}")
+    f32 = _runs_f32("sum_by_token_biased", y, bias, row_weights)
+    if bias.numel() != e * width:
+        raise ValueError(f"bias {tuple(bias.shape)} for {e} experts of {width}")
     out = torch.empty(tokens, width, dtype=y.dtype, device=y.device)
-    _lib.check(lib().bux_token_sums_biased(
-        ptr(y), y.shape[0], ptr(inverse), tokens, k, width, ptr(bias.contiguous()), ptr(offsets), e,
-        ptr(row_weights), ptr(out), stream()))
+    sums = lib().bux_token_sums_biased_f32 if f32 else lib().bux_token_sums_biased
+    _lib.check(sums(ptr(y), y.shape[0], ptr(inverse), tokens, k, width, ptr(bias.contiguous()),
+                    ptr(offsets), e, ptr(row_weights), ptr(out), stream()))
     return out
 
 
@@ -284,13 +301,14 @@ def add_bias_weight_grad(d_weights: torch.Tensor, dy: torch.Tensor, order: torch
                          bias: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
     """Add the down bias's share of the row weights' gradient to `d_weights` (m,) in
     place: ``sum_c dy[order[r] // k, c] bias[e(r), c]`` (weighted's VJP,
-    moe.py:922-925)."""
+    moe.py:922-925), in dy's dtype (d_weights and bias the same)."""
     require(d_weights, dy, order, bias, offsets)
     e = _experts(offsets)
     m, width = order.numel(), dy.shape[-1]
-    _lib.check(lib().bux_expert_bias_weight_grad(ptr(dy), ptr(order), k, dy.shape[0], m, width,
-                                                 ptr(bias.contiguous()), ptr(offsets), e,
-                                                 ptr(d_weights), stream()))
+    f32 = _runs_f32("add_bias_weight_grad", dy, d_weights, bias)
+    grad = lib().bux_expert_bias_weight_grad_f32 if f32 else lib().bux_expert_bias_weight_grad
+    _lib.check(grad(ptr(dy), ptr(order), k, dy.shape[0], m, width, ptr(bias.contiguous()),
+                    ptr(offsets), e, ptr(d_weights), stream()))
     return d_weights
 
 
@@ -300,8 +318,8 @@ def add_bias_weight_grad(d_weights: torch.Tensor, dy: torch.Tensor, order: torch
 class ExpertNorm(NamedTuple):
     """The norm of each expert's output rows (MoEConfig.expert_norm, config.py:306): a
     NormalizationConfig (config.py:71-92) of layernorm or rmsnorm, its gain (`scale`)
-    and bias given as bfloat16 (d,) tensors, as the model casts its parameters for the
-    forward (train/trainer.py:129-140)."""
+    and bias given as (d,) tensors of the layer's dtype, as the model casts its
+    parameters for the forward (train/trainer.py:129-140)."""
 
     kind: str = "rmsnorm"  # or "layernorm"
     eps: float = 1e-6
@@ -323,15 +341,17 @@ def expert_norm_forward(y: torch.Tensor, offsets: torch.Tensor, norm: ExpertNorm
                         row_weights: torch.Tensor, down_bias: torch.Tensor | None = None
                         ) -> torch.Tensor:
     """Return ``weighted(norm(y + down_bias), weights)`` of the down GEMM's rows y
-    (m, d) (moe.py:871-872), bfloat16 (m, d); rows in no expert 0."""
+    (m, d) (moe.py:871-872) in y's dtype, bfloat16 or float32 (the other tensors the
+    same); rows in no expert 0."""
     require(y, offsets, scale, bias, row_weights, down_bias)
     e = _experts(offsets)
     m, d = y.shape
+    f32 = _runs_f32("expert_norm_forward", y, scale, bias, row_weights, down_bias)
     out = torch.empty_like(y)
     st = norm.struct()
-    _lib.check(lib().bux_expert_norm_forward(
-        ptr(y), m, d, ptr(down_bias), ptr(offsets), e, ctypes.byref(st), ptr(scale), ptr(bias),
-        ptr(row_weights), ptr(out), stream()))
+    forward = lib().bux_expert_norm_forward_f32 if f32 else lib().bux_expert_norm_forward
+    _lib.check(forward(ptr(y), m, d, ptr(down_bias), ptr(offsets), e, ctypes.byref(st), ptr(scale),
+                       ptr(bias), ptr(row_weights), ptr(out), stream()))
     return out
 
 
@@ -342,20 +362,22 @@ def expert_norm_backward(dy: torch.Tensor, order: torch.Tensor, k: int, y: torch
                          ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None,
                                     torch.Tensor | None]:
     """Return the VJP of `expert_norm_forward` given the tokens' gradient dy (t, d):
-    the gradient to y (m, d) bfloat16 (the down bias's, by expert), to the row weights
-    (m,) bfloat16, and to the norm's scale and bias (d,) float32 (None where it has
-    none)."""
+    the gradient to y (m, d) (the down bias's, by expert) and to the row weights (m,)
+    in y's dtype, and to the norm's scale and bias (d,) float32 (None where it has
+    none). dy and the other tensors in y's dtype, bfloat16 or float32."""
     require(dy, order, y, offsets, scale, bias, row_weights, down_bias)
     e = _experts(offsets)
     m, d = y.shape
+    f32 = _runs_f32("expert_norm_backward", y, dy, scale, bias, row_weights, down_bias)
     dev = y.device
     dv = torch.empty_like(y)
-    dw = torch.empty(m, dtype=torch.bfloat16, device=dev)
+    dw = torch.empty(m, dtype=y.dtype, device=dev)
     d_scale = torch.empty(d, dtype=torch.float32, device=dev) if norm.affine else None
     d_bias = torch.empty(d, dtype=torch.float32, device=dev) if norm.bias else None
     ws = workspace(lib().bux_expert_norm_backward_workspace_size(m, d), dev)
     st = norm.struct()
-    _lib.check(lib().bux_expert_norm_backward(
+    backward = lib().bux_expert_norm_backward_f32 if f32 else lib().bux_expert_norm_backward
+    _lib.check(backward(
         ptr(dy), ptr(order), k, dy.shape[0], ptr(y), m, d, ptr(down_bias), ptr(offsets), e,
         ctypes.byref(st),
         ptr(scale), ptr(bias), ptr(row_weights), ptr(dv), ptr(dw), ptr(d_scale), ptr(d_bias),
@@ -437,9 +459,9 @@ class Saved(NamedTuple):
 
     sorted: Sorted
     k: int
-    row_weights: torch.Tensor  # bfloat16 (m,)
-    projected: torch.Tensor  # bfloat16 (m, p f), with the up bias added
-    h: torch.Tensor | None  # bfloat16 (m, f): wgrad in bfloat16, or kept for inspection
+    row_weights: torch.Tensor  # the layer's dtype (m,)
+    projected: torch.Tensor  # the layer's dtype (m, p f), with the up bias added
+    h: torch.Tensor | None  # (m, f): wgrad in bfloat16, or kept for inspection
     x_m: Tiled | None  # x^T along the rows (wgrad of up in MXFP8)
     up_n: Tiled | None  # each W_up along n (dgrad of up in MXFP8)
     h_m: Tiled | None  # h^T along the rows (wgrad of down in MXFP8)
@@ -457,15 +479,18 @@ def _layer_dtype(name: str, x: torch.Tensor) -> torch.dtype:
     return x.dtype
 
 
-def _float32_built(name: str, fmt: str, passes: tuple[bool, bool, bool], up_bias, down_bias,
-                   norm) -> None:
-    """Raise for what a float32 layer does not run here: every GEMM in MXFP8 (the
-    bfloat16 "compute" GEMMs take bfloat16 operands), no biases, no expert norm."""
+def _float32_built(name: str, fmt: str, passes: tuple[bool, bool, bool]) -> None:
+    """Raise for what a float32 layer does not run here: a GEMM outside MXFP8 (the
+    bfloat16 "compute" GEMMs take bfloat16 operands)."""
     if fmt not in MX_FORMATS or not all(passes):
         raise NotImplementedError(f"{name}: float32 tokens take every GEMM in MXFP8 "
                                   f"(fmt {fmt!r}, passes {passes})")
-    if up_bias is not None or down_bias is not None or norm is not None:
-        raise NotImplementedError(f"{name}: float32 tokens with biases or an expert norm")
+
+
+def _cast(dt: torch.dtype, *tensors: torch.Tensor | None) -> tuple[torch.Tensor | None, ...]:
+    """The tensors in the layer's dtype (None stays None): the biases as by_expert casts
+    them (moe.py:848-849), and the norm's parameters as the model's forward does."""
+    return tuple(None if t is None else t.to(dt) for t in tensors)
 
 
 def experts_forward(
@@ -484,8 +509,8 @@ def experts_forward(
     (the kernels and weights cast to it, experts/moe.py:846; the GEMMs' outputs in it,
     grouped_blockscaled.Dtypes, grouped_blockscaled.py:129): in float32 no value is
     rounded to bfloat16 between the steps (the MXFP8 operands are quantized from the
-    float32 values), and every GEMM multiplies in MXFP8 with no biases or expert norm
-    (others raise NotImplementedError).
+    float32 values), and every GEMM multiplies in MXFP8 (others raise
+    NotImplementedError). The biases and the norm's parameters are cast to z's dtype.
 
     Args:
         z: the tokens, bfloat16 or float32 (t, d).
@@ -507,12 +532,12 @@ def experts_forward(
             bits, in one GEMM kernel instead of the GEMM and the activation's quantizer.
         passes: the GEMMs (of "fprop", "dgrad", "wgrad") that multiply in `fmt`; None
             for all. The others multiply in bfloat16.
-        up_bias: the experts' up biases, bfloat16 (E, f, p), added to the up GEMM's
-            product; None for none (MLPConfig.bias, moe.py:857-861).
-        down_bias: the experts' down biases, bfloat16 (E, d): each pick adds its
-            expert's, times its weight (moe.py:866-870).
+        up_bias: the experts' up biases (E, f, p), added to the up GEMM's product;
+            None for none (MLPConfig.bias, moe.py:857-861).
+        down_bias: the experts' down biases (E, d): each pick adds its expert's, times
+            its weight (moe.py:866-870).
         norm: a norm of each expert's output rows (MoEConfig.expert_norm), with its
-            gain `norm_scale` and bias `norm_bias` (bfloat16 (d,)): the activation is
+            gain `norm_scale` and bias `norm_bias` ((d,)): the activation is
             then unweighted and each row is ``weighted(norm(y + down_bias), w)``
             (moe.py:871-872).
     """
@@ -523,9 +548,10 @@ def experts_forward(
     # the kernels and the weights take x's dtype (moe.py:846); y, dx and dW then come in
     # it (grouped_blockscaled.py:129)
     up, down, weights = up.to(dt), down.to(dt), weights.to(dt)
+    up_bias, down_bias, norm_scale, norm_bias = _cast(dt, up_bias, down_bias, norm_scale, norm_bias)
     fprop, dgrad, wgrad = passes_of(fmt, passes)
     if dt == torch.float32:
-        _float32_built("experts_forward", fmt, (fprop, dgrad, wgrad), up_bias, down_bias, norm)
+        _float32_built("experts_forward", fmt, (fprop, dgrad, wgrad))
         fused = False  # the fused up GEMM's epilogue is bfloat16's
     if quantized is not None:
         quantized.check(fmt, up, down)
@@ -632,6 +658,7 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         raise TypeError(f"experts_backward: dy is {dy.dtype}, the forward's tokens {dt}")
     up_dtype, down_dtype = up.dtype, down.dtype
     up, down = up.to(dt), down.to(dt)
+    up_bias, down_bias, norm_scale, norm_bias = _cast(dt, up_bias, down_bias, norm_scale, norm_bias)
     if dt == torch.float32:
         fused = False
     e, d, f, p = up.shape

@@ -355,13 +355,132 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxMxGroupedDglu, MxGroupedDglu,
                                   .Arg<In>().Arg<In>().Arg<In>().Arg<In>() BUX_FFN_ATTRS
                                   .Ret<In>().Ret<In>().Ret<In>().Ret<In>().Ret<In>().Ret<In>());
 
+// The bias and norm entry points by element type: the bfloat16 ones (T uint16_t) or
+// their float32 twins (T float); each handler picks by its rows' element type.
+namespace {
+int bias_add(uint16_t* x, int64_t m, int64_t w, const uint16_t* b, const int32_t* o, int32_t e,
+             hipStream_t s) {
+  return bux_expert_bias_add(x, m, w, b, o, e, s);
+}
+int bias_add(float* x, int64_t m, int64_t w, const float* b, const int32_t* o, int32_t e,
+             hipStream_t s) {
+  return bux_expert_bias_add_f32(x, m, w, b, o, e, s);
+}
+int expert_sums(const uint16_t* x, const int32_t* i, int32_t div, int64_t src,
+                const uint16_t* w, int64_t m, int64_t width, const int32_t* o, int32_t e,
+                float* out, hipStream_t s) {
+  return bux_expert_sums(x, i, div, src, w, m, width, o, e, out, s);
+}
+int expert_sums(const float* x, const int32_t* i, int32_t div, int64_t src, const float* w,
+                int64_t m, int64_t width, const int32_t* o, int32_t e, float* out,
+                hipStream_t s) {
+  return bux_expert_sums_f32(x, i, div, src, w, m, width, o, e, out, s);
+}
+int sums_biased(const uint16_t* y, int64_t rows, const int32_t* inv, int64_t t, int32_t k,
+                int64_t width, const uint16_t* b, const int32_t* o, int32_t e,
+                const uint16_t* w, uint16_t* out, hipStream_t s) {
+  return bux_token_sums_biased(y, rows, inv, t, k, width, b, o, e, w, out, s);
+}
+int sums_biased(const float* y, int64_t rows, const int32_t* inv, int64_t t, int32_t k,
+                int64_t width, const float* b, const int32_t* o, int32_t e, const float* w,
+                float* out, hipStream_t s) {
+  return bux_token_sums_biased_f32(y, rows, inv, t, k, width, b, o, e, w, out, s);
+}
+int weight_grad(const uint16_t* dy, const int32_t* i, int32_t div, int64_t src, int64_t m,
+                int64_t width, const uint16_t* b, const int32_t* o, int32_t e, uint16_t* dw,
+                hipStream_t s) {
+  return bux_expert_bias_weight_grad(dy, i, div, src, m, width, b, o, e, dw, s);
+}
+int weight_grad(const float* dy, const int32_t* i, int32_t div, int64_t src, int64_t m,
+                int64_t width, const float* b, const int32_t* o, int32_t e, float* dw,
+                hipStream_t s) {
+  return bux_expert_bias_weight_grad_f32(dy, i, div, src, m, width, b, o, e, dw, s);
+}
+int norm_forward(const uint16_t* y, int64_t m, int64_t d, const uint16_t* db, const int32_t* o,
+                 int32_t e, const bux_norm* n, const uint16_t* sc, const uint16_t* b,
+                 const uint16_t* w, uint16_t* out, hipStream_t s) {
+  return bux_expert_norm_forward(y, m, d, db, o, e, n, sc, b, w, out, s);
+}
+int norm_forward(const float* y, int64_t m, int64_t d, const float* db, const int32_t* o,
+                 int32_t e, const bux_norm* n, const float* sc, const float* b, const float* w,
+                 float* out, hipStream_t s) {
+  return bux_expert_norm_forward_f32(y, m, d, db, o, e, n, sc, b, w, out, s);
+}
+int norm_backward(const uint16_t* dy, const int32_t* i, int32_t div, int64_t src,
+                  const uint16_t* y, int64_t m, int64_t d, const uint16_t* db, const int32_t* o,
+                  int32_t e, const bux_norm* n, const uint16_t* sc, const uint16_t* b,
+                  const uint16_t* w, uint16_t* dv, uint16_t* dw, float* dsc, float* dbias,
+                  void* ws, size_t bytes, hipStream_t s) {
+  return bux_expert_norm_backward(dy, i, div, src, y, m, d, db, o, e, n, sc, b, w, dv, dw, dsc,
+                                  dbias, ws, bytes, s);
+}
+int norm_backward(const float* dy, const int32_t* i, int32_t div, int64_t src, const float* y,
+                  int64_t m, int64_t d, const float* db, const int32_t* o, int32_t e,
+                  const bux_norm* n, const float* sc, const float* b, const float* w, float* dv,
+                  float* dw, float* dsc, float* dbias, void* ws, size_t bytes, hipStream_t s) {
+  return bux_expert_norm_backward_f32(dy, i, div, src, y, m, d, db, o, e, n, sc, b, w, dv, dw,
+                                      dsc, dbias, ws, bytes, s);
+}
+int32_t experts_in(const In& offsets) { return static_cast<int32_t>(offsets.element_count() - 1); }
+
+template <typename T>
+ffi::Error expert_bias_add_as(hipStream_t s, In bias, In offsets, Out& x_out) {
+  return status(bias_add(at<T>(x_out), dim(x_out, 0),
+                         static_cast<int64_t>(x_out->element_count()) / dim(x_out, 0),
+                         at<const T>(bias), at<const int32_t>(offsets), experts_in(offsets), s));
+}
+template <typename T>
+ffi::Error expert_sums_as(hipStream_t s, In x, In index, In weights, In offsets,
+                          int64_t index_div, Out& out) {
+  const int64_t m = index.size_bytes() ? static_cast<int64_t>(index.element_count()) : dim(x, 0);
+  return status(expert_sums(at<const T>(x), at<const int32_t>(index),
+                            static_cast<int32_t>(index_div), dim(x, 0), at<const T>(weights), m,
+                            dim(out, 1), at<const int32_t>(offsets), experts_in(offsets),
+                            at<float>(out), s));
+}
+template <typename T>
+ffi::Error token_sums_biased_as(hipStream_t s, In y, In inverse, In bias, In offsets,
+                                In weights, Out& out) {
+  return status(sums_biased(at<const T>(y), dim(y, 0), at<const int32_t>(inverse),
+                            dim(inverse, 0), static_cast<int32_t>(dim(inverse, 1)), dim(y, 1),
+                            at<const T>(bias), at<const int32_t>(offsets), experts_in(offsets),
+                            at<const T>(weights), at<T>(out), s));
+}
+template <typename T>
+ffi::Error bias_weight_grad_as(hipStream_t s, In dy, In index, In bias, In offsets,
+                               int64_t index_div, Out& d_weights_out) {
+  return status(weight_grad(at<const T>(dy), at<const int32_t>(index),
+                            static_cast<int32_t>(index_div), dim(dy, 0),
+                            static_cast<int64_t>(d_weights_out->element_count()), dim(dy, 1),
+                            at<const T>(bias), at<const int32_t>(offsets), experts_in(offsets),
+                            at<T>(d_weights_out), s));
+}
+template <typename T>
+ffi::Error norm_forward_as(hipStream_t s, In y, In down_bias, In offsets, In scale, In bias,
+                           In weights, const bux_norm& norm, Out& out) {
+  return status(norm_forward(at<const T>(y), dim(y, 0), dim(y, 1), at<const T>(down_bias),
+                             at<const int32_t>(offsets), experts_in(offsets), &norm,
+                             at<const T>(scale), at<const T>(bias), at<const T>(weights),
+                             at<T>(out), s));
+}
+template <typename T>
+ffi::Error norm_backward_as(hipStream_t s, In dy, In index, In y, In down_bias, In offsets,
+                            In scale, In bias, In weights, int64_t index_div,
+                            const bux_norm& norm, Out& dv, Out& d_weights, Out& d_scale,
+                            Out& d_bias, Out& ws) {
+  return status(norm_backward(
+      at<const T>(dy), at<const int32_t>(index), static_cast<int32_t>(index_div), dim(dy, 0),
+      at<const T>(y), dim(y, 0), dim(y, 1), at<const T>(down_bias), at<const int32_t>(offsets),
+      experts_in(offsets), &norm, at<const T>(scale), at<const T>(bias), at<const T>(weights),
+      at<T>(dv), at<T>(d_weights), at<float>(d_scale), at<float>(d_bias), at<void>(ws),
+      ws->size_bytes(), s));
+}
+}  // namespace
+
 // x is aliased to the result (in place): the caller passes input_output_aliases={0: 0}.
 static ffi::Error ExpertBiasAdd(hipStream_t s, In x, In bias, In offsets, Out x_out) {
-  (void)x;
-  return status(bux_expert_bias_add(at<uint16_t>(x_out), dim(x_out, 0),
-                                    static_cast<int64_t>(x_out->element_count()) / dim(x_out, 0),
-                                    at<const uint16_t>(bias), at<const int32_t>(offsets),
-                                    static_cast<int32_t>(offsets.element_count() - 1), s));
+  return f32(x) ? expert_bias_add_as<float>(s, bias, offsets, x_out)
+                : expert_bias_add_as<uint16_t>(s, bias, offsets, x_out);
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertBiasAdd, ExpertBiasAdd,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
@@ -370,13 +489,8 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertBiasAdd, ExpertBiasAdd,
 // index and weights may be empty; m = the index's entries, or x's rows.
 static ffi::Error ExpertSums(hipStream_t s, In x, In index, In weights, In offsets,
                              int64_t index_div, Out out) {
-  const int64_t m = index.size_bytes() ? static_cast<int64_t>(index.element_count()) : dim(x, 0);
-  return status(bux_expert_sums(at<const uint16_t>(x), at<const int32_t>(index),
-                                static_cast<int32_t>(index_div), dim(x, 0),
-                                at<const uint16_t>(weights), m,
-                                dim(out, 1), at<const int32_t>(offsets),
-                                static_cast<int32_t>(offsets.element_count() - 1),
-                                at<float>(out), s));
+  return f32(x) ? expert_sums_as<float>(s, x, index, weights, offsets, index_div, out)
+                : expert_sums_as<uint16_t>(s, x, index, weights, offsets, index_div, out);
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertSums, ExpertSums,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
@@ -385,11 +499,8 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertSums, ExpertSums,
 // inverse [t, k]; weights are the sorted rows'.
 static ffi::Error TokenSumsBiased(hipStream_t s, In y, In inverse, In bias, In offsets,
                                   In weights, Out out) {
-  return status(bux_token_sums_biased(
-      at<const uint16_t>(y), dim(y, 0), at<const int32_t>(inverse), dim(inverse, 0),
-      static_cast<int32_t>(dim(inverse, 1)), dim(y, 1), at<const uint16_t>(bias),
-      at<const int32_t>(offsets), static_cast<int32_t>(offsets.element_count() - 1),
-      at<const uint16_t>(weights), at<uint16_t>(out), s));
+  return f32(y) ? token_sums_biased_as<float>(s, y, inverse, bias, offsets, weights, out)
+                : token_sums_biased_as<uint16_t>(s, y, inverse, bias, offsets, weights, out);
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxTokenSumsBiased, TokenSumsBiased,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
@@ -399,12 +510,9 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxTokenSumsBiased, TokenSumsBiased,
 static ffi::Error ExpertBiasWeightGrad(hipStream_t s, In dy, In index, In bias, In offsets,
                                        In d_weights, int64_t index_div, Out d_weights_out) {
   (void)d_weights;
-  return status(bux_expert_bias_weight_grad(
-      at<const uint16_t>(dy), at<const int32_t>(index), static_cast<int32_t>(index_div),
-      dim(dy, 0), static_cast<int64_t>(d_weights_out->element_count()), dim(dy, 1),
-      at<const uint16_t>(bias),
-      at<const int32_t>(offsets), static_cast<int32_t>(offsets.element_count() - 1),
-      at<uint16_t>(d_weights_out), s));
+  return f32(dy) ? bias_weight_grad_as<float>(s, dy, index, bias, offsets, index_div, d_weights_out)
+                 : bias_weight_grad_as<uint16_t>(s, dy, index, bias, offsets, index_div,
+                                                 d_weights_out);
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertBiasWeightGrad, ExpertBiasWeightGrad,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
@@ -414,11 +522,9 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertBiasWeightGrad, ExpertBiasWeightGrad,
 static ffi::Error ExpertNormForward(hipStream_t s, In y, In down_bias, In offsets, In scale,
                                     In bias, In weights, BUX_NORM_PARAMS, Out out) {
   const bux_norm norm = BUX_NORM;
-  return status(bux_expert_norm_forward(
-      at<const uint16_t>(y), dim(y, 0), dim(y, 1), at<const uint16_t>(down_bias),
-      at<const int32_t>(offsets), static_cast<int32_t>(offsets.element_count() - 1), &norm,
-      at<const uint16_t>(scale), at<const uint16_t>(bias), at<const uint16_t>(weights),
-      at<uint16_t>(out), s));
+  return f32(y) ? norm_forward_as<float>(s, y, down_bias, offsets, scale, bias, weights, norm, out)
+                : norm_forward_as<uint16_t>(s, y, down_bias, offsets, scale, bias, weights, norm,
+                                            out);
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertNormForward, ExpertNormForward,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()
@@ -429,13 +535,11 @@ static ffi::Error ExpertNormBackward(hipStream_t s, In dy, In index, In y, In do
                                      BUX_NORM_PARAMS, Out dv, Out d_weights, Out d_scale,
                                      Out d_bias, Out ws) {
   const bux_norm norm = BUX_NORM;
-  return status(bux_expert_norm_backward(
-      at<const uint16_t>(dy), at<const int32_t>(index), static_cast<int32_t>(index_div),
-      dim(dy, 0), at<const uint16_t>(y), dim(y, 0), dim(y, 1), at<const uint16_t>(down_bias),
-      at<const int32_t>(offsets), static_cast<int32_t>(offsets.element_count() - 1), &norm,
-      at<const uint16_t>(scale), at<const uint16_t>(bias), at<const uint16_t>(weights),
-      at<uint16_t>(dv), at<uint16_t>(d_weights), at<float>(d_scale), at<float>(d_bias),
-      at<void>(ws), ws->size_bytes(), s));
+  if (f32(y))
+    return norm_backward_as<float>(s, dy, index, y, down_bias, offsets, scale, bias, weights,
+                                   index_div, norm, dv, d_weights, d_scale, d_bias, ws);
+  return norm_backward_as<uint16_t>(s, dy, index, y, down_bias, offsets, scale, bias, weights,
+                                    index_div, norm, dv, d_weights, d_scale, d_bias, ws);
 }
 XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxExpertNormBackward, ExpertNormBackward,
                               ffi::Ffi::Bind().Ctx<Stream>().Arg<In>().Arg<In>().Arg<In>()

@@ -369,6 +369,22 @@ int bux_expert_bias_weight_grad(const uint16_t* dy, const int32_t* index, int32_
                                 int64_t sources, int64_t m, int64_t width, const uint16_t* bias,
                                 const int32_t* offsets, int32_t experts, uint16_t* d_weights,
                                 void* stream);
+/* The same four for a layer in float32 (moe.py:848-849: by_expert casts the biases to
+ * x's dtype): every bfloat16 buffer above float32, each rounding float32 arithmetic's own
+ * (the sums the same sums in the same order). */
+int bux_expert_bias_add_f32(float* x, int64_t m, int64_t width, const float* bias,
+                            const int32_t* offsets, int32_t experts, void* stream);
+int bux_expert_sums_f32(const float* x, const int32_t* index, int32_t index_div, int64_t sources,
+                        const float* weights, int64_t m, int64_t width, const int32_t* offsets,
+                        int32_t experts, float* out, void* stream);
+int bux_token_sums_biased_f32(const float* y, int64_t y_rows, const int32_t* inverse,
+                              int64_t tokens, int32_t k, int64_t width, const float* bias,
+                              const int32_t* offsets, int32_t experts, const float* weights,
+                              float* out, void* stream);
+int bux_expert_bias_weight_grad_f32(const float* dy, const int32_t* index, int32_t index_div,
+                                    int64_t sources, int64_t m, int64_t width, const float* bias,
+                                    const int32_t* offsets, int32_t experts, float* d_weights,
+                                    void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-8. The per-expert norm of the experts' outputs (MoEConfig.expert_norm,
@@ -415,6 +431,20 @@ int bux_expert_norm_backward(const uint16_t* dy, const int32_t* index, int32_t i
                              const uint16_t* weights, uint16_t* dv, uint16_t* d_weights,
                              float* d_scale, float* d_bias, void* workspace,
                              size_t workspace_bytes, void* stream);
+/* The same for a layer in float32 (layers/norm.py:14-78 in float32 compute): y, dy,
+ * down_bias, scale, bias, weights, out, dv and d_weights float32, each rounding float32
+ * arithmetic's own; the same workspace. */
+int bux_expert_norm_forward_f32(const float* y, int64_t m, int64_t d, const float* down_bias,
+                                const int32_t* offsets, int32_t experts, const bux_norm* norm,
+                                const float* scale, const float* bias, const float* weights,
+                                float* out, void* stream);
+int bux_expert_norm_backward_f32(const float* dy, const int32_t* index, int32_t index_div,
+                                 int64_t sources, const float* y, int64_t m, int64_t d,
+                                 const float* down_bias, const int32_t* offsets, int32_t experts,
+                                 const bux_norm* norm, const float* scale, const float* bias,
+                                 const float* weights, float* dv, float* d_weights,
+                                 float* d_scale, float* d_bias, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-8 with a-4. The activation and its gradient, quantized as they are computed.

@@ -384,18 +384,32 @@ def _expert_of_rows(sizes: np.ndarray, m: int) -> np.ndarray:
     return np.where(r < ends[-1] if ends.size else False, e, -1)
 
 
+def _values(x: np.ndarray) -> np.ndarray:
+    """bfloat16 bits (uint16) or float32 values as float32, exactly."""
+    x = np.asarray(x)
+    return bf16.to_f32(x) if x.dtype == np.uint16 else x.astype(np.float32)
+
+
+def _is_f32(x: np.ndarray) -> bool:
+    """Whether x holds a float32 layer's values (float32), not bfloat16 bits."""
+    return np.asarray(x).dtype == np.float32
+
+
 def by_expert(bias: np.ndarray, sizes: np.ndarray, m: int) -> np.ndarray:
-    """Return each row's expert's row of `bias` (E, c), 0 past the groups, float32
-    (moe.by_expert, moe.py:876-885: a one-hot product, exact here)."""
-    b = bf16.to_f32(bias).reshape(len(sizes), -1)
+    """Return each row's expert's row of `bias` (E, c; bfloat16 bits or float32), 0
+    past the groups, float32 (moe.by_expert, moe.py:876-885: a one-hot product, exact
+    here)."""
+    b = _values(bias).reshape(len(sizes), -1)
     e = _expert_of_rows(sizes, m)
     return np.where((e >= 0)[:, None], b[np.maximum(e, 0)], np.float32(0))
 
 
 def add_expert_bias(x: np.ndarray, bias: np.ndarray, sizes: np.ndarray) -> np.ndarray:
-    """Return ``x + by_expert(bias)`` in bfloat16 (moe.py:857-861), bits."""
-    xf = bf16.to_f32(x).reshape(x.shape[0], -1)
-    return bf16.to_bf16(xf + by_expert(bias, sizes, x.shape[0])).reshape(x.shape)
+    """Return ``x + by_expert(bias)`` in x's dtype (moe.py:848-849,857-861): bfloat16
+    bits, or float32 values for a float32 layer's x."""
+    xf = _values(x).reshape(x.shape[0], -1)
+    total = xf + by_expert(bias, sizes, x.shape[0])  # one float32 rounding
+    return (total if _is_f32(x) else bf16.to_bf16(total)).reshape(x.shape)
 
 
 def expert_sums(v: np.ndarray, sizes: np.ndarray) -> np.ndarray:
@@ -408,10 +422,12 @@ def expert_sums(v: np.ndarray, sizes: np.ndarray) -> np.ndarray:
 
 
 def weighted_bias_rows(bias: np.ndarray, sizes: np.ndarray, row_weights: np.ndarray, m: int) -> np.ndarray:
-    """Return ``weighted(by_expert(down_bias), weights)``, bfloat16 bits (moe.py:869,
-    922-925): each row's expert's bias times the row's weight, rounded."""
-    w = bf16.to_f32(row_weights)[:, None]
-    return bf16.to_bf16(by_expert(bias, sizes, m) * w)
+    """Return ``weighted(by_expert(down_bias), weights)`` in the row weights' dtype
+    (bfloat16 bits, or float32) (moe.py:869,922-925): each row's expert's bias times the
+    row's weight, rounded."""
+    w = _values(row_weights)[:, None]
+    b = by_expert(bias, sizes, m) * w  # a float32 product
+    return b if _is_f32(row_weights) else bf16.to_bf16(b)
 
 
 # --- The experts' output norm -------------------------------------------------------
@@ -429,15 +445,21 @@ class Norm(NamedTuple):
     scale_input: bool = False
 
 
-def _norm_parts(norm: Norm, v: np.ndarray, scale, nbias):
-    """The forward's pieces in float64 with the reference's bfloat16 roundings
-    (layers/norm.py:55-78 in bfloat16 compute): gain, x (the normalization's input), u,
-    rs, xn (its rounded output) and n (the norm's output)."""
-    r = bf16.round_f32
+def _rounding(f32: bool):
+    """The rounding of each of the norm's ops: to float32 (a float32 layer), else to
+    bfloat16 (through float32, as the float32 result of a bfloat16 op is rounded)."""
+    return (lambda a: np.asarray(a, np.float64).astype(np.float32)) if f32 else bf16.round_f32
+
+
+def _norm_parts(norm: Norm, v: np.ndarray, scale, nbias, f32: bool = False):
+    """The forward's pieces in float64 with the reference's roundings (layers/norm.py:
+    55-78 in bfloat16 compute, or float32 with `f32`): gain, x (the normalization's
+    input), u, rs, xn (its rounded output) and n (the norm's output)."""
+    r = _rounding(f32)
     d = v.shape[-1]
     gain = np.ones(d)
     if norm.affine:
-        s_ = bf16.to_f32(scale).astype(np.float64)
+        s_ = _values(scale).astype(np.float64)
         gain = r(1.0 + s_).astype(np.float64) if norm.zero_centered else s_
     x = r(v * gain).astype(np.float64) if norm.affine and norm.scale_input else v
     u = x - x.mean(-1, keepdims=True) if norm.kind == "layernorm" else x
@@ -447,39 +469,44 @@ def _norm_parts(norm: Norm, v: np.ndarray, scale, nbias):
     if norm.affine and not norm.scale_input:
         n = r(n * gain).astype(np.float64)
     if norm.bias:
-        n = r(n + bf16.to_f32(nbias).astype(np.float64)).astype(np.float64)
+        n = r(n + _values(nbias).astype(np.float64)).astype(np.float64)
     return gain, x, u, rs, xn, n
 
 
 def _norm_input(y: np.ndarray, sizes: np.ndarray, down_bias) -> np.ndarray:
-    v = bf16.to_f32(y).astype(np.float64)
+    v = _values(y).astype(np.float64)
     if down_bias is not None:
-        v = bf16.round_f32(v + by_expert(down_bias, sizes, y.shape[0])).astype(np.float64)
+        v = _rounding(_is_f32(y))(v + by_expert(down_bias, sizes, y.shape[0])).astype(np.float64)
     return v
 
 
 def expert_norm_forward(norm: Norm, y: np.ndarray, sizes: np.ndarray, row_weights: np.ndarray,
                         scale=None, nbias=None, down_bias=None) -> np.ndarray:
     """Return ``weighted(norm(y + down_bias), weights)`` of the down GEMM's rows y (m, d)
-    (moe.py:871-872), bfloat16 bits; rows past the groups 0."""
+    (moe.py:871-872) in y's dtype (bfloat16 bits, or float32 values: then every rounding
+    float32's); rows past the groups 0."""
+    f32 = _is_f32(y)
     v = _norm_input(y, sizes, down_bias)
-    *_, n = _norm_parts(norm, v, scale, nbias)
-    w = bf16.to_f32(row_weights).astype(np.float64)[:, None]
+    *_, n = _norm_parts(norm, v, scale, nbias, f32)
+    w = _values(row_weights).astype(np.float64)[:, None]
     live = (_expert_of_rows(sizes, y.shape[0]) >= 0)[:, None]
-    return bf16.to_bf16(np.where(live, n * w, 0.0).astype(np.float32))
+    out = np.where(live, n * w, 0.0).astype(np.float32)
+    return out if f32 else bf16.to_bf16(out)
 
 
 def expert_norm_backward(norm: Norm, g: np.ndarray, y: np.ndarray, sizes: np.ndarray,
                          row_weights: np.ndarray, scale=None, nbias=None, down_bias=None):
     """Return the VJP of `expert_norm_forward` given each row's upstream gradient g
-    (m, d) bfloat16 bits (its token's dy): dv (m, d) and d weights (m,) as bfloat16
-    bits, d scale and d bias (d,) as float64 sums (None where the norm has none); jax's
-    VJP of the bfloat16 chain, the normalization's in float32 (here float64)."""
-    r = bf16.round_f32
+    (m, d) (its token's dy), in y's dtype: dv (m, d) and d weights (m,) as bfloat16 bits
+    (float32 values for a float32 y), d scale and d bias (d,) as float64 sums (None
+    where the norm has none); jax's VJP of the chain, the normalization's in float32
+    (here float64)."""
+    f32 = _is_f32(y)
+    r = _rounding(f32)
     v = _norm_input(y, sizes, down_bias)
-    gain, x, u, rs, xn, n = _norm_parts(norm, v, scale, nbias)
-    gf = bf16.to_f32(g).astype(np.float64)
-    w = bf16.to_f32(row_weights).astype(np.float64)[:, None]
+    gain, x, u, rs, xn, n = _norm_parts(norm, v, scale, nbias, f32)
+    gf = _values(g).astype(np.float64)
+    w = _values(row_weights).astype(np.float64)[:, None]
     live = (_expert_of_rows(sizes, y.shape[0]) >= 0)[:, None]
     gf = np.where(live, gf, 0.0)
     d_w = r(r(gf * n).sum(-1)).astype(np.float64)
@@ -496,9 +523,11 @@ def expert_norm_backward(norm: Norm, g: np.ndarray, y: np.ndarray, sizes: np.nda
     if norm.affine and norm.scale_input:
         d_scale = r(dx * v).sum(0)
         dx = r(dx * gain).astype(np.float64)
-    dv = np.where(live, dx, 0.0)
-    return (bf16.to_bf16(dv.astype(np.float32)), bf16.to_bf16(np.where(live[:, 0], d_w, 0.0).astype(np.float32)),
-            d_scale, d_bias)
+    dv = np.where(live, dx, 0.0).astype(np.float32)
+    d_w = np.where(live[:, 0], d_w, 0.0).astype(np.float32)
+    if f32:
+        return dv, d_w, d_scale, d_bias
+    return bf16.to_bf16(dv), bf16.to_bf16(d_w), d_scale, d_bias
 
 
 # --- The layer: routed -> experts, forward and backward ----------------------------
@@ -522,13 +551,17 @@ class Saved(NamedTuple):
     y: np.ndarray | None = None  # with a norm: the down GEMM's rows, bf16 bits (m, d)
 
 
-def _float32_built(fmt: str, passes, up_bias, down_bias, norm) -> None:
+def _float32_built(fmt: str, passes) -> None:
     """The float32 layer this build runs (bux_amd.moe._float32_built): every GEMM in
-    MXFP8, no biases, no norm."""
+    MXFP8."""
     if _passes(fmt, passes) != (True, True, True):
         raise NotImplementedError("float32 tokens take every GEMM in MXFP8")
-    if up_bias is not None or down_bias is not None or norm is not None:
-        raise NotImplementedError("float32 tokens with biases or an expert norm")
+
+
+def _ones(m: int, f32: bool) -> np.ndarray:
+    """Weights of 1 in the layer's dtype (the unweighted activation before a norm)."""
+    ones = np.ones(m, np.float32)
+    return ones if f32 else bf16.to_bf16(ones)
 
 
 def _passes(fmt: str, passes) -> tuple[bool, bool, bool]:
@@ -581,7 +614,7 @@ def layer_forward(
     e, d, f, p = up.shape
     f32 = np.asarray(z).dtype == np.float32
     if f32:
-        _float32_built(fmt, passes, up_bias, down_bias, norm)
+        _float32_built(fmt, passes)
     gemm_out = "f32" if f32 else "bf16"
     s = sort_by_expert(idx, e)
     m = t * k
@@ -607,7 +640,7 @@ def layer_forward(
         projected = ragged_dot_bf16(z[tokens], up2, s.sizes, exact=exact)
     if up_bias is not None:
         projected = add_expert_bias(projected, up_bias, s.sizes)
-    act_weights = row_weights if norm is None else bf16.to_bf16(np.ones(m, np.float32))
+    act_weights = row_weights if norm is None else _ones(m, f32)
     h = weighted_units(ffn, projected.reshape(m, f, p), act_weights)
     if fprop or wgrad:
         h_k, h_m = mxfp8.quantized_twice(h, filled, True, height=whole(m))
@@ -622,8 +655,9 @@ def layer_forward(
     out = sum_by_token(y, s.inverse.reshape(t, k), out_bf16=not f32, exact=exact)
     if down_bias is not None and norm is None:
         b = weighted_bias_rows(down_bias, s.sizes, row_weights, m)
-        bsum = sum_by_token(b, s.inverse.reshape(t, k), exact=exact)
-        out = bf16.to_bf16(bf16.to_f32(out) + bf16.to_f32(bsum))
+        bsum = sum_by_token(b, s.inverse.reshape(t, k), out_bf16=not f32, exact=exact)
+        total = _values(out) + _values(bsum)
+        out = total if f32 else bf16.to_bf16(total)
     return out, Saved(s, row_weights, projected, h, x_m, up_n, h_m, down_n, (fprop, dgrad, wgrad),
                       y_rows)
 
@@ -657,7 +691,7 @@ def layer_backward(
             norm, dy[tokens], saved.y, s.sizes, saved.row_weights, norm_scale, norm_bias, down_bias)
         grads.update(norm_scale=d_scale, norm_bias=d_nbias)
         if down_bias is not None:
-            grads["down_bias"] = expert_sums(bf16.to_f32(dv), s.sizes)
+            grads["down_bias"] = expert_sums(_values(dv), s.sizes)
         dy_rows = dv
         if dgrad or wgrad:
             dy_n, dy_m = mxfp8.quantized_twice(dv, filled, True, height=whole(m))
@@ -674,7 +708,7 @@ def layer_backward(
         d_down = contract_mx(saved.h_m, dy_m, s.sizes, out=gemm_out, exact=exact)
     else:
         d_down = weight_grad_bf16(saved.h, dy_rows, s.sizes, exact=exact)
-    act_weights = saved.row_weights if norm is None else bf16.to_bf16(np.ones(m, np.float32))
+    act_weights = saved.row_weights if norm is None else _ones(m, f32)
     dp, d_rows_w = weighted_units_backward(ffn, saved.projected.reshape(m, f, p), act_weights, dh)
     if norm is not None:
         d_rows_w = d_norm_w
@@ -691,17 +725,19 @@ def layer_backward(
     else:
         d_up = weight_grad_bf16(z[tokens], dp, s.sizes, exact=exact)
     if up_bias is not None:
-        grads["up_bias"] = expert_sums(bf16.to_f32(dp), s.sizes).reshape(e, f, p)
+        grads["up_bias"] = expert_sums(_values(dp), s.sizes).reshape(e, f, p)
     if down_bias is not None and norm is None:
-        # weighted(b_rows, w)'s VJP: to b_rows ct * w (bfloat16), to w sum_c ct * b_rows
-        # (products in bfloat16, summed in float32); ct = dy at each row's token
-        g = bf16.to_f32(dy_rows)
-        w = bf16.to_f32(saved.row_weights)[:, None]
+        # weighted(b_rows, w)'s VJP: to b_rows ct * w, to w sum_c ct * b_rows (products
+        # in the layer's dtype, summed in float32); ct = dy at each row's token
+        rd = (lambda a: np.asarray(a, np.float32)) if f32 else bf16.round_f32
+        g = _values(dy_rows)
+        w = _values(saved.row_weights)[:, None]
         b_rows = by_expert(down_bias, s.sizes, m)
         live = (_expert_of_rows(s.sizes, m) >= 0)[:, None]
-        grads["down_bias"] = expert_sums(np.where(live, bf16.round_f32(g * w), 0), s.sizes)
-        extra = bf16.round_f32(bf16.round_f32(g * b_rows).sum(-1, dtype=np.float32))
-        d_rows_w = bf16.to_bf16(bf16.to_f32(d_rows_w) + extra)
+        grads["down_bias"] = expert_sums(np.where(live, rd(g * w), 0), s.sizes)
+        extra = rd(rd(g * b_rows).sum(-1, dtype=np.float32))
+        total = _values(d_rows_w) + extra
+        d_rows_w = total if f32 else bf16.to_bf16(total)
     dz = sum_by_token(dx, s.inverse.reshape(t, k), out_bf16=not f32, exact=exact)
     d_weights = d_rows_w[s.inverse].reshape(t, k)
     grads.update(z=dz, weights=d_weights, up=d_up.reshape(e, d, f, p), down=d_down, dh=dh, dp=dp)

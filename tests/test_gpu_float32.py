@@ -3,7 +3,8 @@ experts/moe.py:846, grouped_blockscaled.py:129): the float32 quantizer bit for b
 against the oracle (which quantizes any float dtype in float32, blockscaled.py:323-343),
 the float32 activation within a few float32 ulps (hardware exp and reciprocal) with its
 copies bit-exact on the GPU's own values, the float32 token sums bit for bit, and the
-whole layer forward and backward against the oracle's float32 layer."""
+whole layer forward and backward against the oracle's float32 layer; the bias and norm
+ops in float32, and the layer with them."""
 
 import numpy as np
 import pytest
@@ -185,6 +186,118 @@ def test_float32_token_sums(lib):
     np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
+def test_float32_bias_ops(lib):
+    """The bias ops of a float32 layer against the oracle's float32 ones: the bias add and
+    the biased token sums bit for bit (the same float32 operations in the same order),
+    each expert's sums (plain, and through the picks' tokens times the row weights) and
+    the down bias's share of the weights' gradient to float32 sums in another order;
+    empty experts and rows past the groups included."""
+    from bux_amd import moe
+    from tests.test_gpu_ffn import _sorted_case
+    rng = np.random.default_rng(68)
+    t, k, e, width, d = 700, 4, 16, 384, 256
+    m = t * k
+    idx, s = _sorted_case(rng, t, k, e)
+    filled = int(s.sizes.sum())
+    offsets = np.concatenate([s.offsets, [filled]]).astype(np.int32)
+    x = _f32(rng, (m, width), 2.0)
+    up_bias = _f32(rng, (e, width))
+    down_bias = _f32(rng, (e, d))
+    y = _f32(rng, (m, d))
+    dy = _f32(rng, (t, d))
+    rw = rng.random(m).astype(np.float32)
+    rw[filled:] = 0
+    dwg = (rng.standard_normal(m) * 0.1).astype(np.float32)
+    announce("float32 bias ops", t, k, e)
+    go, gorder, ginv = to_gpu(offsets), to_gpu(s.order.astype(np.int32)), to_gpu(s.inverse.reshape(t, k))
+    gx = to_gpu(x)
+    moe.add_expert_bias(gx, to_gpu(up_bias), go)
+    sums = moe.expert_sums(to_gpu(x), go)
+    dsums = moe.expert_sums(to_gpu(dy), go, gorder, k, to_gpu(rw))
+    out = moe.sum_by_token_biased(to_gpu(y), ginv, to_gpu(down_bias), go, to_gpu(rw))
+    gdw = to_gpu(dwg)
+    moe.add_bias_weight_grad(gdw, to_gpu(dy), gorder, k, to_gpu(down_bias), go)
+    torch.cuda.synchronize()
+    assert gx.dtype == out.dtype == gdw.dtype == torch.float32
+
+    np.testing.assert_array_equal(gx.cpu().numpy(), omoe.add_expert_bias(x, up_bias, s.sizes))
+    np.testing.assert_allclose(sums.cpu().numpy(), omoe.expert_sums(x, s.sizes), rtol=1e-5, atol=1e-4)
+    assert (sums.cpu().numpy()[s.sizes == 0] == 0).all()
+    g = dy[s.order // k]
+    live = (np.arange(m) < filled)[:, None]
+    wd = np.where(live, g * rw[:, None], 0).astype(np.float32)
+    np.testing.assert_allclose(dsums.cpu().numpy(), omoe.expert_sums(wd, s.sizes), rtol=1e-5, atol=1e-4)
+    b = omoe.weighted_bias_rows(down_bias, s.sizes, rw, m)
+    inv = s.inverse.reshape(t, k)
+    want_out = (omoe.sum_by_token(y, inv, out_bf16=False) + omoe.sum_by_token(b, inv, out_bf16=False))
+    np.testing.assert_array_equal(out.cpu().numpy(), want_out)
+    b_rows = omoe.by_expert(down_bias, s.sizes, m)
+    prods = (g * b_rows).astype(np.float32)  # float32 products
+    want_dw = dwg.astype(np.float64) + prods.astype(np.float64).sum(-1)
+    got_dw = gdw.cpu().numpy().astype(np.float64)
+    tol = np.abs(prods).astype(np.float64).sum(-1) * 2e-6 + np.abs(want_dw) * 2e-7
+    assert (np.abs(got_dw - want_dw) <= tol).all(), float(np.max(np.abs(got_dw - want_dw) - tol))
+    np.testing.assert_array_equal(got_dw[filled:], dwg[filled:])
+
+
+NORMS_F32 = [
+    # (kind, eps, affine, bias, zero_centered, scale_input)
+    ("rmsnorm", 1e-6, True, False, False, False),
+    ("layernorm", 1e-5, True, True, False, False),
+    ("rmsnorm", 1e-6, True, False, True, False),
+    ("layernorm", 1e-6, True, True, False, True),
+]
+
+
+@pytest.mark.parametrize("d", [2048, 1440])
+@pytest.mark.parametrize("nc", NORMS_F32, ids=lambda c: f"{c[0]}-b{int(c[3])}-zc{int(c[4])}-si{int(c[5])}")
+def test_float32_expert_norm(lib, nc, d):
+    """The experts' output norm of a float32 layer and its VJP against the oracle's float32
+    norm (float64 statistics, each op rounded to float32): within 1e-6 in norm forward
+    (float32 statistics in another order and the hardware's reciprocal square root;
+    measured 5e-8 to 7e-8), 1e-5 for the gradients (measured up to 7e-7, the gain's);
+    rows in no expert exactly 0."""
+    from bux_amd import moe
+    from tests.test_gpu_ffn import _sorted_case
+    rng = np.random.default_rng(69)
+    t, k, e = 300, 4, 12
+    m = t * k
+    idx, s = _sorted_case(rng, t, k, e)
+    filled = int(s.sizes.sum())
+    offsets = np.concatenate([s.offsets, [filled]]).astype(np.int32)
+    y = _f32(rng, (m, d), 2.0, 0.0)
+    y[filled:] = 0
+    db = _f32(rng, (e, d), 1.0, 0.0)
+    scale = (1 + 0.3 * rng.standard_normal(d)).astype(np.float32)
+    nb = (0.2 * rng.standard_normal(d)).astype(np.float32)
+    rw = rng.random(m).astype(np.float32)
+    dy = _f32(rng, (t, d), 1.0, 0.0)
+    o, g = omoe.Norm(*nc), moe.ExpertNorm(*nc)
+    announce("float32 expert norm", nc, d)
+    gs = to_gpu(scale) if g.affine else None
+    gb = to_gpu(nb) if g.bias else None
+    go = to_gpu(offsets)
+    out = moe.expert_norm_forward(to_gpu(y), go, g, gs, gb, to_gpu(rw), to_gpu(db))
+    dv, dw, dscale, dbias = moe.expert_norm_backward(
+        to_gpu(dy), to_gpu(s.order.astype(np.int32)), k, to_gpu(y), go, g, gs, gb, to_gpu(rw),
+        to_gpu(db))
+    torch.cuda.synchronize()
+    assert out.dtype == dv.dtype == dw.dtype == torch.float32
+    want = omoe.expert_norm_forward(o, y, s.sizes, rw, scale, nb, db)
+    wdv, wdw, wds, wdb = omoe.expert_norm_backward(o, dy[s.order // k], y, s.sizes, rw, scale, nb, db)
+    got, gdv, gdw = out.cpu().numpy(), dv.cpu().numpy(), dw.cpu().numpy()
+    assert (got[filled:] == 0).all() and (gdv[filled:] == 0).all() and (gdw[filled:] == 0).all()
+    errs = {"out": rel_err(got, want), "dv": rel_err(gdv, wdv), "dw": rel_err(gdw, wdw)}
+    if g.affine:
+        errs["d_scale"] = rel_err(dscale.cpu().numpy(), wds)
+    if g.bias:
+        errs["d_bias"] = rel_err(dbias.cpu().numpy(), wdb)
+    print(f"[norm f32] {nc} d={d} " + " ".join(f"{k_}={v:.2e}" for k_, v in errs.items()), flush=True)
+    assert errs["out"] <= 1e-6, errs
+    for key, err in errs.items():
+        assert err <= 1e-5, (key, err)
+
+
 def _inputs(rng, t, k, e, d, f, outliers=0.0):
     z = _f32(rng, (t, d), 1.0, outliers)
     idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)]).astype(np.int32)
@@ -271,6 +384,55 @@ def test_float32_layer_with_outlier_tokens(lib, name, t, k, e, d, f, act, fmt):
                  for key in ("z", "weights", "up", "down")})
     print(f"[err] float32 {name} outlier tokens", {k_: f"{v:.2e}" for k_, v in errs.items()},
           flush=True)
+    assert max(errs.values()) <= FLOAT32_CEILING, errs
+
+
+BIASED_F32 = [
+    # name, activation, biased, norm
+    ("gptoss_biased", "clamped", True, None),
+    ("rmsnorm", "swiglu", False, ("rmsnorm", 1e-6, True, False, False, False)),
+    ("layernorm_biased", "clamped", True, ("layernorm", 1e-5, True, True, False, False)),
+]
+
+
+@pytest.mark.parametrize("name,act,biased,nc", BIASED_F32)
+def test_float32_layer_with_biases_and_norm(lib, name, act, biased, nc):
+    """The float32 layer with the experts' biases and/or a norm of their outputs
+    (moe.py:857-872; biases and the norm's parameters in float32) against the oracle's
+    float32 layer: y and every gradient, the biases' and the norm's included, within
+    FLOAT32_CEILING (measured up to 4.2e-3, dz with an rmsnorm: the norm's VJP carries
+    the forward's drift into the backward's upstream)."""
+    from bux_amd import moe
+    o = {"swiglu": omoe.Ffn(), "clamped": omoe.Ffn("quick_gelu", 7.0, 1.0)}[act]
+    g = moe.Ffn(o.activation, o.limit, o.up_offset)
+    rng = np.random.default_rng(70)
+    t, k, e, d, f = 1024, 4, 16, 256, 256
+    z, idx, w, up, down, dy = _inputs(rng, t, k, e, d, f)
+    ub = (rng.standard_normal((e, f, 2)) * 0.5).astype(np.float32) if biased else None
+    db = (rng.standard_normal((e, d)) * 0.5).astype(np.float32) if biased else None
+    norm = omoe.Norm(*nc) if nc else None
+    gnorm = moe.ExpertNorm(*nc) if nc else None
+    ns = (1 + 0.3 * rng.standard_normal(d)).astype(np.float32) if nc else None
+    nb = (0.2 * rng.standard_normal(d)).astype(np.float32) if nc and nc[3] else None
+    gpu_of = lambda a: None if a is None else to_gpu(a)
+    kw = dict(up_bias=gpu_of(ub), down_bias=gpu_of(db), norm=gnorm, norm_scale=gpu_of(ns),
+              norm_bias=gpu_of(nb))
+    announce("float32 layer with biases / norm", name)
+    out, saved = moe.experts_forward(to_gpu(z), to_gpu(idx), to_gpu(w), to_gpu(up), to_gpu(down),
+                                     g, "mxfp8", **kw)
+    grads = moe.experts_backward(saved, to_gpu(dy), to_gpu(up), to_gpu(down), g, "mxfp8", **kw)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    okw = dict(up_bias=ub, down_bias=db, norm=norm, norm_scale=ns, norm_bias=nb)
+    want_y, osaved = omoe.layer_forward(z, idx, w, up, down, o, "mxfp8", **okw)
+    want = omoe.layer_backward(osaved, dy, z, up, down, k, o, "mxfp8", **okw)
+    keys = ["z", "weights", "up", "down"]
+    keys += ["up_bias", "down_bias"] if biased else []
+    keys += ["norm_scale"] + (["norm_bias"] if nb is not None else []) if nc else []
+    errs = {"y": rel_err(out.cpu().numpy(), want_y)}
+    for key in keys:
+        errs[key] = rel_err(grads[key].cpu().numpy(), want[key])
+    print(f"[err] float32 {name}", {k_: f"{v:.2e}" for k_, v in errs.items()}, flush=True)
     assert max(errs.values()) <= FLOAT32_CEILING, errs
 
 

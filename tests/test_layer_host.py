@@ -40,7 +40,7 @@ def test_kernels_in_mxfp8_are_checked_against_the_recipe_and_the_kernels():
 def test_the_layer_takes_bfloat16_or_float32_tokens():
     """y, dx and dW take x's dtype, the kernels cast to it (moe.py:846,
     grouped_blockscaled.py:129): bfloat16 or float32 tokens, others refused; float32
-    runs every GEMM in MXFP8, without biases or a norm (refused before any launch)."""
+    runs every GEMM in MXFP8 (refused before any launch)."""
     idx = torch.zeros(8, 2, dtype=torch.int32)
     up, down = torch.empty(4, 64, 32, 2), torch.empty(4, 32, 64)
     w = torch.empty(8, 2)
@@ -51,8 +51,20 @@ def test_the_layer_takes_bfloat16_or_float32_tokens():
         moe.experts_forward(z, idx, w, up, down, fmt="compute")
     with pytest.raises(NotImplementedError, match="every GEMM in MXFP8"):
         moe.experts_forward(z, idx, w, up, down, passes=("fprop",))
-    with pytest.raises(NotImplementedError, match="biases or an expert norm"):
-        moe.experts_forward(z, idx, w, up, down, down_bias=torch.empty(4, 64))
+    with pytest.raises(NotImplementedError, match="every GEMM in MXFP8"):
+        moe.experts_forward(z, idx, w, up, down, fmt="compute", down_bias=torch.empty(4, 64))
+
+
+def test_the_bias_and_norm_ops_take_one_dtype():
+    """Each bias and norm op runs in its rows' dtype, bfloat16 or float32, and refuses a
+    tensor of another dtype beside them before any launch."""
+    x = torch.empty(8, 16)
+    assert moe._runs_f32("add_expert_bias", x, torch.empty(2, 16))
+    assert not moe._runs_f32("add_expert_bias", x.bfloat16(), torch.empty(2, 16).bfloat16(), None)
+    with pytest.raises(TypeError, match="torch.bfloat16 tensor beside torch.float32 rows"):
+        moe._runs_f32("expert_norm_forward", x, torch.empty(16).bfloat16())
+    with pytest.raises(TypeError, match="bfloat16 or float32 rows, not torch.float16"):
+        moe._runs_f32("expert_sums", x.half())
 
 
 def test_an_ffn_names_one_of_the_ten_activations():

@@ -556,6 +556,87 @@ def test_the_expert_norm_and_its_gradient_are_torchs(norm):
         close(dbias, bt.grad, 2e-2)
 
 
+@pytest.mark.parametrize("norm", NORMS)
+def test_a_float32_expert_norm_rounds_only_to_float32(norm):
+    """The oracle's norm of a float32 layer (float32 y, weights, biases and parameters)
+    against torch's layer_norm / rms_norm and autograd in float64: within float32's
+    rounding (each op rounded once to float32, not to bfloat16), rows past the groups 0,
+    the results float32."""
+    rng = np.random.default_rng(14)
+    m, d, sizes = 96, 64, np.array([30, 0, 50, 6])
+    filled = int(sizes.sum())
+    f32 = np.float32
+    y = (rng.standard_normal((m, d)) * 3 + 0.5).astype(f32)
+    db = rng.standard_normal((4, d)).astype(f32)
+    scale = (1 + 0.3 * rng.standard_normal(d)).astype(f32)
+    nb = (0.2 * rng.standard_normal(d)).astype(f32)
+    w = rng.random(m).astype(f32)
+    g = rng.standard_normal((m, d)).astype(f32)
+    out = moe.expert_norm_forward(norm, y, sizes, w, scale, nb, db)
+    dv, dw, dscale, dbias = moe.expert_norm_backward(norm, g, y, sizes, w, scale, nb, db)
+    assert out.dtype == dv.dtype == dw.dtype == np.float32
+
+    def t(a, grad=False):
+        return torch.tensor(a, dtype=torch.float64, requires_grad=grad)
+
+    yt, wt, st, bt = t(y[:filled], True), t(w[:filled], True), t(scale, True), t(nb, True)
+    rows = torch.tensor(np.repeat(np.arange(4), sizes))
+    want = _torch_norm(norm, yt + t(db)[rows], st, bt) * wt[:, None]
+    want.backward(t(g[:filled]))
+
+    def close(got, ref, tol):
+        ref = ref.detach().numpy()
+        err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert err < tol, err
+
+    # bfloat16 roundings anywhere would put these near 1e-3
+    close(out[:filled], want, 2e-6)
+    assert (out[filled:] == 0).all() and (dv[filled:] == 0).all() and (dw[filled:] == 0).all()
+    close(dv[:filled], yt.grad, 2e-5)
+    close(dw[:filled], wt.grad, 2e-5)
+    if norm.affine:
+        close(dscale, st.grad, 2e-5)
+    if norm.bias:
+        close(dbias, bt.grad, 2e-5)
+
+
+def test_a_float32_layers_down_bias_adds_each_picks_weighted_bias():
+    """The down bias of a float32 MXFP8 layer (moe.py:866-870): the output with it less
+    the output without it is each token's sum of w b[e] over its picks, in float32; its
+    gradient each expert's sum of dy w over its picks, and the weights' gradient gains
+    dy . b[e] (float64 sums here, float32 there); the up bias's gradient each expert's
+    sum of the layer's own d projected."""
+    rng = np.random.default_rng(15)
+    t, k, e, d, f = 64, 2, 4, 64, 64
+    f32 = np.float32
+    z = rng.standard_normal((t, d)).astype(f32)
+    idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)])
+    w = rng.random((t, k)).astype(f32)
+    up = (rng.standard_normal((e, d, f, 2)) * 0.1).astype(f32)
+    down = (rng.standard_normal((e, f, d)) * 0.1).astype(f32)
+    dy = rng.standard_normal((t, d)).astype(f32)
+    ub = rng.standard_normal((e, f, 2)).astype(f32)
+    db = rng.standard_normal((e, d)).astype(f32)
+    ffn = moe.Ffn()
+    y0, s0 = moe.layer_forward(z, idx, w, up, down, ffn, up_bias=ub)
+    y1, s1 = moe.layer_forward(z, idx, w, up, down, ffn, up_bias=ub, down_bias=db)
+    g0 = moe.layer_backward(s0, dy, z, up, down, k, ffn, up_bias=ub)
+    g1 = moe.layer_backward(s1, dy, z, up, down, k, ffn, up_bias=ub, down_bias=db)
+    assert y1.dtype == np.float32 and g1["down_bias"].dtype == np.float64
+    picks = (w.astype(np.float64)[:, :, None] * db.astype(np.float64)[idx]).sum(1)
+    np.testing.assert_allclose(y1.astype(np.float64) - y0, picks, rtol=1e-5, atol=1e-5)
+    want_db = np.zeros((e, d))
+    np.add.at(want_db, idx.reshape(-1), np.repeat(dy.astype(np.float64), k, 0) * w.reshape(-1, 1))
+    np.testing.assert_allclose(g1["down_bias"], want_db, rtol=1e-5, atol=1e-5)
+    dots = (dy.astype(np.float64)[:, None, :] * db.astype(np.float64)[idx]).sum(-1)
+    np.testing.assert_allclose(g1["weights"].astype(np.float64) - g0["weights"], dots,
+                               rtol=1e-4, atol=1e-4)
+    sorted_experts = np.sort(idx.reshape(-1), kind="stable")
+    want_ub = np.zeros((e, f * 2))
+    np.add.at(want_ub, sorted_experts, g1["dp"].astype(np.float64))
+    np.testing.assert_allclose(g1["up_bias"].reshape(e, -1), want_ub, rtol=1e-6, atol=1e-9)
+
+
 DENSE = [
     # (ffn, p, biased, norm)
     (moe.Ffn("quick_gelu", 7.0, 1.0), 2, False, None),
