@@ -83,6 +83,9 @@ SIGNATURES = {
         _int, [_p, _p, _int, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
     "bux_bf16_grouped_contract_workspace_size": (_size, [_i32]),
     "bux_bf16_grouped_contract": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
+    "bux_bf16_grouped_rows_f32": (
+        _int, [_p, _p, _int, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
+    "bux_bf16_grouped_contract_f32": (_int, [_p, _p, _p, _i32, _i64, _i64, _i64, _p, _p, _size, _p]),
     "bux_token_rows": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
     "bux_token_sums_f32": (_int, [_p, _i64, _p, _i64, _i32, _i64, _p, _p]),
@@ -105,6 +108,8 @@ SIGNATURES = {
                _p, _size, _p]),
     "bux_glu_forward": (_int, [_p, _p, _p, _i64, _i64, _ffn, _p, _p]),
     "bux_glu_backward": (_int, [_p, _p, _p, _p, _i64, _i64, _ffn, _p, _p, _p]),
+    "bux_glu_forward_f32": (_int, [_p, _p, _p, _i64, _i64, _ffn, _p, _p]),
+    "bux_glu_backward_f32": (_int, [_p, _p, _p, _p, _i64, _i64, _ffn, _p, _p, _p]),
     "bux_glu_quantize": (
         _int, [_p, _p, _p, _i64, _i64, _ffn, _i64, _p, _p, _p, _p, _p, _p]),
     "bux_glu_quantize_f32": (

@@ -36,4 +36,7 @@ extern "C" const char* bux_last_error(void) { return bux::last_error; }
 // 0.3.1: float32 twins of the bias ops (bux_expert_bias_add_f32, bux_expert_sums_f32,
 // bux_token_sums_biased_f32, bux_expert_bias_weight_grad_f32) and of the expert norm
 // (bux_expert_norm_forward_f32, bux_expert_norm_backward_f32).
-extern "C" int bux_version(void) { return 301; }
+// 0.3.2: float32 twins of the compute format's GEMMs (bux_bf16_grouped_rows_f32,
+// bux_bf16_grouped_contract_f32) and of the activation (bux_glu_forward_f32,
+// bux_glu_backward_f32): a float32 layer runs any pass outside MXFP8.
+extern "C" int bux_version(void) { return 302; }

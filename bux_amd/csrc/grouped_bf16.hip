@@ -573,6 +573,173 @@ __global__ __launch_bounds__(THREADS) void contract_any_kernel(
   any_store(acc, dw + (static_cast<int64_t>(g) * k + row0) * n + col0, n, rows, cols);
 }
 
+// --- float32 --------------------------------------------------------------------------
+//
+// The compute format's GEMMs for a layer in float32 (the reference's ragged_dot and its
+// transpose on float32 operands, float32 sums and outputs, grouped.py:90-146): the
+// any-shape kernels' tiles and element loads, 4 bytes each, with v_mfma_f32_32x32x2_f32
+// (float32 products, float32 sums). K goes 16 a step; in MFMA kk of a step, lane half h
+// takes K 8 h + kk, so that a lane's 8 operands of a step are one 32-byte LDS row
+// segment. Rows are 20 floats apart in LDS (16 and a pad).
+
+constexpr int F32_PITCH = ANY_BK + 4;
+
+struct F32Stage {
+  float a[BM][F32_PITCH];
+  float b[ANY_BN][F32_PITCH];
+};
+
+__device__ __forceinline__ void f32_step(const F32Stage& st, v16f acc[2][2]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  float a[2][8], b[2][8];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float4* ar = reinterpret_cast<const float4*>(&st.a[wave * 64 + p * 32 + r][8 * h]);
+    const float4* br = reinterpret_cast<const float4*>(&st.b[p * 32 + r][8 * h]);
+    const float4 a0 = ar[0], a1 = ar[1], b0 = br[0], b1 = br[1];
+    a[p][0] = a0.x; a[p][1] = a0.y; a[p][2] = a0.z; a[p][3] = a0.w;
+    a[p][4] = a1.x; a[p][5] = a1.y; a[p][6] = a1.z; a[p][7] = a1.w;
+    b[p][0] = b0.x; b[p][1] = b0.y; b[p][2] = b0.z; b[p][3] = b0.w;
+    b[p][4] = b1.x; b[p][5] = b1.y; b[p][6] = b1.z; b[p][7] = b1.w;
+  }
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        acc[p][q] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[p][kk], b[q][kk], acc[p][q], 0, 0, 0);
+}
+
+__device__ __forceinline__ void f32_store(const v16f acc[2][2], float* tile, int64_t ld,
+                                          int32_t rows, int32_t cols) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int32_t col = q * 32 + (lane & 31);
+      if (col >= cols) continue;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int32_t row = wave * 64 + p * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        if (row < rows) tile[row * ld + col] = acc[p][q][j];
+      }
+    }
+}
+
+__device__ __forceinline__ float f32_at(const float* p, bool inside) { return inside ? *p : 0.0f; }
+
+__device__ __forceinline__ void zero_acc2(v16f acc[2][2]) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[p][q][j] = 0.0f;
+}
+
+// rows in float32: y[i] = x[i] w[g(i)] (w [g, k, n]; BKM: w [g, n, k] and x[i] w[g(i)]^T),
+// as rows_any_kernel.
+template <bool BKM>
+__global__ __launch_bounds__(THREADS) void rows_f32_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, int32_t groups, int64_t m,
+    int64_t n, int64_t k, const int32_t* __restrict__ starts, const Tile* __restrict__ tiles,
+    int64_t col_tiles, float* __restrict__ y) {
+  __shared__ __align__(16) F32Stage st;
+  if (!list_fits(starts, groups, static_cast<int32_t>(m), static_cast<int32_t>(m))) return;
+  const int64_t id = blockIdx.x / col_tiles;
+  if (id >= starts[groups + 1]) return;
+  const Tile t = tiles[id];
+  const int64_t col0 = (blockIdx.x % col_tiles) * ANY_BN;
+  const int64_t hi = t.hi < m ? t.hi : m;
+  const int32_t rows = static_cast<int32_t>(hi - t.lo);
+  if (rows <= 0) return;
+  const int32_t cols = static_cast<int32_t>(n - col0 < ANY_BN ? n - col0 : ANY_BN);
+  v16f acc[2][2];
+  zero_acc2(acc);
+  if (t.group < groups) {  // the rows past the groups: zeros
+    const float* wg = w + static_cast<int64_t>(t.group) * n * k;
+    const int tid = threadIdx.x, kk = tid & 15;
+    for (int64_t k0 = 0; k0 < k; k0 += ANY_BK) {
+      const bool kin = k0 + kk < k;
+      float av[16], bv[4];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int32_t r = (tid >> 4) + 16 * i;
+        av[i] = f32_at(x + (t.lo + r) * k + k0 + kk, kin && r < rows);
+      }
+      if constexpr (BKM) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int32_t c = (tid >> 4) + 16 * i;
+          bv[i] = f32_at(wg + (col0 + c) * k + k0 + kk, kin && c < cols);
+        }
+      } else {
+        const int64_t kr = k0 + (tid >> 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int32_t c = 4 * (tid & 15) + i;
+          bv[i] = f32_at(wg + kr * n + col0 + c, kr < k && c < cols);
+        }
+      }
+      __syncthreads();  // the last step's reads are done
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st.a[(tid >> 4) + 16 * i][kk] = av[i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (BKM) st.b[(tid >> 4) + 16 * i][kk] = bv[i];
+        else st.b[4 * (tid & 15) + i][tid >> 4] = bv[i];
+      }
+      __syncthreads();
+      f32_step(st, acc);
+    }
+  }
+  f32_store(acc, y + t.lo * n + col0, n, rows, cols);
+}
+
+// contract in float32: dw[g] = x[rows of g]^T dy[rows of g], as contract_any_kernel.
+__global__ __launch_bounds__(THREADS) void contract_f32_kernel(
+    const float* __restrict__ x, const float* __restrict__ dy, int32_t groups, int64_t m,
+    int64_t k, int64_t n, const int32_t* __restrict__ starts, int64_t k_tiles, int64_t col_tiles,
+    float* __restrict__ dw) {
+  __shared__ __align__(16) F32Stage st;
+  if (!list_fits(starts, groups, -1, 0)) return;
+  const int64_t per = k_tiles * col_tiles;
+  const int32_t g = static_cast<int32_t>(blockIdx.x / per);
+  const int64_t row0 = (blockIdx.x / col_tiles % k_tiles) * BM, col0 = (blockIdx.x % col_tiles) * ANY_BN;
+  const int32_t rows = static_cast<int32_t>(k - row0 < BM ? k - row0 : BM);
+  const int32_t cols = static_cast<int32_t>(n - col0 < ANY_BN ? n - col0 : ANY_BN);
+  v16f acc[2][2];
+  zero_acc2(acc);
+  const int64_t start = starts[g], end = starts[g + 1] < m ? starts[g + 1] : m;
+  const int tid = threadIdx.x;
+  for (int64_t i0 = start; i0 < end; i0 += ANY_BK) {
+    float av[16], bv[4];
+    // A(r, i) = x[i][r]: thread tid takes r = tid of the 16 rows i
+#pragma unroll
+    for (int i = 0; i < 16; ++i) av[i] = f32_at(x + (i0 + i) * k + row0 + tid, i0 + i < end && tid < rows);
+    // B(c, i) = dy[i][c]: row i0 + tid / 16, 4 consecutive columns
+    const int64_t ir = i0 + (tid >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int32_t c = 4 * (tid & 15) + i;
+      bv[i] = f32_at(dy + ir * n + col0 + c, ir < end && c < cols);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<float4*>(&st.a[tid][4 * i]) =
+          make_float4(av[4 * i], av[4 * i + 1], av[4 * i + 2], av[4 * i + 3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.b[4 * (tid & 15) + i][tid >> 4] = bv[i];
+    __syncthreads();
+    f32_step(st, acc);
+  }
+  f32_store(acc, dw + (static_cast<int64_t>(g) * k + row0) * n + col0, n, rows, cols);
+}
+
 // Whether every offset a kernel forms into an operand of `rows` rows of `cols` elements
 // (a tile's reads past it included) fits the 32-bit buffer offsets.
 bool fits(int64_t rows, int64_t cols) { return (rows + BM) * (cols + BM) * 2 < (1LL << 31); }
@@ -694,4 +861,70 @@ extern "C" int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, 
                      static_cast<int32_t>(k), static_cast<int32_t>(n), starts_in(workspace),
                      static_cast<int32_t>(d_tiles), static_cast<int32_t>(f_tiles), dw);
   return launched("bf16 contract_kernel");
+}
+
+extern "C" int bux_bf16_grouped_rows_f32(const float* x, const float* w, int w_transposed,
+                                         const int32_t* sizes, int32_t groups, int64_t m,
+                                         int64_t n, int64_t k, float* y, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS,
+            "bux_bf16_grouped_rows_f32: groups=%d outside [1, %d]", groups, MAX_GROUPS);
+  BUX_CHECK(m >= 0 && n > 0 && k > 0, "bux_bf16_grouped_rows_f32: bad shape m=%lld n=%lld k=%lld",
+            (long long)m, (long long)n, (long long)k);
+  BUX_CHECK(m < INT32_MAX, "bux_bf16_grouped_rows_f32: m=%lld rows", (long long)m);
+  BUX_CHECK(sizes && w && y && (m == 0 || x), "bux_bf16_grouped_rows_f32: NULL buffer");
+  const size_t need = bux_bf16_grouped_rows_workspace_size(groups, m);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(BUX_E_WORKSPACE, "bux_bf16_grouped_rows_f32: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  if (m == 0) return BUX_OK;
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, m,
+                     row_slots(groups, m, m), 1, starts_in(workspace), tiles_in(workspace, groups),
+                     header_in(workspace), m, nullptr);
+  if (int rc = launched("prologue_kernel")) return rc;
+  const int64_t col_tiles = ceil_div(n, ANY_BN), slots = row_slots(groups, m, m);
+  const int64_t blocks = slots * col_tiles;
+  BUX_CHECK(blocks < (1LL << 31), "bux_bf16_grouped_rows_f32: too many tiles");
+  if (w_transposed)
+    hipLaunchKernelGGL(rows_f32_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0,
+                       s, x, w, groups, m, n, k, starts_in(workspace), tiles_in(workspace, groups),
+                       col_tiles, y);
+  else
+    hipLaunchKernelGGL(rows_f32_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(THREADS),
+                       0, s, x, w, groups, m, n, k, starts_in(workspace),
+                       tiles_in(workspace, groups), col_tiles, y);
+  return launched("rows_f32_kernel");
+}
+
+extern "C" int bux_bf16_grouped_contract_f32(const float* x, const float* dy, const int32_t* sizes,
+                                             int32_t groups, int64_t m, int64_t k, int64_t n,
+                                             float* dw, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  using namespace bux;
+  clear_error();
+  BUX_CHECK(groups >= 1 && groups <= MAX_GROUPS,
+            "bux_bf16_grouped_contract_f32: groups=%d outside [1, %d]", groups, MAX_GROUPS);
+  BUX_CHECK(m >= 0 && n > 0 && k > 0,
+            "bux_bf16_grouped_contract_f32: bad shape m=%lld k=%lld n=%lld", (long long)m,
+            (long long)k, (long long)n);
+  BUX_CHECK(m < INT32_MAX, "bux_bf16_grouped_contract_f32: m=%lld rows", (long long)m);
+  BUX_CHECK(sizes && dw && (m == 0 || (x && dy)), "bux_bf16_grouped_contract_f32: NULL buffer");
+  const size_t need = bux_bf16_grouped_contract_workspace_size(groups);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(BUX_E_WORKSPACE,
+                "bux_bf16_grouped_contract_f32: workspace of %zu bytes, %zu needed",
+                workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(prologue_kernel, dim3(1), dim3(THREADS), 0, s, sizes, groups, 0, 0, 1,
+                     starts_in(workspace), nullptr, header_in(workspace), m, nullptr);
+  if (int rc = launched("prologue_kernel")) return rc;
+  const int64_t k_tiles = ceil_div(k, BM), col_tiles = ceil_div(n, ANY_BN);
+  const int64_t blocks = static_cast<int64_t>(groups) * k_tiles * col_tiles;
+  BUX_CHECK(blocks < (1LL << 31), "bux_bf16_grouped_contract_f32: too many tiles");
+  hipLaunchKernelGGL(contract_f32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0, s,
+                     x, dy, groups, m, k, n, starts_in(workspace), k_tiles, col_tiles, dw);
+  return launched("contract_f32_kernel");
 }

@@ -15,6 +15,8 @@
 // lanes takes 2048 columns of a row. The activation computes in float32 and rounds
 // once to bfloat16 (XLA fuses the elementwise chain and keeps float32 inside).
 
+#include <type_traits>
+
 #include "common.h"
 #include "glu.h"
 
@@ -228,84 +230,107 @@ __global__ __launch_bounds__(THREADS) void token_sums_f32_kernel(const float* __
   o[1] = acc[1];
 }
 
-// A lane takes 4 units of a row: 16 bytes of projected gated (4 up-gate pairs), 8 plain.
-template <typename K>
+// A row's 4 units from u on, as a lane takes them: gated, 8 values (4 up-gate pairs, up j
+// at v[2 j]); plain, up j at v[2 j] and 0 beside it. T the layer's element type.
+template <typename T, bool GATED>
+__device__ __forceinline__ void load_units(const T* projected, int64_t i, int64_t f, int64_t u,
+                                           float* v) {
+  if constexpr (GATED) {
+    Elem<T>::load8(projected + (i * f + u) * 2, v);
+  } else if constexpr (std::is_same<T, float>::value) {
+    const float4 r = *reinterpret_cast<const float4*>(projected + i * f + u);
+    v[0] = r.x; v[2] = r.y; v[4] = r.z; v[6] = r.w;
+    v[1] = v[3] = v[5] = v[7] = 0.0f;
+  } else {
+    unpack8(spread4(*reinterpret_cast<const uint2*>(projected + i * f + u)), v);
+  }
+}
+
+// 4 values of a row (8 bytes of bfloat16, 16 of float32), stored or loaded.
+__device__ __forceinline__ void store4(uint16_t* p, const float* v) {
+  *reinterpret_cast<uint2*>(p) =
+      make_uint2(f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16),
+                 f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16));
+}
+__device__ __forceinline__ void store4(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void load4(const uint16_t* p, float* v) {
+  const uint2 d = *reinterpret_cast<const uint2*>(p);
+  v[0] = bf16_to_f32(d.x & 0xffffu);
+  v[1] = bf16_to_f32(d.x >> 16);
+  v[2] = bf16_to_f32(d.y & 0xffffu);
+  v[3] = bf16_to_f32(d.y >> 16);
+}
+__device__ __forceinline__ void load4(const float* p, float* v) {
+  const float4 d = *reinterpret_cast<const float4*>(p);
+  v[0] = d.x; v[1] = d.y; v[2] = d.z; v[3] = d.w;
+}
+
+// A lane takes 4 units of a row: 16 bytes of projected gated (4 up-gate pairs), 8 plain
+// (32 and 16 for float32). T the layer's element type: the activation computes in
+// float32 and rounds once to T.
+template <typename K, typename T>
 __global__ __launch_bounds__(THREADS) void glu_forward_kernel(
-    const uint16_t* __restrict__ projected, const uint16_t* __restrict__ weights,
-    const int32_t* __restrict__ filled_ptr, int64_t m, int64_t f, Act act,
-    uint16_t* __restrict__ h) {
+    const T* __restrict__ projected, const T* __restrict__ weights,
+    const int32_t* __restrict__ filled_ptr, int64_t m, int64_t f, Act act, T* __restrict__ h) {
+  constexpr bool F32 = std::is_same<T, float>::value;
   const int64_t chunks = (f + THREADS * 4 - 1) / (THREADS * 4);
   const int64_t i = blockIdx.x / chunks;
   const int64_t u = ((blockIdx.x % chunks) * THREADS + threadIdx.x) * 4;
   if (u >= f) return;
   const int64_t filled = filled_ptr ? *filled_ptr : m;
-  uint2 packed = make_uint2(0, 0);
+  float out[4] = {0, 0, 0, 0};
   if (i < filled) {
     float p[8];
-    if constexpr (K::gated) {
-      unpack8(*reinterpret_cast<const uint4*>(projected + (i * f + u) * 2), p);
-    } else {
-      const uint2 r = *reinterpret_cast<const uint2*>(projected + i * f + u);
-      unpack8(spread4(r), p);  // up j at p[2 j]
-    }
-    const float w = bf16_to_f32(weights[i]);
-    float out[4];
+    load_units<T, K::gated>(projected, i, f, u, p);
+    const float w = Elem<T>::value(weights[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = glu_unit<K>(act, p[2 * j], p[2 * j + 1], w);
-    packed.x = f32_to_bf16(out[0]) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
-    packed.y = f32_to_bf16(out[2]) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
+    for (int j = 0; j < 4; ++j) out[j] = glu_unit<K, F32>(act, p[2 * j], p[2 * j + 1], w);
   }
-  *reinterpret_cast<uint2*>(h + i * f + u) = packed;
+  store4(h + i * f + u, out);
 }
 
 // One wave a row: d projected elementwise, d weight summed over the row's units.
-template <typename K>
+template <typename K, typename T>
 __global__ __launch_bounds__(THREADS) void glu_backward_kernel(
-    const uint16_t* __restrict__ projected, const uint16_t* __restrict__ weights,
-    const uint16_t* __restrict__ dh, const int32_t* __restrict__ filled_ptr, int64_t m, int64_t f,
-    Act act, uint16_t* __restrict__ d_projected, uint16_t* __restrict__ d_weights) {
+    const T* __restrict__ projected, const T* __restrict__ weights, const T* __restrict__ dh,
+    const int32_t* __restrict__ filled_ptr, int64_t m, int64_t f, Act act,
+    T* __restrict__ d_projected, T* __restrict__ d_weights) {
+  constexpr bool F32 = std::is_same<T, float>::value;
   const int lane = threadIdx.x & 63;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * (THREADS / 64) + (threadIdx.x >> 6);
   if (i >= m) return;
   const int64_t filled = filled_ptr ? *filled_ptr : m;
   const bool live = i < filled;
-  const float w = live ? bf16_to_f32(weights[i]) : 0.0f;
+  const float w = live ? Elem<T>::value(weights[i]) : 0.0f;
   float dw = 0.0f;
   for (int64_t u = 4 * lane; u < f; u += 256) {
     float p[8] = {0, 0, 0, 0, 0, 0, 0, 0}, g[4] = {0, 0, 0, 0};
     if (live) {
-      if constexpr (K::gated) {
-        unpack8(*reinterpret_cast<const uint4*>(projected + (i * f + u) * 2), p);
-      } else {
-        const uint2 r = *reinterpret_cast<const uint2*>(projected + i * f + u);
-        unpack8(spread4(r), p);
-      }
-      const uint2 d = *reinterpret_cast<const uint2*>(dh + i * f + u);
-      g[0] = bf16_to_f32(d.x & 0xffffu);
-      g[1] = bf16_to_f32(d.x >> 16);
-      g[2] = bf16_to_f32(d.y & 0xffffu);
-      g[3] = bf16_to_f32(d.y >> 16);
+      load_units<T, K::gated>(projected, i, f, u, p);
+      load4(dh + i * f + u, g);
     }
     float dp[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // rows past `filled`: +0 (not 0 x offset)
     if (live) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float term;
-        glu_unit_grad<K>(act, p[2 * j], p[2 * j + 1], w, g[j], &dp[2 * j], &dp[2 * j + 1], &term);
+        glu_unit_grad<K, F32>(act, p[2 * j], p[2 * j + 1], w, g[j], &dp[2 * j], &dp[2 * j + 1],
+                              &term);
         dw += term;
       }
     }
     if constexpr (K::gated) {
-      *reinterpret_cast<uint4*>(d_projected + (i * f + u) * 2) = pack8(dp);
+      Elem<T>::store8(d_projected + (i * f + u) * 2, dp);
     } else {
-      const uint4 q = pack8(dp);  // d up j in the low half of word j
-      *reinterpret_cast<uint2*>(d_projected + i * f + u) =
-          make_uint2((q.x & 0xffffu) | (q.y << 16), (q.z & 0xffffu) | (q.w << 16));
+      const float up[4] = {dp[0], dp[2], dp[4], dp[6]};
+      store4(d_projected + i * f + u, up);
     }
   }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) dw += __shfl_xor(dw, s);
-  if (lane == 0) d_weights[i] = f32_to_bf16(dw);
+  if (lane == 0) d_weights[i] = Elem<T>::make(dw);
 }
 
 // --- The experts' biases --------------------------------------------------------------
@@ -652,45 +677,75 @@ extern "C" int bux_expert_bias_weight_grad_f32(const float* dy, const int32_t* i
                                m, width, bias, offsets, experts, d_weights, stream);
 }
 
-extern "C" int bux_glu_forward(const uint16_t* projected, const uint16_t* weights,
-                               const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
-                               uint16_t* h, void* stream) {
-  using namespace bux;
-  clear_error();
+namespace bux {
+namespace {
+template <typename T>
+int glu_forward(const char* name, const T* projected, const T* weights, const int32_t* filled,
+                int64_t m, int64_t f, const bux_ffn* ffn, T* h, void* stream) {
   BUX_CHECK(m >= 0 && m <= 2147483647LL && f > 0 && f % 4 == 0,
-            "bux_glu_forward: bad shape m=%lld f=%lld (f a multiple of 4)", (long long)m,
-            (long long)f);
+            "%s: bad shape m=%lld f=%lld (f a multiple of 4)", name, (long long)m, (long long)f);
   Act act;
-  if (int rc = act_of("bux_glu_forward", ffn, &act)) return rc;
+  if (int rc = act_of(name, ffn, &act)) return rc;
   if (m == 0) return BUX_OK;
-  BUX_CHECK(projected && weights && h, "bux_glu_forward: NULL buffer");
-  BUX_CHECK(m * ceil_div(f, THREADS * 4) < (1LL << 31), "bux_glu_forward: too large");
+  BUX_CHECK(projected && weights && h, "%s: NULL buffer", name);
+  BUX_CHECK(m * ceil_div(f, THREADS * 4) < (1LL << 31), "%s: too large", name);
   dim3 grid(static_cast<unsigned>(m * ceil_div(f, THREADS * 4)));
   return with_kind(act, [&](auto kind) {
-    hipLaunchKernelGGL(glu_forward_kernel<decltype(kind)>, grid, dim3(THREADS), 0,
+    hipLaunchKernelGGL((glu_forward_kernel<decltype(kind), T>), grid, dim3(THREADS), 0,
                        as_stream(stream), projected, weights, filled, m, f, act, h);
     return launched("glu_forward_kernel");
   });
+}
+
+template <typename T>
+int glu_backward(const char* name, const T* projected, const T* weights, const T* dh,
+                 const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn, T* d_projected,
+                 T* d_weights, void* stream) {
+  BUX_CHECK(m >= 0 && m <= 2147483647LL && f > 0 && f % 4 == 0,
+            "%s: bad shape m=%lld f=%lld (f a multiple of 4)", name, (long long)m, (long long)f);
+  Act act;
+  if (int rc = act_of(name, ffn, &act)) return rc;
+  if (m == 0) return BUX_OK;
+  BUX_CHECK(projected && weights && dh && d_projected && d_weights, "%s: NULL buffer", name);
+  dim3 grid(static_cast<unsigned>(ceil_div(m, THREADS / 64)));
+  return with_kind(act, [&](auto kind) {
+    hipLaunchKernelGGL((glu_backward_kernel<decltype(kind), T>), grid, dim3(THREADS), 0,
+                       as_stream(stream), projected, weights, dh, filled, m, f, act, d_projected,
+                       d_weights);
+    return launched("glu_backward_kernel");
+  });
+}
+}  // namespace
+}  // namespace bux
+
+extern "C" int bux_glu_forward(const uint16_t* projected, const uint16_t* weights,
+                               const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
+                               uint16_t* h, void* stream) {
+  bux::clear_error();
+  return bux::glu_forward("bux_glu_forward", projected, weights, filled, m, f, ffn, h, stream);
+}
+
+extern "C" int bux_glu_forward_f32(const float* projected, const float* weights,
+                                   const int32_t* filled, int64_t m, int64_t f,
+                                   const bux_ffn* ffn, float* h, void* stream) {
+  bux::clear_error();
+  return bux::glu_forward("bux_glu_forward_f32", projected, weights, filled, m, f, ffn, h, stream);
 }
 
 extern "C" int bux_glu_backward(const uint16_t* projected, const uint16_t* weights,
                                 const uint16_t* dh, const int32_t* filled, int64_t m, int64_t f,
                                 const bux_ffn* ffn, uint16_t* d_projected, uint16_t* d_weights,
                                 void* stream) {
-  using namespace bux;
-  clear_error();
-  BUX_CHECK(m >= 0 && m <= 2147483647LL && f > 0 && f % 4 == 0,
-            "bux_glu_backward: bad shape m=%lld f=%lld (f a multiple of 4)", (long long)m,
-            (long long)f);
-  Act act;
-  if (int rc = act_of("bux_glu_backward", ffn, &act)) return rc;
-  if (m == 0) return BUX_OK;
-  BUX_CHECK(projected && weights && dh && d_projected && d_weights, "bux_glu_backward: NULL buffer");
-  dim3 grid(static_cast<unsigned>(ceil_div(m, THREADS / 64)));
-  return with_kind(act, [&](auto kind) {
-    hipLaunchKernelGGL(glu_backward_kernel<decltype(kind)>, grid, dim3(THREADS), 0,
-                       as_stream(stream), projected, weights, dh, filled, m, f, act, d_projected,
-                       d_weights);
-    return launched("glu_backward_kernel");
-  });
+  bux::clear_error();
+  return bux::glu_backward("bux_glu_backward", projected, weights, dh, filled, m, f, ffn,
+                           d_projected, d_weights, stream);
+}
+
+extern "C" int bux_glu_backward_f32(const float* projected, const float* weights,
+                                    const float* dh, const int32_t* filled, int64_t m, int64_t f,
+                                    const bux_ffn* ffn, float* d_projected, float* d_weights,
+                                    void* stream) {
+  bux::clear_error();
+  return bux::glu_backward("bux_glu_backward_f32", projected, weights, dh, filled, m, f, ffn,
+                           d_projected, d_weights, stream);
 }

@@ -142,13 +142,16 @@ def weighted_units(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
                    filled: torch.Tensor | None = None) -> torch.Tensor:
     """Return each row's hidden units times its weight, (m, f), from projected
     (m, f, 2) ([..., 0] up, [..., 1] gate) or (m, f, 1) (up) and the rows' weights
-    (m,); rows from `filled` on are 0."""
+    (m,); rows from `filled` on are 0. In projected's dtype (bfloat16, or float32 with
+    float32 weights)."""
     require(projected, weights, filled)
     m, f, gated = _gating(projected)
-    h = torch.empty(m, f, dtype=torch.bfloat16, device=projected.device)
+    f32 = _f32(projected, weights)
+    h = torch.empty(m, f, dtype=projected.dtype, device=projected.device)
     st = ffn.struct(gated)
-    _lib.check(lib().bux_glu_forward(ptr(projected), ptr(weights), ptr(filled), m, f,
-                                     ctypes.byref(st), ptr(h), stream()))
+    forward = lib().bux_glu_forward_f32 if f32 else lib().bux_glu_forward
+    _lib.check(forward(ptr(projected), ptr(weights), ptr(filled), m, f, ctypes.byref(st), ptr(h),
+                       stream()))
     return h
 
 
@@ -211,14 +214,16 @@ def weighted_units_backward(ffn: Ffn, projected: torch.Tensor, weights: torch.Te
                             dh: torch.Tensor, filled: torch.Tensor | None = None
                             ) -> tuple[torch.Tensor, torch.Tensor]:
     """Return the gradients of `weighted_units` to projected (m, f, p) and to the
-    weights (m,)."""
+    weights (m,), in projected's dtype (weights and dh the same)."""
     require(projected, weights, dh, filled)
     m, f, gated = _gating(projected)
-    dp = torch.empty(projected.shape, dtype=torch.bfloat16, device=projected.device)
-    dw = torch.empty(m, dtype=torch.bfloat16, device=projected.device)
+    f32 = _f32(projected, weights, dh)
+    dp = torch.empty(projected.shape, dtype=projected.dtype, device=projected.device)
+    dw = torch.empty(m, dtype=projected.dtype, device=projected.device)
     st = ffn.struct(gated)
-    _lib.check(lib().bux_glu_backward(ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f,
-                                      ctypes.byref(st), ptr(dp), ptr(dw), stream()))
+    backward = lib().bux_glu_backward_f32 if f32 else lib().bux_glu_backward
+    _lib.check(backward(ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f,
+                        ctypes.byref(st), ptr(dp), ptr(dw), stream()))
     return dp, dw
 
 
@@ -479,14 +484,6 @@ def _layer_dtype(name: str, x: torch.Tensor) -> torch.dtype:
     return x.dtype
 
 
-def _float32_built(name: str, fmt: str, passes: tuple[bool, bool, bool]) -> None:
-    """Raise for what a float32 layer does not run here: a GEMM outside MXFP8 (the
-    bfloat16 "compute" GEMMs take bfloat16 operands)."""
-    if fmt not in MX_FORMATS or not all(passes):
-        raise NotImplementedError(f"{name}: float32 tokens take every GEMM in MXFP8 "
-                                  f"(fmt {fmt!r}, passes {passes})")
-
-
 def _cast(dt: torch.dtype, *tensors: torch.Tensor | None) -> tuple[torch.Tensor | None, ...]:
     """The tensors in the layer's dtype (None stays None): the biases as by_expert casts
     them (moe.py:848-849), and the norm's parameters as the model's forward does."""
@@ -509,8 +506,8 @@ def experts_forward(
     (the kernels and weights cast to it, experts/moe.py:846; the GEMMs' outputs in it,
     grouped_blockscaled.Dtypes, grouped_blockscaled.py:129): in float32 no value is
     rounded to bfloat16 between the steps (the MXFP8 operands are quantized from the
-    float32 values), and every GEMM multiplies in MXFP8 (others raise
-    NotImplementedError). The biases and the norm's parameters are cast to z's dtype.
+    float32 values; a pass outside MXFP8 multiplies float32 operands, as ragged_dot of
+    float32 does). The biases and the norm's parameters are cast to z's dtype.
 
     Args:
         z: the tokens, bfloat16 or float32 (t, d).
@@ -551,7 +548,6 @@ def experts_forward(
     up_bias, down_bias, norm_scale, norm_bias = _cast(dt, up_bias, down_bias, norm_scale, norm_bias)
     fprop, dgrad, wgrad = passes_of(fmt, passes)
     if dt == torch.float32:
-        _float32_built("experts_forward", fmt, (fprop, dgrad, wgrad))
         fused = False  # the fused up GEMM's epilogue is bfloat16's
     if quantized is not None:
         quantized.check(fmt, up, down)

@@ -202,8 +202,16 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxMxContractListed, MxContractListed,
 // --- a-10: the bfloat16 grouped GEMMs ----------------------------------------------------
 
 // ws: a u8 result of bux_bf16_grouped_rows_workspace_size (_contract_) bytes.
+// float32 x (a layer in float32): bux_bf16_grouped_rows_f32 (_contract_f32), the same
+// workspace.
 static ffi::Error Bf16Rows(hipStream_t s, In x, In w, In sizes, int64_t transposed, Out y,
                            Out ws) {
+  if (f32(x))
+    return status(bux_bf16_grouped_rows_f32(at<const float>(x), at<const float>(w),
+                                            static_cast<int>(transposed), at<const int32_t>(sizes),
+                                            static_cast<int32_t>(dim(w, 0)), dim(x, 0), dim(y, 1),
+                                            dim(x, 1), at<float>(y), at<void>(ws),
+                                            ws->size_bytes(), s));
   return status(bux_bf16_grouped_rows(at<const uint16_t>(x), at<const uint16_t>(w),
                                       static_cast<int>(transposed), at<const int32_t>(sizes),
                                       static_cast<int32_t>(dim(w, 0)), dim(x, 0), dim(y, 1),
@@ -215,6 +223,12 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxBf16Rows, Bf16Rows,
                                   .Attr<int64_t>("transposed").Ret<In>().Ret<In>());
 
 static ffi::Error Bf16Contract(hipStream_t s, In x, In dy, In sizes, Out dw, Out ws) {
+  if (f32(x))
+    return status(bux_bf16_grouped_contract_f32(at<const float>(x), at<const float>(dy),
+                                                at<const int32_t>(sizes),
+                                                static_cast<int32_t>(sizes.element_count()),
+                                                dim(x, 0), dim(x, 1), dim(dy, 1), at<float>(dw),
+                                                at<void>(ws), ws->size_bytes(), s));
   return status(bux_bf16_grouped_contract(at<const uint16_t>(x), at<const uint16_t>(dy),
                                           at<const int32_t>(sizes),
                                           static_cast<int32_t>(sizes.element_count()), dim(x, 0),
@@ -255,6 +269,10 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxTokenSums, TokenSums,
 static ffi::Error GluForward(hipStream_t s, In projected, In weights, In filled, BUX_FFN_PARAMS,
                              Out h) {
   const bux_ffn ffn = BUX_FFN;
+  if (f32(projected))  // a layer in float32
+    return status(bux_glu_forward_f32(at<const float>(projected), at<const float>(weights),
+                                      at<const int32_t>(filled), dim(h, 0), dim(h, 1), &ffn,
+                                      at<float>(h), s));
   return status(bux_glu_forward(at<const uint16_t>(projected), at<const uint16_t>(weights),
                                 at<const int32_t>(filled), dim(h, 0), dim(h, 1), &ffn,
                                 at<uint16_t>(h), s));
@@ -266,6 +284,11 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(BuxGluForward, GluForward,
 static ffi::Error GluBackward(hipStream_t s, In projected, In weights, In dh, In filled,
                               BUX_FFN_PARAMS, Out d_projected, Out d_weights) {
   const bux_ffn ffn = BUX_FFN;
+  if (f32(projected))  // a layer in float32
+    return status(bux_glu_backward_f32(at<const float>(projected), at<const float>(weights),
+                                       at<const float>(dh), at<const int32_t>(filled), dim(dh, 0),
+                                       dim(dh, 1), &ffn, at<float>(d_projected),
+                                       at<float>(d_weights), s));
   return status(bux_glu_backward(at<const uint16_t>(projected), at<const uint16_t>(weights),
                                  at<const uint16_t>(dh), at<const int32_t>(filled), dim(dh, 0),
                                  dim(dh, 1), &ffn, at<uint16_t>(d_projected),

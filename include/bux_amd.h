@@ -266,6 +266,16 @@ size_t bux_bf16_grouped_contract_workspace_size(int32_t groups);
 int bux_bf16_grouped_contract(const uint16_t* x, const uint16_t* dy, const int32_t* sizes,
                               int32_t groups, int64_t m, int64_t k, int64_t n, uint16_t* dw,
                               void* workspace, size_t workspace_bytes, void* stream);
+/* The same two GEMMs for a layer in float32 (ragged_dot and its transpose of float32
+ * operands, grouped.py:90-146 with x in float32): x, w, dy, y and dw float32, float32
+ * products and sums (v_mfma_f32_32x32x2_f32), any n and k; the same workspaces. */
+int bux_bf16_grouped_rows_f32(const float* x, const float* w, int w_transposed,
+                              const int32_t* sizes, int32_t groups, int64_t m, int64_t n,
+                              int64_t k, float* y, void* workspace, size_t workspace_bytes,
+                              void* stream);
+int bux_bf16_grouped_contract_f32(const float* x, const float* dy, const int32_t* sizes,
+                                  int32_t groups, int64_t m, int64_t k, int64_t n, float* dw,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-2 / a-3. The token path's gathers and sums.
@@ -331,6 +341,13 @@ int bux_glu_forward(const uint16_t* projected, const uint16_t* weights, const in
 int bux_glu_backward(const uint16_t* projected, const uint16_t* weights, const uint16_t* dh,
                      const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
                      uint16_t* d_projected, uint16_t* d_weights, void* stream);
+/* The same for a layer in float32: every buffer above float32, one rounding to float32,
+ * quick_gelu's 1.702 as a float32 (as bux_glu_quantize_f32). */
+int bux_glu_forward_f32(const float* projected, const float* weights, const int32_t* filled,
+                        int64_t m, int64_t f, const bux_ffn* ffn, float* h, void* stream);
+int bux_glu_backward_f32(const float* projected, const float* weights, const float* dh,
+                         const int32_t* filled, int64_t m, int64_t f, const bux_ffn* ffn,
+                         float* d_projected, float* d_weights, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * a-8. The experts' biases (MLPConfig.bias, config.py:214).

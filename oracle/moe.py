@@ -189,13 +189,15 @@ def contract_mx(a: Blocks, b: Blocks, sizes: np.ndarray, out: str = "bf16",
     return _cast(dw, out)
 
 
-def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = "bf16",
+def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str | None = None,
                     exact: bool = False) -> np.ndarray:
-    """Return ``jax.lax.ragged_dot`` of bfloat16 x (m, k) and w (g, k, n): float32
-    sums rounded to bfloat16, rows past the groups 0 (grouped.py:42-62,90-102).
-    `exact`: sums in float64, one rounding (`_sums`)."""
+    """Return ``jax.lax.ragged_dot`` of x (m, k) and w (g, k, n), bfloat16 bits or (a
+    layer in float32) float32 values: float32 sums rounded to x's dtype (`out` None;
+    else as `_cast`), rows past the groups 0 (grouped.py:42-62,90-102). `exact`: sums in
+    float64, one rounding (`_sums`)."""
     t = _sums(exact)
-    xf, wf = bf16.to_f32(x).astype(t), bf16.to_f32(w).astype(t)
+    out = out or ("f32" if _is_f32(x) else "bf16")
+    xf, wf = _values(x).astype(t), _values(w).astype(t)
     y = np.zeros((xf.shape[0], wf.shape[2]), t)
     start = 0
     for g, size in enumerate(np.asarray(sizes).tolist()):
@@ -205,12 +207,13 @@ def ragged_dot_bf16(x: np.ndarray, w: np.ndarray, sizes: np.ndarray, out: str = 
     return _cast(y, out)
 
 
-def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str = "bf16",
+def weight_grad_bf16(x: np.ndarray, dy: np.ndarray, sizes: np.ndarray, out: str | None = None,
                      exact: bool = False) -> np.ndarray:
-    """Return x^T dy per group (grouped.py:105-146), float32 sums (`exact`: float64,
-    one rounding)."""
+    """Return x^T dy per group (grouped.py:105-146) of bfloat16 bits or float32 values,
+    float32 sums (`exact`: float64, one rounding) in x's dtype (`out` None)."""
     t = _sums(exact)
-    xf, gf = bf16.to_f32(x).astype(t), bf16.to_f32(dy).astype(t)
+    out = out or ("f32" if _is_f32(x) else "bf16")
+    xf, gf = _values(x).astype(t), _values(dy).astype(t)
     sizes = np.asarray(sizes).tolist()
     dw = np.zeros((len(sizes), xf.shape[1], gf.shape[1]), t)
     start = 0
@@ -551,13 +554,6 @@ class Saved(NamedTuple):
     y: np.ndarray | None = None  # with a norm: the down GEMM's rows, bf16 bits (m, d)
 
 
-def _float32_built(fmt: str, passes) -> None:
-    """The float32 layer this build runs (bux_amd.moe._float32_built): every GEMM in
-    MXFP8."""
-    if _passes(fmt, passes) != (True, True, True):
-        raise NotImplementedError("float32 tokens take every GEMM in MXFP8")
-
-
 def _ones(m: int, f32: bool) -> np.ndarray:
     """Weights of 1 in the layer's dtype (the unweighted activation before a norm)."""
     ones = np.ones(m, np.float32)
@@ -613,8 +609,6 @@ def layer_forward(
     t, k = idx.shape
     e, d, f, p = up.shape
     f32 = np.asarray(z).dtype == np.float32
-    if f32:
-        _float32_built(fmt, passes)
     gemm_out = "f32" if f32 else "bf16"
     s = sort_by_expert(idx, e)
     m = t * k

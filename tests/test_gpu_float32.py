@@ -436,6 +436,161 @@ def test_float32_layer_with_biases_and_norm(lib, name, act, biased, nc):
     assert max(errs.values()) <= FLOAT32_CEILING, errs
 
 
+# float32 "compute" GEMMs: (sizes, m, k, n); None: 64 groups of 0 .. 40 rows, some empty.
+# The rows past the groups hold NaN in the operands.
+F32_GEMMS = {
+    "five groups": ([70, 0, 100, 3, 77], 256, 256, 512),
+    "k and n off 16": ([33, 0, 95, 1, 200], 400, 45, 37),
+    "k and n of 1": ([5, 0, 3], 10, 1, 1),
+    "64 small groups": (None, 1500, 64, 70),
+    "all groups empty": ([0, 0], 100, 64, 64),
+}
+
+
+def _gemm_sizes(rng, sizes, m):
+    if sizes is None:
+        sizes = rng.integers(0, 41, 64)
+        sizes[rng.choice(64, 8, replace=False)] = 0
+    sizes = np.asarray(sizes, np.int32)
+    assert sizes.sum() <= m
+    return sizes
+
+
+def _within_f32_sums(got, exact, magnitude, terms, what):
+    """Each float32 sum within 4 terms x 2^-24 of the sum of its products' magnitudes from
+    the exact (float64) sum: float32 products and sums in any order."""
+    bound = 4.0 * max(terms, 1) * 2.0 ** -24 * magnitude + 1e-30
+    excess = np.abs(got.astype(np.float64) - exact) - bound
+    assert (excess <= 0).all(), f"{what}: {int((excess > 0).sum())} sums past the bound"
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("case", list(F32_GEMMS))
+def test_float32_compute_rows(lib, case, transposed):
+    """The compute format's rows GEMM of a float32 layer (ragged_dot of float32 operands,
+    grouped.py:90-102): float32 out, each sum within float32 summation error of the exact
+    one, rows past the groups 0 (their NaN operands unread)."""
+    from bux_amd import grouped
+    rng = np.random.default_rng(71)
+    sizes, m, k, n = F32_GEMMS[case]
+    sizes = _gemm_sizes(rng, sizes, m)
+    filled = int(sizes.sum())
+    x = _f32(rng, (m, k))
+    x[filled:] = np.nan
+    w = (rng.standard_normal((len(sizes), k, n)) * 0.02).astype(np.float32)
+    announce("float32 compute rows", case, transposed)
+    wt = np.ascontiguousarray(np.swapaxes(w, 1, 2)) if transposed else w
+    y = grouped.dot(to_gpu(x), to_gpu(wt), to_gpu(sizes), transposed=transposed)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float32
+    got = y.cpu().numpy()
+    assert (got[filled:] == 0).all()
+    exact = omoe.ragged_dot_bf16(x[:filled], w, sizes, out="f64", exact=True)
+    mag = omoe.ragged_dot_bf16(np.abs(x[:filled]), np.abs(w), sizes, out="f64", exact=True)
+    _within_f32_sums(got[:filled], exact, mag, k, "rows")
+
+
+@pytest.mark.parametrize("case", list(F32_GEMMS))
+def test_float32_compute_weight_grad(lib, case):
+    """The compute format's wgrad of a float32 layer (grouped.py:105-146): float32 out,
+    each sum within float32 summation error of the exact one, empty groups 0, the rows
+    past the groups (NaN) unread."""
+    from bux_amd import grouped
+    rng = np.random.default_rng(72)
+    sizes, m, k, n = F32_GEMMS[case]
+    sizes = _gemm_sizes(rng, sizes, m)
+    filled = int(sizes.sum())
+    x = _f32(rng, (m, k))
+    dy = (rng.standard_normal((m, n)) * 0.01).astype(np.float32)
+    x[filled:] = np.nan
+    dy[filled:] = np.nan
+    announce("float32 compute weight_grad", case)
+    dw = grouped.weight_grad(to_gpu(x), to_gpu(dy), to_gpu(sizes))
+    torch.cuda.synchronize()
+    assert dw.dtype == torch.float32
+    got = dw.cpu().numpy()
+    assert (got[sizes == 0] == 0).all()
+    exact = omoe.weight_grad_bf16(x[:filled], dy[:filled], sizes, out="f64", exact=True)
+    mag = omoe.weight_grad_bf16(np.abs(x[:filled]), np.abs(dy[:filled]), sizes, out="f64", exact=True)
+    _within_f32_sums(got, exact, mag, int(sizes.max()) if sizes.size else 1, "weight_grad")
+
+
+@pytest.mark.parametrize("name", ["swiglu", "clamped", "gelu_plain"])
+def test_float32_activation_twins_agree(lib, name):
+    """The float32 activation outside the quantizer (a pass in the compute format) is the
+    quantizer's own float32 h bit for bit, and its gradient the quantizer's d projected
+    bit for bit (the same float32 arithmetic), the weights' gradient within float32 sums
+    in another order."""
+    from bux_amd import moe
+    ffn, p = {"swiglu": (moe.Ffn(), 2), "clamped": (moe.Ffn("quick_gelu", 7.0, 1.0), 2),
+              "gelu_plain": (moe.Ffn("gelu", None, 0.0, 3.0), 1)}[name]
+    rng = np.random.default_rng(73)
+    m, f, filled = 700, 256, 650
+    proj = to_gpu((rng.standard_normal((m, f, p)) * 3).astype(np.float32))
+    w = to_gpu(rng.random(m).astype(np.float32))
+    dh = to_gpu((rng.standard_normal((m, f)) * 0.1).astype(np.float32))
+    gf = to_gpu(np.array([filled], np.int32))
+    announce("float32 activation twins", name)
+    h = moe.weighted_units(ffn, proj, w, gf)
+    from bux_amd import grouped_mxfp8
+    height = grouped_mxfp8.whole(m)
+    _, _, h_kept = moe.weighted_units_quantized(ffn, proj, w, gf, height, keep=True)
+    dp, dw = moe.weighted_units_backward(ffn, proj, w, dh, gf)
+    _, _, dw_q, dp_q = moe.weighted_units_backward_quantized(ffn, proj, w, dh, gf, height, True)
+    torch.cuda.synchronize()
+    assert h.dtype == dp.dtype == dw.dtype == torch.float32
+    assert torch.equal(h, h_kept)
+    assert (h[filled:] == 0).all() and (dp[filled:] == 0).all()
+    assert torch.equal(dp.reshape(m, -1), dp_q.reshape(m, -1))
+    # f terms a row, each summed in float32 in another order: within f float32 ulps of
+    # the largest row's magnitude (measured 1.9e-6 at most against 1.2e-3 allowed)
+    got, ref = dw.cpu().numpy(), dw_q.cpu().numpy()
+    np.testing.assert_allclose(got, ref, rtol=0, atol=f * 2.0 ** -24 * float(np.abs(ref).max()))
+
+
+COMPUTE_F32 = [
+    # name, fmt, passes, biased
+    ("compute", "compute", None, False),
+    ("compute_biased", "compute", None, True),
+    ("fprop_in_mxfp8", "mxfp8", ("fprop",), False),
+    ("dgrad_wgrad_in_mxfp8", "mxfp8", ("dgrad", "wgrad"), True),
+]
+
+
+@pytest.mark.parametrize("name,fmt,passes,biased", COMPUTE_F32)
+def test_float32_layer_outside_mxfp8(lib, name, fmt, passes, biased):
+    """The float32 layer with passes in the compute format (float32 GEMMs, as ragged_dot
+    of float32 operands): y and every gradient against the oracle's float32 layer;
+    within 1e-5 with no pass in MXFP8 (measured 5e-7 at most: float32 sums in another
+    order, the activation's hardware exp), within FLOAT32_CEILING with some (measured
+    1.2e-3 at most)."""
+    from bux_amd import moe
+    o = omoe.Ffn("quick_gelu", 7.0, 1.0)
+    g = moe.Ffn(o.activation, o.limit, o.up_offset)
+    rng = np.random.default_rng(74)
+    t, k, e, d, f = 512, 4, 8, 256, 256
+    z, idx, w, up, down, dy = _inputs(rng, t, k, e, d, f)
+    ub = (rng.standard_normal((e, f, 2)) * 0.5).astype(np.float32) if biased else None
+    db = (rng.standard_normal((e, d)) * 0.5).astype(np.float32) if biased else None
+    gpu_of = lambda a: None if a is None else to_gpu(a)
+    announce("float32 layer outside MXFP8", name)
+    out, saved = moe.experts_forward(to_gpu(z), to_gpu(idx), to_gpu(w), to_gpu(up), to_gpu(down),
+                                     g, fmt, passes=passes, up_bias=gpu_of(ub), down_bias=gpu_of(db))
+    grads = moe.experts_backward(saved, to_gpu(dy), to_gpu(up), to_gpu(down), g, fmt,
+                                 up_bias=gpu_of(ub), down_bias=gpu_of(db))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    want_y, osaved = omoe.layer_forward(z, idx, w, up, down, o, fmt, passes, up_bias=ub, down_bias=db)
+    want = omoe.layer_backward(osaved, dy, z, up, down, k, o, fmt, up_bias=ub, down_bias=db)
+    keys = ["z", "weights", "up", "down"] + (["up_bias", "down_bias"] if biased else [])
+    errs = {"y": rel_err(out.cpu().numpy(), want_y)}
+    for key in keys:
+        errs[key] = rel_err(grads[key].cpu().numpy(), want[key])
+    print(f"[err] float32 {name}", {k_: f"{v:.2e}" for k_, v in errs.items()}, flush=True)
+    bar = 1e-5 if fmt == "compute" else FLOAT32_CEILING
+    assert max(errs.values()) <= bar, errs
+
+
 def _run_layer(args, o, fmt, exact):
     z, idx, w, up, down, dy = args
     y, saved = omoe.layer_forward(z, idx, w, up, down, o, fmt, exact=exact)

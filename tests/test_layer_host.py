@@ -39,20 +39,13 @@ def test_kernels_in_mxfp8_are_checked_against_the_recipe_and_the_kernels():
 
 def test_the_layer_takes_bfloat16_or_float32_tokens():
     """y, dx and dW take x's dtype, the kernels cast to it (moe.py:846,
-    grouped_blockscaled.py:129): bfloat16 or float32 tokens, others refused; float32
-    runs every GEMM in MXFP8 (refused before any launch)."""
+    grouped_blockscaled.py:129): bfloat16 or float32 tokens, others refused before any
+    launch."""
     idx = torch.zeros(8, 2, dtype=torch.int32)
     up, down = torch.empty(4, 64, 32, 2), torch.empty(4, 32, 64)
     w = torch.empty(8, 2)
     with pytest.raises(TypeError, match="bfloat16 or float32, not torch.float16"):
         moe.experts_forward(torch.empty(8, 64, dtype=torch.float16), idx, w, up, down)
-    z = torch.empty(8, 64)
-    with pytest.raises(NotImplementedError, match="every GEMM in MXFP8"):
-        moe.experts_forward(z, idx, w, up, down, fmt="compute")
-    with pytest.raises(NotImplementedError, match="every GEMM in MXFP8"):
-        moe.experts_forward(z, idx, w, up, down, passes=("fprop",))
-    with pytest.raises(NotImplementedError, match="every GEMM in MXFP8"):
-        moe.experts_forward(z, idx, w, up, down, fmt="compute", down_bias=torch.empty(4, 64))
 
 
 def test_the_bias_and_norm_ops_take_one_dtype():

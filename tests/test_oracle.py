@@ -648,33 +648,39 @@ DENSE = [
 ]
 
 
+@pytest.mark.parametrize("f32", [False, True], ids=["bf16", "f32"])
 @pytest.mark.parametrize("ffn,p,biased,norm", DENSE)
-def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased, norm):
+def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased, norm, f32):
     """``sorted`` equals ``dense`` with gradients (tests/test_moe.py:475-484): the
-    oracle's layer, in bfloat16 ("compute"), against every token through each of its
-    experts one by one, differentiated by torch.autograd in float64; gated or plain,
-    with the experts' up and down biases (moe.py:857-870) or without."""
+    oracle's layer, in the compute format (bfloat16, or float32 for float32 inputs),
+    against every token through each of its experts one by one, differentiated by
+    torch.autograd in float64; gated or plain, with the experts' up and down biases
+    (moe.py:857-870) or without, with an expert norm or without. In float32 the layer
+    is within float32's rounding (a bfloat16 rounding anywhere would show at 1e-3)."""
     rng = np.random.default_rng(10)
     t, k, e, d, f = 48, 2, 5, 32, 24
-    z = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
+    cast = (lambda a: a.astype(np.float32)) if f32 else (lambda a: bf16.to_bf16(a.astype(np.float32)))
+    z = cast(rng.standard_normal((t, d)))
     idx = np.stack([rng.choice(e, k, replace=False) for _ in range(t)])
-    w = bf16.to_bf16(rng.random((t, k)).astype(np.float32))
-    up = bf16.to_bf16((rng.standard_normal((e, d, f, p)) * 0.3).astype(np.float32))
-    down = bf16.to_bf16((rng.standard_normal((e, f, d)) * 0.3).astype(np.float32))
-    dy = bf16.to_bf16(rng.standard_normal((t, d)).astype(np.float32))
-    ub = bf16.to_bf16((rng.standard_normal((e, f, p))).astype(np.float32)) if biased else None
-    db = bf16.to_bf16((rng.standard_normal((e, d))).astype(np.float32)) if biased else None
-    ns = bf16.to_bf16((1 + 0.3 * rng.standard_normal(d)).astype(np.float32)) if norm else None
-    nb = bf16.to_bf16((0.2 * rng.standard_normal(d)).astype(np.float32)) if norm else None
+    w = cast(rng.random((t, k)))
+    up = cast(rng.standard_normal((e, d, f, p)) * 0.3)
+    down = cast(rng.standard_normal((e, f, d)) * 0.3)
+    dy = cast(rng.standard_normal((t, d)))
+    ub = cast(rng.standard_normal((e, f, p))) if biased else None
+    db = cast(rng.standard_normal((e, d))) if biased else None
+    ns = cast(1 + 0.3 * rng.standard_normal(d)) if norm else None
+    nb = cast(0.2 * rng.standard_normal(d)) if norm else None
     y, saved = moe.layer_forward(z, idx, w, up, down, ffn, fmt="compute", up_bias=ub, down_bias=db,
                                  norm=norm, norm_scale=ns, norm_bias=nb)
     grads = moe.layer_backward(saved, dy, z, up, down, k, ffn, fmt="compute", up_bias=ub,
                                down_bias=db, norm=norm, norm_scale=ns, norm_bias=nb)
 
     def tensor(a):
-        return torch.tensor(bf16.to_f32(a), dtype=torch.float64, requires_grad=True)
+        return torch.tensor(moe._values(a), dtype=torch.float64, requires_grad=True)
 
     zt, wt, upt, downt = tensor(z), tensor(w), tensor(up), tensor(down)
+    # quick_gelu's 1.702: a float32 constant times a float32 gate, 1.703125 for bfloat16
+    alpha = float(np.float32(1.702)) if f32 else None
     ubt, dbt = (tensor(ub), tensor(db)) if biased else (None, None)
     nst, nbt = (tensor(ns), tensor(nb)) if norm else (None, None)
     out = torch.zeros(t, d, dtype=torch.float64)
@@ -685,18 +691,22 @@ def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased, norm):
             if biased:
                 pr = pr + ubt[g].reshape(p * f)
             if norm is None:
-                h = _torch_units(ffn, pr.reshape(1, f, p), wt[tok, j].reshape(1))[0]
+                h = _torch_units(ffn, pr.reshape(1, f, p), wt[tok, j].reshape(1), alpha)[0]
                 row = h @ downt[g]
                 if biased:
                     row = row + dbt[g] * wt[tok, j]
             else:  # moe.py:871-872: unweighted, biased, normed, then weighted
-                h = _torch_units(ffn, pr.reshape(1, f, p), torch.ones(1, dtype=torch.float64))[0]
+                h = _torch_units(ffn, pr.reshape(1, f, p), torch.ones(1, dtype=torch.float64),
+                                 alpha)[0]
                 row = h @ downt[g]
                 if biased:
                     row = row + dbt[g]
                 row = _torch_norm(norm, row, nst, nbt) * wt[tok, j]
             out = out.index_add(0, torch.tensor([tok]), row[None])
-    out.backward(torch.tensor(bf16.to_f32(dy), dtype=torch.float64))
+    out.backward(torch.tensor(moe._values(dy), dtype=torch.float64))
+    if f32:
+        assert y.dtype == grads["z"].dtype == grads["up"].dtype == np.float32
+    fwd, bwd = (2e-6, 2e-5) if f32 else (1e-2, 2e-2)
 
     def close(got, want, rtol):
         got = bf16.to_f32(got).astype(np.float64) if got.dtype == np.uint16 else got
@@ -704,18 +714,18 @@ def test_the_sorted_layer_is_the_dense_one_with_gradients(ffn, p, biased, norm):
         err = np.linalg.norm(got - want) / np.linalg.norm(want)
         assert err < rtol, err
 
-    close(y, out, 1e-2)
-    close(grads["z"], zt.grad, 2e-2)
-    close(grads["weights"], wt.grad, 2e-2)
-    close(grads["up"], upt.grad, 2e-2)
-    close(grads["down"], downt.grad, 2e-2)
+    close(y, out, fwd)
+    close(grads["z"], zt.grad, bwd)
+    close(grads["weights"], wt.grad, bwd)
+    close(grads["up"], upt.grad, bwd)
+    close(grads["down"], downt.grad, bwd)
     if biased:
-        close(grads["up_bias"], ubt.grad, 2e-2)
-        close(grads["down_bias"], dbt.grad, 2e-2)
+        close(grads["up_bias"], ubt.grad, bwd)
+        close(grads["down_bias"], dbt.grad, bwd)
     if norm is not None:
-        close(grads["norm_scale"], nst.grad, 2e-2)
+        close(grads["norm_scale"], nst.grad, bwd)
         if norm.bias:
-            close(grads["norm_bias"], nbt.grad, 2e-2)
+            close(grads["norm_bias"], nbt.grad, bwd)
         else:
             assert grads["norm_bias"] is None
 
