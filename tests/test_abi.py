@@ -216,6 +216,34 @@ def test_bias_ops_reject_bad_arguments(lib):
     assert rc == 1 and "0 experts" in _msg(lib)
 
 
+def test_float32_twins_reject_what_their_bfloat16_twins_reject(lib):
+    """Each float32 twin checks its arguments as its bfloat16 twin does, before any
+    launch, and names itself in the error."""
+    p = ctypes.c_void_p(16)
+    norm = _lib.NormStruct(_lib.RMSNORM, 1, 0, 0, 0, 1e-6)
+    ffn = _lib.FfnStruct(0, 1, 0, 0.0, 0, 0.0, 0.0)
+    cases = [
+        ("bux_expert_bias_add", (p, 10, 12, p, p, 4, None), 1, "width=12"),
+        ("bux_expert_sums", (p, p, 0, 10, None, 10, 16, p, 4, p, None), 1, "index_div=0"),
+        ("bux_token_sums_biased", (p, 10, p, 5, 2, 16, None, p, 4, p, p, None), 1, "NULL bias"),
+        ("bux_expert_bias_weight_grad", (p, p, 1, -1, 10, 16, p, p, 4, p, None), 1, "sources=-1"),
+        ("bux_expert_norm_forward", (p, 10, 12, None, p, 4, ctypes.byref(norm), p, None, p, p, None),
+         1, "d=12"),
+        ("bux_expert_norm_backward", (p, None, 1, 0, p, 10, 16, None, p, 4, ctypes.byref(norm), p, None,
+                                      p, p, p, p, None, p, 4, None), 2, "workspace"),
+        ("bux_glu_forward", (p, p, None, 10, 6, ctypes.byref(ffn), p, None), 1, "f=6"),
+        ("bux_glu_backward", (p, p, p, None, 10, 6, ctypes.byref(ffn), p, p, None), 1, "f=6"),
+        ("bux_bf16_grouped_rows", (p, p, 0, p, 4, 64, 100, 37, p, p, 8, None), 2, "workspace"),
+        ("bux_bf16_grouped_rows", (p, p, 1, p, 4, 1 << 31, 128, 2048, p, p, 1 << 30, None), 1,
+         "m=2147483648 rows"),
+        ("bux_bf16_grouped_contract", (p, p, p, 0, 64, 45, 100, p, p, 1 << 10, None), 1, "groups=0"),
+    ]
+    for name, args, code, text in cases:
+        for twin in (name, name + "_f32"):
+            rc = getattr(lib, twin)(*args)
+            assert rc == code and text in _msg(lib) and twin in _msg(lib), (twin, rc, _msg(lib))
+
+
 def test_route_rejects_bad_arguments(lib):
     p = ctypes.c_void_p(16)
     f = ctypes.c_float
