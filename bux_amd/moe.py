@@ -567,7 +567,10 @@ def experts_forward(
             listed = grouped_mxfp8.tiles_of(s.sizes, height, m)
     if fprop or wgrad:
         with span("quantize x"):
-            x_k, x_m = grouped_mxfp8.quantized_twice(z, filled, True, s.order, k, height)
+            # the copies its passes take (grouped_blockscaled.py:180-183): x along k for
+            # fprop, x^T along m for wgrad
+            x_k, x_m = grouped_mxfp8.quantized_twice(z, filled, wgrad, s.order, k, height,
+                                                     rows=fprop)
     if not (fprop and wgrad):
         with span("gather x"):
             rows = token_rows(z, s.order, k)
@@ -576,7 +579,9 @@ def experts_forward(
             up_n, up_k = quantized.up_n, quantized.up_k
         else:
             with span("quantize W_up"):
-                up_n, up_k = grouped_mxfp8.quantized_twice(up2, tiles=tiles)
+                # W along n for dgrad, along k for fprop
+                up_n, up_k = grouped_mxfp8.quantized_twice(up2, columns=fprop, rows=dgrad,
+                                                           tiles=tiles)
     h = None
     if (fused and not intermediates and fprop and dgrad and wgrad and up_bias is None
             and norm is None and ffn.fusable(p == 2)):
@@ -605,7 +610,8 @@ def experts_forward(
             down_n, down_k = quantized.down_n, quantized.down_k
         else:
             with span("quantize W_down"):
-                down_n, down_k = grouped_mxfp8.quantized_twice(down, tiles=tiles)
+                down_n, down_k = grouped_mxfp8.quantized_twice(down, columns=fprop, rows=dgrad,
+                                                               tiles=tiles)
     with span("down fprop"):
         if fprop:
             y = grouped_mxfp8.rows(h_k, down_k, s.sizes, dt, height=m, tiles=listed)
@@ -682,12 +688,15 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         # the down GEMM's upstream is dv, a row each (no longer the tokens' dy)
         if dgrad or wgrad:
             with span("quantize dv"):
-                dy_n, dy_m = grouped_mxfp8.quantized_twice(dv, filled, True, height=height)
+                dy_n, dy_m = grouped_mxfp8.quantized_twice(dv, filled, wgrad, height=height,
+                                                           rows=dgrad)
         dy_rows = dv
     else:
         if dgrad or wgrad:
             with span("quantize dy"):
-                dy_n, dy_m = grouped_mxfp8.quantized_twice(dy, filled, True, s.order, k, height)
+                # dy along n for dgrad, dy^T along m for wgrad (grouped_blockscaled.py:204-206)
+                dy_n, dy_m = grouped_mxfp8.quantized_twice(dy, filled, wgrad, s.order, k, height,
+                                                           rows=dgrad)
         if not (dgrad and wgrad):
             with span("gather dy"):
                 dy_rows = token_rows(dy, s.order, k)
