@@ -590,6 +590,12 @@ extern "C" int bux_mx_quantize_f32(const float* x, const int32_t* index, int32_t
 
 namespace bux {
 namespace {
+// The copies an activation's quantizer writes: along the rows where `values` is given,
+// the transpose where `t_values` is (a copy not wanted: NULL; at least one).
+int copies(const uint8_t* values, const uint8_t* t_values) {
+  return (values ? BUX_MX_ROWS : 0) | (t_values ? BUX_MX_COLUMNS : 0);
+}
+
 template <typename V>
 int glu_quantize(const char* name, const V* projected, const V* weights, const int32_t* filled,
                  int64_t m, int64_t f, const bux_ffn* ffn, int64_t height, V* h, uint8_t* values,
@@ -601,7 +607,7 @@ int glu_quantize(const char* name, const V* projected, const V* weights, const i
   return with_kind(act, [&](auto kind) {
     using K = decltype(kind);
     const GluForward<K, V> src{projected, weights, h, act, m, f};
-    return launch_quantize(name, src, 1, m, f, height, filled, BUX_MX_ROWS | BUX_MX_COLUMNS,
+    return launch_quantize(name, src, 1, m, f, height, filled, copies(values, t_values),
                            values, scales, t_values, t_scales, as_stream(stream));
   });
 }
@@ -655,7 +661,7 @@ int glu_backward_quantize(const char* name, const V* projected, const V* weights
   const int rc = with_kind(act, [&](auto kind) {
     using K = decltype(kind);
     const GluBackward<K, V> src{projected, weights, dh, d_projected, partials, act, m, f, tiles};
-    return launch_quantize(name, src, 1, m, cols, height, filled, BUX_MX_ROWS | BUX_MX_COLUMNS,
+    return launch_quantize(name, src, 1, m, cols, height, filled, copies(values, t_values),
                            values, scales, t_values, t_scales, s);
   });
   if (rc != BUX_OK) return rc;

@@ -155,48 +155,67 @@ def weighted_units(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
     return h
 
 
+def _copies(rows: int, cols: int, height: int, along_rows: bool, along_m: bool,
+             dev: torch.device) -> tuple[Tiled | None, Tiled | None]:
+    """Buffers for an (rows, cols) matrix's MXFP8 copies (`height` rows of the row copy),
+    each only if asked for: along its rows (K = cols) and, transposed, along m."""
+    kc, kh = grouped_mxfp8.whole(cols, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
+    row = col = None
+    if along_rows:
+        row = Tiled(torch.empty(kc // 64, height, 64, dtype=torch.uint8, device=dev),
+                    torch.empty(kc // 128, height, 4, dtype=torch.uint8, device=dev))
+    if along_m:
+        col = Tiled(torch.empty(kh // 64, cols, 64, dtype=torch.uint8, device=dev),
+                    torch.empty(kh // 128, cols, 4, dtype=torch.uint8, device=dev))
+    return row, col
+
+
+def _ptrs(copy: Tiled | None) -> tuple[int | None, int | None]:
+    return (None, None) if copy is None else (ptr(copy.values), ptr(copy.scales))
+
+
 def weighted_units_quantized(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
-                             filled: torch.Tensor | None, height: int, keep: bool = False
-                             ) -> tuple[Tiled, Tiled, torch.Tensor | None]:
-    """Return `weighted_units` in MXFP8 along its rows and, as h^T, along m (both tiled,
-    `height` rows of the copies), computed and quantized in one pass; with `keep`, h
-    itself (projected's dtype (m, f)) too, else None. In float32 (projected and weights
-    float32) h is the float32 result, quantized as it is."""
+                             filled: torch.Tensor | None, height: int, keep: bool = False,
+                             rows: bool = True, columns: bool = True,
+                             ) -> tuple[Tiled | None, Tiled | None, torch.Tensor | None]:
+    """Return `weighted_units` in MXFP8 along its rows (if `rows`) and, as h^T, along m
+    (if `columns`; both tiled, `height` rows of the copies, None for a copy not asked
+    for), computed and quantized in one pass; with `keep`, h itself (projected's dtype
+    (m, f)) too, else None. In float32 (projected and weights float32) h is the float32
+    result, quantized as it is."""
     require(projected, weights, filled)
+    if not (rows or columns):
+        raise ValueError("weighted_units_quantized: no copy asked for")
     m, f, gated = _gating(projected)
     dev = projected.device
-    kf, kh = grouped_mxfp8.whole(f, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
-    vals = torch.empty(kf // 64, height, 64, dtype=torch.uint8, device=dev)
-    scales = torch.empty(kf // 128, height, 4, dtype=torch.uint8, device=dev)
-    t_vals = torch.empty(kh // 64, f, 64, dtype=torch.uint8, device=dev)
-    t_scales = torch.empty(kh // 128, f, 4, dtype=torch.uint8, device=dev)
+    row, col = _copies(m, f, height, rows, columns, dev)
     h = torch.empty(m, f, dtype=projected.dtype, device=dev) if keep else None
     st = ffn.struct(gated)
     quantize = lib().bux_glu_quantize_f32 if _f32(projected, weights) else lib().bux_glu_quantize
     _lib.check(quantize(
         ptr(projected), ptr(weights), ptr(filled), m, f, ctypes.byref(st), height, ptr(h),
-        ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), stream()))
-    return Tiled(vals, scales), Tiled(t_vals, t_scales), h
+        *_ptrs(row), *_ptrs(col), stream()))
+    return row, col, h
 
 
 def weighted_units_backward_quantized(
     ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor, dh: torch.Tensor,
     filled: torch.Tensor | None, height: int, keep: bool = False,
-) -> tuple[Tiled, Tiled, torch.Tensor, torch.Tensor | None]:
-    """Return the gradient of `weighted_units` to projected in MXFP8 along its rows (p f)
-    and, transposed, along m (both tiled, `height` rows of the copies), the gradient to
-    the weights (m,), and with `keep` the gradient to projected (m, f, p), in projected's
-    dtype (bfloat16, or float32 with weights and dh float32 too)."""
+    rows: bool = True, columns: bool = True,
+) -> tuple[Tiled | None, Tiled | None, torch.Tensor, torch.Tensor | None]:
+    """Return the gradient of `weighted_units` to projected in MXFP8 along its rows (p f;
+    if `rows`) and, transposed, along m (if `columns`; both tiled, `height` rows of the
+    copies, None for a copy not asked for), the gradient to the weights (m,), and with
+    `keep` the gradient to projected (m, f, p), in projected's dtype (bfloat16, or
+    float32 with weights and dh float32 too)."""
     require(projected, weights, dh, filled)
+    if not (rows or columns):
+        raise ValueError("weighted_units_backward_quantized: no copy asked for")
     f32 = _f32(projected, weights, dh)
     m, f, gated = _gating(projected)
     p = projected.shape[2]
     dev = projected.device
-    kp, kh = grouped_mxfp8.whole(p * f, grouped_mxfp8.K_ALIGN), grouped_mxfp8.whole(height, grouped_mxfp8.K_ALIGN)
-    vals = torch.empty(kp // 64, height, 64, dtype=torch.uint8, device=dev)
-    scales = torch.empty(kp // 128, height, 4, dtype=torch.uint8, device=dev)
-    t_vals = torch.empty(kh // 64, p * f, 64, dtype=torch.uint8, device=dev)
-    t_scales = torch.empty(kh // 128, p * f, 4, dtype=torch.uint8, device=dev)
+    row, col = _copies(m, p * f, height, rows, columns, dev)
     dtype = torch.float32 if f32 else torch.bfloat16
     dw = torch.empty(m, dtype=dtype, device=dev)
     dp = torch.empty(m, f, p, dtype=dtype, device=dev) if keep else None
@@ -205,9 +224,8 @@ def weighted_units_backward_quantized(
     backward = lib().bux_glu_backward_quantize_f32 if f32 else lib().bux_glu_backward_quantize
     _lib.check(backward(
         ptr(projected), ptr(weights), ptr(dh), ptr(filled), m, f, ctypes.byref(st), height,
-        ptr(dp), ptr(vals), ptr(scales), ptr(t_vals), ptr(t_scales), ptr(dw), ptr(ws), ws.numel(),
-        stream()))
-    return Tiled(vals, scales), Tiled(t_vals, t_scales), dw, dp
+        ptr(dp), *_ptrs(row), *_ptrs(col), ptr(dw), ptr(ws), ws.numel(), stream()))
+    return row, col, dw, dp
 
 
 def weighted_units_backward(ffn: Ffn, projected: torch.Tensor, weights: torch.Tensor,
@@ -600,8 +618,10 @@ def experts_forward(
         pv = projected.view(m, f, p)
         if fprop or wgrad:
             with span("activation + quantize h"):
+                # h along f for the down fprop, h^T along m for the down wgrad
                 h_k, h_m, h = weighted_units_quantized(ffn, pv, act_weights, filled, height,
-                                                       intermediates or not (fprop and wgrad))
+                                                       intermediates or not (fprop and wgrad),
+                                                       rows=fprop, columns=wgrad)
         else:
             with span("activation"):
                 h = weighted_units(ffn, pv, act_weights, filled)
@@ -727,7 +747,7 @@ def experts_backward(saved: Saved, dy: torch.Tensor, up: torch.Tensor, down: tor
         keep = intermediates or up_bias is not None or not (dgrad and wgrad)
         with span("activation backward + quantize dp"):
             dp_n, dp_m, d_rows_w, dp = weighted_units_backward_quantized(
-                ffn, pv, act_weights, dh, filled, height, keep)
+                ffn, pv, act_weights, dh, filled, height, keep, rows=dgrad, columns=wgrad)
     else:
         with span("activation backward"):
             dp, d_rows_w = weighted_units_backward(ffn, pv, act_weights, dh, filled)

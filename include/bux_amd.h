@@ -479,10 +479,12 @@ int bux_expert_norm_backward_f32(const float* dy, const int32_t* index, int32_t 
  *   rows' weights (m);
  *   values/scales: h along its rows (K = f rounded up to 128), height rows;
  *   t_values/t_scales: h^T along its rows (K = height rounded up to 128), f rows;
+ *   either copy NULL where its GEMM does not multiply in MXFP8 (at least one given);
  *   h: NULL, or bfloat16 [m, f] to store h as well.
  * bux_glu_backward_quantize: d projected (m, p f; p = 2 gated, 1 plain) of projected,
  *   the weights and dh (m, f); values/scales along its rows (K = p f rounded up to
- *   128), t_values/t_scales of its transpose; d_projected: NULL, or bfloat16 [m, p f]
+ *   128), t_values/t_scales of its transpose (either NULL, as above); d_projected: NULL,
+ *   or bfloat16 [m, p f]
  *   to store it as well; d_weights [m] as bux_glu_backward's (its float32 sum taken in
  *   another fixed order). workspace: bux_glu_backward_quantize_workspace_size(m, f)
  *   bytes.

@@ -120,6 +120,19 @@ def test_activation_forward_backward_and_their_quantized_copies(lib, case):
         v, sc = untiled(tiled, cols)
         np.testing.assert_array_equal(v, want.values)
         np.testing.assert_array_equal(sc, want.scales)
+    # one copy asked for (a pass outside MXFP8 takes none of the other): the same bytes,
+    # and the weights' gradient bit for bit
+    for rows, columns in ((True, False), (False, True)):
+        k1, m1, _ = moe.weighted_units_quantized(g, gp, gw, fg, height, rows=rows, columns=columns)
+        n1, pm1, dw1, _ = moe.weighted_units_backward_quantized(g, gp, gw, gdh, fg, height,
+                                                                rows=rows, columns=columns)
+        torch.cuda.synchronize()
+        assert (k1 is None) != rows and (m1 is None) != columns
+        assert (n1 is None) != rows and (pm1 is None) != columns
+        for one, both in ((k1, h_k), (m1, h_m), (n1, dp_n), (pm1, dp_m)):
+            if one is not None:
+                assert torch.equal(one.values, both.values) and torch.equal(one.scales, both.scales)
+        assert torch.equal(dw1, dw2)
 
 
 def _sorted_case(rng, t, k, e, skew_empty=True):
