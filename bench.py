@@ -345,7 +345,9 @@ def other_config(t, d, e, k, f, act, seed, skew, fmt, sample, device, reps=10):
     """One config's MXFP8 forward (the layer as training runs it: x^T and h^T quantized
     for the wgrad too), timed as HIP graph replays, with the weights quantized inside
     (`ms`) and given already in MXFP8 (`ms_weights_given`: the reference's `quantized`,
-    quantized once an optimizer step). Router logits N(0,1), plus a
+    quantized once an optimizer step); and with only the fprop pass in MXFP8
+    (`ms_fprop_pass_only`: one MXFP8 copy of each operand, the weights quantized inside,
+    what the bfloat16 dgrad and wgrad take kept in bfloat16). Router logits N(0,1), plus a
     per-expert bias N(0, 0.5) (config 4), softmax, top-k, normalised; config 5's picks
     built from Zipf(1.2) loads (`zipf_picks`), each token's k weights a softmax of
     N(0, 1) draws."""
@@ -405,6 +407,13 @@ def other_config(t, d, e, k, f, act, seed, skew, fmt, sample, device, reps=10):
                                                         quantized=given))
         out.update(ms_weights_given=round(ms_given, 4),
                    tflops_weights_given=round(flops / (ms_given * 1e-3) / 1e12, 1))
+        # only the fprop pass in MXFP8 (passes=("fprop",), grouped_blockscaled.py:180-183):
+        # one MXFP8 copy each of x, W and h, along the GEMMs' K; x's rows and h kept in
+        # bfloat16 for the dgrad and wgrad, which then multiply in bfloat16
+        ms_fprop = graph_ms(lambda: moe.experts_forward(z, idx, weights, up, down, ffn, fmt,
+                                                        passes=("fprop",)))
+        out.update(ms_fprop_pass_only=round(ms_fprop, 4),
+                   tflops_fprop_pass_only=round(flops / (ms_fprop * 1e-3) / 1e12, 1))
     out.update(largest_group_share=round(float(loads.max()) / m, 4),
                empty_experts=int((loads == 0).sum()))
     return out
