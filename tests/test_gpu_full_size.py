@@ -59,12 +59,12 @@ def _inputs(cfg, seed):
     return z.to(torch.bfloat16), idx, w, up, down, dy
 
 
-def _layer(z, idx, w, up, down, dy, ffn):
+def _layer(z, idx, w, up, down, dy, ffn, **kw):
     from bux_amd import moe
-    out, saved = moe.experts_forward(z, idx, w, up, down, ffn)
-    grads = moe.experts_backward(saved, dy, up, down, ffn)
+    out, saved = moe.experts_forward(z, idx, w, up, down, ffn, **kw)
+    grads = moe.experts_backward(saved, dy, up, down, ffn, **kw)
     del saved
-    return out, grads
+    return out, {key: g for key, g in grads.items() if g is not None}
 
 
 def _bits(x):
@@ -106,6 +106,38 @@ def test_a_float32_layers_gradients_double_with_dy_and_its_forward_repeats(lib, 
     assert out1.dtype == torch.float32
     assert torch.equal(out1.view(torch.int32), out2.view(torch.int32)), "the forward differs"
     assert torch.isfinite(out1).all()
+    for key in g1:
+        assert g1[key].dtype == torch.float32, key
+        assert torch.isfinite(g1[key]).all(), key
+        assert g1[key].abs().max() > 0, key
+        assert torch.equal((g1[key] * 2).view(torch.int32), g2[key].view(torch.int32)), \
+            f"d{key} is not doubled exactly"
+
+
+def test_a_float32_layer_with_biases_and_a_norm_at_full_size(lib):
+    """Config 3 in float32 with the experts' up and down biases and a layernorm of their
+    outputs (gain and bias, moe.py:857-872): the forward repeats bit for bit and doubling
+    dy doubles every gradient exactly, the biases' and the norm's included (each is
+    linear in dy, and doubling is exact in float32)."""
+    from bux_amd import moe
+    cfg = CONFIGS["config3"]
+    z, idx, w, up, down, dy = (x.float() if x.dtype == torch.bfloat16 else x
+                               for x in _inputs(cfg, 5))
+    e, d, f = cfg["e"], cfg["d"], cfg["f"]
+    g = torch.Generator(device="cuda").manual_seed(6)
+    kw = dict(up_bias=torch.randn(e, f, 2, generator=g, device="cuda") * 0.5,
+              down_bias=torch.randn(e, d, generator=g, device="cuda") * 0.5,
+              norm=moe.ExpertNorm("layernorm", 1e-5, True, True),
+              norm_scale=1 + 0.3 * torch.randn(d, generator=g, device="cuda"),
+              norm_bias=0.2 * torch.randn(d, generator=g, device="cuda"))
+    ffn = moe.Ffn(*cfg["act"])
+    announce("full size float32, biases and a norm", "dy and 2 dy")
+    out1, g1 = _layer(z, idx, w, up, down, dy, ffn, **kw)
+    out2, g2 = _layer(z, idx, w, up, down, dy * 2, ffn, **kw)
+    torch.cuda.synchronize()
+    assert out1.dtype == torch.float32 and torch.isfinite(out1).all()
+    assert torch.equal(out1.view(torch.int32), out2.view(torch.int32)), "the forward differs"
+    assert {"up_bias", "down_bias", "norm_scale", "norm_bias"} <= set(g1)
     for key in g1:
         assert g1[key].dtype == torch.float32, key
         assert torch.isfinite(g1[key]).all(), key
